@@ -1,0 +1,71 @@
+/*
+ * qlm_engine.h - C ABI of the C++17 host engine (quicklm_amd/libqlm_engine.so).
+ *
+ * The engine is the MI355X counterpart of the reference's DecoderModel
+ * (src/model/model.hpp:16-91): it loads a Qwen3.5-hybrid checkpoint from a
+ * directory of safetensors + config.json, keeps every weight and state on
+ * the GPU, and runs the decode loop as a replayed hipGraph. It reaches the
+ * GPU only through libqlm_hip.so (qlm_hip.h).
+ *
+ * All functions return 0 on success or a nonzero code; qlm_engine_last_error()
+ * then holds the message (the reference throws std::runtime_error with the
+ * same texts, e.g. "context length exceeded max_seq_len (...)").
+ */
+#ifndef QLM_ENGINE_H
+#define QLM_ENGINE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+const char* qlm_engine_last_error(void);
+
+/* DecoderModel::load(dir, max_seq_len, precision) (model.cpp:34-131) plus a
+ * batch capacity. precision "int8" = Q8_0 group-32 scales (reference
+ * parity), "int8_row" = one scale per output row. */
+int qlm_engine_load(const char* dir, int max_seq_len, int max_batch, const char* precision,
+                    void** handle);
+int qlm_engine_free(void* handle);
+
+/* vocab, hidden, layers, group size (0 = per row), max_seq, max_batch. */
+int qlm_engine_info(void* handle, int* vocab, int* hidden, int* layers, int* group,
+                    int* max_seq, int* max_batch, size_t* weight_bytes);
+
+/* DecoderModel::reset_states (model.cpp:133-137). */
+int qlm_engine_reset(void* handle);
+
+/* DecoderModel::forward(token, logits, ctx) with ctx.pos = pos
+ * (model.cpp:151-211), sequence 0; logits copied to a host array [vocab]. */
+int qlm_engine_forward(void* handle, int token, int pos, float* logits);
+
+/* Greedy generation with the CLI convention (main.cpp:574-690): prompts
+ * [B, n] host int32; out [B, n_new]; timings in seconds (prefill = the n-1
+ * prompt forwards, decode = the n_new steps). use_graph 0 launches eagerly. */
+int qlm_engine_generate(void* handle, const int* prompts, int B, int n, int n_new, int* out,
+                        double* prefill_s, double* decode_s, int use_graph);
+
+/* Logits of sequence b after the last step, host array [vocab]. */
+int qlm_engine_last_logits(void* handle, int b, float* logits);
+
+/* Kernel launches in one captured decode step of batch B (after a step ran). */
+int qlm_engine_kernels_per_step(void* handle);
+
+/* ---- synthetic checkpoints (no reference counterpart) ----
+ * Deterministic counter-based generators used to write random-init weights
+ * of a given architecture: element i of a tensor with seed s depends only on
+ * (s, i), so a tensor can be filled in parallel and identically on any host.
+ * normal: mean + std * N(0,1) (Box-Muller over splitmix64 uniforms, double
+ * precision, rounded to the output type); uniform: lo + (hi-lo)*U[0,1). */
+int qlm_synth_normal_f32(float* out, size_t n, uint64_t seed, float mean, float std_dev);
+int qlm_synth_normal_bf16(uint16_t* out, size_t n, uint64_t seed, float mean, float std_dev);
+int qlm_synth_uniform_f32(float* out, size_t n, uint64_t seed, float lo, float hi);
+uint64_t qlm_synth_tensor_seed(uint64_t base, const char* name);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QLM_ENGINE_H */

@@ -1,0 +1,194 @@
+/*
+ * qlm_hip.h - C ABI of the MI355X (gfx950) decode kernels.
+ *
+ * Every compute entry point replaces one operator of the reference CPU path
+ * (treesoft-ai/quicklm); the comment above each one names the reference
+ * interface it stands in for (file:line in the reference tree).
+ *
+ * Conventions
+ *   - All tensor arguments are DEVICE pointers, row-major, fp32 unless noted.
+ *   - `stream` is a hipStream_t passed as void* (NULL = the null stream).
+ *   - Every call is asynchronous, allocates nothing, never synchronises the
+ *     host and reads no device memory back, so a sequence of calls can be
+ *     captured into a hipGraph.
+ *   - Return value: QLM_OK (0) or a negative QLM_ERR_* code; on a HIP error
+ *     the HIP error code is returned as a positive number. Shape checks are
+ *     done here, on the host, before any launch: kernels trust their shapes.
+ *   - int8 weights use the reference's Q8_0 layout (tensor.hpp:30-41):
+ *     q[n*K + k] int8, scale[n*ceil(K/G) + k/G] fp32, with the group size G
+ *     either 32 (reference block size) or K (one scale per output row).
+ */
+#ifndef QLM_HIP_H
+#define QLM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QLM_OK 0
+#define QLM_ERR_ARG (-1)      /* null pointer or non-positive size */
+#define QLM_ERR_SHAPE (-2)    /* shape the kernels do not support */
+#define QLM_ERR_NO_DEVICE (-3)
+
+/* ---- runtime plumbing (no reference counterpart: the reference is host-only) ---- */
+
+const char* qlm_error_string(int status);
+int qlm_device_count(int* count);
+int qlm_set_device(int device);
+int qlm_device_name(char* buf, int len);
+int qlm_malloc(void** ptr, size_t bytes);
+int qlm_free(void* ptr);
+int qlm_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream);
+int qlm_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream);
+int qlm_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream);
+/* Fill with a byte value by a kernel (capturable; no hipMemset node). */
+int qlm_fill_u8(void* dst, uint8_t value, size_t bytes, void* stream);
+int qlm_stream_create(void** stream);
+int qlm_stream_destroy(void* stream);
+int qlm_stream_sync(void* stream);
+int qlm_device_sync(void);
+int qlm_event_create(void** event);
+int qlm_event_destroy(void* event);
+int qlm_event_record(void* event, void* stream);
+int qlm_event_elapsed_ms(float* ms, void* start, void* stop);
+int qlm_graph_begin(void* stream);
+int qlm_graph_end(void* stream, void** graph_exec);
+int qlm_graph_launch(void* graph_exec, void* stream);
+int qlm_graph_destroy(void* graph_exec);
+
+/* ---- A2: load-time int8 quantiser --------------------------------------
+ * Replaces st_quantize_row_f32 / st_quantize_row_bf16 driven by
+ * SafetensorsLoader::get_tensor_keep_int8 (safetensors.cpp:296-391, :517-585).
+ * Per group of G elements: m = max|x|; s = m > 0 ? m/127 : 1; inv = 1/s;
+ * q = clamp(round-half-even(x*inv), -127, 127). IEEE division, no FMA: the
+ * bytes and scales are bit-identical to the reference's IEEE semantics.
+ * K must be a multiple of G; G is 32 or K. */
+int qlm_quantize_q8_f32(const float* w, int rows, int K, int group, int8_t* q, float* scales,
+                        void* stream);
+int qlm_quantize_q8_bf16(const uint16_t* w, int rows, int K, int group, int8_t* q,
+                         float* scales, void* stream);
+
+/* ---- A3/A4: int8 weight-only matmul  y = x . (q*s)^T ----------------------
+ * Replaces math::matmul's int8 branch (math_ops.hpp:92, math_ops.cpp:820-900,
+ * int8_gemv_range :558-579). x is [M, ldx], y is [M, ldy], weights [N, K].
+ * fp32 accumulation. M <= 64; K a multiple of 16 (of 32 when G = 32). */
+int qlm_gemv_i8(const float* x, int ldx, const int8_t* q, const float* scales, int group,
+                float* y, int ldy, int M, int N, int K, void* stream);
+
+/* Fused forms used by the decode step (same arithmetic as the unfused
+ * reference sequence, one launch instead of two or three):
+ *   _rmsnorm: x is first replaced by rms_norm(x, norm_w, eps) (zero-centred
+ *             gain, math_ops.cpp:1055-1072) -- RMSNorm::forward + matmul.
+ *   _residual: y[m,n] += result  -- matmul + elementwise_add into the
+ *             residual stream (modules.hpp:225-240).
+ *   _swiglu:  weights hold 2F rows, gate rows [0,F) then up rows [F,2F);
+ *             y[m,n] = silu(gate_n) * up_n for n < F -- SwiGLU_MLP::forward
+ *             (modules.hpp:139-167). N here is F. */
+int qlm_gemv_i8_rmsnorm(const float* x, int ldx, const float* norm_w, float eps,
+                        const int8_t* q, const float* scales, int group, float* y, int ldy,
+                        int M, int N, int K, void* stream);
+int qlm_gemv_i8_residual(const float* x, int ldx, const int8_t* q, const float* scales,
+                         int group, float* y, int ldy, int M, int N, int K, void* stream);
+int qlm_gemv_i8_swiglu_rmsnorm(const float* x, int ldx, const float* norm_w, float eps,
+                               const int8_t* q, const float* scales, int group, float* y,
+                               int ldy, int M, int F, int K, void* stream);
+
+/* ---- A5/A6/A7: elementwise ------------------------------------------------ */
+/* math::rms_norm (math_ops.cpp:1055-1072): y = x*rsqrt(mean(x^2)+eps)*(1+w). */
+int qlm_rms_norm(const float* x, const float* w, float* y, int rows, int n, float eps,
+                 void* stream);
+/* math::add_rms_norm (math_ops.cpp:1133-1172): res += delta; y = rms_norm(res). */
+int qlm_add_rms_norm(float* res, const float* delta, const float* w, float* y, int rows, int n,
+                     float eps, void* stream);
+/* math::silu_mul (math_ops.cpp:1122-1129): a = a/(1+exp(-a)) * b. */
+int qlm_silu_mul(float* a, const float* b, int n, void* stream);
+
+/* ---- A8: partial NeoX RoPE --------------------------------------------------
+ * math::apply_rope_neox (math_ops.cpp:1237-1289) on t[num_heads, head_stride]
+ * (the first head_dim values of each head row are the head). cos/sin come
+ * from a host-built table [n_pos, rot/2] (qlm_rope_table layout); the
+ * position is read from pos[0] on the device. */
+int qlm_rope_neox(float* t, int num_heads, int head_stride, int rot_dim, const float* cos_tab,
+                  const float* sin_tab, const int* pos, void* stream);
+
+/* ---- A10: causal depthwise conv1d step, tap-major ring ---------------------
+ * math::causal_conv1d_update_tapmajor (math_ops.cpp:1321-1364). state is
+ * [kernel_size-1, conv_dim], weight_t is [kernel_size, conv_dim]. */
+int qlm_conv1d_update(const float* in, float* state, int oldest_tap, const float* weight_t,
+                      float* out, int conv_dim, int kernel_size, void* stream);
+
+/* ---- A11/A12: Gated DeltaNet recurrent step (isolated) ----------------------
+ * The recurrence inlined in Qwen3_5GatedDeltaNet::forward (attention.cpp:
+ * 498-571), per sequence b and head h, state S[b,h] is [d, d] (key i, value j):
+ *   S <- decay*S; kv = k.S; S += beta*k (v - kv)^T; o = (q.S)/sqrt(d).
+ * q,k,v,o are [B, H, d]; decay, beta are [B, H]. d = 128. */
+int qlm_gated_delta_step(const float* q, const float* k, const float* v, const float* decay,
+                         const float* beta, float* state, float* out, int B, int H, int d,
+                         void* stream);
+
+/* ---- A10-A12 fused: the whole DeltaNet mixer core of one decode step -------
+ * Qwen3_5GatedDeltaNet::forward (attention.cpp:414-590) from the projection
+ * output to the gated head output, for B sequences:
+ *   proj[b] = [qkv (3*H*d) | z (H*d) | b (H) | a (H)] (row stride ldp);
+ *   conv1d on qkv with the tap-major ring state conv_state[b] [3, 3*H*d]
+ *   (oldest tap row = pos[b] % 3), SiLU, per-head L2 norm of q and k,
+ *   decay = exp(-exp(A_log)*softplus(a+dt_bias)), beta = sigmoid(b),
+ *   recurrence on state[b] [H, d, d], head RMSNorm (gain norm_w, eps 1e-6),
+ *   SiLU(z) gate. Output out[b] is [H*d] (row stride ldo). d = 128,
+ *   conv kernel 4. pos may be NULL (then the ring index is 0 for all b). */
+int qlm_deltanet_decode(const float* proj, int ldp, float* conv_state, const float* conv_w_t,
+                        const float* A_log, const float* dt_bias, const float* norm_w,
+                        float* state, const int* pos, float* out, int ldo, int B, int H, int d,
+                        void* stream);
+
+/* ---- A8/A9: GQA decode attention over a contiguous KV cache -----------------
+ * Qwen3_5Attention::forward steps 2-6 (attention.cpp:160-227) for B
+ * sequences at positions pos[b]:
+ *   qkv[b] = [q+gate (n_q * 2*hd if gated else n_q*hd) | k (n_kv*hd) | v (n_kv*hd)]
+ *   QK-norm (zero-centred, eps 1e-6), partial NeoX RoPE from the table,
+ *   k/v written to the cache at pos[b], softmax(q.K^T/sqrt(hd)) . V over
+ *   positions 0..pos[b], sigmoid(gate) output gate when gated.
+ * Cache layout [B, max_seq, n_kv, hd] fp32 (position-major, as the reference,
+ * attention.cpp:134-135). out[b] is [n_q*hd]. work is a device workspace of
+ * qlm_gqa_workspace_bytes(...) bytes. */
+size_t qlm_gqa_workspace_bytes(int B, int n_q, int hd, int max_seq);
+int qlm_gqa_decode(float* qkv, int ldqkv, const float* q_norm, const float* k_norm,
+                   const float* cos_tab, const float* sin_tab, int rot_dim, float* k_cache,
+                   float* v_cache, int max_seq, const int* pos, float* out, int ldo, int B,
+                   int n_q, int n_kv, int hd, int gated, void* work, void* stream);
+
+/* Isolated attention core (no norm/RoPE/write): out[b, h] = softmax(q.K^T *
+ * scale) . V over the first ctx positions of a [B, max_seq, n_kv, hd] cache,
+ * kv_dtype 0 = fp32, 1 = bf16. q, out are [B, n_q, hd] fp32. */
+int qlm_attention_decode(const float* q, const void* k_cache, const void* v_cache,
+                         int kv_dtype, int max_seq, int ctx, float* out, int B, int n_q,
+                         int n_kv, int hd, void* work, void* stream);
+
+/* ---- A14: greedy sampling ---------------------------------------------------
+ * DecoderModel::sample with temperature <= 0 (model.cpp:263-274): index of
+ * the first maximum (strict >, lowest index wins ties) of each of the B rows
+ * of logits [B, ldl] over n entries. idx is [B] int32. */
+int qlm_argmax(const float* logits, int ldl, int n, int B, int* idx, void* work, void* stream);
+size_t qlm_argmax_workspace_bytes(int B, int n);
+
+/* ---- A14/A15: device-resident greedy loop ------------------------------------
+ * The CLI's decode loop (main.cpp:659-676) with the token stream kept on the
+ * device: argmax as qlm_argmax, then for each b with p = pos[b]: if p+1 is
+ * past the prompt (p+1 >= prompt_len[b]) the winner is stored as
+ * tokens[b, p+1]; then pos[b] = p+1. tokens is [B, ld_tokens] int32. */
+int qlm_greedy_advance(const float* logits, int ldl, int n, int B, void* work, int* tokens,
+                       int ld_tokens, int* pos, const int* prompt_len, void* stream);
+
+/* Embedding gather (model.cpp:157-164, F32 table): out[b] = table[tokens[b,
+ * pos[b]]] for a [vocab, H] fp32 table (pos NULL: tokens[b, 0]). */
+int qlm_embed_tokens(const float* table, int vocab, int H, const int* tokens, int ld_tokens,
+                     const int* pos, float* out, int ldo, int B, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QLM_HIP_H */

@@ -1,0 +1,105 @@
+// extern "C" face of the host engine (include/qlm_engine.h). Exceptions never
+// cross the ABI: they become a nonzero return plus qlm_engine_last_error().
+
+#include <cstring>
+#include <exception>
+#include <string>
+
+#include "model.hpp"
+#include "qlm_engine.h"
+
+namespace {
+thread_local std::string g_err;
+
+template <typename F>
+int guarded(F&& f) {
+    try {
+        f();
+        g_err.clear();
+        return 0;
+    } catch (const std::exception& e) {
+        g_err = e.what();
+    } catch (...) {
+        g_err = "unknown error";
+    }
+    return 1;
+}
+
+qlm::DecoderModel* M(void* h) {
+    if (!h) throw std::runtime_error("null engine handle");
+    return static_cast<qlm::DecoderModel*>(h);
+}
+}  // namespace
+
+extern "C" {
+
+const char* qlm_engine_last_error(void) { return g_err.c_str(); }
+
+int qlm_engine_load(const char* dir, int max_seq_len, int max_batch, const char* precision,
+                    void** handle) {
+    return guarded([&] {
+        if (!dir || !precision || !handle) throw std::runtime_error("null argument");
+        *handle = nullptr;
+        auto* m = new qlm::DecoderModel();
+        try {
+            m->load(dir, max_seq_len, precision, max_batch);
+        } catch (...) {
+            delete m;
+            throw;
+        }
+        *handle = m;
+    });
+}
+
+int qlm_engine_free(void* handle) {
+    return guarded([&] { delete static_cast<qlm::DecoderModel*>(handle); });
+}
+
+int qlm_engine_info(void* handle, int* vocab, int* hidden, int* layers, int* group, int* max_seq,
+                    int* max_batch, size_t* weight_bytes) {
+    return guarded([&] {
+        auto* m = M(handle);
+        const auto& c = m->config();
+        if (vocab) *vocab = c.vocab_size;
+        if (hidden) *hidden = c.hidden_size;
+        if (layers) *layers = c.num_hidden_layers;
+        if (group) *group = m->group();
+        if (max_seq) *max_seq = m->max_seq();
+        if (max_batch) *max_batch = m->max_batch();
+        if (weight_bytes) *weight_bytes = m->weight_bytes();
+    });
+}
+
+int qlm_engine_reset(void* handle) { return guarded([&] { M(handle)->reset_states(); }); }
+
+int qlm_engine_forward(void* handle, int token, int pos, float* logits) {
+    return guarded([&] {
+        if (!logits) throw std::runtime_error("null logits");
+        M(handle)->forward(token, pos, logits);
+    });
+}
+
+int qlm_engine_generate(void* handle, const int* prompts, int B, int n, int n_new, int* out,
+                        double* prefill_s, double* decode_s, int use_graph) {
+    return guarded([&] {
+        if (!prompts || !out) throw std::runtime_error("null argument");
+        qlm::GenStats st;
+        M(handle)->generate(prompts, B, n, n_new, out, &st, use_graph != 0);
+        if (prefill_s) *prefill_s = st.prefill_s;
+        if (decode_s) *decode_s = st.decode_s;
+    });
+}
+
+int qlm_engine_last_logits(void* handle, int b, float* logits) {
+    return guarded([&] { M(handle)->last_logits(b, logits); });
+}
+
+int qlm_engine_kernels_per_step(void* handle) {
+    try {
+        return M(handle)->kernels_per_step();
+    } catch (...) {
+        return -1;
+    }
+}
+
+}  // extern "C"

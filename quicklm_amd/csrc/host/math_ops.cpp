@@ -1,0 +1,120 @@
+#include "math_ops.hpp"
+
+#include <cmath>
+#include <stdexcept>
+#include <string>
+
+#include "device.hpp"
+
+namespace qlm {
+namespace math {
+
+namespace {
+void* g_stream = nullptr;
+
+void need(bool ok, const char* what) {
+    if (!ok) throw std::runtime_error(std::string("math: ") + what);
+}
+
+void check_int8(const Tensor& B) {
+    need(B.is_int8(), "weight operand must be int8 on the device (bf16/int4 forms are not built)");
+    need(B.shape.size() == 2, "int8 weight must be [N, K]");
+}
+}  // namespace
+
+void set_stream(void* s) { g_stream = s; }
+void* stream() { return g_stream; }
+
+void matmul(const Tensor& A, const Tensor& B, Tensor& C, bool transpose_B) {
+    need(transpose_B, "only the x * W^T form exists on the device");
+    check_int8(B);
+    const int64_t K = A.cols(), M = A.rows(), N = B.shape[0];
+    need(B.shape[1] == K, "matmul: K mismatch");
+    need(C.cols() >= N || C.row_stride() >= N, "matmul: output too small");
+    check(qlm_gemv_i8(A.data, (int)A.row_stride(), B.int8_data, B.int8_scales, B.int8_group, C.data,
+                      (int)C.row_stride(), (int)M, (int)N, (int)K, g_stream),
+          "qlm_gemv_i8");
+}
+
+void matmul_rmsnorm(const Tensor& A, const Tensor& norm_w, float eps, const Tensor& B, Tensor& C) {
+    check_int8(B);
+    const int64_t K = A.cols(), M = A.rows(), N = B.shape[0];
+    need(B.shape[1] == K && norm_w.size() == K, "matmul_rmsnorm: K mismatch");
+    check(qlm_gemv_i8_rmsnorm(A.data, (int)A.row_stride(), norm_w.data, eps, B.int8_data,
+                              B.int8_scales, B.int8_group, C.data, (int)C.row_stride(), (int)M,
+                              (int)N, (int)K, g_stream),
+          "qlm_gemv_i8_rmsnorm");
+}
+
+void matmul_residual(const Tensor& A, const Tensor& B, Tensor& residual) {
+    check_int8(B);
+    const int64_t K = A.cols(), M = A.rows(), N = B.shape[0];
+    need(B.shape[1] == K && residual.cols() == N, "matmul_residual: shape mismatch");
+    check(qlm_gemv_i8_residual(A.data, (int)A.row_stride(), B.int8_data, B.int8_scales,
+                               B.int8_group, residual.data, (int)residual.row_stride(), (int)M,
+                               (int)N, (int)K, g_stream),
+          "qlm_gemv_i8_residual");
+}
+
+void matmul_swiglu_rmsnorm(const Tensor& A, const Tensor& norm_w, float eps, const Tensor& B,
+                           Tensor& C) {
+    check_int8(B);
+    const int64_t K = A.cols(), M = A.rows(), F = B.shape[0] / 2;
+    need(B.shape[0] % 2 == 0 && B.shape[1] == K && C.cols() == F, "matmul_swiglu: shape mismatch");
+    check(qlm_gemv_i8_swiglu_rmsnorm(A.data, (int)A.row_stride(), norm_w.data, eps, B.int8_data,
+                                     B.int8_scales, B.int8_group, C.data, (int)C.row_stride(),
+                                     (int)M, (int)F, (int)K, g_stream),
+          "qlm_gemv_i8_swiglu_rmsnorm");
+}
+
+void rms_norm(const Tensor& input, const Tensor& weight, Tensor& output, float eps) {
+    const int64_t n = weight.size();
+    check(qlm_rms_norm(input.data, weight.data, output.data, (int)(input.size() / n), (int)n, eps,
+                       g_stream),
+          "qlm_rms_norm");
+}
+
+void add_rms_norm(Tensor& residual, const Tensor& delta, const Tensor& weight, Tensor& output,
+                  float eps) {
+    const int64_t n = weight.size();
+    check(qlm_add_rms_norm(residual.data, delta.data, weight.data, output.data,
+                           (int)(residual.size() / n), (int)n, eps, g_stream),
+          "qlm_add_rms_norm");
+}
+
+void silu_mul(Tensor& A, const Tensor& B) {
+    check(qlm_silu_mul(A.data, B.data, (int)A.size(), g_stream), "qlm_silu_mul");
+}
+
+void apply_rope_neox(Tensor& t, const int* d_pos, const float* cos_tab, const float* sin_tab,
+                     int rotary_dim) {
+    check(qlm_rope_neox(t.data, (int)t.rows(), (int)t.row_stride(), rotary_dim, cos_tab, sin_tab,
+                        d_pos, g_stream),
+          "qlm_rope_neox");
+}
+
+// Same float arithmetic as the reference's cached tables (math_ops.cpp:
+// 1255-1272): inv[i] = 1/powf(theta, 2i/rot); angle = (float)pos * inv[i].
+void rope_table(float theta, int rotary_dim, int n_pos, float* cos_tab, float* sin_tab) {
+    const int half = rotary_dim / 2;
+    std::vector<float> inv(half);
+    for (int i = 0; i < half; ++i)
+        inv[i] = 1.0f / std::pow(theta, (2.0f * i) / rotary_dim);
+    for (int p = 0; p < n_pos; ++p)
+        for (int i = 0; i < half; ++i) {
+            const float ang = p * inv[i];
+            cos_tab[(size_t)p * half + i] = std::cos(ang);
+            sin_tab[(size_t)p * half + i] = std::sin(ang);
+        }
+}
+
+void causal_conv1d_update_tapmajor(const float* input, float* state, int oldest_tap,
+                                   const float* weight_t, float* output, int conv_dim,
+                                   int kernel_size) {
+    check(qlm_conv1d_update(input, state, oldest_tap, weight_t, output, conv_dim, kernel_size,
+                            g_stream),
+          "qlm_conv1d_update");
+}
+
+}  // namespace math
+}  // namespace qlm

@@ -1,0 +1,387 @@
+#include "model.hpp"
+
+#include <algorithm>
+#include <chrono>
+#include <climits>
+#include <cstring>
+#include <stdexcept>
+
+#include "math_ops.hpp"
+#include "safetensors.hpp"
+
+namespace qlm {
+
+namespace {
+
+std::string lp(int i) { return "model.layers." + std::to_string(i) + "."; }
+
+std::vector<float> to_f32(const TensorView& t) {
+    std::vector<float> out((size_t)t.numel());
+    if (t.dtype == "F32") {
+        std::memcpy(out.data(), t.data, out.size() * sizeof(float));
+    } else if (t.dtype == "BF16") {
+        const uint16_t* src = reinterpret_cast<const uint16_t*>(t.data);
+        for (size_t i = 0; i < out.size(); ++i) {
+            uint32_t bits = (uint32_t)src[i] << 16;
+            std::memcpy(&out[i], &bits, 4);
+        }
+    } else {
+        throw std::runtime_error("Unsupported tensor datatype: " + t.dtype +
+                                 " (only F32 and BF16 supported)");
+    }
+    return out;
+}
+
+double now_s() {
+    return std::chrono::duration<double>(std::chrono::steady_clock::now().time_since_epoch()).count();
+}
+
+}  // namespace
+
+DecoderModel::~DecoderModel() {
+    for (auto& kv : graphs_) qlm_graph_destroy(kv.second);
+    if (stream_) qlm_stream_destroy(stream_);
+}
+
+void DecoderModel::alloc_linear(LinearI8& lin, int N, int K) {
+    lin.N = N;
+    lin.K = K;
+    lin.group = (group_ == 0) ? K : group_;
+    lin.q.alloc((size_t)N * K);
+    lin.s.alloc((size_t)N * lin.blocks_per_row() * sizeof(float));
+    weight_bytes_ += (size_t)N * K + (size_t)N * lin.blocks_per_row() * sizeof(float);
+}
+
+// Device-side equivalent of get_weight -> get_tensor_keep_int8
+// (weights.cpp:54-70, safetensors.cpp:517-585): the raw F32/BF16 rows are
+// uploaded and quantised on the GPU straight into rows [row_off, row_off+N).
+void DecoderModel::quantize_into(LinearI8& lin, int row_off, const std::string& name) {
+    TensorView t = ws_->get(name);
+    if (t.shape.size() != 2 || t.shape[1] != lin.K || row_off + t.shape[0] > lin.N)
+        throw std::runtime_error("weight '" + name + "' has an unexpected shape");
+    if (t.dtype != "F32" && t.dtype != "BF16")
+        throw std::runtime_error("Unsupported tensor datatype for '" + name + "': " + t.dtype +
+                                 " (only F32 and BF16 supported for int8 quantization)");
+    if (staging_.bytes() < t.nbytes) {
+        check(qlm_stream_sync(stream_), "sync");
+        staging_.alloc(t.nbytes);
+    }
+    check(qlm_memcpy_h2d(staging_.get(), t.data, t.nbytes, stream_), "upload");
+    const int rows = (int)t.shape[0];
+    int8_t* q = lin.q.get<int8_t>() + (size_t)row_off * lin.K;
+    float* s = lin.s.get<float>() + (size_t)row_off * lin.blocks_per_row();
+    if (t.dtype == "F32")
+        check(qlm_quantize_q8_f32(staging_.get<float>(), rows, lin.K, lin.group, q, s, stream_),
+              "quantize");
+    else
+        check(qlm_quantize_q8_bf16(staging_.get<uint16_t>(), rows, lin.K, lin.group, q, s, stream_),
+              "quantize");
+}
+
+void DecoderModel::upload_f32(DeviceBuffer& dst, const std::string& name, int64_t expect) {
+    TensorView t = ws_->get(name);
+    if (expect >= 0 && t.numel() != expect)
+        throw std::runtime_error("tensor '" + name + "' has " + std::to_string(t.numel()) +
+                                 " elements, expected " + std::to_string(expect));
+    std::vector<float> v = to_f32(t);
+    dst.alloc(v.size() * sizeof(float));
+    check(qlm_memcpy_h2d(dst.get(), v.data(), v.size() * sizeof(float), stream_), "upload");
+    check(qlm_stream_sync(stream_), "sync");  // v is freed on return
+}
+
+void DecoderModel::load(const std::string& dir, int max_seq_len, const std::string& precision,
+                        int max_batch) {
+    if (max_seq_len <= 0 || max_batch <= 0) throw std::runtime_error("load: bad sizes");
+    if (precision == "int8") group_ = 32;
+    else if (precision == "int8_row") group_ = 0;  // resolved per matrix to K
+    else throw std::runtime_error("load: precision must be int8 or int8_row, got " + precision);
+    cfg_ = parse_model_config(dir);
+    ws_ = std::make_unique<WeightStore>(dir);
+    max_seq_ = max_seq_len;
+    max_batch_ = max_batch;
+    check(qlm_stream_create(&stream_), "stream");
+    math::set_stream(stream_);
+
+    const int H = cfg_.hidden_size, F = cfg_.intermediate_size, L = cfg_.num_hidden_layers;
+    const int nh = cfg_.linear_num_heads, d = cfg_.linear_head_dim;
+    const int nq = cfg_.num_attention_heads, nkv = cfg_.num_key_value_heads, hd = cfg_.head_dim;
+    HD_ = nh * d;
+    PD_ = 4 * HD_ + 2 * nh;
+    QR_ = 0;
+    for (int i = 0; i < L; ++i)
+        if (!cfg_.is_linear(i)) {
+            QR_ = (int)ws_->get(lp(i) + "self_attn.q_proj.weight").shape[0];
+            break;
+        }
+    PQ_ = QR_ + 2 * nkv * hd;
+    CORE_ = std::max(HD_, nq * hd);
+
+    layers_.resize(L);
+    for (int i = 0; i < L; ++i) {
+        LayerWeights& w = layers_[i];
+        const std::string p = lp(i);
+        w.linear = cfg_.is_linear(i);
+        upload_f32(w.in_ln, p + "input_layernorm.weight", H);
+        upload_f32(w.post_ln, p + "post_attention_layernorm.weight", H);
+        if (w.linear) {
+            if (d != 128) throw std::runtime_error("DeltaNet head_dim must be 128");
+            alloc_linear(w.dn_in, PD_, H);
+            quantize_into(w.dn_in, 0, p + "linear_attn.in_proj_qkv.weight");
+            quantize_into(w.dn_in, 3 * HD_, p + "linear_attn.in_proj_z.weight");
+            quantize_into(w.dn_in, 4 * HD_, p + "linear_attn.in_proj_b.weight");
+            quantize_into(w.dn_in, 4 * HD_ + nh, p + "linear_attn.in_proj_a.weight");
+            alloc_linear(w.dn_out, H, HD_);
+            quantize_into(w.dn_out, 0, p + "linear_attn.out_proj.weight");
+            // conv1d.weight [3HD, 1, ks] -> tap-major [ks, 3HD]
+            TensorView cw = ws_->get(p + "linear_attn.conv1d.weight");
+            const int C = 3 * HD_;
+            const int ks = (int)cw.shape.back();
+            if (ks != 4 || cw.numel() != (int64_t)C * ks)
+                throw std::runtime_error("conv1d weight must be [3*H*d, 1, 4]");
+            std::vector<float> cv = to_f32(cw), ct((size_t)C * ks);
+            for (int c = 0; c < C; ++c)
+                for (int k = 0; k < ks; ++k) ct[(size_t)k * C + c] = cv[(size_t)c * ks + k];
+            w.conv_wt.alloc(ct.size() * sizeof(float));
+            check(qlm_memcpy_h2d(w.conv_wt.get(), ct.data(), ct.size() * 4, stream_), "upload");
+            check(qlm_stream_sync(stream_), "sync");
+            upload_f32(w.A_log, p + "linear_attn.A_log", nh);
+            upload_f32(w.dt_bias, p + "linear_attn.dt_bias", nh);
+            upload_f32(w.dn_norm, p + "linear_attn.norm.weight", d);
+        } else {
+            if (ws_->has(p + "self_attn.q_proj.bias"))
+                throw std::runtime_error("attention projection biases are not supported");
+            const int qr = (int)ws_->get(p + "self_attn.q_proj.weight").shape[0];
+            if (qr != QR_) throw std::runtime_error("q_proj rows differ between layers");
+            w.gated = (qr == 2 * nq * hd);
+            if (!w.gated && qr != nq * hd) throw std::runtime_error("q_proj has unexpected rows");
+            alloc_linear(w.at_qkv, PQ_, H);
+            quantize_into(w.at_qkv, 0, p + "self_attn.q_proj.weight");
+            quantize_into(w.at_qkv, qr, p + "self_attn.k_proj.weight");
+            quantize_into(w.at_qkv, qr + nkv * hd, p + "self_attn.v_proj.weight");
+            alloc_linear(w.at_o, H, nq * hd);
+            quantize_into(w.at_o, 0, p + "self_attn.o_proj.weight");
+            if (ws_->has(p + "self_attn.q_norm.weight")) {
+                upload_f32(w.q_norm, p + "self_attn.q_norm.weight", hd);
+                upload_f32(w.k_norm, p + "self_attn.k_norm.weight", hd);
+            }
+        }
+        alloc_linear(w.gate_up, 2 * F, H);
+        quantize_into(w.gate_up, 0, p + "mlp.gate_proj.weight");
+        quantize_into(w.gate_up, F, p + "mlp.up_proj.weight");
+        alloc_linear(w.down, H, F);
+        quantize_into(w.down, 0, p + "mlp.down_proj.weight");
+    }
+    upload_f32(final_norm_, "model.norm.weight", H);
+    // Embedding gathered as fp32 (model.cpp:157-164); tied lm_head is the
+    // int8-quantised embedding (model.cpp:116-120).
+    TensorView et = ws_->get("model.embed_tokens.weight");
+    if (et.shape.size() != 2 || et.shape[1] != H) throw std::runtime_error("embed_tokens shape");
+    const int V = (int)et.shape[0];
+    upload_f32(embed_, "model.embed_tokens.weight", (int64_t)V * H);
+    if (ws_->has("lm_head.weight")) {
+        const int Vh = (int)ws_->get("lm_head.weight").shape[0];
+        alloc_linear(lm_head_, Vh, H);
+        quantize_into(lm_head_, 0, "lm_head.weight");
+    } else {
+        alloc_linear(lm_head_, V, H);
+        check(qlm_quantize_q8_f32(embed_.get<float>(), V, H, lm_head_.group, lm_head_.q.get<int8_t>(),
+                                  lm_head_.s.get<float>(), stream_),
+              "quantize lm_head");
+    }
+    cfg_.vocab_size = lm_head_.N;  // model.cpp:123
+    check(qlm_stream_sync(stream_), "sync");
+    staging_.release();
+
+    // RoPE table for every position the cache can hold.
+    const int rot = cfg_.rotary_dim();
+    if (QR_ > 0) {
+        std::vector<float> ct((size_t)max_seq_ * (rot / 2)), st(ct.size());
+        math::rope_table(cfg_.rope_theta, rot, max_seq_, ct.data(), st.data());
+        rope_cos_.alloc(ct.size() * 4);
+        rope_sin_.alloc(st.size() * 4);
+        check(qlm_memcpy_h2d(rope_cos_.get(), ct.data(), ct.size() * 4, stream_), "upload");
+        check(qlm_memcpy_h2d(rope_sin_.get(), st.data(), st.size() * 4, stream_), "upload");
+        check(qlm_stream_sync(stream_), "sync");
+    }
+
+    // Per-sequence state and activations for max_batch sequences.
+    const size_t B = (size_t)max_batch_;
+    for (int i = 0; i < L; ++i) {
+        if (cfg_.is_linear(i)) {
+            conv_state_.emplace_back(B * 3 * 3 * HD_ * sizeof(float));
+            dn_state_.emplace_back(B * nh * d * d * sizeof(float));
+        } else {
+            k_cache_.emplace_back(B * max_seq_ * nkv * hd * sizeof(float));
+            v_cache_.emplace_back(B * max_seq_ * nkv * hd * sizeof(float));
+        }
+    }
+    ld_tokens_ = max_seq_ + 1;
+    tokens_.alloc(B * ld_tokens_ * sizeof(int));
+    pos_.alloc(B * sizeof(int));
+    prompt_len_.alloc(B * sizeof(int));
+    const int Pmax = std::max(PD_, PQ_);
+    h_.alloc(B * H * sizeof(float));
+    proj_.alloc(B * Pmax * sizeof(float));
+    core_.alloc(B * CORE_ * sizeof(float));
+    act_.alloc(B * F * sizeof(float));
+    logits_.alloc(B * cfg_.vocab_size * sizeof(float));
+    argmax_work_.alloc(qlm_argmax_workspace_bytes((int)B, cfg_.vocab_size));
+    if (QR_ > 0) attn_work_.alloc(qlm_gqa_workspace_bytes((int)B, nq, hd, max_seq_));
+    reset_states();
+}
+
+void DecoderModel::reset_states() {
+    for (auto& b : conv_state_) check(qlm_fill_u8(b.get(), 0, b.bytes(), stream_), "fill");
+    for (auto& b : dn_state_) check(qlm_fill_u8(b.get(), 0, b.bytes(), stream_), "fill");
+    for (auto& b : k_cache_) check(qlm_fill_u8(b.get(), 0, b.bytes(), stream_), "fill");
+    for (auto& b : v_cache_) check(qlm_fill_u8(b.get(), 0, b.bytes(), stream_), "fill");
+    check(qlm_fill_u8(tokens_.get(), 0, tokens_.bytes(), stream_), "fill");
+    check(qlm_fill_u8(pos_.get(), 0, pos_.bytes(), stream_), "fill");
+    check(qlm_stream_sync(stream_), "sync");
+}
+
+// One decode step for sequences [0, B): the forward of DecoderModel::forward
+// (model.cpp:151-199) with every layer's elementwise work fused into the
+// projections, followed by greedy sampling and the position advance.
+void DecoderModel::enqueue_step(int B) {
+    math::set_stream(stream_);
+    const int H = cfg_.hidden_size, F = cfg_.intermediate_size, V = cfg_.vocab_size;
+    const int nh = cfg_.linear_num_heads, d = cfg_.linear_head_dim;
+    const int nq = cfg_.num_attention_heads, nkv = cfg_.num_key_value_heads, hd = cfg_.head_dim;
+    const float eps = cfg_.rms_norm_eps;
+    const int Pmax = std::max(PD_, PQ_);
+    int n = 0;
+    check(qlm_embed_tokens(embed_.get<float>(), V, H, tokens_.get<int>(), ld_tokens_,
+                           pos_.get<int>(), h_.get<float>(), H, B, stream_),
+          "embed");
+    ++n;
+    Tensor hx({B, H}, h_.get<float>());
+    int dn_i = 0, at_i = 0;
+    for (auto& w : layers_) {
+        Tensor in_ln({H}, w.in_ln.get<float>()), post_ln({H}, w.post_ln.get<float>());
+        if (w.linear) {
+            Tensor proj({B, PD_}, proj_.get<float>());
+            proj.strides = {Pmax, 1};
+            math::matmul_rmsnorm(hx, in_ln, eps, w.dn_in.view(), proj);
+            check(qlm_deltanet_decode(proj_.get<float>(), Pmax, conv_state_[dn_i].get<float>(),
+                                      w.conv_wt.get<float>(), w.A_log.get<float>(),
+                                      w.dt_bias.get<float>(), w.dn_norm.get<float>(),
+                                      dn_state_[dn_i].get<float>(), pos_.get<int>(),
+                                      core_.get<float>(), CORE_, B, nh, d, stream_),
+                  "deltanet");
+            Tensor core({B, HD_}, core_.get<float>());
+            core.strides = {CORE_, 1};
+            math::matmul_residual(core, w.dn_out.view(), hx);
+            ++dn_i;
+            n += 3;
+        } else {
+            Tensor proj({B, PQ_}, proj_.get<float>());
+            proj.strides = {Pmax, 1};
+            math::matmul_rmsnorm(hx, in_ln, eps, w.at_qkv.view(), proj);
+            check(qlm_gqa_decode(proj_.get<float>(), Pmax, w.q_norm.get<float>(),
+                                 w.k_norm.get<float>(), rope_cos_.get<float>(),
+                                 rope_sin_.get<float>(), cfg_.rotary_dim(),
+                                 k_cache_[at_i].get<float>(), v_cache_[at_i].get<float>(), max_seq_,
+                                 pos_.get<int>(), core_.get<float>(), CORE_, B, nq, nkv, hd,
+                                 w.gated ? 1 : 0, attn_work_.get(), stream_),
+                  "gqa");
+            Tensor core({B, nq * hd}, core_.get<float>());
+            core.strides = {CORE_, 1};
+            math::matmul_residual(core, w.at_o.view(), hx);
+            ++at_i;
+            n += 5;
+        }
+        Tensor act({B, F}, act_.get<float>());
+        math::matmul_swiglu_rmsnorm(hx, post_ln, eps, w.gate_up.view(), act);
+        math::matmul_residual(act, w.down.view(), hx);
+        n += 2 * ((B + 3) / 4);
+    }
+    Tensor fn({H}, final_norm_.get<float>());
+    Tensor lg({B, V}, logits_.get<float>());
+    math::matmul_rmsnorm(hx, fn, eps, lm_head_.view(), lg);
+    check(qlm_greedy_advance(logits_.get<float>(), V, V, B, argmax_work_.get(), tokens_.get<int>(),
+                             ld_tokens_, pos_.get<int>(), prompt_len_.get<int>(), stream_),
+          "argmax");
+    kernels_per_step_ = n + 3;
+}
+
+void* DecoderModel::graph_for(int B) {
+    auto it = graphs_.find(B);
+    if (it != graphs_.end()) return it->second;
+    check(qlm_graph_begin(stream_), "graph begin");
+    try {
+        enqueue_step(B);
+    } catch (...) {
+        void* g = nullptr;
+        qlm_graph_end(stream_, &g);
+        if (g) qlm_graph_destroy(g);
+        throw;
+    }
+    void* g = nullptr;
+    check(qlm_graph_end(stream_, &g), "graph end");
+    graphs_[B] = g;
+    return g;
+}
+
+void DecoderModel::forward(int token, int pos, float* logits_host) {
+    if (pos < 0 || pos >= max_seq_)
+        throw std::runtime_error("KV cache index out of bounds: pos = " + std::to_string(pos) +
+                                 ", max_seq_len = " + std::to_string(max_seq_));
+    const int big = INT_MAX;
+    check(qlm_memcpy_h2d(tokens_.get<int>() + pos, &token, sizeof(int), stream_), "upload");
+    check(qlm_memcpy_h2d(pos_.get<int>(), &pos, sizeof(int), stream_), "upload");
+    check(qlm_memcpy_h2d(prompt_len_.get<int>(), &big, sizeof(int), stream_), "upload");
+    check(qlm_graph_launch(graph_for(1), stream_), "graph launch");
+    check(qlm_memcpy_d2h(logits_host, logits_.get(), (size_t)cfg_.vocab_size * sizeof(float),
+                         stream_),
+          "download");
+    check(qlm_stream_sync(stream_), "sync");
+}
+
+void DecoderModel::last_logits(int b, float* host) const {
+    check(qlm_memcpy_d2h(host, logits_.get<float>() + (size_t)b * cfg_.vocab_size,
+                         (size_t)cfg_.vocab_size * sizeof(float), stream_),
+          "download");
+    check(qlm_stream_sync(stream_), "sync");
+}
+
+void DecoderModel::generate(const int* prompts, int B, int n, int n_new, int* out, GenStats* st,
+                            bool use_graph) {
+    if (B <= 0 || B > max_batch_) throw std::runtime_error("generate: batch exceeds max_batch");
+    if (n <= 0 || n_new < 0) throw std::runtime_error("generate: empty prompt");
+    if (n + n_new - 1 > max_seq_)
+        throw std::runtime_error("context length exceeded max_seq_len (" + std::to_string(max_seq_) +
+                                 ")");
+    for (int i = 0; i < B * n; ++i)
+        if (prompts[i] < 0 || prompts[i] >= cfg_.vocab_size)
+            throw std::runtime_error("generate: token id out of range");
+    reset_states();
+    std::vector<int> tok((size_t)B * ld_tokens_, 0), pl(B, n), zero(B, 0);
+    for (int b = 0; b < B; ++b) std::memcpy(&tok[(size_t)b * ld_tokens_], prompts + (size_t)b * n, n * 4);
+    check(qlm_memcpy_h2d(tokens_.get(), tok.data(), tok.size() * 4, stream_), "upload");
+    check(qlm_memcpy_h2d(prompt_len_.get(), pl.data(), B * 4, stream_), "upload");
+    check(qlm_memcpy_h2d(pos_.get(), zero.data(), B * 4, stream_), "upload");
+    void* g = use_graph ? graph_for(B) : nullptr;
+    auto step = [&]() {
+        if (g) check(qlm_graph_launch(g, stream_), "graph launch");
+        else enqueue_step(B);
+    };
+    const double t0 = now_s();
+    for (int s = 0; s < n - 1; ++s) step();
+    check(qlm_stream_sync(stream_), "sync");
+    const double t1 = now_s();
+    for (int s = 0; s < n_new; ++s) step();
+    check(qlm_stream_sync(stream_), "sync");
+    const double t2 = now_s();
+    check(qlm_memcpy_d2h(tok.data(), tokens_.get(), tok.size() * 4, stream_), "download");
+    check(qlm_stream_sync(stream_), "sync");
+    for (int b = 0; b < B; ++b)
+        for (int i = 0; i < n_new; ++i) out[(size_t)b * n_new + i] = tok[(size_t)b * ld_tokens_ + n + i];
+    if (st) {
+        st->prefill_s = t1 - t0;
+        st->decode_s = t2 - t1;
+        st->steps = n - 1 + n_new;
+    }
+}
+
+}  // namespace qlm

@@ -1,0 +1,130 @@
+// Device-resident decoder for the Qwen3.5 hybrid (Gated DeltaNet + GQA)
+// family: the MI355X counterpart of the reference's DecoderModel
+// (src/model/model.hpp:16-91, model.cpp:34-274) and its module tree
+// (DecoderLayer / Qwen3_5GatedDeltaNet / Qwen3_5Attention / SwiGLU_MLP,
+// modules.hpp:100-282, attention.cpp).
+//
+// Differences in shape, not in arithmetic:
+//   - weights live in HBM as int8 + fp32 group scales (quantised on the
+//     device at load, bit-identical to the reference quantiser); the
+//     projections that share an input are stacked into one matrix
+//     (DeltaNet qkv|z|b|a, attention q|k|v, MLP gate|up);
+//   - every sequence of a batch has its own position, token stream, KV cache
+//     and DeltaNet state (the reference holds one sequence);
+//   - one decode step is a fixed launch sequence captured once into a
+//     hipGraph per batch size and replayed; positions and tokens stay on the
+//     device, the argmax runs on the device.
+#pragma once
+
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "config.hpp"
+#include "device.hpp"
+#include "safetensors.hpp"
+#include "tensor.hpp"
+
+namespace qlm {
+
+struct LinearI8 {
+    DeviceBuffer q, s;
+    int N = 0, K = 0, group = 32;
+    Tensor view() const {
+        return Tensor::int8(q.get<int8_t>(), s.get<float>(), N, K, group);
+    }
+    int blocks_per_row() const { return group >= K ? 1 : K / group; }
+};
+
+struct LayerWeights {
+    bool linear = true;
+    DeviceBuffer in_ln, post_ln;   // zero-centred RMSNorm gains [H]
+    // Gated DeltaNet
+    LinearI8 dn_in;                // [3HD + HD + nh + nh, H]: qkv | z | b | a
+    LinearI8 dn_out;               // [H, HD]
+    DeviceBuffer conv_wt;          // [4, 3HD] (tap-major, reference attention.cpp:397-408)
+    DeviceBuffer A_log, dt_bias;   // [nh]
+    DeviceBuffer dn_norm;          // [d] plain gain
+    // GQA
+    LinearI8 at_qkv;               // [q_rows + 2 n_kv hd, H]
+    LinearI8 at_o;                 // [H, n_q hd]
+    DeviceBuffer q_norm, k_norm;   // [hd] zero-centred (may be empty)
+    bool gated = true;
+    // MLP
+    LinearI8 gate_up;              // [2F, H]
+    LinearI8 down;                 // [H, F]
+};
+
+struct GenStats {
+    double prefill_s = 0.0;
+    double decode_s = 0.0;
+    int steps = 0;
+};
+
+class DecoderModel {
+   public:
+    DecoderModel() = default;
+    ~DecoderModel();
+
+    // precision: "int8" (reference Q8_0, group 32) or "int8_row" (one scale
+    // per output row). max_batch sequences of up to max_seq_len positions.
+    void load(const std::string& dir, int max_seq_len, const std::string& precision,
+              int max_batch);
+
+    void reset_states();
+
+    // Reference-shaped single-sequence step (model.cpp:151-211) on sequence 0:
+    // forwards `token` at position `pos` and copies the logits to the host.
+    void forward(int token, int pos, float* logits_host);
+
+    // Greedy generation, main.cpp:574-690 convention: for each of B
+    // sequences, positions 0..n-2 of the prompt are forwarded as prefill,
+    // then n_new steps each forward the newest token and append the argmax.
+    // prompts [B, n], out [B, n_new]. use_graph = false launches eagerly.
+    void generate(const int* prompts, int B, int n, int n_new, int* out, GenStats* st,
+                  bool use_graph = true);
+
+    // Logits of sequence b from the most recent step (host copy).
+    void last_logits(int b, float* host) const;
+
+    const ModelConfig& config() const { return cfg_; }
+    size_t weight_bytes() const { return weight_bytes_; }
+    int max_batch() const { return max_batch_; }
+    int max_seq() const { return max_seq_; }
+    int group() const { return group_; }
+    int kernels_per_step() const { return kernels_per_step_; }
+
+   private:
+    void enqueue_step(int B);
+    void* graph_for(int B);
+    void quantize_into(LinearI8& lin, int row_off, const std::string& name);
+    void upload_f32(DeviceBuffer& dst, const std::string& name, int64_t expect);
+    void alloc_linear(LinearI8& lin, int N, int K);
+
+    ModelConfig cfg_;
+    std::unique_ptr<WeightStore> ws_;
+    int max_seq_ = 0, max_batch_ = 0, group_ = 32;
+    int HD_ = 0, PD_ = 0, QR_ = 0, PQ_ = 0, CORE_ = 0;
+    size_t weight_bytes_ = 0;
+    int kernels_per_step_ = 0;
+    void* stream_ = nullptr;
+
+    std::vector<LayerWeights> layers_;
+    DeviceBuffer final_norm_, embed_;
+    LinearI8 lm_head_;
+    DeviceBuffer rope_cos_, rope_sin_;
+
+    // per-sequence state
+    std::vector<DeviceBuffer> conv_state_, dn_state_;   // per DeltaNet layer
+    std::vector<DeviceBuffer> k_cache_, v_cache_;       // per attention layer
+    DeviceBuffer tokens_, pos_, prompt_len_;
+    int ld_tokens_ = 0;
+    // activations
+    DeviceBuffer h_, proj_, core_, act_, logits_, argmax_work_, attn_work_;
+    DeviceBuffer staging_;
+
+    std::map<int, void*> graphs_;
+};
+
+}  // namespace qlm

@@ -1,0 +1,114 @@
+#include "safetensors.hpp"
+
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <algorithm>
+#include <cstring>
+#include <dirent.h>
+#include <stdexcept>
+
+#include "json.hpp"
+
+namespace qlm {
+
+SafetensorsFile::SafetensorsFile(const std::string& path) : path_(path) {
+    fd_ = ::open(path.c_str(), O_RDONLY);
+    if (fd_ < 0) throw std::runtime_error("safetensors: cannot open " + path);
+    struct stat st;
+    if (fstat(fd_, &st) != 0) throw std::runtime_error("safetensors: cannot stat " + path);
+    size_ = (size_t)st.st_size;
+    if (size_ < 8) throw std::runtime_error("safetensors: truncated file " + path);
+    void* m = mmap(nullptr, size_, PROT_READ, MAP_SHARED, fd_, 0);
+    if (m == MAP_FAILED) throw std::runtime_error("safetensors: mmap failed " + path);
+    map_ = static_cast<uint8_t*>(m);
+    uint64_t hlen = 0;
+    std::memcpy(&hlen, map_, 8);
+    if (hlen > size_ - 8) throw std::runtime_error("safetensors: header overruns file " + path);
+    data_start_ = 8 + (size_t)hlen;
+    Json root = Json::parse(std::string_view(reinterpret_cast<const char*>(map_) + 8, (size_t)hlen));
+    if (!root.is_object()) throw std::runtime_error("safetensors: header is not an object");
+    for (const auto& kv : root.obj) {
+        if (kv.first == "__metadata__") continue;
+        const Json& t = kv.second;
+        Info info;
+        info.dtype = t.at("dtype").string();
+        for (const auto& d : t.at("shape").arr) info.shape.push_back((int64_t)d.number());
+        const auto& off = t.at("data_offsets").arr;
+        if (off.size() != 2) throw std::runtime_error("safetensors: bad data_offsets for " + kv.first);
+        info.begin = (size_t)off[0].number();
+        info.end = (size_t)off[1].number();
+        if (info.end < info.begin || data_start_ + info.end > size_)
+            throw std::runtime_error("safetensors: tensor '" + kv.first + "' is out of file bounds");
+        infos_[kv.first] = std::move(info);
+    }
+}
+
+SafetensorsFile::~SafetensorsFile() {
+    if (map_) munmap(map_, size_);
+    if (fd_ >= 0) ::close(fd_);
+}
+
+TensorView SafetensorsFile::get(const std::string& name) const {
+    auto it = infos_.find(name);
+    if (it == infos_.end()) throw std::runtime_error("safetensors: no tensor " + name);
+    TensorView v;
+    v.dtype = it->second.dtype;
+    v.shape = it->second.shape;
+    v.data = map_ + data_start_ + it->second.begin;
+    v.nbytes = it->second.end - it->second.begin;
+    return v;
+}
+
+std::vector<std::string> SafetensorsFile::names() const {
+    std::vector<std::string> out;
+    for (const auto& kv : infos_) out.push_back(kv.first);
+    return out;
+}
+
+WeightStore::WeightStore(const std::string& dir) {
+    DIR* d = opendir(dir.c_str());
+    if (!d) throw std::runtime_error("weights: cannot open directory " + dir);
+    std::vector<std::string> paths;
+    while (dirent* e = readdir(d)) {
+        std::string n = e->d_name;
+        if (n.size() > 12 && n.substr(n.size() - 12) == ".safetensors") paths.push_back(dir + "/" + n);
+    }
+    closedir(d);
+    std::sort(paths.begin(), paths.end());
+    if (paths.empty()) throw std::runtime_error("weights: no .safetensors files in " + dir);
+    for (const auto& p : paths) files_.push_back(std::make_unique<SafetensorsFile>(p));
+}
+
+const SafetensorsFile* WeightStore::find(const std::string& name, std::string& resolved) const {
+    for (const auto& f : files_)
+        if (f->has(name)) {
+            resolved = name;
+            return f.get();
+        }
+    if (name.rfind("model.", 0) == 0) {
+        std::string alt = "model.language_model." + name.substr(6);
+        for (const auto& f : files_)
+            if (f->has(alt)) {
+                resolved = alt;
+                return f.get();
+            }
+    }
+    return nullptr;
+}
+
+bool WeightStore::has(const std::string& name) const {
+    std::string r;
+    return find(name, r) != nullptr;
+}
+
+TensorView WeightStore::get(const std::string& name) const {
+    std::string r;
+    const SafetensorsFile* f = find(name, r);
+    if (!f) throw std::runtime_error("Tensor not found in any safetensors files: " + name);
+    return f->get(r);
+}
+
+}  // namespace qlm

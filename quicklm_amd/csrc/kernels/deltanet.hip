@@ -1,0 +1,222 @@
+// Gated DeltaNet decode step (reference: Qwen3_5GatedDeltaNet::forward,
+// attention.cpp:414-590; recurrence :498-571).
+//
+// One workgroup per (sequence, head), 512 threads. The head's fp32 state
+// S[d=128][d=128] (key i, value j) is read once into registers, updated in
+// place and written once: thread (ig, jg) owns rows ig*8..ig*8+7 and columns
+// jg*4..jg*4+3 (8 float4 = 32 values). A wave covers two 512-byte row
+// segments per load, so state traffic is fully coalesced.
+//
+// The reference reduces kv[j] and o[j] sequentially over i; here each thread
+// reduces its 8 rows sequentially and the 16 row-groups are then summed in
+// fixed order through LDS (deterministic, not bit-identical).
+//
+// The fused decode form also does the head's slice of the causal conv1d
+// (3 x 128 channels, tap-major ring indexed by pos % 3), SiLU, L2 norm of q
+// and k, the decay/beta gates, head RMSNorm and the SiLU(z) output gate, so
+// one launch replaces steps 2-9 of the reference forward.
+
+#include "common.hpp"
+
+namespace {
+
+constexpr int kD = 128;
+constexpr int kThreads = 512;
+constexpr int kRowGroups = kThreads / 32;     // 16
+constexpr int kRowsPer = kD / kRowGroups;      // 8
+
+struct DnShared {
+    float q[kD], k[kD], v[kD];
+    float red[kRowGroups][kD];
+    float vec[kD];
+    float scal[8];
+};
+
+// Recurrence core. q,k,v in LDS (q already L2-normalised, k too). Leaves the
+// un-normalised, 1/sqrt(d)-scaled output in sh.vec.
+__device__ __forceinline__ void dn_recurrence(DnShared& sh, float* __restrict__ S, float dec,
+                                              float beta) {
+    const int tid = threadIdx.x;
+    const int jg = tid & 31;
+    const int ig = tid >> 5;
+    float4 s[kRowsPer];
+    float4* S4 = reinterpret_cast<float4*>(S);
+#pragma unroll
+    for (int r = 0; r < kRowsPer; ++r) s[r] = S4[(ig * kRowsPer + r) * (kD / 4) + jg];
+
+    // (1) decay and kv = k . S_decayed
+    float4 kv = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int r = 0; r < kRowsPer; ++r) {
+        const float ki = sh.k[ig * kRowsPer + r];
+        s[r].x *= dec;
+        s[r].y *= dec;
+        s[r].z *= dec;
+        s[r].w *= dec;
+        kv.x = fmaf(ki, s[r].x, kv.x);
+        kv.y = fmaf(ki, s[r].y, kv.y);
+        kv.z = fmaf(ki, s[r].z, kv.z);
+        kv.w = fmaf(ki, s[r].w, kv.w);
+    }
+    reinterpret_cast<float4*>(sh.red[ig])[jg] = kv;
+    __syncthreads();
+    if (tid < kD) {
+        float t = 0.0f;
+#pragma unroll
+        for (int g = 0; g < kRowGroups; ++g) t += sh.red[g][tid];
+        sh.vec[tid] = sh.v[tid] - t;  // delta
+    }
+    __syncthreads();
+
+    // (2) S += (beta*k) delta^T ; (3) o = q . S_new
+    const float4 dl = reinterpret_cast<const float4*>(sh.vec)[jg];
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int r = 0; r < kRowsPer; ++r) {
+        const int i = ig * kRowsPer + r;
+        const float bk = beta * sh.k[i];
+        const float qi = sh.q[i];
+        s[r].x = fmaf(bk, dl.x, s[r].x);
+        s[r].y = fmaf(bk, dl.y, s[r].y);
+        s[r].z = fmaf(bk, dl.z, s[r].z);
+        s[r].w = fmaf(bk, dl.w, s[r].w);
+        o.x = fmaf(qi, s[r].x, o.x);
+        o.y = fmaf(qi, s[r].y, o.y);
+        o.z = fmaf(qi, s[r].z, o.z);
+        o.w = fmaf(qi, s[r].w, o.w);
+        S4[i * (kD / 4) + jg] = s[r];
+    }
+    __syncthreads();  // everyone has consumed sh.vec (delta)
+    reinterpret_cast<float4*>(sh.red[ig])[jg] = o;
+    __syncthreads();
+    if (tid < kD) {
+        float t = 0.0f;
+#pragma unroll
+        for (int g = 0; g < kRowGroups; ++g) t += sh.red[g][tid];
+        sh.vec[tid] = t * (1.0f / sqrtf((float)kD));
+    }
+    __syncthreads();
+}
+
+// Isolated step: q,k,v,o [B,H,d], decay/beta [B,H], state [B,H,d,d].
+__global__ __launch_bounds__(kThreads) void k_gated_delta_step(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+    const float* __restrict__ decay, const float* __restrict__ beta, float* __restrict__ state,
+    float* __restrict__ out, int H) {
+    __shared__ DnShared sh;
+    const int bh = blockIdx.x;  // b*H + h
+    const int tid = threadIdx.x;
+    if (tid < kD) {
+        sh.q[tid] = q[(size_t)bh * kD + tid];
+        sh.k[tid] = k[(size_t)bh * kD + tid];
+        sh.v[tid] = v[(size_t)bh * kD + tid];
+    }
+    __syncthreads();
+    dn_recurrence(sh, state + (size_t)bh * kD * kD, decay[bh], beta[bh]);
+    if (tid < kD) out[(size_t)bh * kD + tid] = sh.vec[tid];
+}
+
+// Fused decode mixer core. proj row: [qkv 3*H*d | z H*d | b H | a H].
+__global__ __launch_bounds__(kThreads) void k_deltanet_decode(
+    const float* __restrict__ proj, int ldp, float* __restrict__ conv_state,
+    const float* __restrict__ wt, const float* __restrict__ A_log,
+    const float* __restrict__ dt_bias, const float* __restrict__ norm_w,
+    float* __restrict__ state, const int* __restrict__ pos, float* __restrict__ out, int ldo,
+    int H) {
+    __shared__ DnShared sh;
+    const int h = blockIdx.x;
+    const int b = blockIdx.y;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int HD = H * kD;
+    const int C = 3 * HD;
+    const float* pr = proj + (size_t)b * ldp;
+    float* cs = conv_state + (size_t)b * 3 * C;
+
+    // conv1d (kernel 4, taps chronological from the oldest ring row) + SiLU
+    if (tid < 3 * kD) {
+        const int sec = tid / kD, t = tid % kD;
+        const int ch = sec * HD + h * kD + t;
+        const int oldest = pos ? (pos[b] % 3) : 0;
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+            const int row = (oldest + j) % 3;
+            acc = nc_add_mul(acc, cs[(size_t)row * C + ch], wt[(size_t)j * C + ch]);
+        }
+        const float x = pr[ch];
+        acc = nc_add_mul(acc, x, wt[(size_t)3 * C + ch]);
+        cs[(size_t)oldest * C + ch] = x;
+        const float y = silu_f(acc);
+        if (sec == 0) sh.q[t] = y;
+        else if (sec == 1) sh.k[t] = y;
+        else sh.v[t] = y;
+    }
+    __syncthreads();
+
+    // L2 norms (wave 0: q, wave 1: k) and gates (wave 2)
+    if (wave < 2) {
+        float* vv = wave == 0 ? sh.q : sh.k;
+        const float a0 = vv[lane], a1 = vv[lane + 64];
+        float ss = fmaf(a0, a0, a1 * a1);
+        ss = wave_sum(ss);
+        const float nrm = sqrtf(ss + 1e-6f);
+        vv[lane] = a0 / nrm;
+        vv[lane + 64] = a1 / nrm;
+    } else if (wave == 2 && lane == 0) {
+        const float a = pr[4 * HD + H + h];
+        const float bb = pr[4 * HD + h];
+        const float dt = a + dt_bias[h];
+        const float sp = dt > 20.0f ? dt : log1pf(expf(dt));
+        const float alpha = -expf(A_log[h]) * sp;
+        sh.scal[0] = expf(alpha);
+        sh.scal[1] = 1.0f / (1.0f + expf(-bb));
+    }
+    __syncthreads();
+
+    dn_recurrence(sh, state + ((size_t)b * H + h) * kD * kD, sh.scal[0], sh.scal[1]);
+
+    // head RMSNorm (plain gain, attention.cpp:574-578) + SiLU(z) gate (:582-585)
+    float o = 0.0f;
+    if (wave < 2) {
+        o = sh.vec[tid];
+        const float ss = wave_sum(o * o);
+        if (lane == 0) sh.scal[2 + wave] = ss;
+    }
+    __syncthreads();
+    if (wave < 2) {
+        const int j = tid;  // 0..127
+        const float tot = sh.scal[2] + sh.scal[3];
+        const float s = 1.0f / sqrtf(tot / (float)kD + 1e-6f);
+        const float z = pr[3 * HD + h * kD + j];
+        const float r = (o * s) * norm_w[j];
+        out[(size_t)b * ldo + h * kD + j] = r * silu_f(z);
+    }
+}
+
+}  // namespace
+
+extern "C" int qlm_gated_delta_step(const float* q, const float* k, const float* v,
+                                    const float* decay, const float* beta, float* state,
+                                    float* out, int B, int H, int d, void* stream) {
+    if (!q || !k || !v || !decay || !beta || !state || !out || B <= 0 || H <= 0)
+        return QLM_ERR_ARG;
+    if (d != kD) return QLM_ERR_SHAPE;
+    hipLaunchKernelGGL(k_gated_delta_step, dim3(B * H), dim3(kThreads), 0, as_stream(stream), q, k,
+                       v, decay, beta, state, out, H);
+    return qlm_launch_status();
+}
+
+extern "C" int qlm_deltanet_decode(const float* proj, int ldp, float* conv_state,
+                                   const float* conv_w_t, const float* A_log, const float* dt_bias,
+                                   const float* norm_w, float* state, const int* pos, float* out,
+                                   int ldo, int B, int H, int d, void* stream) {
+    if (!proj || !conv_state || !conv_w_t || !A_log || !dt_bias || !norm_w || !state || !out ||
+        B <= 0 || H <= 0)
+        return QLM_ERR_ARG;
+    if (d != kD) return QLM_ERR_SHAPE;
+    if (ldp < 4 * H * d + 2 * H || ldo < H * d) return QLM_ERR_SHAPE;
+    hipLaunchKernelGGL(k_deltanet_decode, dim3(H, B), dim3(kThreads), 0, as_stream(stream), proj,
+                       ldp, conv_state, conv_w_t, A_log, dt_bias, norm_w, state, pos, out, ldo, H);
+    return qlm_launch_status();
+}

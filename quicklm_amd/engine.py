@@ -1,0 +1,100 @@
+"""ctypes binding of the host engine's C ABI (include/qlm_engine.h)."""
+
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+from . import hip as _hip  # noqa: F401  (loads libqlm_hip.so first; raises if missing)
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG, "libqlm_engine.so")
+_lib = None
+
+_vp, _i = C.c_void_p, C.c_int
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        _hip.lib()
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(f"{LIB_PATH} is missing: run `python -m quicklm_amd.build`")
+        L = C.CDLL(LIB_PATH)
+        L.qlm_engine_last_error.restype = C.c_char_p
+        L.qlm_engine_load.argtypes = [C.c_char_p, _i, _i, C.c_char_p, C.POINTER(_vp)]
+        L.qlm_engine_free.argtypes = [_vp]
+        L.qlm_engine_info.argtypes = [_vp] + [C.POINTER(_i)] * 6 + [C.POINTER(C.c_size_t)]
+        L.qlm_engine_reset.argtypes = [_vp]
+        L.qlm_engine_forward.argtypes = [_vp, _i, _i, _vp]
+        L.qlm_engine_generate.argtypes = [_vp, _vp, _i, _i, _i, _vp, C.POINTER(C.c_double),
+                                          C.POINTER(C.c_double), _i]
+        L.qlm_engine_last_logits.argtypes = [_vp, _i, _vp]
+        L.qlm_engine_kernels_per_step.argtypes = [_vp]
+        _lib = L
+    return _lib
+
+
+class EngineError(RuntimeError):
+    pass
+
+
+def _check(rc: int) -> None:
+    if rc != 0:
+        raise EngineError(lib().qlm_engine_last_error().decode())
+
+
+class Engine:
+    """DecoderModel on the GPU: load a checkpoint directory, decode greedily."""
+
+    def __init__(self, model_dir: str, max_seq_len: int = 2048, max_batch: int = 1,
+                 precision: str = "int8"):
+        h = _vp()
+        _check(lib().qlm_engine_load(model_dir.encode(), max_seq_len, max_batch,
+                                     precision.encode(), C.byref(h)))
+        self.h = h.value
+        vals = [_i() for _ in range(6)]
+        wb = C.c_size_t()
+        _check(lib().qlm_engine_info(self.h, *[C.byref(v) for v in vals], C.byref(wb)))
+        (self.vocab, self.hidden, self.layers, self.group, self.max_seq,
+         self.max_batch) = [v.value for v in vals]
+        self.weight_bytes = wb.value
+
+    def reset(self) -> None:
+        _check(lib().qlm_engine_reset(self.h))
+
+    def forward(self, token: int, pos: int) -> np.ndarray:
+        lg = np.empty(self.vocab, np.float32)
+        _check(lib().qlm_engine_forward(self.h, token, pos, lg.ctypes.data))
+        return lg
+
+    def generate(self, prompts: np.ndarray, n_new: int, use_graph: bool = True):
+        """prompts [B, n] int32 -> (tokens [B, n_new], prefill_s, decode_s)."""
+        p = np.ascontiguousarray(np.atleast_2d(prompts), np.int32)
+        B, n = p.shape
+        out = np.empty((B, n_new), np.int32)
+        pre, dec = C.c_double(), C.c_double()
+        _check(lib().qlm_engine_generate(self.h, p.ctypes.data, B, n, n_new, out.ctypes.data,
+                                         C.byref(pre), C.byref(dec), 1 if use_graph else 0))
+        return out, pre.value, dec.value
+
+    def last_logits(self, b: int = 0) -> np.ndarray:
+        lg = np.empty(self.vocab, np.float32)
+        _check(lib().qlm_engine_last_logits(self.h, b, lg.ctypes.data))
+        return lg
+
+    def kernels_per_step(self) -> int:
+        return int(lib().qlm_engine_kernels_per_step(self.h))
+
+    def close(self) -> None:
+        if getattr(self, "h", None):
+            lib().qlm_engine_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

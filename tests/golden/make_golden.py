@@ -1,0 +1,72 @@
+"""Write the committed golden fixtures for the model-level parity tests.
+
+Runs in the build container only (it needs the reference compiled from its
+own sources into oracle/_ref by `make -C oracle ref`). It writes the tiny
+hybrid model (config 0 shapes) with quicklm_amd.synth, runs the reference
+DecoderModel on it with the CLI's greedy convention (batched prefill of
+prompt[0..126], 64 decode steps, no EOS stop) and stores:
+  prompt, tokens                 the 128 prompt ids and 64 greedy tokens
+  top_idx/top_val [64, 32]       the 32 largest logits of every decode step
+  margin [64]                    top-1 minus top-2 logit per step
+  logits0_head/logits63_head     logits[:4096] of the first and last step
+  tensor_sha                     sha256 of a few synthetic tensors (pins the
+                                 generator across hosts)
+plus the same stream from the reference's own -O3 -ffast-math build
+(tokens_fast) for the record. Usage: python tests/golden/make_golden.py
+"""
+import hashlib
+import os
+import sys
+import tempfile
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+sys.path.insert(0, ROOT)
+
+from oracle.oracle import Reference  # noqa: E402
+from quicklm_amd import synth  # noqa: E402
+
+SHA_TENSORS = ["model.embed_tokens.weight", "model.layers.0.linear_attn.in_proj_qkv.weight",
+               "model.layers.3.self_attn.q_proj.weight", "model.layers.0.linear_attn.A_log",
+               "model.layers.0.linear_attn.dt_bias"]
+
+
+def tensor_sha(model_dir):
+    from oracle.oracle import read_safetensors
+    t = read_safetensors(os.path.join(model_dir, "model.safetensors"))
+    return {n: hashlib.sha256(t[n].tobytes()).hexdigest() for n in SHA_TENSORS}
+
+
+def main():
+    out = os.path.join(os.path.dirname(os.path.abspath(__file__)), "tiny_greedy.npz")
+    with tempfile.TemporaryDirectory() as d:
+        synth.write_model(d, "tiny")
+        prompt = synth.prompt_tokens(128, seed=0)[0]
+        res = {}
+        for kind in ("ieee", "fast"):
+            ref = Reference(kind)
+            ref.init_threads(os.cpu_count() or 1)
+            m = ref.load_model(d, 2048, "int8")
+            t0 = time.time()
+            toks, pre, dec, lg = m.generate(prompt, 64, keep_logits=True)
+            print(f"{ref.kind}: prefill {pre:.2f}s decode {dec:.2f}s ({64/dec:.2f} tok/s) "
+                  f"tokens {toks[:8]}...", flush=True)
+            res[kind] = (toks, lg)
+            del m
+        toks, lg = res["ieee"]
+        order = np.argsort(-lg, axis=1, kind="stable")[:, :32]
+        top_val = np.take_along_axis(lg, order, axis=1)
+        np.savez_compressed(
+            out, prompt=prompt.astype(np.int32), tokens=toks.astype(np.int32),
+            tokens_fast=res["fast"][0].astype(np.int32), top_idx=order.astype(np.int32),
+            top_val=top_val.astype(np.float32), margin=(top_val[:, 0] - top_val[:, 1]),
+            logits0_head=lg[0, :4096].copy(), logits63_head=lg[63, :4096].copy(),
+            tensor_names=np.array(SHA_TENSORS), tensor_sha=np.array(
+                [tensor_sha(d)[n] for n in SHA_TENSORS]))
+    print("wrote", out, "fast==ieee tokens:", bool(np.array_equal(res["fast"][0], toks)))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,367 @@
+"""Operator parity: each HIP kernel (through the C ABI) against the CPU oracle.
+
+Bars (north_star): int8 quantisation and argmax bit-exact; fp32-accumulating
+ops within a normwise relative error of 1e-3 (FP32_TOL). Where the GPU
+evaluates exactly the reference's per-element arithmetic (conv1d tap sums,
+RoPE from the reference's own cos/sin table), the bar is bit-exactness.
+"""
+
+import numpy as np
+import pytest
+
+from tests.util import FP32_TOL, bf16_bits, bf16_to_f32, rel_err, say
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(hip, a):
+    return hip.DeviceBuffer.from_numpy(np.ascontiguousarray(a))
+
+
+# ---------------------------------------------------------------- A2 quantiser
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("group", [32, "K"])
+def test_quantize_bitexact(hip, orc, rng, dtype, group):
+    rows, K = 97, 2560
+    w = (rng.standard_normal((rows, K)) * 0.02).astype(np.float32)
+    w[3] = 0.0                                   # all-zero row -> scale 1, q 0
+    w[5, :32] = np.arange(32, dtype=np.float32) - 16.0   # exact halves after scaling
+    w[7, 5] = 1e30                               # one huge value dominates its group
+    g = K if group == "K" else 32
+    src = bf16_bits(w) if dtype == "bf16" else w
+    q_ref, s_ref = orc.quantize(src, g)
+    say("quantize", dtype, g, rows, K)
+    dw = dev(hip, src)
+    dq = hip.DeviceBuffer(rows * K)
+    ds = hip.DeviceBuffer(s_ref.nbytes)
+    fn = "qlm_quantize_q8_bf16" if dtype == "bf16" else "qlm_quantize_q8_f32"
+    hip.call(fn, dw, rows, K, g, dq, ds, None)
+    q = dq.to_numpy((rows, K), np.int8)
+    s = ds.to_numpy(s_ref.shape, np.float32)
+    assert np.array_equal(s.view(np.uint32), s_ref.view(np.uint32))
+    assert np.array_equal(q, q_ref)
+
+
+def test_quantize_rejects_bad_group(hip):
+    d = hip.DeviceBuffer(64 * 4)
+    with pytest.raises(hip.HipError):
+        hip.call("qlm_quantize_q8_f32", d, 1, 64, 16, d, d, None)
+
+
+# ---------------------------------------------------------------- A3 GEMV
+def _weights(orc, rng, N, K, group):
+    w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    return orc.quantize(w, group)
+
+
+GEMV_SHAPES = [  # (N, K): model projections and the config-1 matrices
+    (4096, 4096), (12288, 4096), (4096, 12288), (151936, 2560),
+    (8224, 2560), (2560, 2048), (16, 2560), (77, 1024), (3, 3584),
+]
+
+
+@pytest.mark.parametrize("N,K", GEMV_SHAPES)
+@pytest.mark.parametrize("group", [32, "K"])
+def test_gemv_parity(hip, orc, rng, N, K, group):
+    g = K if group == "K" else 32
+    q, s = _weights(orc, rng, N, K, g)
+    dq, ds = dev(hip, q), dev(hip, s)
+    for M in (1, 4):
+        x = rng.standard_normal((M, K)).astype(np.float32)
+        ref = orc.matmul_i8(x, q, s, g)
+        say("gemv", N, K, g, M)
+        dx = dev(hip, x)
+        dy = hip.DeviceBuffer(M * N * 4)
+        hip.call("qlm_gemv_i8", dx, K, dq, ds, g, dy, N, M, N, K, None)
+        y = dy.to_numpy((M, N), np.float32)
+        err = rel_err(y, ref)
+        assert err <= FP32_TOL, err
+        assert err < 1e-5, err  # fp32 accumulation: far inside the bar
+
+
+def test_gemv_exact_integers(hip, orc, rng):
+    """Integer activations and power-of-two scales make every sum exact in
+    fp32, so any accumulation order must agree bit for bit with the oracle."""
+    N, K = 1000, 2048
+    q = rng.integers(-127, 128, (N, K), dtype=np.int8)
+    s = (2.0 ** rng.integers(-8, -2, (N, K // 32))).astype(np.float32)
+    x = rng.integers(-16, 17, (3, K)).astype(np.float32)
+    ref = orc.matmul_i8(x, q, s, 32)
+    dy = hip.DeviceBuffer(3 * N * 4)
+    hip.call("qlm_gemv_i8", dev(hip, x), K, dev(hip, q), dev(hip, s), 32, dy, N, 3, N, K, None)
+    assert np.array_equal(dy.to_numpy((3, N), np.float32), ref)
+
+
+def test_gemv_batched_m(hip, orc, rng):
+    """M > 4 runs in slices of four activation rows; strided output rows."""
+    N, K, M = 300, 1024, 11
+    q, s = _weights(orc, rng, N, K, 32)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    ref = orc.matmul_i8(x, q, s, 32)
+    ldy = N + 20
+    dy = hip.DeviceBuffer(M * ldy * 4)
+    hip.call("qlm_gemv_i8", dev(hip, x), K, dev(hip, q), dev(hip, s), 32, dy, ldy, M, N, K, None)
+    y = dy.to_numpy((M, ldy), np.float32)[:, :N]
+    assert rel_err(y, ref) < 1e-5
+
+
+@pytest.mark.parametrize("M", [1, 3])
+def test_gemv_rmsnorm_prologue(hip, orc, rng, M):
+    N, K, eps = 8224, 2560, 1e-6
+    q, s = _weights(orc, rng, N, K, 32)
+    x = (rng.standard_normal((M, K)) * 3).astype(np.float32)
+    nw = (rng.standard_normal(K) * 0.02).astype(np.float32)
+    ref = orc.matmul_i8(orc.rms_norm(x, nw, eps), q, s, 32)
+    dy = hip.DeviceBuffer(M * N * 4)
+    hip.call("qlm_gemv_i8_rmsnorm", dev(hip, x), K, dev(hip, nw), eps, dev(hip, q), dev(hip, s),
+             32, dy, N, M, N, K, None)
+    assert rel_err(dy.to_numpy((M, N), np.float32), ref) < 1e-5
+
+
+def test_gemv_residual_epilogue(hip, orc, rng):
+    N, K = 2560, 9728
+    q, s = _weights(orc, rng, N, K, 32)
+    x = rng.standard_normal((1, K)).astype(np.float32)
+    h = rng.standard_normal((1, N)).astype(np.float32)
+    ref = h + orc.matmul_i8(x, q, s, 32)
+    dh = dev(hip, h)
+    hip.call("qlm_gemv_i8_residual", dev(hip, x), K, dev(hip, q), dev(hip, s), 32, dh, N, 1, N, K,
+             None)
+    assert rel_err(dh.to_numpy((1, N), np.float32), ref) < 1e-5
+
+
+@pytest.mark.parametrize("M", [1, 2])
+def test_gemv_swiglu_epilogue(hip, orc, rng, M):
+    F, K, eps = 3584, 1024, 1e-6
+    qg, sg = _weights(orc, rng, F, K, 32)
+    qu, su = _weights(orc, rng, F, K, 32)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    nw = (rng.standard_normal(K) * 0.02).astype(np.float32)
+    xn = orc.rms_norm(x, nw, eps)
+    g = orc.matmul_i8(xn, qg, sg, 32)
+    u = orc.matmul_i8(xn, qu, su, 32)
+    ref = np.stack([orc.silu_mul(g[m], u[m]) for m in range(M)])
+    dq = dev(hip, np.concatenate([qg, qu]))
+    ds = dev(hip, np.concatenate([sg, su]))
+    dy = hip.DeviceBuffer(M * F * 4)
+    hip.call("qlm_gemv_i8_swiglu_rmsnorm", dev(hip, x), K, dev(hip, nw), eps, dq, ds, 32, dy, F, M,
+             F, K, None)
+    assert rel_err(dy.to_numpy((M, F), np.float32), ref) < 1e-5
+
+
+def test_gemv_rejects_bad_shapes(hip):
+    d = hip.DeviceBuffer(4096)
+    with pytest.raises(hip.HipError):  # K not a multiple of 16
+        hip.call("qlm_gemv_i8", d, 40, d, d, 40, d, 4, 1, 4, 40, None)
+    with pytest.raises(hip.HipError):  # G = 32 needs K % 32 == 0
+        hip.call("qlm_gemv_i8", d, 48, d, d, 32, d, 4, 1, 4, 48, None)
+
+
+# ---------------------------------------------------------------- A5-A7
+def test_rms_norm_and_add(hip, orc, rng):
+    rows, n, eps = 5, 2560, 1e-6
+    x = rng.standard_normal((rows, n)).astype(np.float32)
+    d = rng.standard_normal((rows, n)).astype(np.float32)
+    w = (rng.standard_normal(n) * 0.02).astype(np.float32)
+    dy = hip.DeviceBuffer(x.nbytes)
+    hip.call("qlm_rms_norm", dev(hip, x), dev(hip, w), dy, rows, n, eps, None)
+    assert rel_err(dy.to_numpy(x.shape, np.float32), orc.rms_norm(x, w, eps)) < 1e-6
+    res_ref, y_ref = orc.add_rms_norm(x, d, w, eps)
+    dr = dev(hip, x)
+    hip.call("qlm_add_rms_norm", dr, dev(hip, d), dev(hip, w), dy, rows, n, eps, None)
+    assert np.array_equal(dr.to_numpy(x.shape, np.float32), res_ref)
+    assert rel_err(dy.to_numpy(x.shape, np.float32), y_ref) < 1e-6
+
+
+def test_silu_mul(hip, orc, rng):
+    a = (rng.standard_normal(9728) * 4).astype(np.float32)
+    b = rng.standard_normal(9728).astype(np.float32)
+    da = dev(hip, a)
+    hip.call("qlm_silu_mul", da, dev(hip, b), a.size, None)
+    assert rel_err(da.to_numpy(a.shape, np.float32), orc.silu_mul(a, b)) < 1e-6
+
+
+@pytest.mark.parametrize("rot", [32, 128])
+def test_rope_bitexact(hip, orc, rng, rot):
+    theta, n_pos, heads, hd = 1e6, 2304, 6, 128
+    cos_t, sin_t = orc.rope_table(theta, rot, n_pos)
+    dc, dsn = dev(hip, cos_t), dev(hip, sin_t)
+    t = rng.standard_normal((heads, hd)).astype(np.float32)
+    for pos in (0, 1, 1000, n_pos - 1):
+        ref = orc.rope_neox(t, pos, theta, rot)
+        dt = dev(hip, t)
+        hip.call("qlm_rope_neox", dt, heads, hd, rot, dc, dsn, dev(hip, np.array([pos], np.int32)),
+                 None)
+        assert np.array_equal(dt.to_numpy(t.shape, np.float32), ref), pos
+
+
+def test_conv1d_bitexact(hip, orc, rng):
+    C = 6144
+    x = rng.standard_normal(C).astype(np.float32)
+    st = rng.standard_normal((3, C)).astype(np.float32)
+    wt = rng.standard_normal((4, C)).astype(np.float32)
+    for oldest in range(3):
+        out_ref, st_ref = orc.conv1d_tapmajor(x, st, oldest, wt)
+        dst = dev(hip, st)
+        do = hip.DeviceBuffer(C * 4)
+        hip.call("qlm_conv1d_update", dev(hip, x), dst, oldest, dev(hip, wt), do, C, 4, None)
+        assert np.array_equal(do.to_numpy(C, np.float32), out_ref)
+        assert np.array_equal(dst.to_numpy((3, C), np.float32), st_ref)
+
+
+# ---------------------------------------------------------------- A14 argmax
+def test_argmax_first_max_wins(hip, orc, rng):
+    B, V = 3, 151936
+    lg = rng.standard_normal((B, V)).astype(np.float32)
+    lg[0, 100] = 50.0
+    lg[0, 90000] = 50.0           # tie: lowest index wins
+    lg[1, V - 1] = 60.0           # last element
+    lg[2, :] = -np.inf
+    lg[2, 7] = 0.0
+    work = hip.DeviceBuffer(hip.lib().qlm_argmax_workspace_bytes(B, V))
+    di = hip.DeviceBuffer(B * 4)
+    hip.call("qlm_argmax", dev(hip, lg), V, V, B, di, work, None)
+    got = di.to_numpy(B, np.int32)
+    assert list(got) == [orc.argmax(lg[b]) for b in range(B)] == [100, V - 1, 7]
+
+
+def test_greedy_advance_and_embed(hip, rng):
+    B, V, H, L = 2, 5000, 64, 16
+    lg = rng.standard_normal((B, V)).astype(np.float32)
+    tokens = np.zeros((B, L), np.int32)
+    tokens[:, :4] = [[5, 6, 7, 8], [9, 10, 11, 12]]
+    pos = np.array([3, 1], np.int32)          # seq 0 generating, seq 1 still in its prompt
+    plen = np.array([4, 4], np.int32)
+    dt, dp = dev(hip, tokens), dev(hip, pos)
+    work = hip.DeviceBuffer(hip.lib().qlm_argmax_workspace_bytes(B, V))
+    hip.call("qlm_greedy_advance", dev(hip, lg), V, V, B, work, dt, L, dp, dev(hip, plen), None)
+    t2 = dt.to_numpy((B, L), np.int32)
+    assert t2[0, 4] == int(np.argmax(lg[0])) and t2[1, 2] == 11
+    assert list(dp.to_numpy(B, np.int32)) == [4, 2]
+    table = rng.standard_normal((V, H)).astype(np.float32)
+    out = hip.DeviceBuffer(B * H * 4)
+    hip.call("qlm_embed_tokens", dev(hip, table), V, H, dt, L, dp, out, H, B, None)
+    e = out.to_numpy((B, H), np.float32)
+    assert np.array_equal(e[0], table[t2[0, 4]]) and np.array_equal(e[1], table[11])
+
+
+# ---------------------------------------------------------------- A12 DeltaNet
+def _l2n(x):
+    return (x / np.linalg.norm(x, axis=-1, keepdims=True)).astype(np.float32)
+
+
+@pytest.mark.parametrize("B,H", [(1, 32), (8, 32), (3, 5)])
+def test_gated_delta_step(hip, orc, rng, B, H):
+    d = 128
+    S = (rng.standard_normal((B, H, d, d)) * 0.01).astype(np.float32)
+    dS = dev(hip, S)
+    Sref = S.copy()
+    for step in range(3):
+        q = _l2n(rng.standard_normal((B, H, d)))
+        k = _l2n(rng.standard_normal((B, H, d)))
+        v = rng.standard_normal((B, H, d)).astype(np.float32)
+        a = (1 / (1 + np.exp(-(rng.standard_normal((B, H)) + 2)))).astype(np.float32)
+        b = (1 / (1 + np.exp(-rng.standard_normal((B, H))))).astype(np.float32)
+        o_ref, Sref = orc.gated_delta_step(q, k, v, a, b, Sref)
+        do = hip.DeviceBuffer(q.nbytes)
+        say("delta", B, H, step)
+        hip.call("qlm_gated_delta_step", dev(hip, q), dev(hip, k), dev(hip, v), dev(hip, a),
+                 dev(hip, b), dS, do, B, H, d, None)
+        assert rel_err(do.to_numpy(q.shape, np.float32), o_ref) < 1e-5
+        assert rel_err(dS.to_numpy(S.shape, np.float32), Sref) < 1e-5
+
+
+def test_deltanet_decode_fused(hip, orc, rng):
+    """Fused mixer core over 5 steps (ring index pos % 3) for 2 sequences."""
+    B, H, d = 2, 16, 128
+    HD = H * d
+    ldp = 4 * HD + 2 * H
+    wt = (rng.standard_normal((4, 3 * HD)) * 0.3).astype(np.float32)
+    A_log = np.log(rng.uniform(1, 16, H)).astype(np.float32)
+    dtb = (rng.standard_normal(H) * 0.5 - 4).astype(np.float32)
+    nw = (1 + rng.standard_normal(d) * 0.02).astype(np.float32)
+    conv = np.zeros((B, 3, 3 * HD), np.float32)
+    S = (rng.standard_normal((B, H, d, d)) * 0.01).astype(np.float32)
+    dconv, dS = dev(hip, conv), dev(hip, S)
+    conv_ref = [conv[b].copy() for b in range(B)]
+    S_ref = [S[b].copy() for b in range(B)]
+    dwt, dA, ddt, dnw = dev(hip, wt), dev(hip, A_log), dev(hip, dtb), dev(hip, nw)
+    for step in range(5):
+        proj = (rng.standard_normal((B, ldp)) * 0.6).astype(np.float32)
+        pos = np.array([step, step + 7], np.int32)
+        ref = np.stack([orc.deltanet_core(proj[b], conv_ref[b], int(pos[b] % 3), wt, A_log, dtb,
+                                          nw, S_ref[b], H, d) for b in range(B)])
+        do = hip.DeviceBuffer(B * HD * 4)
+        say("deltanet_decode", step)
+        hip.call("qlm_deltanet_decode", dev(hip, proj), ldp, dconv, dwt, dA, ddt, dnw, dS,
+                 dev(hip, pos), do, HD, B, H, d, None)
+        assert rel_err(do.to_numpy((B, HD), np.float32), ref) < 1e-4
+        assert np.array_equal(dconv.to_numpy(conv.shape, np.float32), np.stack(conv_ref))
+        assert rel_err(dS.to_numpy(S.shape, np.float32), np.stack(S_ref)) < 1e-5
+
+
+# ---------------------------------------------------------------- A8/A9 GQA
+@pytest.mark.parametrize("n_q,n_kv,hd,rot,gated", [(16, 4, 128, 32, 1), (8, 2, 128, 128, 1),
+                                                   (16, 2, 256, 64, 0)])
+def test_gqa_decode_fused(hip, orc, rng, n_q, n_kv, hd, rot, gated):
+    B, max_seq, theta = 2, 600, 1e6
+    qs = (2 if gated else 1) * hd
+    ld = n_q * qs + 2 * n_kv * hd
+    qn = (rng.standard_normal(hd) * 0.02).astype(np.float32)
+    kn = (rng.standard_normal(hd) * 0.02).astype(np.float32)
+    cos_t, sin_t = orc.rope_table(theta, rot, max_seq)
+    kc = np.zeros((B, max_seq, n_kv, hd), np.float32)
+    vc = np.zeros_like(kc)
+    dkc, dvc = dev(hip, kc), dev(hip, vc)
+    kref = [kc[b].copy() for b in range(B)]
+    vref = [vc[b].copy() for b in range(B)]
+    # fill a history so the chunked split (256 positions) is exercised
+    start = [300, 511]
+    for b in range(B):
+        kref[b][: start[b] + 40] = rng.standard_normal((start[b] + 40, n_kv, hd))
+        vref[b][: start[b] + 40] = rng.standard_normal((start[b] + 40, n_kv, hd))
+    dkc.upload(np.stack(kref))
+    dvc.upload(np.stack(vref))
+    work = hip.DeviceBuffer(hip.lib().qlm_gqa_workspace_bytes(B, n_q, hd, max_seq))
+    dcos, dsin = dev(hip, cos_t), dev(hip, sin_t)
+    for step in range(3):
+        pos = np.array([start[0] + step, start[1] + step], np.int32)
+        qkv = rng.standard_normal((B, ld)).astype(np.float32)
+        ref = np.stack([orc.gqa_core(qkv[b].copy(), qn, kn, theta, rot, kref[b], vref[b],
+                                     int(pos[b]), n_q, n_kv, hd, gated) for b in range(B)])
+        do = hip.DeviceBuffer(B * n_q * hd * 4)
+        say("gqa", n_q, n_kv, hd, step)
+        hip.call("qlm_gqa_decode", dev(hip, qkv), ld, dev(hip, qn), dev(hip, kn), dcos, dsin, rot,
+                 dkc, dvc, max_seq, dev(hip, pos), do, n_q * hd, B, n_q, n_kv, hd, gated, work,
+                 None)
+        assert rel_err(do.to_numpy((B, n_q * hd), np.float32), ref) < 1e-5
+        got_k = dkc.to_numpy(kc.shape, np.float32)
+        got_v = dvc.to_numpy(vc.shape, np.float32)
+        for b in range(B):
+            # K went through QK-norm (sum-of-squares order differs) and RoPE
+            assert rel_err(got_k[b, pos[b]], kref[b][pos[b]]) < 1e-6
+            assert np.array_equal(got_v[b, pos[b]], vref[b][pos[b]])
+
+
+@pytest.mark.parametrize("kv", ["f32", "bf16"])
+@pytest.mark.parametrize("ctx", [1, 257, 2048])
+def test_attention_decode(hip, orc, rng, kv, ctx):
+    B, n_q, n_kv, hd, max_seq = 2, 16, 2, 256, 2048
+    q = rng.standard_normal((B, n_q, hd)).astype(np.float32)
+    k = rng.standard_normal((B, max_seq, n_kv, hd)).astype(np.float32)
+    v = rng.standard_normal((B, max_seq, n_kv, hd)).astype(np.float32)
+    if kv == "bf16":
+        kb, vb = bf16_bits(k), bf16_bits(v)
+        k, v = bf16_to_f32(kb), bf16_to_f32(vb)
+        dk, dv = dev(hip, kb), dev(hip, vb)
+    else:
+        dk, dv = dev(hip, k), dev(hip, v)
+    ref = np.stack([orc.attention(q[b], k[b], v[b], ctx) for b in range(B)])
+    work = hip.DeviceBuffer(hip.lib().qlm_gqa_workspace_bytes(B, n_q, hd, max_seq))
+    do = hip.DeviceBuffer(q.nbytes)
+    hip.call("qlm_attention_decode", dev(hip, q), dk, dv, 0 if kv == "f32" else 1, max_seq, ctx,
+             do, B, n_q, n_kv, hd, work, None)
+    assert rel_err(do.to_numpy(q.shape, np.float32), ref) < 1e-5
+    if ctx == 1:  # one position: the output is V[0] exactly up to rounding
+        assert rel_err(do.to_numpy(q.shape, np.float32)[:, :n_q // n_kv],
+                       np.broadcast_to(v[:, 0, :1], (B, n_q // n_kv, hd))) < 1e-6

@@ -1,0 +1,118 @@
+"""Model-level parity: the GPU engine against the reference CPU path.
+
+Golden fixture tests/golden/tiny_greedy.npz was produced by the reference
+sources compiled with IEEE flags (tests/golden/make_golden.py) on the tiny
+hybrid model (1024 hidden, 24 layers 3:1 DeltaNet/GQA, vocab 151936, seeded
+random weights, 128-token prompt, 64 greedy tokens).
+"""
+
+import hashlib
+import os
+import tempfile
+
+import numpy as np
+import pytest
+
+from tests.util import say
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "tiny_greedy.npz")
+
+
+@pytest.fixture(scope="module")
+def golden():
+    return np.load(GOLDEN)
+
+
+@pytest.fixture(scope="module")
+def tiny_dir():
+    from quicklm_amd import synth
+
+    base = "/dev/shm" if os.path.isdir("/dev/shm") else None
+    with tempfile.TemporaryDirectory(dir=base) as d:
+        say("writing tiny model", d)
+        synth.write_model(d, "tiny")
+        yield d
+
+
+@pytest.fixture(scope="module")
+def engine(hip, tiny_dir):
+    from quicklm_amd.engine import Engine
+
+    e = Engine(tiny_dir, max_seq_len=2048, max_batch=2, precision="int8")
+    yield e
+    e.close()
+
+
+def test_synthetic_weights_match_golden(tiny_dir, golden):
+    from oracle.oracle import read_safetensors
+
+    t = read_safetensors(os.path.join(tiny_dir, "model.safetensors"))
+    for name, sha in zip(golden["tensor_names"], golden["tensor_sha"]):
+        assert hashlib.sha256(t[str(name)].tobytes()).hexdigest() == str(sha), name
+
+
+def test_teacher_forced_logits(engine, golden):
+    """Feed the reference's own token stream; every step's top-32 logits must
+    agree with the reference within 1e-3 (normwise, fp32 accumulation)."""
+    prompt, toks = golden["prompt"], golden["tokens"]
+    engine.reset()
+    for p in range(127):
+        engine.forward(int(prompt[p]), p)
+    feed = np.concatenate([prompt[-1:], toks[:-1]])
+    worst = 0.0
+    devs = []
+    for i, t in enumerate(feed):
+        lg = engine.forward(int(t), 127 + i)
+        idx = golden["top_idx"][i]
+        ref = golden["top_val"][i]
+        dev = float(np.abs(lg[idx] - ref).max())
+        devs.append(dev)
+        worst = max(worst, dev / float(np.abs(ref).max()))
+        if i == 0:
+            head = golden["logits0_head"]
+            assert float(np.abs(lg[:4096] - head).max() / np.abs(head).max()) < 1e-3
+    say("teacher-forced max |dlogit| per 8 steps", np.round(devs[::8], 6), "worst rel", worst)
+    assert worst < 1e-3
+
+
+def test_tiny_greedy_matches_reference(engine, golden):
+    out, pre, dec = engine.generate(golden["prompt"][None, :], 64)
+    toks = golden["tokens"]
+    got = out[0]
+    diff = np.nonzero(got != toks)[0]
+    say(f"prefill {pre:.3f}s decode {dec:.3f}s; first divergence:",
+        int(diff[0]) if diff.size else None,
+        "margin there:", float(golden["margin"][diff[0]]) if diff.size else None)
+    assert diff.size == 0, f"first divergence at step {diff[0]} (reference top-2 margin " \
+                           f"{golden['margin'][diff[0]]:.6f})"
+
+
+def test_graph_replay_equals_eager(engine, golden):
+    p = golden["prompt"][None, :40]
+    a, _, _ = engine.generate(p, 16, use_graph=True)
+    la = engine.last_logits(0)
+    b, _, _ = engine.generate(p, 16, use_graph=False)
+    lb = engine.last_logits(0)
+    assert np.array_equal(a, b)
+    assert np.array_equal(la, lb)
+
+
+def test_batch_rows_equal_single(engine, golden):
+    """Two sequences in one batch give exactly the single-sequence results."""
+    p0 = golden["prompt"][:48]
+    p1 = golden["prompt"][48:96]
+    s0, _, _ = engine.generate(p0[None, :], 12)
+    s1, _, _ = engine.generate(p1[None, :], 12)
+    both, _, _ = engine.generate(np.stack([p0, p1]), 12)
+    assert np.array_equal(both[0], s0[0]) and np.array_equal(both[1], s1[0])
+
+
+def test_context_overflow_rejected(engine):
+    from quicklm_amd.engine import EngineError
+
+    with pytest.raises(EngineError, match="context length exceeded"):
+        engine.generate(np.zeros((1, 2000), np.int32), 100)
+    with pytest.raises(EngineError):
+        engine.forward(1, 5000)
