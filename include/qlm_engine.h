@@ -47,6 +47,14 @@ int qlm_engine_forward(void* handle, int token, int pos, float* logits);
 int qlm_engine_generate(void* handle, const int* prompts, int B, int n, int n_new, int* out,
                         double* prefill_s, double* decode_s, int use_graph);
 
+/* Stepwise generation for benchmarks: start() resets and installs B prompts
+ * of length n; steps() runs k decode steps (prompt forwards first) as graph
+ * replays and reports their GPU time in ms (HIP events on the engine's
+ * stream); tokens() copies count tokens of sequence b from position first. */
+int qlm_engine_start(void* handle, const int* prompts, int B, int n);
+int qlm_engine_steps(void* handle, int k, int use_graph, double* gpu_ms);
+int qlm_engine_tokens(void* handle, int b, int first, int count, int* out);
+
 /* Logits of sequence b after the last step, host array [vocab]. */
 int qlm_engine_last_logits(void* handle, int b, float* logits);
 

@@ -90,6 +90,27 @@ int qlm_engine_generate(void* handle, const int* prompts, int B, int n, int n_ne
     });
 }
 
+int qlm_engine_start(void* handle, const int* prompts, int B, int n) {
+    return guarded([&] {
+        if (!prompts) throw std::runtime_error("null prompts");
+        M(handle)->start(prompts, B, n);
+    });
+}
+
+int qlm_engine_steps(void* handle, int k, int use_graph, double* gpu_ms) {
+    return guarded([&] {
+        const double ms = M(handle)->steps(k, use_graph != 0);
+        if (gpu_ms) *gpu_ms = ms;
+    });
+}
+
+int qlm_engine_tokens(void* handle, int b, int first, int count, int* out) {
+    return guarded([&] {
+        if (!out) throw std::runtime_error("null output");
+        M(handle)->tokens(b, first, count, out);
+    });
+}
+
 int qlm_engine_last_logits(void* handle, int b, float* logits) {
     return guarded([&] { M(handle)->last_logits(b, logits); });
 }

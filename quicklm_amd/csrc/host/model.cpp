@@ -345,11 +345,10 @@ void DecoderModel::last_logits(int b, float* host) const {
     check(qlm_stream_sync(stream_), "sync");
 }
 
-void DecoderModel::generate(const int* prompts, int B, int n, int n_new, int* out, GenStats* st,
-                            bool use_graph) {
+void DecoderModel::start(const int* prompts, int B, int n) {
     if (B <= 0 || B > max_batch_) throw std::runtime_error("generate: batch exceeds max_batch");
-    if (n <= 0 || n_new < 0) throw std::runtime_error("generate: empty prompt");
-    if (n + n_new - 1 > max_seq_)
+    if (n <= 0) throw std::runtime_error("generate: empty prompt");
+    if (n > max_seq_)
         throw std::runtime_error("context length exceeded max_seq_len (" + std::to_string(max_seq_) +
                                  ")");
     for (int i = 0; i < B * n; ++i)
@@ -361,22 +360,59 @@ void DecoderModel::generate(const int* prompts, int B, int n, int n_new, int* ou
     check(qlm_memcpy_h2d(tokens_.get(), tok.data(), tok.size() * 4, stream_), "upload");
     check(qlm_memcpy_h2d(prompt_len_.get(), pl.data(), B * 4, stream_), "upload");
     check(qlm_memcpy_h2d(pos_.get(), zero.data(), B * 4, stream_), "upload");
-    void* g = use_graph ? graph_for(B) : nullptr;
-    auto step = [&]() {
+    check(qlm_stream_sync(stream_), "sync");
+    run_B_ = B;
+    run_n_ = n;
+    run_steps_ = 0;
+}
+
+double DecoderModel::steps(int k, bool use_graph) {
+    if (run_B_ == 0) throw std::runtime_error("steps: call start() first");
+    // positions 0 .. run_steps_+k-1 are forwarded; the last token is written
+    // at position run_steps_+k, which the token array must hold
+    if (run_steps_ + k > max_seq_)
+        throw std::runtime_error("context length exceeded max_seq_len (" + std::to_string(max_seq_) +
+                                 ")");
+    void* g = use_graph ? graph_for(run_B_) : nullptr;
+    void *e0 = nullptr, *e1 = nullptr;
+    check(qlm_event_create(&e0), "event");
+    check(qlm_event_create(&e1), "event");
+    check(qlm_event_record(e0, stream_), "event");
+    for (int s = 0; s < k; ++s) {
         if (g) check(qlm_graph_launch(g, stream_), "graph launch");
-        else enqueue_step(B);
-    };
+        else enqueue_step(run_B_);
+    }
+    check(qlm_event_record(e1, stream_), "event");
+    float ms = 0.0f;
+    check(qlm_event_elapsed_ms(&ms, e0, e1), "event");
+    qlm_event_destroy(e0);
+    qlm_event_destroy(e1);
+    run_steps_ += k;
+    return ms;
+}
+
+void DecoderModel::tokens(int b, int first, int count, int* out) const {
+    if (b < 0 || b >= run_B_ || first < 0 || first + count > ld_tokens_)
+        throw std::runtime_error("tokens: range outside the token stream");
+    check(qlm_memcpy_d2h(out, tokens_.get<int>() + (size_t)b * ld_tokens_ + first,
+                         (size_t)count * sizeof(int), stream_),
+          "download");
+    check(qlm_stream_sync(stream_), "sync");
+}
+
+void DecoderModel::generate(const int* prompts, int B, int n, int n_new, int* out, GenStats* st,
+                            bool use_graph) {
+    if (n_new < 0) throw std::runtime_error("generate: negative token count");
+    if (n + n_new - 1 > max_seq_)
+        throw std::runtime_error("context length exceeded max_seq_len (" + std::to_string(max_seq_) +
+                                 ")");
+    start(prompts, B, n);
     const double t0 = now_s();
-    for (int s = 0; s < n - 1; ++s) step();
-    check(qlm_stream_sync(stream_), "sync");
+    steps(n - 1, use_graph);
     const double t1 = now_s();
-    for (int s = 0; s < n_new; ++s) step();
-    check(qlm_stream_sync(stream_), "sync");
+    steps(n_new, use_graph);
     const double t2 = now_s();
-    check(qlm_memcpy_d2h(tok.data(), tokens_.get(), tok.size() * 4, stream_), "download");
-    check(qlm_stream_sync(stream_), "sync");
-    for (int b = 0; b < B; ++b)
-        for (int i = 0; i < n_new; ++i) out[(size_t)b * n_new + i] = tok[(size_t)b * ld_tokens_ + n + i];
+    for (int b = 0; b < B; ++b) tokens(b, n, n_new, out + (size_t)b * n_new);
     if (st) {
         st->prefill_s = t1 - t0;
         st->decode_s = t2 - t1;

@@ -85,6 +85,15 @@ class DecoderModel {
     void generate(const int* prompts, int B, int n, int n_new, int* out, GenStats* st,
                   bool use_graph = true);
 
+    // Stepwise form of generate() for benchmarking: start() resets the state
+    // and installs B prompts of length n; steps(k) replays k decode steps of
+    // batch B (the first n-1 are prompt forwards) and returns the GPU time in
+    // milliseconds measured with events on the engine stream; tokens() reads
+    // back count tokens of sequence b from position first.
+    void start(const int* prompts, int B, int n);
+    double steps(int k, bool use_graph = true);
+    void tokens(int b, int first, int count, int* out) const;
+
     // Logits of sequence b from the most recent step (host copy).
     void last_logits(int b, float* host) const;
 
@@ -125,6 +134,7 @@ class DecoderModel {
     DeviceBuffer staging_;
 
     std::map<int, void*> graphs_;
+    int run_B_ = 0, run_n_ = 0, run_steps_ = 0;
 };
 
 }  // namespace qlm

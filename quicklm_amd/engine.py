@@ -32,6 +32,9 @@ def lib() -> C.CDLL:
         L.qlm_engine_generate.argtypes = [_vp, _vp, _i, _i, _i, _vp, C.POINTER(C.c_double),
                                           C.POINTER(C.c_double), _i]
         L.qlm_engine_last_logits.argtypes = [_vp, _i, _vp]
+        L.qlm_engine_start.argtypes = [_vp, _vp, _i, _i]
+        L.qlm_engine_steps.argtypes = [_vp, _i, _i, C.POINTER(C.c_double)]
+        L.qlm_engine_tokens.argtypes = [_vp, _i, _i, _i, _vp]
         L.qlm_engine_kernels_per_step.argtypes = [_vp]
         _lib = L
     return _lib
@@ -79,6 +82,22 @@ class Engine:
         _check(lib().qlm_engine_generate(self.h, p.ctypes.data, B, n, n_new, out.ctypes.data,
                                          C.byref(pre), C.byref(dec), 1 if use_graph else 0))
         return out, pre.value, dec.value
+
+    def start(self, prompts: np.ndarray) -> None:
+        p = np.ascontiguousarray(np.atleast_2d(prompts), np.int32)
+        self._prompts = p
+        _check(lib().qlm_engine_start(self.h, p.ctypes.data, p.shape[0], p.shape[1]))
+
+    def steps(self, k: int, use_graph: bool = True) -> float:
+        """Run k decode steps; returns their GPU time in ms."""
+        ms = C.c_double()
+        _check(lib().qlm_engine_steps(self.h, k, 1 if use_graph else 0, C.byref(ms)))
+        return ms.value
+
+    def tokens(self, b: int, first: int, count: int) -> np.ndarray:
+        out = np.empty(count, np.int32)
+        _check(lib().qlm_engine_tokens(self.h, b, first, count, out.ctypes.data))
+        return out
 
     def last_logits(self, b: int = 0) -> np.ndarray:
         lg = np.empty(self.vocab, np.float32)
