@@ -82,20 +82,20 @@ def bench_gemv(hip, shapes, Ms, group_kind, iters=100, pool_bytes=2 << 30):
     return out
 
 
-def run_decode(eng, prompts, warmup, steps):
+def run_decode(eng, prompts, warmup, steps, graph=True):
     """Prefill (n-1 prompt forwards), warmup, then exactly `steps` timed steps."""
     B, n = prompts.shape
     eng.start(prompts)
     t0 = time.perf_counter()
-    eng.steps(n - 1)
+    eng.steps(n - 1, graph)
     prefill_s = time.perf_counter() - t0
     if warmup:
-        eng.steps(warmup)
+        eng.steps(warmup, graph)
     from quicklm_amd import hip
 
     hip.sync()
     t1 = time.perf_counter()
-    gpu_ms = eng.steps(steps)
+    gpu_ms = eng.steps(steps, graph)
     hip.sync()
     wall_s = time.perf_counter() - t1
     toks = np.stack([eng.tokens(b, n, warmup + steps) for b in range(B)])
@@ -135,6 +135,9 @@ def main():
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-gemv", action="store_true")
     ap.add_argument("--model-dir", default=None)
+    ap.add_argument("--eager", action="store_true",
+                    help="launch each step's kernels directly instead of replaying the "
+                         "captured hipGraph (for tracers that cannot follow graphs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
@@ -172,12 +175,13 @@ def main():
         log(f"engine load + device quantisation {time.perf_counter() - t0:.1f}s, "
             f"{eng.weight_bytes / 1e9:.3f} GB of int8 weights+scales")
         prompts = synth.prompt_tokens(args.prompt_len, seed=4, batch=Bmax)
-        r1 = run_decode(eng, prompts[:1], args.warmup, args.steps)
+        graph = not args.eager
+        r1 = run_decode(eng, prompts[:1], args.warmup, args.steps, graph)
         log(f"batch 1: {r1['tok_s']:.1f} tok/s ({r1['ms_per_step']:.3f} ms/step), prefill "
             f"{r1['prefill_s']:.1f}s, kernels/step {eng.kernels_per_step()}")
         rB = None
         if args.batch > 1:
-            rB = run_decode(eng, prompts[:args.batch], args.warmup, args.steps)
+            rB = run_decode(eng, prompts[:args.batch], args.warmup, args.steps, graph)
             log(f"batch {args.batch}: {rB['tok_s']:.1f} tok/s ({rB['ms_per_step']:.3f} ms/step)")
             same = bool(np.array_equal(rB["tokens"][0], r1["tokens"][0]))
             log(f"batch row 0 == batch-1 stream: {same}")
@@ -222,6 +226,7 @@ def main():
                                "151936, tied embeddings; 2048-token prompt, greedy decode, "
                                "one hipGraph per step",
                    "batch": 1, "prompt_len": args.prompt_len, "scale_group": 32,
+                   "launch": "eager" if args.eager else "hipGraph",
                    "weight_bytes": wbytes, "parallelism": "single GPU"},
         "batch16": None if rB is None else {"tok_s": round(rB["tok_s"], 2),
                                             "ms_per_step": round(rB["ms_per_step"], 4),

@@ -78,6 +78,13 @@ int qlm_quantize_q8_bf16(const uint16_t* w, int rows, int K, int group, int8_t* 
 int qlm_gemv_i8(const float* x, int ldx, const int8_t* q, const float* scales, int group,
                 float* y, int ldy, int M, int N, int K, void* stream);
 
+/* M = 1 with an explicit launch shape, for tuning sweeps (qlm_gemv_i8 picks
+ * these from N and K): lanes_per_row in {16,...,256} (power of two, at most
+ * 6 16-byte chunks per lane), rows in {1,2} rows per lane group and block,
+ * grid = workgroups (grid-stride over row blocks). */
+int qlm_gemv_i8_config(const float* x, const int8_t* q, const float* scales, int group, float* y,
+                       int N, int K, int lanes_per_row, int rows, int grid, void* stream);
+
 /* Fused forms used by the decode step (same arithmetic as the unfused
  * reference sequence, one launch instead of two or three):
  *   _rmsnorm: x is first replaced by rms_norm(x, norm_w, eps) (zero-centred
@@ -153,7 +160,8 @@ int qlm_deltanet_decode(const float* proj, int ldp, float* conv_state, const flo
  *   positions 0..pos[b], sigmoid(gate) output gate when gated.
  * Cache layout [B, max_seq, n_kv, hd] fp32 (position-major, as the reference,
  * attention.cpp:134-135). out[b] is [n_q*hd]. work is a device workspace of
- * qlm_gqa_workspace_bytes(...) bytes. */
+ * qlm_gqa_workspace_bytes(...) bytes, zero-filled once before its first use
+ * (it holds completion counters that every call leaves at zero). */
 size_t qlm_gqa_workspace_bytes(int B, int n_q, int hd, int max_seq);
 int qlm_gqa_decode(float* qkv, int ldqkv, const float* q_norm, const float* k_norm,
                    const float* cos_tab, const float* sin_tab, int rot_dim, float* k_cache,
@@ -181,6 +189,18 @@ size_t qlm_argmax_workspace_bytes(int B, int n);
  * tokens[b, p+1]; then pos[b] = p+1. tokens is [B, ld_tokens] int32. */
 int qlm_greedy_advance(const float* logits, int ldl, int n, int B, void* work, int* tokens,
                        int ld_tokens, int* pos, const int* prompt_len, void* stream);
+
+/* The whole tail of a batch-1 decode step in one launch: final RMSNorm +
+ * lm_head GEMV (logits [V] stored) + greedy argmax + the advance of
+ * qlm_greedy_advance + the embedding gather of the token now at pos[0] into
+ * h_next [H] (model.cpp:193-199 and :263-274, main.cpp:659-663, then
+ * model.cpp:157-164 for the next step). work is 256 bytes, zero-filled once
+ * before first use (each call leaves it zeroed). */
+size_t qlm_lm_head_greedy_workspace_bytes(void);
+int qlm_lm_head_greedy(const float* x, const float* norm_w, float eps, const int8_t* q,
+                       const float* scales, int group, float* logits, int V, int K, void* work,
+                       int* tokens, int ld_tokens, int* pos, const int* prompt_len,
+                       const float* embed, int H, float* h_next, void* stream);
 
 /* Embedding gather (model.cpp:157-164, F32 table): out[b] = table[tokens[b,
  * pos[b]]] for a [vocab, H] fp32 table (pos NULL: tokens[b, 0]). */

@@ -226,7 +226,12 @@ void DecoderModel::load(const std::string& dir, int max_seq_len, const std::stri
     act_.alloc(B * F * sizeof(float));
     logits_.alloc(B * cfg_.vocab_size * sizeof(float));
     argmax_work_.alloc(qlm_argmax_workspace_bytes((int)B, cfg_.vocab_size));
-    if (QR_ > 0) attn_work_.alloc(qlm_gqa_workspace_bytes((int)B, nq, hd, max_seq_));
+    tail_work_.alloc(qlm_lm_head_greedy_workspace_bytes());
+    check(qlm_fill_u8(tail_work_.get(), 0, tail_work_.bytes(), stream_), "fill");
+    if (QR_ > 0) {
+        attn_work_.alloc(qlm_gqa_workspace_bytes((int)B, nq, hd, max_seq_));
+        check(qlm_fill_u8(attn_work_.get(), 0, attn_work_.bytes(), stream_), "fill");
+    }
     reset_states();
 }
 
@@ -251,10 +256,6 @@ void DecoderModel::enqueue_step(int B) {
     const float eps = cfg_.rms_norm_eps;
     const int Pmax = std::max(PD_, PQ_);
     int n = 0;
-    check(qlm_embed_tokens(embed_.get<float>(), V, H, tokens_.get<int>(), ld_tokens_,
-                           pos_.get<int>(), h_.get<float>(), H, B, stream_),
-          "embed");
-    ++n;
     Tensor hx({B, H}, h_.get<float>());
     int dn_i = 0, at_i = 0;
     for (auto& w : layers_) {
@@ -294,15 +295,38 @@ void DecoderModel::enqueue_step(int B) {
         Tensor act({B, F}, act_.get<float>());
         math::matmul_swiglu_rmsnorm(hx, post_ln, eps, w.gate_up.view(), act);
         math::matmul_residual(act, w.down.view(), hx);
-        n += 2 * ((B + 3) / 4);
+        n += B == 1 ? 2 : 2 * ((B + 3) / 4);
     }
-    Tensor fn({H}, final_norm_.get<float>());
-    Tensor lg({B, V}, logits_.get<float>());
-    math::matmul_rmsnorm(hx, fn, eps, lm_head_.view(), lg);
-    check(qlm_greedy_advance(logits_.get<float>(), V, V, B, argmax_work_.get(), tokens_.get<int>(),
-                             ld_tokens_, pos_.get<int>(), prompt_len_.get<int>(), stream_),
-          "argmax");
-    kernels_per_step_ = n + 3;
+    // Step tail: final norm + lm_head + greedy sample + advance, then the
+    // embedding of the token now at pos (the next step's input, or the next
+    // prompt token) -- model.cpp:193-199, :263-274, :157-164.
+    if (B == 1) {
+        check(qlm_lm_head_greedy(h_.get<float>(), final_norm_.get<float>(), eps,
+                                 lm_head_.q.get<int8_t>(), lm_head_.s.get<float>(), lm_head_.group,
+                                 logits_.get<float>(), V, H, tail_work_.get(), tokens_.get<int>(),
+                                 ld_tokens_, pos_.get<int>(), prompt_len_.get<int>(),
+                                 embed_.get<float>(), H, h_.get<float>(), stream_),
+              "lm_head");
+        n += 1;
+    } else {
+        Tensor fn({H}, final_norm_.get<float>());
+        Tensor lg({B, V}, logits_.get<float>());
+        math::matmul_rmsnorm(hx, fn, eps, lm_head_.view(), lg);
+        check(qlm_greedy_advance(logits_.get<float>(), V, V, B, argmax_work_.get(),
+                                 tokens_.get<int>(), ld_tokens_, pos_.get<int>(),
+                                 prompt_len_.get<int>(), stream_),
+              "argmax");
+        embed_current(B);
+        n += (B + 3) / 4 + 3;
+    }
+    kernels_per_step_ = n;
+}
+
+void DecoderModel::embed_current(int B) {
+    check(qlm_embed_tokens(embed_.get<float>(), cfg_.vocab_size, cfg_.hidden_size,
+                           tokens_.get<int>(), ld_tokens_, pos_.get<int>(), h_.get<float>(),
+                           cfg_.hidden_size, B, stream_),
+          "embed");
 }
 
 void* DecoderModel::graph_for(int B) {
@@ -331,6 +355,7 @@ void DecoderModel::forward(int token, int pos, float* logits_host) {
     check(qlm_memcpy_h2d(tokens_.get<int>() + pos, &token, sizeof(int), stream_), "upload");
     check(qlm_memcpy_h2d(pos_.get<int>(), &pos, sizeof(int), stream_), "upload");
     check(qlm_memcpy_h2d(prompt_len_.get<int>(), &big, sizeof(int), stream_), "upload");
+    embed_current(1);
     check(qlm_graph_launch(graph_for(1), stream_), "graph launch");
     check(qlm_memcpy_d2h(logits_host, logits_.get(), (size_t)cfg_.vocab_size * sizeof(float),
                          stream_),
@@ -360,6 +385,7 @@ void DecoderModel::start(const int* prompts, int B, int n) {
     check(qlm_memcpy_h2d(tokens_.get(), tok.data(), tok.size() * 4, stream_), "upload");
     check(qlm_memcpy_h2d(prompt_len_.get(), pl.data(), B * 4, stream_), "upload");
     check(qlm_memcpy_h2d(pos_.get(), zero.data(), B * 4, stream_), "upload");
+    embed_current(B);
     check(qlm_stream_sync(stream_), "sync");
     run_B_ = B;
     run_n_ = n;

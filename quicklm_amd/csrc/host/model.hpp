@@ -106,6 +106,7 @@ class DecoderModel {
 
    private:
     void enqueue_step(int B);
+    void embed_current(int B);
     void* graph_for(int B);
     void quantize_into(LinearI8& lin, int row_off, const std::string& name);
     void upload_f32(DeviceBuffer& dst, const std::string& name, int64_t expect);
@@ -130,7 +131,7 @@ class DecoderModel {
     DeviceBuffer tokens_, pos_, prompt_len_;
     int ld_tokens_ = 0;
     // activations
-    DeviceBuffer h_, proj_, core_, act_, logits_, argmax_work_, attn_work_;
+    DeviceBuffer h_, proj_, core_, act_, logits_, argmax_work_, attn_work_, tail_work_;
     DeviceBuffer staging_;
 
     std::map<int, void*> graphs_;

@@ -30,7 +30,33 @@ constexpr int kWaves = kThreads / QLM_WAVE;
 constexpr int kLdsBudget = 64 * 1024;
 
 enum { PRO_NONE = 0, PRO_RMSNORM = 1 };
-enum { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2 };
+enum { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_ARGMAX = 3 };
+
+// Greedy tail of a decode step (EPI_ARGMAX, M = 1): the logits are stored,
+// each workgroup folds its rows' maximum (first index wins ties, as
+// DecoderModel::sample, model.cpp:263-274) into a 64-bit key with atomicMax,
+// and the last workgroup to finish advances the sequence (token written
+// unless position p+1 is still prompt, pos += 1) and gathers the embedding
+// of the token now at pos into h for the next step. key/count start at zero
+// and are reset by that last workgroup.
+struct GreedyTail {
+    unsigned long long* key;
+    unsigned* count;
+    int* tokens;
+    int ld_tokens;
+    int* pos;
+    const int* prompt_len;
+    const float* embed;
+    int H;
+    int vocab;
+    float* h;
+};
+
+__device__ __forceinline__ unsigned long long argmax_key(float v, int idx) {
+    unsigned u = __float_as_uint(v);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);  // monotone in v (non-NaN)
+    return ((unsigned long long)u << 32) | (unsigned long long)(0xFFFFFFFFu - (unsigned)idx);
+}
 
 __device__ __forceinline__ float dot16(const int4 w, const float4 a, const float4 b,
                                        const float4 c, const float4 d) {
@@ -269,6 +295,326 @@ __global__ __launch_bounds__(kThreads) void k_gemv_i8(
     }
 }
 
+// ---------------------------------------------------------------------------
+// M = 1, activation-stationary form (the batch-1 decode path).
+//
+// A row is shared by `lpr` lanes (16..256, a power of two); lane li of a row
+// group owns the 16-byte chunks c = li + s*lpr, s < SLOTS, of EVERY row, so
+// its slice of the activation vector (SLOTS x 16 floats, normalised once when
+// the RMSNorm prologue is fused) stays in registers for the whole kernel and
+// is never re-read. A workgroup (256 lanes = 256/lpr row groups) walks row
+// blocks of (256/lpr)*R rows with a grid-stride loop; the next block's weight
+// chunks (and group scales) are loaded before the current block is reduced,
+// so 2*R*SLOTS 16-byte loads per lane are in flight. With lpr chosen so that
+// SLOTS*lpr*16 >= K, every chunk of a row is loaded by exactly one lane.
+// Partial sums are reduced across the lpr lanes of the row (butterfly inside
+// a wave, then through LDS when lpr > 64) in a fixed order.
+template <int SLOTS, int R, bool ROWSCALE, int PRO, int EPI>
+__global__ __launch_bounds__(kThreads) void k_gemv_xs(
+    const float* __restrict__ x, const float* __restrict__ nw, float eps,
+    const int8_t* __restrict__ q, const float* __restrict__ sc, float* __restrict__ y, int N,
+    int K, int F, int lpr, int nblocks, GreedyTail tail) {
+    __shared__ float red[kWaves][R];
+    __shared__ float ssr[kWaves];
+    float best_v = -INFINITY;  // EPI_ARGMAX: this lane's best stored logit
+    int best_i = 0x7fffffff;
+    const int tid = threadIdx.x;
+    const int lane = tid & (QLM_WAVE - 1);
+    const int wave = tid / QLM_WAVE;
+    const int li = tid & (lpr - 1);
+    const int grp = tid / lpr;
+    const int groups = kThreads / lpr;
+    const int nchunk = K >> 4;
+    const int nblk = K >> 5;
+    const int wpg = lpr > QLM_WAVE ? lpr / QLM_WAVE : 1;  // waves per row group
+
+    // ---- activation slice into registers (+ fused RMSNorm) ----
+    float4 xv[SLOTS][4];
+#pragma unroll
+    for (int s = 0; s < SLOTS; ++s) {
+        const int c = li + s * lpr;
+        if (c < nchunk) {
+            const float4* p = reinterpret_cast<const float4*>(x) + c * 4;
+            xv[s][0] = p[0];
+            xv[s][1] = p[1];
+            xv[s][2] = p[2];
+            xv[s][3] = p[3];
+        } else {
+            xv[s][0] = xv[s][1] = xv[s][2] = xv[s][3] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    }
+    if constexpr (PRO == PRO_RMSNORM) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int s = 0; s < SLOTS; ++s)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                ss = fmaf(xv[s][j].x, xv[s][j].x, ss);
+                ss = fmaf(xv[s][j].y, xv[s][j].y, ss);
+                ss = fmaf(xv[s][j].z, xv[s][j].z, ss);
+                ss = fmaf(xv[s][j].w, xv[s][j].w, ss);
+            }
+        // every row group holds all of x: reduce inside group 0's lanes
+        if (lpr <= QLM_WAVE) {
+            for (int m = lpr >> 1; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, QLM_WAVE);
+            if (tid == 0) ssr[0] = ss;
+        } else {
+            ss = wave_sum(ss);
+            if (lane == 0) ssr[wave] = ss;
+        }
+        __syncthreads();
+        float tot = ssr[0];
+        for (int w = 1; w < wpg; ++w) tot += ssr[w];  // waves 0..wpg-1 form group 0
+        const float rs = 1.0f / sqrtf(tot / (float)K + eps);
+#pragma unroll
+        for (int s = 0; s < SLOTS; ++s) {
+            const int c = li + s * lpr;
+            if (c < nchunk) {
+                const float4* wp = reinterpret_cast<const float4*>(nw) + c * 4;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) xv[s][j] = norm4(xv[s][j], rs, wp[j]);
+            }
+        }
+    }
+
+    // ---- row blocks ----
+    // Loads never branch: a lane's chunk index is clamped into the row (the
+    // matching activation slot is zero, so the duplicate contributes 0) and
+    // rows past N are clamped to N-1 (computed, never stored).
+    constexpr int OUT_PER_GRP = (EPI == EPI_SWIGLU) ? R / 2 : R;
+    const int out_per_block = groups * OUT_PER_GRP;
+    int soff[SLOTS], coff[SLOTS];
+#pragma unroll
+    for (int s = 0; s < SLOTS; ++s) {
+        const int c = min(li + s * lpr, nchunk - 1);
+        soff[s] = c << 4;
+        coff[s] = c >> 1;
+    }
+    auto out_row = [&](int rb, int r) -> int {
+        return rb * out_per_block + grp * OUT_PER_GRP + ((EPI == EPI_SWIGLU) ? (r % (R / 2)) : r);
+    };
+    auto load = [&](int rb, int4 (&w)[R][SLOTS], float (&sv)[R][SLOTS]) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            int o = min(out_row(rb, r), N - 1);
+            if constexpr (EPI == EPI_SWIGLU)
+                if (r >= R / 2) o += F;
+            const int8_t* rp = q + (size_t)o * K;
+            const float* sp = sc + (size_t)o * nblk;
+#pragma unroll
+            for (int s = 0; s < SLOTS; ++s) {
+                w[r][s] = *reinterpret_cast<const int4*>(rp + soff[s]);
+                if constexpr (!ROWSCALE) sv[r][s] = sp[coff[s]];
+            }
+        }
+    };
+    auto finish = [&](int rb, const int4 (&w)[R][SLOTS], const float (&sv)[R][SLOTS]) {
+        float acc[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            acc[r] = 0.0f;
+#pragma unroll
+            for (int s = 0; s < SLOTS; ++s) {
+                const float p = dot16(w[r][s], xv[s][0], xv[s][1], xv[s][2], xv[s][3]);
+                if constexpr (ROWSCALE)
+                    acc[r] += p;
+                else
+                    acc[r] = fmaf(p, sv[r][s], acc[r]);
+            }
+        }
+        // reduce each row over its lpr lanes (fixed order)
+        if (lpr <= QLM_WAVE) {
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                for (int m = lpr >> 1; m >= 1; m >>= 1) acc[r] += __shfl_xor(acc[r], m, QLM_WAVE);
+        } else {
+#pragma unroll
+            for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
+            if (lane == 0) {
+#pragma unroll
+                for (int r = 0; r < R; ++r) red[wave][r] = acc[r];
+            }
+            __syncthreads();
+            const int w0 = grp * wpg;
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                float t = red[w0][r];
+                for (int w2 = 1; w2 < wpg; ++w2) t += red[w0 + w2][r];
+                acc[r] = t;
+            }
+            __syncthreads();  // red is rewritten by the next block
+        }
+        if constexpr (ROWSCALE) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                int o = min(out_row(rb, r), N - 1);
+                if constexpr (EPI == EPI_SWIGLU)
+                    if (r >= R / 2) o += F;
+                acc[r] *= sc[o];
+            }
+        }
+        // epilogue: lane li == r of each row group stores output r
+        const int o0 = rb * out_per_block + grp * OUT_PER_GRP;
+#pragma unroll
+        for (int r = 0; r < OUT_PER_GRP; ++r) {
+            if (li == r && o0 + r < N) {
+                float* dst = y + o0 + r;
+                if constexpr (EPI == EPI_SWIGLU)
+                    *dst = silu_f(acc[r]) * acc[r + R / 2];
+                else if constexpr (EPI == EPI_RESID)
+                    *dst = *dst + acc[r];
+                else
+                    *dst = acc[r];
+                if constexpr (EPI == EPI_ARGMAX) {
+                    if (acc[r] > best_v || (acc[r] == best_v && o0 + r < best_i)) {
+                        best_v = acc[r];
+                        best_i = o0 + r;
+                    }
+                }
+            }
+        }
+    };
+
+    // two register buffers used in turn: block b+grid loads while b reduces
+    int4 wa[R][SLOTS], wb[R][SLOTS];
+    float sa[R][SLOTS], sb[R][SLOTS];
+    int rb = blockIdx.x;
+    if (EPI != EPI_ARGMAX && rb >= nblocks) return;  // uniform per workgroup
+    if (rb < nblocks) load(rb, wa, sa);
+    while (rb < nblocks) {
+        int rn = rb + gridDim.x;
+        if (rn < nblocks) load(rn, wb, sb);
+        finish(rb, wa, sa);
+        rb = rn;
+        if (rb >= nblocks) break;
+        rn = rb + gridDim.x;
+        if (rn < nblocks) load(rn, wa, sa);
+        finish(rb, wb, sb);
+        rb = rn;
+    }
+
+    if constexpr (EPI == EPI_ARGMAX) {
+        // workgroup maximum, then the device-wide one through the 64-bit key
+        unsigned long long k = argmax_key(best_v, best_i);
+        if (best_i == 0x7fffffff) k = 0ull;
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) {
+            const unsigned long long o = __shfl_xor(k, m, QLM_WAVE);
+            k = o > k ? o : k;
+        }
+        __shared__ unsigned long long wk[kWaves];
+        __shared__ int last;
+        if (lane == 0) wk[wave] = k;
+        __syncthreads();
+        if (tid == 0) {
+            unsigned long long m = wk[0];
+            for (int w2 = 1; w2 < kWaves; ++w2) m = wk[w2] > m ? wk[w2] : m;
+            if (m) atomicMax(tail.key, m);
+            __threadfence();
+            last = atomicAdd(tail.count, 1u) == gridDim.x - 1;
+        }
+        __syncthreads();
+        if (!last) return;
+        __threadfence();
+        __shared__ int tok;
+        if (tid == 0) {
+            const unsigned long long m = atomicAdd(tail.key, 0ull);
+            int idx = m ? (int)(0xFFFFFFFFu - (unsigned)(m & 0xFFFFFFFFull)) : 0;
+            if (idx < 0 || idx >= N) idx = 0;
+            const int p = tail.pos[0];
+            if (p + 1 < tail.ld_tokens && p + 1 >= tail.prompt_len[0]) tail.tokens[p + 1] = idx;
+            int t = (p + 1 < tail.ld_tokens) ? tail.tokens[p + 1] : idx;
+            t = t < 0 ? 0 : (t >= tail.vocab ? tail.vocab - 1 : t);
+            tok = t;
+            tail.pos[0] = p + 1;
+            atomicExch(tail.key, 0ull);
+            atomicExch(tail.count, 0u);
+        }
+        __syncthreads();
+        const float* src = tail.embed + (size_t)tok * tail.H;
+        for (int i = tid; i < tail.H; i += kThreads) tail.h[i] = src[i];
+    }
+}
+
+struct XsConfig {
+    int lpr, slots, R, grid;
+};
+
+// Launch-shape choice for M = 1, from a sweep over the model and config-1
+// shapes on MI355X: ~2-3 chunk slots per lane (lanes per row 64..256) for
+// the small decode projections, 5 slots and two rows per lane group for the
+// 151936-row logits matrix; a grid of up to N/8 workgroups (512..2048).
+XsConfig xs_config(int N, int K, int epi) {
+    const int nchunk = K >> 4;
+    const bool tall = N >= 65536;
+    int lpr = tall ? 32 : 64;
+    while (lpr < 256 && (nchunk + lpr - 1) / lpr > (tall ? 6 : 3)) lpr *= 2;
+    XsConfig c;
+    c.lpr = lpr;
+    c.slots = (nchunk + lpr - 1) / lpr;
+    const int groups = kThreads / lpr;
+    c.R = (epi == EPI_SWIGLU) ? 2 : ((tall || (K >= 8192 && N <= 4096)) ? 2 : 1);
+    const int out_per_block = groups * ((epi == EPI_SWIGLU) ? c.R / 2 : c.R);
+    const int nblocks = (N + out_per_block - 1) / out_per_block;
+    int cap = N / 8;
+    cap = cap < 512 ? 512 : (cap > 2048 ? 2048 : cap);
+    c.grid = nblocks < cap ? nblocks : cap;
+    return c;
+}
+
+template <int SLOTS, int R, bool ROWSCALE, int PRO, int EPI>
+int launch_xs(const XsConfig& c, const float* x, const float* nw, float eps, const int8_t* q,
+              const float* sc, float* y, int N, int K, int F, hipStream_t st,
+              const GreedyTail& tail) {
+    const int groups = kThreads / c.lpr;
+    const int out_per_block = groups * ((EPI == EPI_SWIGLU) ? R / 2 : R);
+    const int nblocks = (N + out_per_block - 1) / out_per_block;
+    hipLaunchKernelGGL((k_gemv_xs<SLOTS, R, ROWSCALE, PRO, EPI>), dim3(c.grid), dim3(kThreads), 0,
+                       st, x, nw, eps, q, sc, y, N, K, F, c.lpr, nblocks, tail);
+    return qlm_launch_status();
+}
+
+template <bool ROWSCALE, int PRO, int EPI>
+int launch_xs_sr(const XsConfig& c, const float* x, const float* nw, float eps, const int8_t* q,
+                 const float* sc, float* y, int N, int K, int F, hipStream_t st,
+                 const GreedyTail& tail) {
+#define QLM_XS(S, RR)                                                                        \
+    if (c.slots <= S && c.R == RR)                                                           \
+        return launch_xs<S, RR, ROWSCALE, PRO, EPI>(c, x, nw, eps, q, sc, y, N, K, F, st, tail);
+    if (EPI == EPI_SWIGLU) {
+        QLM_XS(2, 2) QLM_XS(3, 2) QLM_XS(4, 2) QLM_XS(5, 2) QLM_XS(6, 2)
+        QLM_XS(2, 4) QLM_XS(3, 4) QLM_XS(4, 4) QLM_XS(5, 4) QLM_XS(6, 4)
+    } else {
+        QLM_XS(2, 1) QLM_XS(3, 1) QLM_XS(4, 1) QLM_XS(5, 1) QLM_XS(6, 1)
+        QLM_XS(2, 2) QLM_XS(3, 2) QLM_XS(4, 2) QLM_XS(5, 2) QLM_XS(6, 2)
+    }
+#undef QLM_XS
+    return QLM_ERR_SHAPE;
+}
+
+int xs_dispatch(int pro, int epi, XsConfig c, const float* x, const float* nw, float eps,
+                const int8_t* q, const float* sc, bool rowscale, float* y, int N, int K,
+                hipStream_t st, const GreedyTail& tail = GreedyTail{}) {
+    const int F = N;
+#define QLM_XS_CALL(RS, P, E) \
+    return launch_xs_sr<RS, P, E>(c, x, nw, eps, q, sc, y, N, K, F, st, tail)
+    if (epi == EPI_ARGMAX) {
+        if (rowscale) QLM_XS_CALL(true, PRO_RMSNORM, EPI_ARGMAX);
+        QLM_XS_CALL(false, PRO_RMSNORM, EPI_ARGMAX);
+    }
+    if (rowscale) {
+        if (pro == PRO_NONE && epi == EPI_STORE) QLM_XS_CALL(true, PRO_NONE, EPI_STORE);
+        if (pro == PRO_RMSNORM && epi == EPI_STORE) QLM_XS_CALL(true, PRO_RMSNORM, EPI_STORE);
+        if (pro == PRO_NONE && epi == EPI_RESID) QLM_XS_CALL(true, PRO_NONE, EPI_RESID);
+        QLM_XS_CALL(true, PRO_RMSNORM, EPI_SWIGLU);
+    }
+    if (pro == PRO_NONE && epi == EPI_STORE) QLM_XS_CALL(false, PRO_NONE, EPI_STORE);
+    if (pro == PRO_RMSNORM && epi == EPI_STORE) QLM_XS_CALL(false, PRO_RMSNORM, EPI_STORE);
+    if (pro == PRO_NONE && epi == EPI_RESID) QLM_XS_CALL(false, PRO_NONE, EPI_RESID);
+    QLM_XS_CALL(false, PRO_RMSNORM, EPI_SWIGLU);
+#undef QLM_XS_CALL
+}
+
 template <int R, int M, bool ROWSCALE, int PRO, int EPI, bool XLDS>
 int launch_one(const float* x, int ldx, int mr, const float* nw, float eps, const int8_t* q,
                const float* sc, float* y, int ldy, int N, int K, int F, hipStream_t st) {
@@ -325,6 +671,9 @@ int gemv_dispatch(int pro, int epi, const float* x, int ldx, const float* nw, fl
     // 16-byte vector loads of activations, weights and norm gains
     if (((uintptr_t)x | (uintptr_t)q | (uintptr_t)nw) & 15u) return QLM_ERR_SHAPE;
     hipStream_t st = as_stream(stream);
+    if (M == 1)
+        return xs_dispatch(pro, epi, xs_config(N, K, epi), x, nw, eps, q, sc, rowscale, y, N, K,
+                           st);
     const int F = N;  // swiglu: up rows start at F
     for (int m0 = 0; m0 < M; m0 += 4) {
         const int mr = (M - m0) < 4 ? (M - m0) : 4;
@@ -364,6 +713,57 @@ extern "C" int qlm_gemv_i8(const float* x, int ldx, const int8_t* q, const float
                            int group, float* y, int ldy, int M, int N, int K, void* stream) {
     return gemv_dispatch(PRO_NONE, EPI_STORE, x, ldx, nullptr, 0.0f, q, scales, group, y, ldy, M,
                          N, K, stream);
+}
+
+extern "C" int qlm_gemv_i8_config(const float* x, const int8_t* q, const float* scales, int group,
+                                  float* y, int N, int K, int lanes_per_row, int rows,
+                                  int grid, void* stream) {
+    if (!x || !q || !scales || !y || N <= 0 || K <= 0 || grid <= 0) return QLM_ERR_ARG;
+    if (K % 16 != 0) return QLM_ERR_SHAPE;
+    const bool rowscale = (group == K);
+    if (!rowscale && (group != 32 || K % 32 != 0)) return QLM_ERR_SHAPE;
+    if (lanes_per_row < 16 || lanes_per_row > 256 || (lanes_per_row & (lanes_per_row - 1)))
+        return QLM_ERR_SHAPE;
+    if (rows != 1 && rows != 2) return QLM_ERR_SHAPE;
+    if (((uintptr_t)x | (uintptr_t)q) & 15u) return QLM_ERR_SHAPE;
+    XsConfig c;
+    c.lpr = lanes_per_row;
+    c.slots = ((K >> 4) + lanes_per_row - 1) / lanes_per_row;
+    if (c.slots > 6) return QLM_ERR_SHAPE;
+    c.R = rows;
+    c.grid = grid;
+    return xs_dispatch(PRO_NONE, EPI_STORE, c, x, nullptr, 0.0f, q, scales, rowscale, y, N, K,
+                       as_stream(stream));
+}
+
+extern "C" size_t qlm_lm_head_greedy_workspace_bytes(void) { return 256; }
+
+extern "C" int qlm_lm_head_greedy(const float* x, const float* norm_w, float eps, const int8_t* q,
+                                  const float* scales, int group, float* logits, int V, int K,
+                                  void* work, int* tokens, int ld_tokens, int* pos,
+                                  const int* prompt_len, const float* embed, int H, float* h_next,
+                                  void* stream) {
+    if (!x || !norm_w || !q || !scales || !logits || !work || !tokens || !pos || !prompt_len ||
+        !embed || !h_next || V <= 0 || K <= 0 || H <= 0 || ld_tokens <= 0)
+        return QLM_ERR_ARG;
+    if (K % 16 != 0) return QLM_ERR_SHAPE;
+    const bool rowscale = (group == K);
+    if (!rowscale && (group != 32 || K % 32 != 0)) return QLM_ERR_SHAPE;
+    if (((uintptr_t)x | (uintptr_t)q | (uintptr_t)norm_w | (uintptr_t)work) & 15u)
+        return QLM_ERR_SHAPE;
+    GreedyTail t;
+    t.key = reinterpret_cast<unsigned long long*>(work);
+    t.count = reinterpret_cast<unsigned*>(reinterpret_cast<char*>(work) + 64);
+    t.tokens = tokens;
+    t.ld_tokens = ld_tokens;
+    t.pos = pos;
+    t.prompt_len = prompt_len;
+    t.embed = embed;
+    t.H = H;
+    t.vocab = V;
+    t.h = h_next;
+    return xs_dispatch(PRO_RMSNORM, EPI_ARGMAX, xs_config(V, K, EPI_STORE), x, norm_w, eps, q,
+                       scales, rowscale, logits, V, K, as_stream(stream), t);
 }
 
 extern "C" int qlm_gemv_i8_rmsnorm(const float* x, int ldx, const float* norm_w, float eps,

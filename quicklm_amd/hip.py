@@ -49,6 +49,7 @@ _SIGS = {
     "qlm_quantize_q8_f32": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp]),
     "qlm_quantize_q8_bf16": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp]),
     "qlm_gemv_i8": (_i, [_vp, _i, _vp, _vp, _i, _vp, _i, _i, _i, _i, _vp]),
+    "qlm_gemv_i8_config": (_i, [_vp, _vp, _vp, _i, _vp, _i, _i, _i, _i, _i, _vp]),
     "qlm_gemv_i8_rmsnorm": (_i, [_vp, _i, _vp, _f, _vp, _vp, _i, _vp, _i, _i, _i, _i, _vp]),
     "qlm_gemv_i8_residual": (_i, [_vp, _i, _vp, _vp, _i, _vp, _i, _i, _i, _i, _vp]),
     "qlm_gemv_i8_swiglu_rmsnorm": (_i, [_vp, _i, _vp, _f, _vp, _vp, _i, _vp, _i, _i, _i, _i,
@@ -68,6 +69,9 @@ _SIGS = {
     "qlm_argmax": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp]),
     "qlm_argmax_workspace_bytes": (_sz, [_i, _i]),
     "qlm_greedy_advance": (_i, [_vp, _i, _i, _i, _vp, _vp, _i, _vp, _vp, _vp]),
+    "qlm_lm_head_greedy_workspace_bytes": (_sz, []),
+    "qlm_lm_head_greedy": (_i, [_vp, _vp, _f, _vp, _vp, _i, _vp, _i, _i, _vp, _vp, _i, _vp, _vp,
+                                _vp, _i, _vp, _vp]),
     "qlm_embed_tokens": (_i, [_vp, _i, _i, _vp, _i, _vp, _vp, _i, _i, _vp]),
 }
 

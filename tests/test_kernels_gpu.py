@@ -79,6 +79,27 @@ def test_gemv_parity(hip, orc, rng, N, K, group):
         assert err < 1e-5, err  # fp32 accumulation: far inside the bar
 
 
+@pytest.mark.parametrize("N,K", [(2560, 9728), (1000, 2560), (77, 1024)])
+def test_gemv_launch_shapes(hip, orc, rng, N, K):
+    """Every lanes-per-row / rows / grid combination of the M = 1 kernel gives
+    the oracle's result (grid-stride loop, ragged last block, idle slots)."""
+    for g in (32, K):
+        q, s = _weights(orc, rng, N, K, g)
+        x = rng.standard_normal((1, K)).astype(np.float32)
+        ref = orc.matmul_i8(x, q, s, g)
+        dq, ds, dx = dev(hip, q), dev(hip, s), dev(hip, x)
+        dy = hip.DeviceBuffer(N * 4)
+        for lpr in (16, 32, 64, 128, 256):
+            if (K // 16 + lpr - 1) // lpr > 6:
+                continue
+            for rows in (1, 2):
+                for grid in (1, 7, 300):
+                    dy.zero()
+                    hip.call("qlm_gemv_i8_config", dx, dq, ds, g, dy, N, K, lpr, rows, grid, None)
+                    err = rel_err(dy.to_numpy((1, N), np.float32), ref)
+                    assert err < 1e-5, (g, lpr, rows, grid, err)
+
+
 def test_gemv_exact_integers(hip, orc, rng):
     """Integer activations and power-of-two scales make every sum exact in
     fp32, so any accumulation order must agree bit for bit with the oracle."""
@@ -245,6 +266,42 @@ def test_greedy_advance_and_embed(hip, rng):
     assert np.array_equal(e[0], table[t2[0, 4]]) and np.array_equal(e[1], table[11])
 
 
+@pytest.mark.parametrize("group", [32, "K"])
+def test_lm_head_greedy_fused(hip, orc, rng, group):
+    """Final norm + lm_head + argmax + advance + next embedding in one launch,
+    three calls in a row (prompt position, then two generated tokens)."""
+    V, K, L = 151936, 1024, 16
+    g = K if group == "K" else 32
+    q, s = _weights(orc, rng, V, K, g)
+    nw = (rng.standard_normal(K) * 0.02).astype(np.float32)
+    table = rng.standard_normal((V, K)).astype(np.float32)
+    tokens = np.zeros(L, np.int32)
+    tokens[:3] = [11, 22, 33]
+    dtok, dpos = dev(hip, tokens), dev(hip, np.array([1], np.int32))
+    dplen = dev(hip, np.array([3], np.int32))
+    work = hip.DeviceBuffer(hip.lib().qlm_lm_head_greedy_workspace_bytes())
+    work.zero()
+    dq, ds, dnw, dtab = dev(hip, q), dev(hip, s), dev(hip, nw), dev(hip, table)
+    dlg, dh = hip.DeviceBuffer(V * 4), hip.DeviceBuffer(K * 4)
+    p = 1
+    for step in range(3):
+        x = (rng.standard_normal((1, K)) * 2).astype(np.float32)
+        lg_ref = orc.matmul_i8(orc.rms_norm(x, nw, 1e-6), q, s, g)[0]
+        hip.call("qlm_lm_head_greedy", dev(hip, x), dnw, 1e-6, dq, ds, g, dlg, V, K, work, dtok, L,
+                 dpos, dplen, dtab, K, dh, None)
+        lg = dlg.to_numpy(V, np.float32)
+        assert rel_err(lg, lg_ref) < 1e-5
+        want = int(np.argmax(lg))  # first maximum of the GPU's own logits
+        t = dtok.to_numpy(L, np.int32)
+        if p + 1 >= 3:
+            assert t[p + 1] == want, step
+            tokens[p + 1] = want
+        assert np.array_equal(t, tokens)
+        p += 1
+        assert int(dpos.to_numpy(1, np.int32)[0]) == p
+        assert np.array_equal(dh.to_numpy(K, np.float32), table[tokens[p]])
+
+
 # ---------------------------------------------------------------- A12 DeltaNet
 def _l2n(x):
     return (x / np.linalg.norm(x, axis=-1, keepdims=True)).astype(np.float32)
@@ -323,6 +380,7 @@ def test_gqa_decode_fused(hip, orc, rng, n_q, n_kv, hd, rot, gated):
     dkc.upload(np.stack(kref))
     dvc.upload(np.stack(vref))
     work = hip.DeviceBuffer(hip.lib().qlm_gqa_workspace_bytes(B, n_q, hd, max_seq))
+    work.zero()  # completion counters start at zero; every call leaves them there
     dcos, dsin = dev(hip, cos_t), dev(hip, sin_t)
     for step in range(3):
         pos = np.array([start[0] + step, start[1] + step], np.int32)
@@ -358,6 +416,7 @@ def test_attention_decode(hip, orc, rng, kv, ctx):
         dk, dv = dev(hip, k), dev(hip, v)
     ref = np.stack([orc.attention(q[b], k[b], v[b], ctx) for b in range(B)])
     work = hip.DeviceBuffer(hip.lib().qlm_gqa_workspace_bytes(B, n_q, hd, max_seq))
+    work.zero()
     do = hip.DeviceBuffer(q.nbytes)
     hip.call("qlm_attention_decode", dev(hip, q), dk, dv, 0 if kv == "f32" else 1, max_seq, ctx,
              do, B, n_q, n_kv, hd, work, None)
