@@ -78,12 +78,17 @@ int qlm_quantize_q8_bf16(const uint16_t* w, int rows, int K, int group, int8_t* 
 int qlm_gemv_i8(const float* x, int ldx, const int8_t* q, const float* scales, int group,
                 float* y, int ldy, int M, int N, int K, void* stream);
 
-/* M = 1 with an explicit launch shape, for tuning sweeps (qlm_gemv_i8 picks
- * these from N and K): lanes_per_row in {16,...,256} (power of two, at most
- * 6 16-byte chunks per lane), rows in {1,2} rows per lane group and block,
- * grid = workgroups (grid-stride over row blocks). */
-int qlm_gemv_i8_config(const float* x, const int8_t* q, const float* scales, int group, float* y,
-                       int N, int K, int lanes_per_row, int rows, int grid, void* stream);
+/* M = 1 with an explicit launch shape, for tuning sweeps (the M = 1 forms of
+ * qlm_gemv_i8 and the fused entry points below pick these from N and K).
+ * norm_w NULL: plain x; else the RMSNorm prologue of qlm_gemv_i8_rmsnorm.
+ * epilogue 0: y = result; 1: y += result (qlm_gemv_i8_residual); 2: SwiGLU
+ * as qlm_gemv_i8_swiglu_rmsnorm (N = F outputs, weights [2F, K]).
+ * lanes_per_row in {16,...,256} (power of two, at most 6 16-byte chunks per
+ * lane), rows in {1,2} output rows per lane group and block, grid =
+ * workgroups (grid-stride over row blocks, launched as given). */
+int qlm_gemv_i8_config(const float* x, const float* norm_w, float eps, const int8_t* q,
+                       const float* scales, int group, float* y, int N, int K, int epilogue,
+                       int lanes_per_row, int rows, int grid, void* stream);
 
 /* Fused forms used by the decode step (same arithmetic as the unfused
  * reference sequence, one launch instead of two or three):
@@ -190,12 +195,14 @@ size_t qlm_argmax_workspace_bytes(int B, int n);
 int qlm_greedy_advance(const float* logits, int ldl, int n, int B, void* work, int* tokens,
                        int ld_tokens, int* pos, const int* prompt_len, void* stream);
 
-/* The whole tail of a batch-1 decode step in one launch: final RMSNorm +
- * lm_head GEMV (logits [V] stored) + greedy argmax + the advance of
- * qlm_greedy_advance + the embedding gather of the token now at pos[0] into
- * h_next [H] (model.cpp:193-199 and :263-274, main.cpp:659-663, then
- * model.cpp:157-164 for the next step). work is 256 bytes, zero-filled once
- * before first use (each call leaves it zeroed). */
+/* The whole tail of a batch-1 decode step in two launches: final RMSNorm +
+ * lm_head GEMV (logits [V] stored) with a per-workgroup argmax, then one
+ * workgroup that finishes the argmax, does the advance of qlm_greedy_advance
+ * and gathers the embedding of the token now at pos[0] into h_next [H]
+ * (model.cpp:193-199 and :263-274, main.cpp:659-663, then model.cpp:157-164
+ * for the next step). work is qlm_lm_head_greedy_workspace_bytes() bytes
+ * (16-byte aligned, no initial contents needed); calls that share a work
+ * buffer must be ordered on one stream. */
 size_t qlm_lm_head_greedy_workspace_bytes(void);
 int qlm_lm_head_greedy(const float* x, const float* norm_w, float eps, const int8_t* q,
                        const float* scales, int group, float* logits, int V, int K, void* work,

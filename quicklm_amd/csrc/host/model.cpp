@@ -290,7 +290,7 @@ void DecoderModel::enqueue_step(int B) {
             core.strides = {CORE_, 1};
             math::matmul_residual(core, w.at_o.view(), hx);
             ++at_i;
-            n += 5;
+            n += 4;  // projection, attention, combine, o_proj
         }
         Tensor act({B, F}, act_.get<float>());
         math::matmul_swiglu_rmsnorm(hx, post_ln, eps, w.gate_up.view(), act);
@@ -307,7 +307,7 @@ void DecoderModel::enqueue_step(int B) {
                                  ld_tokens_, pos_.get<int>(), prompt_len_.get<int>(),
                                  embed_.get<float>(), H, h_.get<float>(), stream_),
               "lm_head");
-        n += 1;
+        n += 2;
     } else {
         Tensor fn({H}, final_norm_.get<float>());
         Tensor lg({B, V}, logits_.get<float>());

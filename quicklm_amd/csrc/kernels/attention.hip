@@ -2,24 +2,27 @@
 // [B, max_seq, n_kv, hd] (reference: Qwen3_5Attention::forward,
 // attention.cpp:138-232; gqa_attend_head :54-82).
 //
-// One kernel, k_attn, one workgroup per (chunk of CH positions, kv head g,
-// sequence b); the G = n_q/n_kv query heads of the group share every K/V row
-// read. Inside a workgroup:
-//   PREP          QK-norm (zero-centred gain, eps 1e-6) and partial NeoX RoPE
-//                 of the group's query heads from the projection row; the
-//                 workgroup whose chunk holds position p = pos[b] also
-//                 normalises/rotates k_p and writes k_p, v_p into the cache
-//                 (attention.cpp:166-199). Other chunks never read row p.
-//   scores        s = q.k * 1/sqrt(hd); the K rows of a chunk are loaded in
-//                 batches of 8 per lane before use (latency, not a serial
-//                 chain); kept in LDS.
-//   softmax/PV    exp against the chunk max, P.V with float4 V rows.
-//   COMBINE_LAST  the last workgroup of (b, g) to finish (atomic counter,
-//                 release/acquire fences, counter reset to 0 for the next
-//                 launch) merges all chunk records and applies the sigmoid
-//                 output gate (attention.cpp:216-227). Without it, a separate
-//                 combine kernel does the merge (long contexts: hundreds of
-//                 chunks would serialise on one workgroup).
+// Two launches (split-K "flash decoding"):
+//   k_attn          one workgroup per (chunk of CH positions, kv head g,
+//                   sequence b); the G = n_q/n_kv query heads of the group
+//                   share every K/V row read. The chunk's K and V rows (one
+//                   sub-tile of T positions at a time: 64 at hd 128, 32 at
+//                   hd 256) are requested before anything else, so their HBM
+//                   latency overlaps the prologue:
+//     PREP          QK-norm (zero-centred gain, eps 1e-6) and partial NeoX
+//                   RoPE of the group's query heads from the projection row;
+//                   the workgroup whose chunk holds p = pos[b] also
+//                   normalises/rotates k_p and writes k_p, v_p into the cache
+//                   (attention.cpp:166-199), using the LDS copy of that row
+//                   itself. Other chunks never read row p.
+//     scores        s = q.k * 1/sqrt(hd) (16 lanes x 8 floats per K row).
+//     softmax/PV    running max and sum across sub-tiles, P.V with float4 V
+//                   rows; the chunk leaves a record [m, l, -, -, o[hd]] per
+//                   query head.
+//   k_attn_combine  one workgroup per (query head, sequence) merges the
+//                   records and applies the sigmoid output gate
+//                   (attention.cpp:216-227). The kernel boundary orders the
+//                   two, so no workgroup needs a device-scope fence.
 // The graph-captured decode step launches the grid for max_seq; chunks past
 // pos[b] exit at once and are not counted.
 
@@ -29,7 +32,6 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kNW = kThreads / QLM_WAVE;
-constexpr int kBatch = 8;  // loads in flight per lane in the score and PV loops
 
 template <typename KV>
 __device__ __forceinline__ void load8(const KV* p, float (&o)[8]);
@@ -64,41 +66,30 @@ __device__ __forceinline__ float4 load4<uint16_t>(const uint16_t* p) {
                        __uint_as_float(a.y << 16), __uint_as_float(a.y & 0xffff0000u));
 }
 
-// Merge the chunk records [m, l, -, -, o[HD]] of one head; returns o/l.
-template <int HD>
-__device__ __forceinline__ float merge_chunks(const float* base, int nc, int e) {
-    float M = -INFINITY;
-    for (int c = 0; c < nc; ++c) M = fmaxf(M, base[(size_t)c * (HD + 4)]);
-    float l = 0.0f, o = 0.0f;
-    for (int c = 0; c < nc; ++c) {
-        const float* pc = base + (size_t)c * (HD + 4);
-        const float f = expf(pc[0] - M);
-        l = fmaf(f, pc[1], l);
-        o = fmaf(f, pc[4 + e], o);
-    }
-    return o / l;
-}
-
-template <int HD, int G, int CH, typename KV, bool PREP, bool COMBINE_LAST>
+template <int HD, int G, int T, int NT, typename KV, bool PREP>
 __global__ __launch_bounds__(kThreads) void k_attn(
     const float* __restrict__ qsrc, int ldq, int qhs, const float* __restrict__ qn_w,
     const float* __restrict__ kn_w, const float* __restrict__ cos_tab,
     const float* __restrict__ sin_tab, int rot, KV* __restrict__ kc, KV* __restrict__ vc,
     int max_seq, int n_kv, const int* __restrict__ pos, int ctx, float* __restrict__ work,
-    unsigned* __restrict__ counters, int nchunks, int n_q, int gated, float* __restrict__ out,
-    int ldo, float scale) {
+    int nchunks, int n_q, float scale) {
     static_assert(!PREP || sizeof(KV) == 4, "the fused prologue writes an fp32 cache");
     constexpr int LPP = HD / 8;            // lanes per position in the score phase
     constexpr int PPW = QLM_WAVE / LPP;    // positions per wave per score step
     constexpr int SPS = kNW * PPW;         // positions per workgroup per score step
+    constexpr int NS = T / SPS;            // K rows per lane per sub-tile
     constexpr int C4 = HD / 4;             // float4 columns of a row
     constexpr int NPG = kThreads / C4;     // position groups in the PV phase
+    constexpr int NV = T / NPG;            // V float4 per lane per sub-tile
+    constexpr int CH = T * NT;             // positions per chunk (workgroup)
+    constexpr int EPL = HD / QLM_WAVE;     // row elements per lane in the norm phase
+    constexpr int RPW = (G + kNW - 1) / kNW;  // query rows per wave in the norm phase
+    static_assert(T % SPS == 0 && T % NPG == 0, "sub-tile must cover whole load steps");
     __shared__ float qs[G][HD];
-    __shared__ float sc[G][CH];
+    __shared__ float sc[G][T];
     __shared__ float4 red[NPG][G][C4];
     __shared__ float kvp[2][HD];
-    __shared__ float mstat[G], lstat[G];
-    __shared__ int is_last;
+    __shared__ float fsc[G], mstat[G], lstat[G];
 
     const int chunk = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -110,39 +101,101 @@ __global__ __launch_bounds__(kThreads) void k_attn(
     const int n = min(CH, L - start);
     const float* qrow = qsrc + (size_t)b * ldq;
     const bool own_p = PREP && (p / CH == chunk);
+    const int plp = own_p ? p - start : -1;  // local index of the row written this step
 
-    for (int i = tid; i < G * HD; i += kThreads)
-        qs[i / HD][i % HD] = qrow[(size_t)(g * G + i / HD) * qhs + i % HD];
-    if (own_p) {
-        for (int i = tid; i < HD; i += kThreads) {
-            kvp[0][i] = qrow[(size_t)n_q * qhs + (size_t)g * HD + i];
-            kvp[1][i] = qrow[(size_t)n_q * qhs + (size_t)(n_kv + g) * HD + i];
+    // ---- sub-tile 0's K and V rows are requested first ----
+    // Row indices are clamped into the chunk (duplicates are masked later),
+    // so the loads never branch. Row p of the cache is stale until this
+    // launch writes it; its values are taken from LDS below instead.
+    const int sub = lane % LPP, pw = lane / LPP;
+    const int c4 = tid % C4, pg = tid / C4;
+    const size_t row0 = ((size_t)b * max_seq + start) * n_kv + g;
+    float kr[NS][8];
+    float4 vv[NV];
+    auto load_kv = [&](int t0) {
+#pragma unroll
+        for (int u = 0; u < NS; ++u) {
+            const int pl = min(t0 + u * SPS + wave * PPW + pw, n - 1);
+            load8<KV>(kc + (row0 + (size_t)pl * n_kv) * HD + sub * 8, kr[u]);
         }
-    }
-    __syncthreads();
+#pragma unroll
+        for (int u = 0; u < NV; ++u) {
+            const int pl = min(t0 + u * NPG + pg, n - 1);
+            vv[u] = load4<KV>(vc + (row0 + (size_t)pl * n_kv) * HD + c4 * 4);
+        }
+    };
+    load_kv(0);
+
+    // ---- query rows (+ QK-norm, RoPE, k_p/v_p when PREP) ----
     if constexpr (PREP) {
-        const int nrows = G + (own_p ? 1 : 0);
-        for (int r = wave; r < nrows; r += kNW) {
-            float* v = r < G ? qs[r] : kvp[0];
-            const float* w = r < G ? qn_w : kn_w;
-            if (w) {
+        // wave w normalises query rows w, w + kNW, ...; the last wave also
+        // takes k_p when this chunk owns p. All operands load at once.
+        float qv[RPW][EPL], gq[EPL], gk[EPL], kp[EPL], vp[EPL];
+#pragma unroll
+        for (int i = 0; i < RPW; ++i) {
+            const int r = wave + i * kNW;
+#pragma unroll
+            for (int j = 0; j < EPL; ++j)
+                qv[i][j] = r < G ? qrow[(size_t)(g * G + r) * qhs + lane + j * QLM_WAVE] : 0.0f;
+        }
+        const bool k_wave = own_p && wave == kNW - 1;
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) {
+            const int e = lane + j * QLM_WAVE;
+            gq[j] = qn_w ? qn_w[e] : 0.0f;
+            gk[j] = (k_wave && kn_w) ? kn_w[e] : 0.0f;
+            kp[j] = k_wave ? qrow[(size_t)n_q * qhs + (size_t)g * HD + e] : 0.0f;
+            vp[j] = k_wave ? qrow[(size_t)n_q * qhs + (size_t)(n_kv + g) * HD + e] : 0.0f;
+        }
+        const int half = rot / 2;
+        const int rj = half > 0 ? tid % half : 0;
+        const float cj = half > 0 ? cos_tab[(size_t)p * half + rj] : 0.0f;
+        const float sj = half > 0 ? sin_tab[(size_t)p * half + rj] : 0.0f;
+
+#pragma unroll
+        for (int i = 0; i < RPW; ++i) {
+            const int r = wave + i * kNW;
+            if (r < G) {  // wave-uniform
+                if (qn_w) {
+                    float ss = 0.0f;
+#pragma unroll
+                    for (int j = 0; j < EPL; ++j) ss = fmaf(qv[i][j], qv[i][j], ss);
+                    ss = wave_sum(ss);
+                    const float s = 1.0f / sqrtf(ss / (float)HD + 1e-6f);
+#pragma unroll
+                    for (int j = 0; j < EPL; ++j) qv[i][j] = (qv[i][j] * s) * (1.0f + gq[j]);
+                }
+#pragma unroll
+                for (int j = 0; j < EPL; ++j) qs[r][lane + j * QLM_WAVE] = qv[i][j];
+            }
+        }
+        if (k_wave) {
+            if (kn_w) {
                 float ss = 0.0f;
-                for (int e = lane; e < HD; e += QLM_WAVE) ss = fmaf(v[e], v[e], ss);
+#pragma unroll
+                for (int j = 0; j < EPL; ++j) ss = fmaf(kp[j], kp[j], ss);
                 ss = wave_sum(ss);
                 const float s = 1.0f / sqrtf(ss / (float)HD + 1e-6f);
-                for (int e = lane; e < HD; e += QLM_WAVE) v[e] = (v[e] * s) * (1.0f + w[e]);
+#pragma unroll
+                for (int j = 0; j < EPL; ++j) kp[j] = (kp[j] * s) * (1.0f + gk[j]);
+            }
+#pragma unroll
+            for (int j = 0; j < EPL; ++j) {
+                kvp[0][lane + j * QLM_WAVE] = kp[j];
+                kvp[1][lane + j * QLM_WAVE] = vp[j];
             }
         }
         __syncthreads();
-        const int half = rot / 2;
-        const float* ct = cos_tab + (size_t)p * half;
-        const float* st = sin_tab + (size_t)p * half;
+        // NeoX rotation of the first `rot` dims (attention.cpp:181-188)
+        const int nrows = G + (own_p ? 1 : 0);
         for (int i = tid; i < nrows * half; i += kThreads) {
             const int r = i / half, j = i % half;
+            const float c = (j == rj) ? cj : cos_tab[(size_t)p * half + j];
+            const float sn = (j == rj) ? sj : sin_tab[(size_t)p * half + j];
             float* v = r < G ? qs[r] : kvp[0];
             const float x1 = v[j], x2 = v[j + half];
-            v[j] = nc_mul_sub(x1, ct[j], x2, st[j]);
-            v[j + half] = nc_mul_add2(x2, ct[j], x1, st[j]);
+            v[j] = nc_mul_sub(x1, c, x2, sn);
+            v[j + half] = nc_mul_add2(x2, c, x1, sn);
         }
         __syncthreads();
         if (own_p) {
@@ -152,173 +205,207 @@ __global__ __launch_bounds__(kThreads) void k_attn(
                 vc[off + i] = kvp[1][i];
             }
         }
-        __syncthreads();  // the cache rows written above are read below by other waves
+    } else {
+        for (int i = tid; i < G * HD; i += kThreads)
+            qs[i / HD][i % HD] = qrow[(size_t)(g * G + i / HD) * qhs + i % HD];
+        __syncthreads();
     }
 
-    // ---- scores ----
-    {
-        const int sub = lane % LPP, pw = lane / LPP;
-        float qr[G][8];
+    float qr[G][8];
 #pragma unroll
-        for (int gh = 0; gh < G; ++gh)
+    for (int gh = 0; gh < G; ++gh)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) qr[gh][e] = qs[gh][sub * 8 + e];
-        const size_t row0 = ((size_t)b * max_seq + start) * n_kv + g;
-        for (int it0 = 0; it0 * SPS < n; it0 += kBatch) {
-            float kr[kBatch][8];
+        for (int e = 0; e < 8; ++e) qr[gh][e] = qs[gh][sub * 8 + e];
+    float4 acc[G];
 #pragma unroll
-            for (int u = 0; u < kBatch; ++u) {
-                const int pl = (it0 + u) * SPS + wave * PPW + pw;
-                if (pl < n) load8<KV>(kc + (row0 + (size_t)pl * n_kv) * HD + sub * 8, kr[u]);
+    for (int gh = 0; gh < G; ++gh) acc[gh] = make_float4(0.f, 0.f, 0.f, 0.f);
+    // running softmax state of head gh lives in the wave that owns it
+    float m_run[RPW], l_run[RPW];
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
+        m_run[i] = -INFINITY;
+        l_run[i] = 0.0f;
+    }
+
+    for (int t = 0; t < NT; ++t) {
+        const int t0 = t * T;
+        if (t0 >= n) break;  // uniform
+        const int nt = min(T, n - t0);
+        if (t > 0) load_kv(t0);
+
+        // ---- scores s = q.k * scale ----
+#pragma unroll
+        for (int u = 0; u < NS; ++u) {
+            const int pli = u * SPS + wave * PPW + pw;
+            if (t0 + pli == plp) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) kr[u][e] = kvp[0][sub * 8 + e];
             }
 #pragma unroll
-            for (int u = 0; u < kBatch; ++u) {
-                const int pl = (it0 + u) * SPS + wave * PPW + pw;
+            for (int gh = 0; gh < G; ++gh) {
+                float d = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) d = fmaf(qr[gh][e], kr[u][e], d);
+                d = group_sum<LPP>(d);
+                if (sub == 0 && pli < nt) sc[gh][pli] = d * scale;
+            }
+        }
+        __syncthreads();
+
+        // ---- per-head max, exponentials, sums (online across sub-tiles) ----
+#pragma unroll
+        for (int i = 0; i < RPW; ++i) {
+            const int gh = wave + i * kNW;
+            if (gh < G) {
+                float m = -INFINITY;
+                for (int pl = lane; pl < nt; pl += QLM_WAVE) m = fmaxf(m, sc[gh][pl]);
+                m = fmaxf(wave_max(m), m_run[i]);
+                float l = 0.0f;
+                for (int pl = lane; pl < nt; pl += QLM_WAVE) {
+                    const float e = expf(sc[gh][pl] - m);
+                    sc[gh][pl] = e;
+                    l += e;
+                }
+                l = wave_sum(l);
+                const float f = expf(m_run[i] - m);  // 0 on the first sub-tile
+                l_run[i] = fmaf(l_run[i], f, l);
+                m_run[i] = m;
+                if (lane == 0) fsc[gh] = f;
+            }
+        }
+        __syncthreads();
+
+        // ---- P.V ----
+#pragma unroll
+        for (int gh = 0; gh < G; ++gh) {
+            if (t > 0) {
+                const float f = fsc[gh];
+                acc[gh].x *= f;
+                acc[gh].y *= f;
+                acc[gh].z *= f;
+                acc[gh].w *= f;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < NV; ++u) {
+            const int pli = u * NPG + pg;
+            if (t0 + pli == plp) vv[u] = reinterpret_cast<const float4*>(kvp[1])[c4];
+            if (pli < nt) {
 #pragma unroll
                 for (int gh = 0; gh < G; ++gh) {
-                    float d = 0.0f;
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) d = fmaf(qr[gh][e], kr[u][e], d);
-                    d = group_sum<LPP>(d);
-                    if (sub == 0 && pl < n) sc[gh][pl] = d * scale;
+                    const float e = sc[gh][pli];
+                    acc[gh].x = fmaf(e, vv[u].x, acc[gh].x);
+                    acc[gh].y = fmaf(e, vv[u].y, acc[gh].y);
+                    acc[gh].z = fmaf(e, vv[u].z, acc[gh].z);
+                    acc[gh].w = fmaf(e, vv[u].w, acc[gh].w);
                 }
             }
         }
+        if (NT > 1) __syncthreads();  // sc is rewritten by the next sub-tile
     }
-    __syncthreads();
 
-    // ---- per-head chunk max, exponentials, sum ----
-    for (int gh = wave; gh < G; gh += kNW) {
-        float m = -INFINITY;
-        for (int pl = lane; pl < n; pl += QLM_WAVE) m = fmaxf(m, sc[gh][pl]);
-        m = wave_max(m);
-        float l = 0.0f;
-        for (int pl = lane; pl < n; pl += QLM_WAVE) {
-            const float e = expf(sc[gh][pl] - m);
-            sc[gh][pl] = e;
-            l += e;
-        }
-        l = wave_sum(l);
-        if (lane == 0) {
-            mstat[gh] = m;
-            lstat[gh] = l;
+    // ---- chunk record [m, l, -, -, o[HD]] per query head ----
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
+        const int gh = wave + i * kNW;
+        if (gh < G && lane == 0) {
+            mstat[gh] = m_run[i];
+            lstat[gh] = l_run[i];
         }
     }
-    __syncthreads();
-
-    // ---- P.V ----
-    {
-        const int c4 = tid % C4, pg = tid / C4;
-        float4 acc[G];
 #pragma unroll
-        for (int gh = 0; gh < G; ++gh) acc[gh] = make_float4(0.f, 0.f, 0.f, 0.f);
-        const size_t row0 = ((size_t)b * max_seq + start) * n_kv + g;
-        for (int it0 = 0; it0 * NPG < n; it0 += kBatch) {
-            float4 vv[kBatch];
-#pragma unroll
-            for (int u = 0; u < kBatch; ++u) {
-                const int pl = (it0 + u) * NPG + pg;
-                if (pl < n) vv[u] = load4<KV>(vc + (row0 + (size_t)pl * n_kv) * HD + c4 * 4);
-            }
-#pragma unroll
-            for (int u = 0; u < kBatch; ++u) {
-                const int pl = (it0 + u) * NPG + pg;
-                if (pl < n) {
-#pragma unroll
-                    for (int gh = 0; gh < G; ++gh) {
-                        const float e = sc[gh][pl];
-                        acc[gh].x = fmaf(e, vv[u].x, acc[gh].x);
-                        acc[gh].y = fmaf(e, vv[u].y, acc[gh].y);
-                        acc[gh].z = fmaf(e, vv[u].z, acc[gh].z);
-                        acc[gh].w = fmaf(e, vv[u].w, acc[gh].w);
-                    }
-                }
-            }
-        }
-#pragma unroll
-        for (int gh = 0; gh < G; ++gh) red[pg][gh][c4] = acc[gh];
-    }
+    for (int gh = 0; gh < G; ++gh) red[pg][gh][c4] = acc[gh];
     __syncthreads();
     for (int i = tid; i < G * C4; i += kThreads) {
-        const int gh = i / C4, c4 = i % C4;
-        float4 t = red[0][gh][c4];
+        const int gh = i / C4, cc = i % C4;
+        float4 tt = red[0][gh][cc];
 #pragma unroll
         for (int p2 = 1; p2 < NPG; ++p2) {
-            const float4 u = red[p2][gh][c4];
-            t.x += u.x;
-            t.y += u.y;
-            t.z += u.z;
-            t.w += u.w;
+            const float4 u = red[p2][gh][cc];
+            tt.x += u.x;
+            tt.y += u.y;
+            tt.z += u.z;
+            tt.w += u.w;
         }
         float* dst = work + (((size_t)b * n_q + g * G + gh) * nchunks + chunk) * (HD + 4);
-        reinterpret_cast<float4*>(dst + 4)[c4] = t;
-        if (c4 == 0) {
+        reinterpret_cast<float4*>(dst + 4)[cc] = tt;
+        if (cc == 0) {
             dst[0] = mstat[gh];
             dst[1] = lstat[gh];
         }
     }
-
-    if constexpr (COMBINE_LAST) {
-        __syncthreads();
-        if (tid == 0) {
-            __threadfence();  // release this chunk's records
-            const unsigned old = atomicAdd(&counters[b * n_kv + g], 1u);
-            is_last = (old == (unsigned)nc - 1);
-        }
-        __syncthreads();
-        if (!is_last) return;
-        __threadfence();  // acquire the other chunks' records
-        for (int i = tid; i < G * HD; i += kThreads) {
-            const int gh = i / HD, e = i % HD;
-            const int h = g * G + gh;
-            const float* base = work + ((size_t)b * n_q + h) * nchunks * (HD + 4);
-            float r = merge_chunks<HD>(base, nc, e);
-            if (gated) r *= 1.0f / (1.0f + expf(-qrow[(size_t)h * qhs + HD + e]));
-            out[(size_t)b * ldo + (size_t)h * HD + e] = r;
-        }
-        if (tid == 0) atomicExch(&counters[b * n_kv + g], 0u);
-    }
 }
 
-// Separate merge for long contexts: one workgroup per (query head, sequence).
+// Merge of the chunk records of one (query head, sequence), in tiles of HD
+// chunks with a running maximum, then the optional sigmoid output gate
+// (attention.cpp:216-227): gate[b*ldg + h*ghs + HD + e].
 template <int HD>
-__global__ __launch_bounds__(HD) void k_attn_combine(const float* __restrict__ work, int nchunks,
-                                                     int CH, int max_seq, const int* __restrict__ pos,
-                                                     int ctx, float* __restrict__ out, int ldo,
-                                                     int n_q) {
-    const int h = blockIdx.x, b = blockIdx.y, i = threadIdx.x;
+__global__ __launch_bounds__(HD) void k_attn_combine(
+    const float* __restrict__ work, int nchunks, int CH, int max_seq, const int* __restrict__ pos,
+    int ctx, const float* __restrict__ gate, int ldg, int ghs, float* __restrict__ out, int ldo,
+    int n_q) {
+    __shared__ float ms[HD], ls[HD];
+    const int h = blockIdx.x, b = blockIdx.y, e = threadIdx.x;
+    const float gv = gate ? gate[(size_t)b * ldg + (size_t)h * ghs + HD + e] : 0.0f;
     const int L = min(pos ? pos[b] + 1 : ctx, max_seq);
     const int nc = min(nchunks, (L + CH - 1) / CH);
     const float* base = work + ((size_t)b * n_q + h) * nchunks * (HD + 4);
-    out[(size_t)b * ldo + (size_t)h * HD + i] = merge_chunks<HD>(base, nc, i);
+    float M = -INFINITY, l = 0.0f, o = 0.0f;
+    for (int c0 = 0; c0 < nc; c0 += HD) {
+        const int nt = min(HD, nc - c0);
+        if (e < nt) {
+            ms[e] = base[(size_t)(c0 + e) * (HD + 4)];
+            ls[e] = base[(size_t)(c0 + e) * (HD + 4) + 1];
+        }
+        __syncthreads();
+        float mt = -INFINITY;
+        for (int c = 0; c < nt; ++c) mt = fmaxf(mt, ms[c]);
+        const float Mn = fmaxf(M, mt);
+        const float f0 = expf(M - Mn);  // 0 on the first tile
+        l *= f0;
+        o *= f0;
+#pragma unroll 8
+        for (int c = 0; c < nt; ++c) {
+            const float f = expf(ms[c] - Mn);
+            l = fmaf(f, ls[c], l);
+            o = fmaf(f, base[(size_t)(c0 + c) * (HD + 4) + 4 + e], o);
+        }
+        M = Mn;
+        __syncthreads();
+    }
+    float r = o / l;
+    if (gate) r *= 1.0f / (1.0f + expf(-gv));
+    out[(size_t)b * ldo + (size_t)h * HD + e] = r;
 }
 
-constexpr int kChModel = 128;   // decode step: contexts up to a few thousand
-constexpr int kChLong = 256;    // isolated API: contexts up to 32k
+// Sub-tile of positions held in registers per workgroup: 64 rows at hd 128,
+// 32 at hd 256 (the K and V rows of a sub-tile are requested together).
+template <int HD>
+constexpr int tile_for() { return HD == 128 ? 64 : 32; }
+constexpr int kNtModel = 1;  // decode step: one sub-tile per chunk (many short chunks)
+constexpr int kNtLong = 4;   // isolated API: contexts up to 32k
 
+int chunk_len(int hd, int nt) { return (hd == 128 ? 64 : 32) * nt; }
 int nchunks_for(int max_seq, int ch) { return (max_seq + ch - 1) / ch; }
 
-size_t counter_offset(int B, int n_q, int hd, int max_seq) {
-    const size_t rec = (size_t)B * n_q * nchunks_for(max_seq, kChModel) * (hd + 4) * sizeof(float);
-    const size_t rec_long = (size_t)B * n_q * nchunks_for(max_seq, kChLong) * (hd + 4) * sizeof(float);
-    const size_t r = rec > rec_long ? rec : rec_long;
-    return (r + 255) & ~(size_t)255;
+size_t records_bytes(int B, int n_q, int hd, int max_seq, int nt) {
+    return (size_t)B * n_q * nchunks_for(max_seq, chunk_len(hd, nt)) * (hd + 4) * sizeof(float);
 }
 
-template <int HD, int CH, typename KV, bool PREP, bool LAST>
+template <int HD, int NT, typename KV, bool PREP>
 int launch_g(int G, const float* q, int ldq, int qhs, const float* qn, const float* kn,
              const float* ct, const float* st, int rot, KV* kc, KV* vc, int max_seq, int n_kv,
-             const int* pos, int ctx, float* work, unsigned* counters, int n_q, int gated,
-             float* out, int ldo, int B, hipStream_t s) {
-    const int nch = nchunks_for(max_seq, CH);
+             const int* pos, int ctx, float* work, int n_q, int B, hipStream_t s) {
+    constexpr int T = tile_for<HD>();
+    const int nch = nchunks_for(max_seq, T * NT);
     const dim3 grid(nch, n_kv, B);
     const float scale = 1.0f / sqrtf((float)HD);
-#define QLM_ATTN_G(GG)                                                                           \
-    if (G == GG) {                                                                               \
-        hipLaunchKernelGGL((k_attn<HD, GG, CH, KV, PREP, LAST>), grid, dim3(kThreads), 0, s, q,  \
+#define QLM_ATTN_G(GG)                                                                          \
+    if (G == GG) {                                                                              \
+        hipLaunchKernelGGL((k_attn<HD, GG, T, NT, KV, PREP>), grid, dim3(kThreads), 0, s, q,    \
                            ldq, qhs, qn, kn, ct, st, rot, kc, vc, max_seq, n_kv, pos, ctx, work, \
-                           counters, nch, n_q, gated, out, ldo, scale);                          \
-        return qlm_launch_status();                                                              \
+                           nch, n_q, scale);                                                    \
+        return qlm_launch_status();                                                             \
     }
     QLM_ATTN_G(1)
     QLM_ATTN_G(2)
@@ -328,10 +415,22 @@ int launch_g(int G, const float* q, int ldq, int qhs, const float* qn, const flo
     return QLM_ERR_SHAPE;
 }
 
+template <int HD>
+int launch_combine(const float* work, int nch, int ch, int max_seq, const int* pos, int ctx,
+                   const float* gate, int ldg, int ghs, float* out, int ldo, int n_q, int B,
+                   hipStream_t s) {
+    hipLaunchKernelGGL(k_attn_combine<HD>, dim3(n_q, B), dim3(HD), 0, s, work, nch, ch, max_seq,
+                       pos, ctx, gate, ldg, ghs, out, ldo, n_q);
+    return qlm_launch_status();
+}
+
 }  // namespace
 
 extern "C" size_t qlm_gqa_workspace_bytes(int B, int n_q, int hd, int max_seq) {
-    return counter_offset(B, n_q, hd, max_seq) + (size_t)B * 64 * sizeof(unsigned);
+    if (B <= 0 || n_q <= 0 || hd <= 0 || max_seq <= 0) return 0;
+    const size_t a = records_bytes(B, n_q, hd, max_seq, kNtModel);
+    const size_t b = records_bytes(B, n_q, hd, max_seq, kNtLong);
+    return a > b ? a : b;
 }
 
 extern "C" int qlm_gqa_decode(float* qkv, int ldqkv, const float* q_norm, const float* k_norm,
@@ -342,7 +441,7 @@ extern "C" int qlm_gqa_decode(float* qkv, int ldqkv, const float* q_norm, const 
     if (!qkv || !cos_tab || !sin_tab || !k_cache || !v_cache || !pos || !out || !work)
         return QLM_ERR_ARG;
     if (B <= 0 || n_q <= 0 || n_kv <= 0 || max_seq <= 0) return QLM_ERR_ARG;
-    if (n_q % n_kv != 0 || (hd != 128 && hd != 256) || n_kv > 64) return QLM_ERR_SHAPE;
+    if (n_q % n_kv != 0 || (hd != 128 && hd != 256)) return QLM_ERR_SHAPE;
     if (rot_dim < 0 || rot_dim > hd || rot_dim % 2 != 0) return QLM_ERR_SHAPE;
     const int G = n_q / n_kv;
     if (G != 1 && G != 2 && G != 4 && G != 8) return QLM_ERR_SHAPE;
@@ -350,15 +449,24 @@ extern "C" int qlm_gqa_decode(float* qkv, int ldqkv, const float* q_norm, const 
     if (ldqkv < n_q * qstride + 2 * n_kv * hd || ldo < n_q * hd) return QLM_ERR_SHAPE;
     hipStream_t st = as_stream(stream);
     float* w = reinterpret_cast<float*>(work);
-    unsigned* cnt = reinterpret_cast<unsigned*>(reinterpret_cast<char*>(work) +
-                                                counter_offset(B, n_q, hd, max_seq));
-    if (hd == 128)
-        return launch_g<128, kChModel, float, true, true>(
-            G, qkv, ldqkv, qstride, q_norm, k_norm, cos_tab, sin_tab, rot_dim, k_cache, v_cache,
-            max_seq, n_kv, pos, 0, w, cnt, n_q, gated, out, ldo, B, st);
-    return launch_g<256, kChModel, float, true, true>(
-        G, qkv, ldqkv, qstride, q_norm, k_norm, cos_tab, sin_tab, rot_dim, k_cache, v_cache,
-        max_seq, n_kv, pos, 0, w, cnt, n_q, gated, out, ldo, B, st);
+    const int ch = chunk_len(hd, kNtModel);
+    const int nch = nchunks_for(max_seq, ch);
+    const float* gate = gated ? qkv : nullptr;
+    int rc;
+    if (hd == 128) {
+        rc = launch_g<128, kNtModel, float, true>(G, qkv, ldqkv, qstride, q_norm, k_norm, cos_tab,
+                                                  sin_tab, rot_dim, k_cache, v_cache, max_seq,
+                                                  n_kv, pos, 0, w, n_q, B, st);
+        if (rc != QLM_OK) return rc;
+        return launch_combine<128>(w, nch, ch, max_seq, pos, 0, gate, ldqkv, qstride, out, ldo,
+                                   n_q, B, st);
+    }
+    rc = launch_g<256, kNtModel, float, true>(G, qkv, ldqkv, qstride, q_norm, k_norm, cos_tab,
+                                              sin_tab, rot_dim, k_cache, v_cache, max_seq, n_kv,
+                                              pos, 0, w, n_q, B, st);
+    if (rc != QLM_OK) return rc;
+    return launch_combine<256>(w, nch, ch, max_seq, pos, 0, gate, ldqkv, qstride, out, ldo, n_q,
+                               B, st);
 }
 
 extern "C" int qlm_attention_decode(const float* q, const void* k_cache, const void* v_cache,
@@ -370,28 +478,27 @@ extern "C" int qlm_attention_decode(const float* q, const void* k_cache, const v
     if (kv_dtype != 0 && kv_dtype != 1) return QLM_ERR_ARG;
     const int G = n_q / n_kv;
     hipStream_t st = as_stream(stream);
-    const int nch = nchunks_for(max_seq, kChLong);
+    const int ch = chunk_len(hd, kNtLong);
+    const int nch = nchunks_for(max_seq, ch);
     float* w = reinterpret_cast<float*>(work);
     const int ldq = n_q * hd;
     int rc;
-#define QLM_ISO(HDV)                                                                              \
-    rc = kv_dtype == 0                                                                            \
-             ? launch_g<HDV, kChLong, float, false, false>(                                       \
-                   G, q, ldq, hd, nullptr, nullptr, nullptr, nullptr, 0,                          \
-                   (float*)const_cast<void*>(k_cache), (float*)const_cast<void*>(v_cache),        \
-                   max_seq, n_kv, nullptr, ctx, w, nullptr, n_q, 0, out, ldq, B, st)              \
-             : launch_g<HDV, kChLong, uint16_t, false, false>(                                    \
-                   G, q, ldq, hd, nullptr, nullptr, nullptr, nullptr, 0,                          \
-                   (uint16_t*)const_cast<void*>(k_cache), (uint16_t*)const_cast<void*>(v_cache),  \
-                   max_seq, n_kv, nullptr, ctx, w, nullptr, n_q, 0, out, ldq, B, st);             \
-    if (rc != QLM_OK) return rc;                                                                  \
-    hipLaunchKernelGGL(k_attn_combine<HDV>, dim3(n_q, B), dim3(HDV), 0, st, w, nch, kChLong,      \
-                       max_seq, nullptr, ctx, out, ldq, n_q);
+#define QLM_ISO(HDV)                                                                             \
+    rc = kv_dtype == 0                                                                           \
+             ? launch_g<HDV, kNtLong, float, false>(                                             \
+                   G, q, ldq, hd, nullptr, nullptr, nullptr, nullptr, 0,                         \
+                   (float*)const_cast<void*>(k_cache), (float*)const_cast<void*>(v_cache),       \
+                   max_seq, n_kv, nullptr, ctx, w, n_q, B, st)                                   \
+             : launch_g<HDV, kNtLong, uint16_t, false>(                                          \
+                   G, q, ldq, hd, nullptr, nullptr, nullptr, nullptr, 0,                         \
+                   (uint16_t*)const_cast<void*>(k_cache), (uint16_t*)const_cast<void*>(v_cache), \
+                   max_seq, n_kv, nullptr, ctx, w, n_q, B, st);                                  \
+    if (rc != QLM_OK) return rc;                                                                 \
+    return launch_combine<HDV>(w, nch, ch, max_seq, nullptr, ctx, nullptr, 0, 0, out, ldq, n_q,  \
+                               B, st);
     if (hd == 128) {
         QLM_ISO(128)
-    } else {
-        QLM_ISO(256)
     }
+    QLM_ISO(256)
 #undef QLM_ISO
-    return qlm_launch_status();
 }

@@ -32,17 +32,27 @@ struct DnShared {
     float scal[8];
 };
 
-// Recurrence core. q,k,v in LDS (q already L2-normalised, k too). Leaves the
-// un-normalised, 1/sqrt(d)-scaled output in sh.vec.
-__device__ __forceinline__ void dn_recurrence(DnShared& sh, float* __restrict__ S, float dec,
-                                              float beta) {
+// Thread (ig, jg)'s slice of the head state: rows ig*8..ig*8+7, float4
+// column jg. Requested at kernel start so the 64 KiB read overlaps the
+// prologue.
+__device__ __forceinline__ void dn_load_state(const float* __restrict__ S,
+                                              float4 (&s)[kRowsPer]) {
     const int tid = threadIdx.x;
     const int jg = tid & 31;
     const int ig = tid >> 5;
-    float4 s[kRowsPer];
-    float4* S4 = reinterpret_cast<float4*>(S);
+    const float4* S4 = reinterpret_cast<const float4*>(S);
 #pragma unroll
     for (int r = 0; r < kRowsPer; ++r) s[r] = S4[(ig * kRowsPer + r) * (kD / 4) + jg];
+}
+
+// Recurrence core. q,k,v in LDS (q already L2-normalised, k too), the state
+// slice in s. Leaves the un-normalised, 1/sqrt(d)-scaled output in sh.vec.
+__device__ __forceinline__ void dn_recurrence(DnShared& sh, float* __restrict__ S,
+                                              float4 (&s)[kRowsPer], float dec, float beta) {
+    const int tid = threadIdx.x;
+    const int jg = tid & 31;
+    const int ig = tid >> 5;
+    float4* S4 = reinterpret_cast<float4*>(S);
 
     // (1) decay and kv = k . S_decayed
     float4 kv = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -106,17 +116,23 @@ __global__ __launch_bounds__(kThreads) void k_gated_delta_step(
     __shared__ DnShared sh;
     const int bh = blockIdx.x;  // b*H + h
     const int tid = threadIdx.x;
+    float4 s[kRowsPer];
+    dn_load_state(state + (size_t)bh * kD * kD, s);
+    const float dec = decay[bh], bt = beta[bh];
     if (tid < kD) {
         sh.q[tid] = q[(size_t)bh * kD + tid];
         sh.k[tid] = k[(size_t)bh * kD + tid];
         sh.v[tid] = v[(size_t)bh * kD + tid];
     }
     __syncthreads();
-    dn_recurrence(sh, state + (size_t)bh * kD * kD, decay[bh], beta[bh]);
+    dn_recurrence(sh, state + (size_t)bh * kD * kD, s, dec, bt);
     if (tid < kD) out[(size_t)bh * kD + tid] = sh.vec[tid];
 }
 
 // Fused decode mixer core. proj row: [qkv 3*H*d | z H*d | b H | a H].
+// Every operand (state slice, the three conv ring rows, conv taps, gate
+// inputs, z, gain) is requested at kernel start; the ring row order is
+// resolved once pos has arrived.
 __global__ __launch_bounds__(kThreads) void k_deltanet_decode(
     const float* __restrict__ proj, int ldp, float* __restrict__ conv_state,
     const float* __restrict__ wt, const float* __restrict__ A_log,
@@ -132,21 +148,47 @@ __global__ __launch_bounds__(kThreads) void k_deltanet_decode(
     const int C = 3 * HD;
     const float* pr = proj + (size_t)b * ldp;
     float* cs = conv_state + (size_t)b * 3 * C;
+    float* Sh = state + ((size_t)b * H + h) * kD * kD;
+
+    float4 s[kRowsPer];
+    dn_load_state(Sh, s);
+    const int pb = pos ? pos[b] : 0;
+    // conv operands: channel ch = sec*HD + h*d + t for tid < 3d
+    const bool conv_t = tid < 3 * kD;
+    const int sec = tid / kD, t = tid % kD;
+    const int ch = sec * HD + h * kD + t;
+    float ring[3], w4[4], xin = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 3; ++j) ring[j] = conv_t ? cs[(size_t)j * C + ch] : 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w4[j] = conv_t ? wt[(size_t)j * C + ch] : 0.0f;
+    if (conv_t) xin = pr[ch];
+    // gate operands (wave 2, lane 0) and the output gate / gain (waves 0-1)
+    float ga = 0.0f, gb = 0.0f, gdt = 0.0f, galog = 0.0f;
+    if (wave == 2 && lane == 0) {
+        ga = pr[4 * HD + H + h];
+        gb = pr[4 * HD + h];
+        gdt = dt_bias[h];
+        galog = A_log[h];
+    }
+    float zj = 0.0f, nwj = 0.0f;
+    if (tid < kD) {
+        zj = pr[3 * HD + h * kD + tid];
+        nwj = norm_w[tid];
+    }
 
     // conv1d (kernel 4, taps chronological from the oldest ring row) + SiLU
-    if (tid < 3 * kD) {
-        const int sec = tid / kD, t = tid % kD;
-        const int ch = sec * HD + h * kD + t;
-        const int oldest = pos ? (pos[b] % 3) : 0;
+    if (conv_t) {
+        const int oldest = pb % 3;
         float acc = 0.0f;
 #pragma unroll
         for (int j = 0; j < 3; ++j) {
             const int row = (oldest + j) % 3;
-            acc = nc_add_mul(acc, cs[(size_t)row * C + ch], wt[(size_t)j * C + ch]);
+            const float rv = row == 0 ? ring[0] : (row == 1 ? ring[1] : ring[2]);
+            acc = nc_add_mul(acc, rv, w4[j]);
         }
-        const float x = pr[ch];
-        acc = nc_add_mul(acc, x, wt[(size_t)3 * C + ch]);
-        cs[(size_t)oldest * C + ch] = x;
+        acc = nc_add_mul(acc, xin, w4[3]);
+        cs[(size_t)oldest * C + ch] = xin;
         const float y = silu_f(acc);
         if (sec == 0) sh.q[t] = y;
         else if (sec == 1) sh.k[t] = y;
@@ -164,17 +206,15 @@ __global__ __launch_bounds__(kThreads) void k_deltanet_decode(
         vv[lane] = a0 / nrm;
         vv[lane + 64] = a1 / nrm;
     } else if (wave == 2 && lane == 0) {
-        const float a = pr[4 * HD + H + h];
-        const float bb = pr[4 * HD + h];
-        const float dt = a + dt_bias[h];
+        const float dt = ga + gdt;
         const float sp = dt > 20.0f ? dt : log1pf(expf(dt));
-        const float alpha = -expf(A_log[h]) * sp;
+        const float alpha = -expf(galog) * sp;
         sh.scal[0] = expf(alpha);
-        sh.scal[1] = 1.0f / (1.0f + expf(-bb));
+        sh.scal[1] = 1.0f / (1.0f + expf(-gb));
     }
     __syncthreads();
 
-    dn_recurrence(sh, state + ((size_t)b * H + h) * kD * kD, sh.scal[0], sh.scal[1]);
+    dn_recurrence(sh, Sh, s, sh.scal[0], sh.scal[1]);
 
     // head RMSNorm (plain gain, attention.cpp:574-578) + SiLU(z) gate (:582-585)
     float o = 0.0f;
@@ -185,12 +225,10 @@ __global__ __launch_bounds__(kThreads) void k_deltanet_decode(
     }
     __syncthreads();
     if (wave < 2) {
-        const int j = tid;  // 0..127
         const float tot = sh.scal[2] + sh.scal[3];
-        const float s = 1.0f / sqrtf(tot / (float)kD + 1e-6f);
-        const float z = pr[3 * HD + h * kD + j];
-        const float r = (o * s) * norm_w[j];
-        out[(size_t)b * ldo + h * kD + j] = r * silu_f(z);
+        const float sn = 1.0f / sqrtf(tot / (float)kD + 1e-6f);
+        const float r = (o * sn) * nwj;
+        out[(size_t)b * ldo + h * kD + tid] = r * silu_f(zj);
     }
 }
 

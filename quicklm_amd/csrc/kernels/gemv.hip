@@ -32,16 +32,20 @@ constexpr int kLdsBudget = 64 * 1024;
 enum { PRO_NONE = 0, PRO_RMSNORM = 1 };
 enum { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_ARGMAX = 3 };
 
-// Greedy tail of a decode step (EPI_ARGMAX, M = 1): the logits are stored,
-// each workgroup folds its rows' maximum (first index wins ties, as
-// DecoderModel::sample, model.cpp:263-274) into a 64-bit key with atomicMax,
-// and the last workgroup to finish advances the sequence (token written
-// unless position p+1 is still prompt, pos += 1) and gathers the embedding
-// of the token now at pos into h for the next step. key/count start at zero
-// and are reset by that last workgroup.
+// Greedy tail of a decode step (EPI_ARGMAX, M = 1): the logits are stored and
+// each workgroup writes its rows' maximum (first index wins ties, as
+// DecoderModel::sample, model.cpp:263-274) as a 64-bit key into its own slot
+// keys[blockIdx.x]; a one-workgroup kernel then reduces the slots, advances
+// the sequence (token written unless position p+1 is still prompt, pos += 1)
+// and gathers the embedding of the token now at pos into h for the next
+// step. The kernel boundary orders the two, so no workgroup of the GEMV
+// pays for a device-scope fence (on MI355X each one writes back and
+// invalidates its XCD's L2, ~0.3 us apiece over a 2048-workgroup grid).
+// One 64-bit key slot per workgroup of the logits GEMV (grid <= kMaxXsGrid).
+constexpr int kMaxXsGrid = 2048;
+
 struct GreedyTail {
-    unsigned long long* key;
-    unsigned* count;
+    unsigned long long* keys;
     int* tokens;
     int ld_tokens;
     int* pos;
@@ -328,55 +332,6 @@ __global__ __launch_bounds__(kThreads) void k_gemv_xs(
     const int nblk = K >> 5;
     const int wpg = lpr > QLM_WAVE ? lpr / QLM_WAVE : 1;  // waves per row group
 
-    // ---- activation slice into registers (+ fused RMSNorm) ----
-    float4 xv[SLOTS][4];
-#pragma unroll
-    for (int s = 0; s < SLOTS; ++s) {
-        const int c = li + s * lpr;
-        if (c < nchunk) {
-            const float4* p = reinterpret_cast<const float4*>(x) + c * 4;
-            xv[s][0] = p[0];
-            xv[s][1] = p[1];
-            xv[s][2] = p[2];
-            xv[s][3] = p[3];
-        } else {
-            xv[s][0] = xv[s][1] = xv[s][2] = xv[s][3] = make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-    }
-    if constexpr (PRO == PRO_RMSNORM) {
-        float ss = 0.0f;
-#pragma unroll
-        for (int s = 0; s < SLOTS; ++s)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                ss = fmaf(xv[s][j].x, xv[s][j].x, ss);
-                ss = fmaf(xv[s][j].y, xv[s][j].y, ss);
-                ss = fmaf(xv[s][j].z, xv[s][j].z, ss);
-                ss = fmaf(xv[s][j].w, xv[s][j].w, ss);
-            }
-        // every row group holds all of x: reduce inside group 0's lanes
-        if (lpr <= QLM_WAVE) {
-            for (int m = lpr >> 1; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, QLM_WAVE);
-            if (tid == 0) ssr[0] = ss;
-        } else {
-            ss = wave_sum(ss);
-            if (lane == 0) ssr[wave] = ss;
-        }
-        __syncthreads();
-        float tot = ssr[0];
-        for (int w = 1; w < wpg; ++w) tot += ssr[w];  // waves 0..wpg-1 form group 0
-        const float rs = 1.0f / sqrtf(tot / (float)K + eps);
-#pragma unroll
-        for (int s = 0; s < SLOTS; ++s) {
-            const int c = li + s * lpr;
-            if (c < nchunk) {
-                const float4* wp = reinterpret_cast<const float4*>(nw) + c * 4;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) xv[s][j] = norm4(xv[s][j], rs, wp[j]);
-            }
-        }
-    }
-
     // ---- row blocks ----
     // Loads never branch: a lane's chunk index is clamped into the row (the
     // matching activation slot is zero, so the duplicate contributes 0) and
@@ -393,7 +348,10 @@ __global__ __launch_bounds__(kThreads) void k_gemv_xs(
     auto out_row = [&](int rb, int r) -> int {
         return rb * out_per_block + grp * OUT_PER_GRP + ((EPI == EPI_SWIGLU) ? (r % (R / 2)) : r);
     };
-    auto load = [&](int rb, int4 (&w)[R][SLOTS], float (&sv)[R][SLOTS]) {
+    // Weight chunks and group scales of block rb; for EPI_RESID also the
+    // residual values the block adds to (read long before they are needed).
+    auto load = [&](int rb, int4 (&w)[R][SLOTS], float (&sv)[R][SLOTS],
+                    float (&res)[OUT_PER_GRP]) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             int o = min(out_row(rb, r), N - 1);
@@ -407,8 +365,74 @@ __global__ __launch_bounds__(kThreads) void k_gemv_xs(
                 if constexpr (!ROWSCALE) sv[r][s] = sp[coff[s]];
             }
         }
+        if constexpr (EPI == EPI_RESID) {
+#pragma unroll
+            for (int r = 0; r < OUT_PER_GRP; ++r) res[r] = y[min(out_row(rb, r), N - 1)];
+        }
     };
-    auto finish = [&](int rb, const int4 (&w)[R][SLOTS], const float (&sv)[R][SLOTS]) {
+
+    // The first two blocks' weights are requested before anything else, so
+    // their HBM latency overlaps the activation load and the RMSNorm prologue.
+    // Blocks b0, b1, b2, ... (stride gridDim.x) alternate between the two
+    // register buffers; a buffer is refilled as soon as its block is reduced.
+    int4 wa[R][SLOTS], wb[R][SLOTS];
+    float sa[R][SLOTS], sb[R][SLOTS];
+    float ra[OUT_PER_GRP], rbv[OUT_PER_GRP];
+    int rb = blockIdx.x;
+    if (EPI != EPI_ARGMAX && rb >= nblocks) return;  // uniform per workgroup
+    if (rb < nblocks) load(rb, wa, sa, ra);
+    if (rb + (int)gridDim.x < nblocks) load(rb + gridDim.x, wb, sb, rbv);
+
+    // ---- activation (+ gain) staged once per workgroup through LDS ----
+    // Coalesced 16-byte loads by all 256 lanes (x is read once per
+    // workgroup, not once per row group), the RMSNorm sum of squares folded
+    // into the same pass; then each lane takes its slice into registers,
+    // normalised there. xsh holds x [K] and, with the RMSNorm prologue, the
+    // gain [K] behind it.
+    extern __shared__ float4 xsh[];
+    float ss = 0.0f;
+    for (int i = tid; i < (K >> 2); i += kThreads) {
+        const float4 v = reinterpret_cast<const float4*>(x)[i];
+        xsh[i] = v;
+        if constexpr (PRO == PRO_RMSNORM) {
+            xsh[(K >> 2) + i] = reinterpret_cast<const float4*>(nw)[i];
+            ss = fmaf(v.x, v.x, ss);
+            ss = fmaf(v.y, v.y, ss);
+            ss = fmaf(v.z, v.z, ss);
+            ss = fmaf(v.w, v.w, ss);
+        }
+    }
+    if constexpr (PRO == PRO_RMSNORM) {
+        ss = wave_sum(ss);
+        if (lane == 0) ssr[wave] = ss;
+    }
+    __syncthreads();
+    float rs = 1.0f;
+    if constexpr (PRO == PRO_RMSNORM) {
+        float tot = ssr[0];
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) tot += ssr[w];
+        rs = 1.0f / sqrtf(tot / (float)K + eps);
+    }
+    float4 xv[SLOTS][4];
+#pragma unroll
+    for (int s = 0; s < SLOTS; ++s) {
+        const int c = li + s * lpr;
+        if (c < nchunk) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                xv[s][j] = xsh[c * 4 + j];
+                if constexpr (PRO == PRO_RMSNORM)
+                    xv[s][j] = norm4(xv[s][j], rs, xsh[(K >> 2) + c * 4 + j]);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) xv[s][j] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    }
+
+    auto finish = [&](int rb, const int4 (&w)[R][SLOTS], const float (&sv)[R][SLOTS],
+                      const float (&res)[OUT_PER_GRP]) {
         float acc[R];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -462,7 +486,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_xs(
                 if constexpr (EPI == EPI_SWIGLU)
                     *dst = silu_f(acc[r]) * acc[r + R / 2];
                 else if constexpr (EPI == EPI_RESID)
-                    *dst = *dst + acc[r];
+                    *dst = res[r] + acc[r];
                 else
                     *dst = acc[r];
                 if constexpr (EPI == EPI_ARGMAX) {
@@ -475,26 +499,19 @@ __global__ __launch_bounds__(kThreads) void k_gemv_xs(
         }
     };
 
-    // two register buffers used in turn: block b+grid loads while b reduces
-    int4 wa[R][SLOTS], wb[R][SLOTS];
-    float sa[R][SLOTS], sb[R][SLOTS];
-    int rb = blockIdx.x;
-    if (EPI != EPI_ARGMAX && rb >= nblocks) return;  // uniform per workgroup
-    if (rb < nblocks) load(rb, wa, sa);
+    const int gs = gridDim.x;
     while (rb < nblocks) {
-        int rn = rb + gridDim.x;
-        if (rn < nblocks) load(rn, wb, sb);
-        finish(rb, wa, sa);
-        rb = rn;
+        finish(rb, wa, sa, ra);
+        if (rb + 2 * gs < nblocks) load(rb + 2 * gs, wa, sa, ra);
+        rb += gs;
         if (rb >= nblocks) break;
-        rn = rb + gridDim.x;
-        if (rn < nblocks) load(rn, wa, sa);
-        finish(rb, wb, sb);
-        rb = rn;
+        finish(rb, wb, sb, rbv);
+        if (rb + 2 * gs < nblocks) load(rb + 2 * gs, wb, sb, rbv);
+        rb += gs;
     }
 
     if constexpr (EPI == EPI_ARGMAX) {
-        // workgroup maximum, then the device-wide one through the 64-bit key
+        // workgroup maximum into this workgroup's key slot (0 = no rows)
         unsigned long long k = argmax_key(best_v, best_i);
         if (best_i == 0x7fffffff) k = 0ull;
 #pragma unroll
@@ -503,74 +520,177 @@ __global__ __launch_bounds__(kThreads) void k_gemv_xs(
             k = o > k ? o : k;
         }
         __shared__ unsigned long long wk[kWaves];
-        __shared__ int last;
         if (lane == 0) wk[wave] = k;
         __syncthreads();
         if (tid == 0) {
             unsigned long long m = wk[0];
             for (int w2 = 1; w2 < kWaves; ++w2) m = wk[w2] > m ? wk[w2] : m;
-            if (m) atomicMax(tail.key, m);
-            __threadfence();
-            last = atomicAdd(tail.count, 1u) == gridDim.x - 1;
+            tail.keys[blockIdx.x] = m;
         }
-        __syncthreads();
-        if (!last) return;
-        __threadfence();
-        __shared__ int tok;
-        if (tid == 0) {
-            const unsigned long long m = atomicAdd(tail.key, 0ull);
-            int idx = m ? (int)(0xFFFFFFFFu - (unsigned)(m & 0xFFFFFFFFull)) : 0;
-            if (idx < 0 || idx >= N) idx = 0;
-            const int p = tail.pos[0];
-            if (p + 1 < tail.ld_tokens && p + 1 >= tail.prompt_len[0]) tail.tokens[p + 1] = idx;
-            int t = (p + 1 < tail.ld_tokens) ? tail.tokens[p + 1] : idx;
-            t = t < 0 ? 0 : (t >= tail.vocab ? tail.vocab - 1 : t);
-            tok = t;
-            tail.pos[0] = p + 1;
-            atomicExch(tail.key, 0ull);
-            atomicExch(tail.count, 0u);
-        }
-        __syncthreads();
-        const float* src = tail.embed + (size_t)tok * tail.H;
-        for (int i = tid; i < tail.H; i += kThreads) tail.h[i] = src[i];
     }
 }
 
+// Second half of the greedy tail: reduce the nkeys workgroup keys, advance
+// the sequence and gather the next embedding (one workgroup).
+__global__ __launch_bounds__(kThreads) void k_greedy_finish(GreedyTail tail, int nkeys, int N) {
+    __shared__ unsigned long long wk[kWaves];
+    __shared__ int tok;
+    const int tid = threadIdx.x, lane = tid & (QLM_WAVE - 1), wave = tid / QLM_WAVE;
+    // nkeys <= kMaxXsGrid: every slot is requested before any is compared
+    unsigned long long v[kMaxXsGrid / kThreads];
+#pragma unroll
+    for (int u = 0; u < kMaxXsGrid / kThreads; ++u) {
+        const int i = tid + u * kThreads;
+        v[u] = i < nkeys ? tail.keys[i] : 0ull;
+    }
+    unsigned long long k = 0ull;
+#pragma unroll
+    for (int u = 0; u < kMaxXsGrid / kThreads; ++u) k = v[u] > k ? v[u] : k;
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        const unsigned long long o = __shfl_xor(k, m, QLM_WAVE);
+        k = o > k ? o : k;
+    }
+    if (lane == 0) wk[wave] = k;
+    __syncthreads();
+    if (tid == 0) {
+        unsigned long long m = wk[0];
+        for (int w2 = 1; w2 < kWaves; ++w2) m = wk[w2] > m ? wk[w2] : m;
+        int idx = m ? (int)(0xFFFFFFFFu - (unsigned)(m & 0xFFFFFFFFull)) : 0;
+        if (idx < 0 || idx >= N) idx = 0;
+        const int p = tail.pos[0];
+        if (p + 1 < tail.ld_tokens && p + 1 >= tail.prompt_len[0]) tail.tokens[p + 1] = idx;
+        int t = (p + 1 < tail.ld_tokens) ? tail.tokens[p + 1] : idx;
+        t = t < 0 ? 0 : (t >= tail.vocab ? tail.vocab - 1 : t);
+        tok = t;
+        tail.pos[0] = p + 1;
+    }
+    __syncthreads();
+    const float* src = tail.embed + (size_t)tok * tail.H;
+    for (int i = tid; i < tail.H; i += kThreads) tail.h[i] = src[i];
+}
+
+// Dynamic LDS of the M = 1 kernel: x, plus the RMSNorm gain.
+size_t xs_lds_bytes(int K, int pro) {
+    return (size_t)K * sizeof(float) * (pro == PRO_RMSNORM ? 2 : 1);
+}
+constexpr size_t kXsLdsMax = 64 * 1024;
+
 struct XsConfig {
     int lpr, slots, R, grid;
+    bool balance;  // grid is an upper bound: fit it to residency, equal blocks per workgroup
 };
 
-// Launch-shape choice for M = 1, from a sweep over the model and config-1
-// shapes on MI355X: ~2-3 chunk slots per lane (lanes per row 64..256) for
-// the small decode projections, 5 slots and two rows per lane group for the
-// 151936-row logits matrix; a grid of up to N/8 workgroups (512..2048).
+// Launch-shape choice for M = 1, from a sweep of the fused forms at the
+// model's decode shapes on MI355X (graph replays): the fewest lanes per row
+// that leave at most 3 16-byte chunks per lane (2 for SwiGLU, whose rows come
+// in gate/up pairs; 5 when K > 8192), one output row per lane group, and for
+// the 151936-row logits matrix 32 lanes per row with two rows. The grid is
+// then fitted to what is resident at once (balanced_grid).
+// Measured best launch shapes for the 4B hybrid's decode projections
+// (N, K, epilogue -> lanes per row, rows, grid), graph replays on MI355X;
+// each beats the rule below by 3-12%.
+struct XsTuned {
+    int N, K, epi, lpr, rows, grid;
+};
+constexpr XsTuned kXsTuned[] = {
+    {9728, 2560, EPI_SWIGLU, 128, 1, 1024},  // gate/up
+    {2560, 9728, EPI_RESID, 128, 1, 512},    // down
+    {8224, 2560, EPI_STORE, 64, 1, 512},     // DeltaNet in_proj [qkv|z|b|a]
+    {5120, 2560, EPI_STORE, 64, 1, 512},     // GQA q(+gate)/k/v
+    {2560, 2048, EPI_RESID, 64, 1, 640},     // out_proj / o_proj
+    {151936, 2560, EPI_STORE, 32, 2, 1280},  // lm_head (also its greedy form)
+};
+
 XsConfig xs_config(int N, int K, int epi) {
+    for (const XsTuned& t : kXsTuned) {
+        const int e = epi == EPI_ARGMAX ? EPI_STORE : epi;
+        if (t.N == N && t.K == K && t.epi == e) {
+            XsConfig c;
+            c.lpr = t.lpr;
+            c.slots = ((K >> 4) + t.lpr - 1) / t.lpr;
+            c.R = epi == EPI_SWIGLU ? 2 * t.rows : t.rows;
+            c.grid = t.grid;
+            c.balance = false;
+            return c;
+        }
+    }
     const int nchunk = K >> 4;
     const bool tall = N >= 65536;
-    int lpr = tall ? 32 : 64;
-    while (lpr < 256 && (nchunk + lpr - 1) / lpr > (tall ? 6 : 3)) lpr *= 2;
+    const int max_slots = tall ? 6 : (K > 8192 ? 5 : (epi == EPI_SWIGLU ? 2 : 3));
+    int lpr = 32;
+    while (lpr < 256 && (nchunk + lpr - 1) / lpr > max_slots) lpr *= 2;
     XsConfig c;
     c.lpr = lpr;
     c.slots = (nchunk + lpr - 1) / lpr;
     const int groups = kThreads / lpr;
-    c.R = (epi == EPI_SWIGLU) ? 2 : ((tall || (K >= 8192 && N <= 4096)) ? 2 : 1);
+    c.R = (epi == EPI_SWIGLU || tall) ? 2 : 1;
     const int out_per_block = groups * ((epi == EPI_SWIGLU) ? c.R / 2 : c.R);
     const int nblocks = (N + out_per_block - 1) / out_per_block;
-    int cap = N / 8;
-    cap = cap < 512 ? 512 : (cap > 2048 ? 2048 : cap);
-    c.grid = nblocks < cap ? nblocks : cap;
+    c.grid = nblocks < 2048 ? nblocks : 2048;
+    c.balance = true;
     return c;
+}
+
+// Compute units and LDS per compute unit of the current device.
+void device_shape(int& cus, size_t& lds_per_cu) {
+    int dev = 0, v = 0;
+    cus = 256;
+    lds_per_cu = 160 * 1024;
+    if (hipGetDevice(&dev) != hipSuccess) return;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+        cus = v;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) ==
+            hipSuccess &&
+        v > 0)
+        lds_per_cu = (size_t)v;
+}
+
+// Grid for a grid-stride launch of nblocks row blocks: never more
+// workgroups than are resident at once (register- and LDS-limited), so there
+// is no straggler round; within that, as many as possible (bytes in flight),
+// then trimmed to give every workgroup the same number of blocks.
+int balanced_grid(int nblocks, int cap, int per_cu_regs, size_t lds) {
+    int cus;
+    size_t lds_cu;
+    device_shape(cus, lds_cu);
+    int per_cu = per_cu_regs > 0 ? per_cu_regs : 1;
+    if (lds > 0 && (int)(lds_cu / lds) < per_cu) per_cu = (int)(lds_cu / lds);
+    if (per_cu < 1) per_cu = 1;
+    int lim = per_cu * cus;
+    if (cap > 0 && cap < lim) lim = cap;
+    const int bpw = (nblocks + lim - 1) / lim;
+    return (nblocks + bpw - 1) / bpw;
 }
 
 template <int SLOTS, int R, bool ROWSCALE, int PRO, int EPI>
 int launch_xs(const XsConfig& c, const float* x, const float* nw, float eps, const int8_t* q,
               const float* sc, float* y, int N, int K, int F, hipStream_t st,
               const GreedyTail& tail) {
+    auto kern = k_gemv_xs<SLOTS, R, ROWSCALE, PRO, EPI>;
     const int groups = kThreads / c.lpr;
     const int out_per_block = groups * ((EPI == EPI_SWIGLU) ? R / 2 : R);
     const int nblocks = (N + out_per_block - 1) / out_per_block;
-    hipLaunchKernelGGL((k_gemv_xs<SLOTS, R, ROWSCALE, PRO, EPI>), dim3(c.grid), dim3(kThreads), 0,
-                       st, x, nw, eps, q, sc, y, N, K, F, c.lpr, nblocks, tail);
+    const size_t lds = xs_lds_bytes(K, PRO);
+    int grid = c.grid < nblocks ? c.grid : nblocks;
+    if (c.balance) {
+        // register-limited workgroups per CU of this instance (LDS aside)
+        static const int per_cu = [kern] {
+            int n = 0;
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, kThreads, 0) != hipSuccess)
+                n = 1;
+            return n;
+        }();
+        grid = balanced_grid(nblocks, c.grid, per_cu, lds);
+    }
+    if (grid < 1) grid = 1;
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), lds, st, x, nw, eps, q, sc, y, N, K, F,
+                       c.lpr, nblocks, tail);
+    if constexpr (EPI == EPI_ARGMAX) {
+        const int rc = qlm_launch_status();
+        if (rc != QLM_OK) return rc;
+        hipLaunchKernelGGL(k_greedy_finish, dim3(1), dim3(kThreads), 0, st, tail, grid, N);
+    }
     return qlm_launch_status();
 }
 
@@ -581,7 +701,7 @@ int launch_xs_sr(const XsConfig& c, const float* x, const float* nw, float eps, 
 #define QLM_XS(S, RR)                                                                        \
     if (c.slots <= S && c.R == RR)                                                           \
         return launch_xs<S, RR, ROWSCALE, PRO, EPI>(c, x, nw, eps, q, sc, y, N, K, F, st, tail);
-    if (EPI == EPI_SWIGLU) {
+    if constexpr (EPI == EPI_SWIGLU) {
         QLM_XS(2, 2) QLM_XS(3, 2) QLM_XS(4, 2) QLM_XS(5, 2) QLM_XS(6, 2)
         QLM_XS(2, 4) QLM_XS(3, 4) QLM_XS(4, 4) QLM_XS(5, 4) QLM_XS(6, 4)
     } else {
@@ -671,7 +791,7 @@ int gemv_dispatch(int pro, int epi, const float* x, int ldx, const float* nw, fl
     // 16-byte vector loads of activations, weights and norm gains
     if (((uintptr_t)x | (uintptr_t)q | (uintptr_t)nw) & 15u) return QLM_ERR_SHAPE;
     hipStream_t st = as_stream(stream);
-    if (M == 1)
+    if (M == 1 && xs_lds_bytes(K, pro) <= kXsLdsMax)
         return xs_dispatch(pro, epi, xs_config(N, K, epi), x, nw, eps, q, sc, rowscale, y, N, K,
                            st);
     const int F = N;  // swiglu: up rows start at F
@@ -715,28 +835,37 @@ extern "C" int qlm_gemv_i8(const float* x, int ldx, const int8_t* q, const float
                          N, K, stream);
 }
 
-extern "C" int qlm_gemv_i8_config(const float* x, const int8_t* q, const float* scales, int group,
-                                  float* y, int N, int K, int lanes_per_row, int rows,
-                                  int grid, void* stream) {
+extern "C" int qlm_gemv_i8_config(const float* x, const float* norm_w, float eps,
+                                  const int8_t* q, const float* scales, int group, float* y, int N,
+                                  int K, int epilogue, int lanes_per_row, int rows, int grid,
+                                  void* stream) {
     if (!x || !q || !scales || !y || N <= 0 || K <= 0 || grid <= 0) return QLM_ERR_ARG;
+    if (epilogue < EPI_STORE || epilogue > EPI_SWIGLU) return QLM_ERR_ARG;
     if (K % 16 != 0) return QLM_ERR_SHAPE;
     const bool rowscale = (group == K);
     if (!rowscale && (group != 32 || K % 32 != 0)) return QLM_ERR_SHAPE;
-    if (lanes_per_row < 16 || lanes_per_row > 256 || (lanes_per_row & (lanes_per_row - 1)))
+    if (((uintptr_t)x | (uintptr_t)q | (uintptr_t)norm_w) & 15u) return QLM_ERR_SHAPE;
+    if (lanes_per_row < 16 || lanes_per_row > kThreads ||
+        (lanes_per_row & (lanes_per_row - 1)) != 0 || (rows != 1 && rows != 2))
         return QLM_ERR_SHAPE;
-    if (rows != 1 && rows != 2) return QLM_ERR_SHAPE;
-    if (((uintptr_t)x | (uintptr_t)q) & 15u) return QLM_ERR_SHAPE;
+    const int pro = norm_w ? PRO_RMSNORM : PRO_NONE;
+    if (epilogue == EPI_SWIGLU && !norm_w) return QLM_ERR_ARG;  // only the fused-norm form exists
     XsConfig c;
     c.lpr = lanes_per_row;
     c.slots = ((K >> 4) + lanes_per_row - 1) / lanes_per_row;
     if (c.slots > 6) return QLM_ERR_SHAPE;
-    c.R = rows;
+    c.R = epilogue == EPI_SWIGLU ? 2 * rows : rows;
     c.grid = grid;
-    return xs_dispatch(PRO_NONE, EPI_STORE, c, x, nullptr, 0.0f, q, scales, rowscale, y, N, K,
+    c.balance = false;
+    if (xs_lds_bytes(K, pro) > kXsLdsMax) return QLM_ERR_SHAPE;
+    if (epilogue == EPI_RESID && pro == PRO_RMSNORM) return QLM_ERR_ARG;
+    return xs_dispatch(pro, epilogue, c, x, norm_w, eps, q, scales, rowscale, y, N, K,
                        as_stream(stream));
 }
 
-extern "C" size_t qlm_lm_head_greedy_workspace_bytes(void) { return 256; }
+extern "C" size_t qlm_lm_head_greedy_workspace_bytes(void) {
+    return (size_t)kMaxXsGrid * sizeof(unsigned long long);
+}
 
 extern "C" int qlm_lm_head_greedy(const float* x, const float* norm_w, float eps, const int8_t* q,
                                   const float* scales, int group, float* logits, int V, int K,
@@ -751,9 +880,10 @@ extern "C" int qlm_lm_head_greedy(const float* x, const float* norm_w, float eps
     if (!rowscale && (group != 32 || K % 32 != 0)) return QLM_ERR_SHAPE;
     if (((uintptr_t)x | (uintptr_t)q | (uintptr_t)norm_w | (uintptr_t)work) & 15u)
         return QLM_ERR_SHAPE;
+    const XsConfig c = xs_config(V, K, EPI_STORE);
+    if (c.grid > kMaxXsGrid || xs_lds_bytes(K, PRO_RMSNORM) > kXsLdsMax) return QLM_ERR_SHAPE;
     GreedyTail t;
-    t.key = reinterpret_cast<unsigned long long*>(work);
-    t.count = reinterpret_cast<unsigned*>(reinterpret_cast<char*>(work) + 64);
+    t.keys = reinterpret_cast<unsigned long long*>(work);
     t.tokens = tokens;
     t.ld_tokens = ld_tokens;
     t.pos = pos;
@@ -762,8 +892,8 @@ extern "C" int qlm_lm_head_greedy(const float* x, const float* norm_w, float eps
     t.H = H;
     t.vocab = V;
     t.h = h_next;
-    return xs_dispatch(PRO_RMSNORM, EPI_ARGMAX, xs_config(V, K, EPI_STORE), x, norm_w, eps, q,
-                       scales, rowscale, logits, V, K, as_stream(stream), t);
+    return xs_dispatch(PRO_RMSNORM, EPI_ARGMAX, c, x, norm_w, eps, q, scales, rowscale, logits, V,
+                       K, as_stream(stream), t);
 }
 
 extern "C" int qlm_gemv_i8_rmsnorm(const float* x, int ldx, const float* norm_w, float eps,

@@ -49,7 +49,7 @@ _SIGS = {
     "qlm_quantize_q8_f32": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp]),
     "qlm_quantize_q8_bf16": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp]),
     "qlm_gemv_i8": (_i, [_vp, _i, _vp, _vp, _i, _vp, _i, _i, _i, _i, _vp]),
-    "qlm_gemv_i8_config": (_i, [_vp, _vp, _vp, _i, _vp, _i, _i, _i, _i, _i, _vp]),
+    "qlm_gemv_i8_config": (_i, [_vp, _vp, _f, _vp, _vp, _i, _vp, _i, _i, _i, _i, _i, _i, _vp]),
     "qlm_gemv_i8_rmsnorm": (_i, [_vp, _i, _vp, _f, _vp, _vp, _i, _vp, _i, _i, _i, _i, _vp]),
     "qlm_gemv_i8_residual": (_i, [_vp, _i, _vp, _vp, _i, _vp, _i, _i, _i, _i, _vp]),
     "qlm_gemv_i8_swiglu_rmsnorm": (_i, [_vp, _i, _vp, _f, _vp, _vp, _i, _vp, _i, _i, _i, _i,

@@ -95,9 +95,38 @@ def test_gemv_launch_shapes(hip, orc, rng, N, K):
             for rows in (1, 2):
                 for grid in (1, 7, 300):
                     dy.zero()
-                    hip.call("qlm_gemv_i8_config", dx, dq, ds, g, dy, N, K, lpr, rows, grid, None)
+                    hip.call("qlm_gemv_i8_config", dx, None, 0.0, dq, ds, g, dy, N, K, 0, lpr,
+                             rows, grid, None)
                     err = rel_err(dy.to_numpy((1, N), np.float32), ref)
                     assert err < 1e-5, (g, lpr, rows, grid, err)
+
+
+@pytest.mark.parametrize("epi", ["norm", "resid", "swiglu"])
+def test_gemv_config_fused(hip, orc, rng, epi):
+    """The fused M = 1 forms under explicit launch shapes (ragged last block,
+    grids smaller and larger than the row-block count)."""
+    N, K, g, eps = 1000, 1536, 32, 1e-6
+    rows_w = 2 * N if epi == "swiglu" else N
+    q, s = _weights(orc, rng, rows_w, K, g)
+    x = rng.standard_normal((1, K)).astype(np.float32)
+    nw = (rng.standard_normal(K) * 0.02).astype(np.float32)
+    y0 = rng.standard_normal((1, N)).astype(np.float32)
+    if epi == "resid":
+        ref = y0 + orc.matmul_i8(x, q, s, g)
+    else:
+        lg = orc.matmul_i8(orc.rms_norm(x, nw, eps), q, s, g)
+        ref = lg if epi == "norm" else orc.silu_mul(lg[:, :N].copy(), lg[:, N:].copy())
+    dq, ds, dx, dnw = dev(hip, q), dev(hip, s), dev(hip, x), dev(hip, nw)
+    dy = hip.DeviceBuffer(N * 4)
+    code = {"norm": 0, "resid": 1, "swiglu": 2}[epi]
+    for lpr in (32, 64, 128):
+        for rows in (1, 2):
+            for grid in (3, 250):
+                dy.upload(y0)
+                hip.call("qlm_gemv_i8_config", dx, None if epi == "resid" else dnw, eps, dq, ds,
+                         g, dy, N, K, code, lpr, rows, grid, None)
+                err = rel_err(dy.to_numpy((1, N), np.float32), ref)
+                assert err < 1e-5, (epi, lpr, rows, grid, err)
 
 
 def test_gemv_exact_integers(hip, orc, rng):
@@ -268,7 +297,7 @@ def test_greedy_advance_and_embed(hip, rng):
 
 @pytest.mark.parametrize("group", [32, "K"])
 def test_lm_head_greedy_fused(hip, orc, rng, group):
-    """Final norm + lm_head + argmax + advance + next embedding in one launch,
+    """Final norm + lm_head + argmax + advance + next embedding (two launches),
     three calls in a row (prompt position, then two generated tokens)."""
     V, K, L = 151936, 1024, 16
     g = K if group == "K" else 32
@@ -279,8 +308,9 @@ def test_lm_head_greedy_fused(hip, orc, rng, group):
     tokens[:3] = [11, 22, 33]
     dtok, dpos = dev(hip, tokens), dev(hip, np.array([1], np.int32))
     dplen = dev(hip, np.array([3], np.int32))
-    work = hip.DeviceBuffer(hip.lib().qlm_lm_head_greedy_workspace_bytes())
-    work.zero()
+    nwork = hip.lib().qlm_lm_head_greedy_workspace_bytes()
+    work = hip.DeviceBuffer(nwork)
+    work.upload(np.full(nwork, 0xA5, np.uint8))  # no initial contents are required
     dq, ds, dnw, dtab = dev(hip, q), dev(hip, s), dev(hip, nw), dev(hip, table)
     dlg, dh = hip.DeviceBuffer(V * 4), hip.DeviceBuffer(K * 4)
     p = 1
@@ -358,10 +388,14 @@ def test_deltanet_decode_fused(hip, orc, rng):
 
 
 # ---------------------------------------------------------------- A8/A9 GQA
-@pytest.mark.parametrize("n_q,n_kv,hd,rot,gated", [(16, 4, 128, 32, 1), (8, 2, 128, 128, 1),
-                                                   (16, 2, 256, 64, 0)])
-def test_gqa_decode_fused(hip, orc, rng, n_q, n_kv, hd, rot, gated):
-    B, max_seq, theta = 2, 600, 1e6
+@pytest.mark.parametrize("n_q,n_kv,hd,rot,gated,max_seq,start",
+                         [(16, 4, 128, 32, 1, 600, (300, 511)),
+                          (8, 2, 128, 128, 1, 600, (300, 511)),
+                          (16, 2, 256, 64, 0, 600, (300, 511)),
+                          # > 128 chunks of 64: the combine runs two tiles
+                          (16, 4, 128, 32, 1, 9000, (8300, 8500))])
+def test_gqa_decode_fused(hip, orc, rng, n_q, n_kv, hd, rot, gated, max_seq, start):
+    B, theta = 2, 1e6
     qs = (2 if gated else 1) * hd
     ld = n_q * qs + 2 * n_kv * hd
     qn = (rng.standard_normal(hd) * 0.02).astype(np.float32)
@@ -372,15 +406,13 @@ def test_gqa_decode_fused(hip, orc, rng, n_q, n_kv, hd, rot, gated):
     dkc, dvc = dev(hip, kc), dev(hip, vc)
     kref = [kc[b].copy() for b in range(B)]
     vref = [vc[b].copy() for b in range(B)]
-    # fill a history so the chunked split (256 positions) is exercised
-    start = [300, 511]
+    # fill a history so the split over chunks is exercised
     for b in range(B):
         kref[b][: start[b] + 40] = rng.standard_normal((start[b] + 40, n_kv, hd))
         vref[b][: start[b] + 40] = rng.standard_normal((start[b] + 40, n_kv, hd))
     dkc.upload(np.stack(kref))
     dvc.upload(np.stack(vref))
     work = hip.DeviceBuffer(hip.lib().qlm_gqa_workspace_bytes(B, n_q, hd, max_seq))
-    work.zero()  # completion counters start at zero; every call leaves them there
     dcos, dsin = dev(hip, cos_t), dev(hip, sin_t)
     for step in range(3):
         pos = np.array([start[0] + step, start[1] + step], np.int32)
