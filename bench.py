@@ -83,12 +83,10 @@ def bench_gemv(hip, shapes, Ms, group_kind, iters=100, pool_bytes=2 << 30):
 
 
 def run_decode(eng, prompts, warmup, steps, graph=True):
-    """Prefill (n-1 prompt forwards), warmup, then exactly `steps` timed steps."""
+    """Batched prefill of positions 0..n-2, warmup, then exactly `steps` timed
+    decode steps."""
     B, n = prompts.shape
-    eng.start(prompts)
-    t0 = time.perf_counter()
-    eng.steps(n - 1, graph)
-    prefill_s = time.perf_counter() - t0
+    prefill_s = eng.start(prompts, batched_prefill=True)
     if warmup:
         eng.steps(warmup, graph)
     from quicklm_amd import hip
@@ -178,7 +176,7 @@ def main():
         graph = not args.eager
         r1 = run_decode(eng, prompts[:1], args.warmup, args.steps, graph)
         log(f"batch 1: {r1['tok_s']:.1f} tok/s ({r1['ms_per_step']:.3f} ms/step), prefill "
-            f"{r1['prefill_s']:.1f}s, kernels/step {eng.kernels_per_step()}")
+            f"{r1['prefill_s']:.3f}s, kernels/step {eng.kernels_per_step()}")
         rB = None
         if args.batch > 1:
             rB = run_decode(eng, prompts[:args.batch], args.warmup, args.steps, graph)

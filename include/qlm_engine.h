@@ -43,15 +43,21 @@ int qlm_engine_forward(void* handle, int token, int pos, float* logits);
 
 /* Greedy generation with the CLI convention (main.cpp:574-690): prompts
  * [B, n] host int32; out [B, n_new]; timings in seconds (prefill = the n-1
- * prompt forwards, decode = the n_new steps). use_graph 0 launches eagerly. */
+ * prompt forwards, decode = the n_new steps). use_graph 0 launches eagerly.
+ * prefill_mode 1: positions 0..n-2 of each sequence go through the batched
+ * prefill (the reference's forward_batch, model.cpp:213-258: every layer
+ * over all prompt rows); 0: each is forwarded by its own decode step. */
 int qlm_engine_generate(void* handle, const int* prompts, int B, int n, int n_new, int* out,
-                        double* prefill_s, double* decode_s, int use_graph);
+                        double* prefill_s, double* decode_s, int use_graph, int prefill_mode);
 
 /* Stepwise generation for benchmarks: start() resets and installs B prompts
- * of length n; steps() runs k decode steps (prompt forwards first) as graph
+ * of length n (prefill_mode 1 also prefills positions 0..n-2, wall time in
+ * *prefill_s, so the first step forwards position n-1); steps() runs k
+ * decode steps (with prefill_mode 0 the prompt forwards come first) as graph
  * replays and reports their GPU time in ms (HIP events on the engine's
  * stream); tokens() copies count tokens of sequence b from position first. */
-int qlm_engine_start(void* handle, const int* prompts, int B, int n);
+int qlm_engine_start(void* handle, const int* prompts, int B, int n, int prefill_mode,
+                     double* prefill_s);
 int qlm_engine_steps(void* handle, int k, int use_graph, double* gpu_ms);
 int qlm_engine_tokens(void* handle, int b, int first, int count, int* out);
 

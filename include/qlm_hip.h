@@ -90,6 +90,16 @@ int qlm_gemv_i8_config(const float* x, const float* norm_w, float eps, const int
                        const float* scales, int group, float* y, int N, int K, int epilogue,
                        int lanes_per_row, int rows, int grid, void* stream);
 
+/* A4: the same matmul for M > 1 on the matrix cores (batched decode, prefill;
+ * math_ops.cpp:845-871). Weights stay exact (int8 in bf16); each activation
+ * is split into bf16 hi + lo and the per-group products are scaled in fp32,
+ * so results match the fp32 path to ~1e-6 normwise (bit-exact when x holds
+ * small integers). epilogue 0: y = x.W^T; 1: y += x.W^T; 2: SwiGLU with
+ * weights [2F, K] and N = F outputs (as qlm_gemv_i8_swiglu_rmsnorm, without
+ * the norm). Any M >= 1; K a multiple of 32; G = 32 or K. */
+int qlm_matmul_i8(const float* x, int ldx, const int8_t* q, const float* scales, int group,
+                  float* y, int ldy, int M, int N, int K, int epilogue, void* stream);
+
 /* Fused forms used by the decode step (same arithmetic as the unfused
  * reference sequence, one launch instead of two or three):
  *   _rmsnorm: x is first replaced by rms_norm(x, norm_w, eps) (zero-centred
@@ -156,7 +166,19 @@ int qlm_deltanet_decode(const float* proj, int ldp, float* conv_state, const flo
                         float* state, const int* pos, float* out, int ldo, int B, int H, int d,
                         void* stream);
 
-/* ---- A8/A9: GQA decode attention over a contiguous KV cache -----------------
+/* ---- A13: DeltaNet prefill of one sequence -----------------------------------
+ * Qwen3_5GatedDeltaNet::forward_chunk (attention.cpp:600-758): the mixer of
+ * qlm_deltanet_decode applied to T consecutive projection rows (row t at
+ * position p0 + t) in order, as the reference does, carrying the conv ring
+ * and the state [H, d, d] of that sequence from row to row; both are left as
+ * a decode step at position p0 + T expects them. Bit-identical to T
+ * qlm_deltanet_decode calls. out[t] is [H*d] (row stride ldo). */
+int qlm_deltanet_prefill(const float* proj, int ldp, int T, float* conv_state,
+                         const float* conv_w_t, const float* A_log, const float* dt_bias,
+                         const float* norm_w, float* state, int p0, float* out, int ldo, int H,
+                         int d, void* stream);
+
+/* ---- A8/A9: GQA decode attention over a contiguous KV cache/* ---- A8/A9: GQA decode attention over a contiguous KV cache -----------------
  * Qwen3_5Attention::forward steps 2-6 (attention.cpp:160-227) for B
  * sequences at positions pos[b]:
  *   qkv[b] = [q+gate (n_q * 2*hd if gated else n_q*hd) | k (n_kv*hd) | v (n_kv*hd)]
@@ -165,15 +187,28 @@ int qlm_deltanet_decode(const float* proj, int ldp, float* conv_state, const flo
  *   positions 0..pos[b], sigmoid(gate) output gate when gated.
  * Cache layout [B, max_seq, n_kv, hd] fp32 (position-major, as the reference,
  * attention.cpp:134-135). out[b] is [n_q*hd]. work is a device workspace of
- * qlm_gqa_workspace_bytes(...) bytes, zero-filled once before its first use
- * (it holds completion counters that every call leaves at zero). */
+ * qlm_gqa_workspace_bytes(...) bytes (no initial contents needed; also large
+ * enough for qlm_attention_decode with the same B, n_q, hd, max_seq). */
 size_t qlm_gqa_workspace_bytes(int B, int n_q, int hd, int max_seq);
 int qlm_gqa_decode(float* qkv, int ldqkv, const float* q_norm, const float* k_norm,
                    const float* cos_tab, const float* sin_tab, int rot_dim, float* k_cache,
                    float* v_cache, int max_seq, const int* pos, float* out, int ldo, int B,
                    int n_q, int n_kv, int hd, int gated, void* work, void* stream);
 
-/* Isolated attention core (no norm/RoPE/write): out[b, h] = softmax(q.K^T *
+/* Prefill of one sequence: the same attention for T consecutive rows of the
+ * projection (row t at position p0 + t, causal over 0..p0+t), as the
+ * reference's batched forward (attention.cpp:138-232 per row). q rows are
+ * normalised and rotated in place; k/v rows go to the cache of that sequence
+ * (k_cache, v_cache point at its [max_seq, n_kv, hd] block) before any row
+ * attends. out[t] is [n_q*hd] (row stride ldo). work is
+ * qlm_gqa_prefill_workspace_bytes(n_q, hd, max_seq) bytes. */
+size_t qlm_gqa_prefill_workspace_bytes(int n_q, int hd, int max_seq);
+int qlm_gqa_prefill(float* qkv, int ldqkv, const float* q_norm, const float* k_norm,
+                    const float* cos_tab, const float* sin_tab, int rot_dim, float* k_cache,
+                    float* v_cache, int max_seq, int p0, int T, float* out, int ldo, int n_q,
+                    int n_kv, int hd, int gated, void* work, void* stream);
+
+/* Isolated attention core (no norm/RoPE/write)/* Isolated attention core (no norm/RoPE/write): out[b, h] = softmax(q.K^T *
  * scale) . V over the first ctx positions of a [B, max_seq, n_kv, hd] cache,
  * kv_dtype 0 = fp32, 1 = bf16. q, out are [B, n_q, hd] fp32. */
 int qlm_attention_decode(const float* q, const void* k_cache, const void* v_cache,

@@ -80,20 +80,22 @@ int qlm_engine_forward(void* handle, int token, int pos, float* logits) {
 }
 
 int qlm_engine_generate(void* handle, const int* prompts, int B, int n, int n_new, int* out,
-                        double* prefill_s, double* decode_s, int use_graph) {
+                        double* prefill_s, double* decode_s, int use_graph, int prefill_mode) {
     return guarded([&] {
         if (!prompts || !out) throw std::runtime_error("null argument");
         qlm::GenStats st;
-        M(handle)->generate(prompts, B, n, n_new, out, &st, use_graph != 0);
+        M(handle)->generate(prompts, B, n, n_new, out, &st, use_graph != 0, prefill_mode != 0);
         if (prefill_s) *prefill_s = st.prefill_s;
         if (decode_s) *decode_s = st.decode_s;
     });
 }
 
-int qlm_engine_start(void* handle, const int* prompts, int B, int n) {
+int qlm_engine_start(void* handle, const int* prompts, int B, int n, int prefill_mode,
+                     double* prefill_s) {
     return guarded([&] {
         if (!prompts) throw std::runtime_error("null prompts");
-        M(handle)->start(prompts, B, n);
+        const double s = M(handle)->start(prompts, B, n, prefill_mode != 0);
+        if (prefill_s) *prefill_s = s;
     });
 }
 

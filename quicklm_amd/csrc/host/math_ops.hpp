@@ -18,6 +18,9 @@ void* stream();
 // C = A * B^T with B an int8 (Q8_0) weight operand; A [M, K] fp32, C [M, N]
 // with row stride C.row_stride() (math_ops.hpp:92; math_ops.cpp:820-900).
 void matmul(const Tensor& A, const Tensor& B, Tensor& C, bool transpose_B = true);
+// Device scratch of at least M*K floats for the matrix-core forms with a
+// fused RMSNorm (M > 4): the normalised rows are written there first.
+void set_norm_scratch(float* p, int64_t floats);
 
 // math_ops.hpp:102 / :139-140 / :132.
 void rms_norm(const Tensor& input, const Tensor& weight, Tensor& output, float eps);

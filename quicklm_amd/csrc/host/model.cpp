@@ -224,6 +224,7 @@ void DecoderModel::load(const std::string& dir, int max_seq_len, const std::stri
     proj_.alloc(B * Pmax * sizeof(float));
     core_.alloc(B * CORE_ * sizeof(float));
     act_.alloc(B * F * sizeof(float));
+    norm_scratch_.alloc(B * H * sizeof(float));
     logits_.alloc(B * cfg_.vocab_size * sizeof(float));
     argmax_work_.alloc(qlm_argmax_workspace_bytes((int)B, cfg_.vocab_size));
     tail_work_.alloc(qlm_lm_head_greedy_workspace_bytes());
@@ -248,8 +249,20 @@ void DecoderModel::reset_states() {
 // One decode step for sequences [0, B): the forward of DecoderModel::forward
 // (model.cpp:151-199) with every layer's elementwise work fused into the
 // projections, followed by greedy sampling and the position advance.
+namespace {
+// Launches of one math::matmul* call over B rows: the M = 1 GEMV, the GEMV
+// in slices of 4 rows, or (B > 4) the matrix-core matmul after a separate
+// RMSNorm when the norm is fused.
+int mm_launches(int B, bool norm) {
+    if (B == 1) return 1;
+    if (B > 4) return norm ? 2 : 1;
+    return (B + 3) / 4;
+}
+}  // namespace
+
 void DecoderModel::enqueue_step(int B) {
     math::set_stream(stream_);
+    math::set_norm_scratch(norm_scratch_.get<float>(), (int64_t)norm_scratch_.bytes() / 4);
     const int H = cfg_.hidden_size, F = cfg_.intermediate_size, V = cfg_.vocab_size;
     const int nh = cfg_.linear_num_heads, d = cfg_.linear_head_dim;
     const int nq = cfg_.num_attention_heads, nkv = cfg_.num_key_value_heads, hd = cfg_.head_dim;
@@ -274,7 +287,7 @@ void DecoderModel::enqueue_step(int B) {
             core.strides = {CORE_, 1};
             math::matmul_residual(core, w.dn_out.view(), hx);
             ++dn_i;
-            n += 3;
+            n += mm_launches(B, true) + 1 + mm_launches(B, false);
         } else {
             Tensor proj({B, PQ_}, proj_.get<float>());
             proj.strides = {Pmax, 1};
@@ -290,12 +303,12 @@ void DecoderModel::enqueue_step(int B) {
             core.strides = {CORE_, 1};
             math::matmul_residual(core, w.at_o.view(), hx);
             ++at_i;
-            n += 4;  // projection, attention, combine, o_proj
+            n += mm_launches(B, true) + 2 + mm_launches(B, false);  // + attention, combine
         }
         Tensor act({B, F}, act_.get<float>());
         math::matmul_swiglu_rmsnorm(hx, post_ln, eps, w.gate_up.view(), act);
         math::matmul_residual(act, w.down.view(), hx);
-        n += B == 1 ? 2 : 2 * ((B + 3) / 4);
+        n += mm_launches(B, true) + mm_launches(B, false);
     }
     // Step tail: final norm + lm_head + greedy sample + advance, then the
     // embedding of the token now at pos (the next step's input, or the next
@@ -317,7 +330,7 @@ void DecoderModel::enqueue_step(int B) {
                                  prompt_len_.get<int>(), stream_),
               "argmax");
         embed_current(B);
-        n += (B + 3) / 4 + 3;
+        n += mm_launches(B, true) + 3;  // + argmax (two passes with advance), embedding
     }
     kernels_per_step_ = n;
 }
@@ -370,7 +383,7 @@ void DecoderModel::last_logits(int b, float* host) const {
     check(qlm_stream_sync(stream_), "sync");
 }
 
-void DecoderModel::start(const int* prompts, int B, int n) {
+double DecoderModel::start(const int* prompts, int B, int n, bool batched_prefill) {
     if (B <= 0 || B > max_batch_) throw std::runtime_error("generate: batch exceeds max_batch");
     if (n <= 0) throw std::runtime_error("generate: empty prompt");
     if (n > max_seq_)
@@ -380,16 +393,115 @@ void DecoderModel::start(const int* prompts, int B, int n) {
         if (prompts[i] < 0 || prompts[i] >= cfg_.vocab_size)
             throw std::runtime_error("generate: token id out of range");
     reset_states();
-    std::vector<int> tok((size_t)B * ld_tokens_, 0), pl(B, n), zero(B, 0);
+    std::vector<int> tok((size_t)B * ld_tokens_, 0), pl(B, n), p(B, 0);
     for (int b = 0; b < B; ++b) std::memcpy(&tok[(size_t)b * ld_tokens_], prompts + (size_t)b * n, n * 4);
     check(qlm_memcpy_h2d(tokens_.get(), tok.data(), tok.size() * 4, stream_), "upload");
     check(qlm_memcpy_h2d(prompt_len_.get(), pl.data(), B * 4, stream_), "upload");
-    check(qlm_memcpy_h2d(pos_.get(), zero.data(), B * 4, stream_), "upload");
+    double prefill_s = 0.0;
+    run_steps_ = 0;
+    if (batched_prefill && n > 1) {
+        check(qlm_stream_sync(stream_), "sync");
+        const double t0 = now_s();
+        for (int b = 0; b < B; ++b) prefill(b, n);
+        check(qlm_stream_sync(stream_), "sync");
+        prefill_s = now_s() - t0;
+        std::fill(p.begin(), p.end(), n - 1);
+        run_steps_ = n - 1;
+    }
+    check(qlm_memcpy_h2d(pos_.get(), p.data(), B * 4, stream_), "upload");
     embed_current(B);
     check(qlm_stream_sync(stream_), "sync");
     run_B_ = B;
     run_n_ = n;
-    run_steps_ = 0;
+    return prefill_s;
+}
+
+namespace {
+constexpr int kPrefillChunk = 1024;  // prompt rows per pass through the layers
+}  // namespace
+
+void DecoderModel::ensure_prefill_buffers(int rows) {
+    if (rows <= pf_rows_) return;
+    const size_t H = cfg_.hidden_size, F = cfg_.intermediate_size;
+    const size_t Pmax = (size_t)std::max(PD_, PQ_);
+    hx_pf_.alloc(rows * H * sizeof(float));
+    proj_pf_.alloc(rows * Pmax * sizeof(float));
+    core_pf_.alloc(rows * (size_t)CORE_ * sizeof(float));
+    act_pf_.alloc(rows * F * sizeof(float));
+    norm_pf_.alloc(rows * H * sizeof(float));
+    if (QR_ > 0 && gqa_pf_work_.bytes() == 0)
+        gqa_pf_work_.alloc(qlm_gqa_prefill_workspace_bytes(cfg_.num_attention_heads,
+                                                           cfg_.head_dim, max_seq_));
+    pf_rows_ = rows;
+}
+
+// Prefill of sequence b: prompt positions 0..n-2 through every layer, in
+// chunks of up to kPrefillChunk rows (the reference's forward_batch,
+// model.cpp:213-258, with main.cpp:590-622's convention that the last prompt
+// token is forwarded by the first decode step). Fills the conv rings,
+// DeltaNet states and KV caches of sequence b; no logits are needed.
+void DecoderModel::prefill(int b, int n) {
+    const int total = n - 1;
+    if (total <= 0) return;
+    const int chunk = std::min(total, kPrefillChunk);
+    ensure_prefill_buffers(chunk);
+    math::set_stream(stream_);
+    math::set_norm_scratch(norm_pf_.get<float>(), (int64_t)norm_pf_.bytes() / 4);
+    const int H = cfg_.hidden_size, F = cfg_.intermediate_size, V = cfg_.vocab_size;
+    const int nh = cfg_.linear_num_heads, d = cfg_.linear_head_dim;
+    const int nq = cfg_.num_attention_heads, nkv = cfg_.num_key_value_heads, hd = cfg_.head_dim;
+    const float eps = cfg_.rms_norm_eps;
+    const int Pmax = std::max(PD_, PQ_);
+    const int C = 3 * HD_;
+    for (int p0 = 0; p0 < total; p0 += chunk) {
+        const int rows = std::min(chunk, total - p0);
+        check(qlm_embed_tokens(embed_.get<float>(), V, H,
+                               tokens_.get<int>() + (size_t)b * ld_tokens_ + p0, 1, nullptr,
+                               hx_pf_.get<float>(), H, rows, stream_),
+              "embed");
+        Tensor hx({rows, H}, hx_pf_.get<float>());
+        int dn_i = 0, at_i = 0;
+        for (auto& w : layers_) {
+            Tensor in_ln({H}, w.in_ln.get<float>()), post_ln({H}, w.post_ln.get<float>());
+            if (w.linear) {
+                Tensor proj({rows, PD_}, proj_pf_.get<float>());
+                proj.strides = {Pmax, 1};
+                math::matmul_rmsnorm(hx, in_ln, eps, w.dn_in.view(), proj);
+                check(qlm_deltanet_prefill(
+                          proj_pf_.get<float>(), Pmax, rows,
+                          conv_state_[dn_i].get<float>() + (size_t)b * 3 * C,
+                          w.conv_wt.get<float>(), w.A_log.get<float>(), w.dt_bias.get<float>(),
+                          w.dn_norm.get<float>(),
+                          dn_state_[dn_i].get<float>() + (size_t)b * nh * d * d, p0,
+                          core_pf_.get<float>(), CORE_, nh, d, stream_),
+                      "deltanet prefill");
+                Tensor core({rows, HD_}, core_pf_.get<float>());
+                core.strides = {CORE_, 1};
+                math::matmul_residual(core, w.dn_out.view(), hx);
+                ++dn_i;
+            } else {
+                Tensor proj({rows, PQ_}, proj_pf_.get<float>());
+                proj.strides = {Pmax, 1};
+                math::matmul_rmsnorm(hx, in_ln, eps, w.at_qkv.view(), proj);
+                const size_t cache_off = (size_t)b * max_seq_ * nkv * hd;
+                check(qlm_gqa_prefill(proj_pf_.get<float>(), Pmax, w.q_norm.get<float>(),
+                                      w.k_norm.get<float>(), rope_cos_.get<float>(),
+                                      rope_sin_.get<float>(), cfg_.rotary_dim(),
+                                      k_cache_[at_i].get<float>() + cache_off,
+                                      v_cache_[at_i].get<float>() + cache_off, max_seq_, p0, rows,
+                                      core_pf_.get<float>(), CORE_, nq, nkv, hd, w.gated ? 1 : 0,
+                                      gqa_pf_work_.get(), stream_),
+                      "gqa prefill");
+                Tensor core({rows, nq * hd}, core_pf_.get<float>());
+                core.strides = {CORE_, 1};
+                math::matmul_residual(core, w.at_o.view(), hx);
+                ++at_i;
+            }
+            Tensor act({rows, F}, act_pf_.get<float>());
+            math::matmul_swiglu_rmsnorm(hx, post_ln, eps, w.gate_up.view(), act);
+            math::matmul_residual(act, w.down.view(), hx);
+        }
+    }
 }
 
 double DecoderModel::steps(int k, bool use_graph) {
@@ -427,14 +539,15 @@ void DecoderModel::tokens(int b, int first, int count, int* out) const {
 }
 
 void DecoderModel::generate(const int* prompts, int B, int n, int n_new, int* out, GenStats* st,
-                            bool use_graph) {
+                            bool use_graph, bool batched_prefill) {
     if (n_new < 0) throw std::runtime_error("generate: negative token count");
     if (n + n_new - 1 > max_seq_)
         throw std::runtime_error("context length exceeded max_seq_len (" + std::to_string(max_seq_) +
                                  ")");
-    start(prompts, B, n);
     const double t0 = now_s();
-    steps(n - 1, use_graph);
+    start(prompts, B, n, batched_prefill);
+    if (!batched_prefill) steps(n - 1, use_graph);
+    check(qlm_stream_sync(stream_), "sync");
     const double t1 = now_s();
     steps(n_new, use_graph);
     const double t2 = now_s();

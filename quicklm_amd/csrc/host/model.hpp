@@ -82,15 +82,20 @@ class DecoderModel {
     // sequences, positions 0..n-2 of the prompt are forwarded as prefill,
     // then n_new steps each forward the newest token and append the argmax.
     // prompts [B, n], out [B, n_new]. use_graph = false launches eagerly.
+    // batched_prefill: positions 0..n-2 go through the prefill kernels (the
+    // reference's forward_batch: every layer over all prompt rows at once);
+    // otherwise each is forwarded by its own decode step.
     void generate(const int* prompts, int B, int n, int n_new, int* out, GenStats* st,
-                  bool use_graph = true);
+                  bool use_graph = true, bool batched_prefill = true);
 
     // Stepwise form of generate() for benchmarking: start() resets the state
-    // and installs B prompts of length n; steps(k) replays k decode steps of
-    // batch B (the first n-1 are prompt forwards) and returns the GPU time in
-    // milliseconds measured with events on the engine stream; tokens() reads
-    // back count tokens of sequence b from position first.
-    void start(const int* prompts, int B, int n);
+    // and installs B prompts of length n (with batched_prefill it also runs
+    // the prefill of positions 0..n-2 and returns its wall time, so the next
+    // step forwards position n-1); steps(k) replays k decode steps of batch B
+    // (without batched_prefill the first n-1 are prompt forwards) and returns
+    // the GPU time in milliseconds measured with events on the engine stream;
+    // tokens() reads back count tokens of sequence b from position first.
+    double start(const int* prompts, int B, int n, bool batched_prefill = false);
     double steps(int k, bool use_graph = true);
     void tokens(int b, int first, int count, int* out) const;
 
@@ -106,6 +111,8 @@ class DecoderModel {
 
    private:
     void enqueue_step(int B);
+    void prefill(int b, int n);
+    void ensure_prefill_buffers(int rows);
     void embed_current(int B);
     void* graph_for(int B);
     void quantize_into(LinearI8& lin, int row_off, const std::string& name);
@@ -132,6 +139,10 @@ class DecoderModel {
     int ld_tokens_ = 0;
     // activations
     DeviceBuffer h_, proj_, core_, act_, logits_, argmax_work_, attn_work_, tail_work_;
+    DeviceBuffer norm_scratch_;  // RMSNorm rows for the matrix-core matmuls (M > 4)
+    // prefill activations for up to pf_rows_ prompt rows per chunk
+    DeviceBuffer hx_pf_, proj_pf_, core_pf_, act_pf_, norm_pf_, gqa_pf_work_;
+    int pf_rows_ = 0;
     DeviceBuffer staging_;
 
     std::map<int, void*> graphs_;

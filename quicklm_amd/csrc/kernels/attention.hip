@@ -71,8 +71,8 @@ __global__ __launch_bounds__(kThreads) void k_attn(
     const float* __restrict__ qsrc, int ldq, int qhs, const float* __restrict__ qn_w,
     const float* __restrict__ kn_w, const float* __restrict__ cos_tab,
     const float* __restrict__ sin_tab, int rot, KV* __restrict__ kc, KV* __restrict__ vc,
-    int max_seq, int n_kv, const int* __restrict__ pos, int ctx, float* __restrict__ work,
-    int nchunks, int n_q, float scale) {
+    int max_seq, int n_kv, const int* __restrict__ pos, int ctx, int pstep, size_t kvb,
+    float* __restrict__ work, int nchunks, int n_q, float scale) {
     static_assert(!PREP || sizeof(KV) == 4, "the fused prologue writes an fp32 cache");
     constexpr int LPP = HD / 8;            // lanes per position in the score phase
     constexpr int PPW = QLM_WAVE / LPP;    // positions per wave per score step
@@ -93,7 +93,9 @@ __global__ __launch_bounds__(kThreads) void k_attn(
 
     const int chunk = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int p = pos ? pos[b] : ctx - 1;
+    // query row b sits at position pos[b], or ctx-1 + pstep*b (pstep = 1:
+    // consecutive prompt rows over one shared cache, kvb = 0)
+    const int p = pos ? pos[b] : ctx - 1 + pstep * b;
     const int L = min(p + 1, max_seq);
     const int nc = (L + CH - 1) / CH;
     if (chunk >= nc || p < 0) return;
@@ -109,7 +111,7 @@ __global__ __launch_bounds__(kThreads) void k_attn(
     // launch writes it; its values are taken from LDS below instead.
     const int sub = lane % LPP, pw = lane / LPP;
     const int c4 = tid % C4, pg = tid / C4;
-    const size_t row0 = ((size_t)b * max_seq + start) * n_kv + g;
+    const size_t row0 = ((size_t)b * kvb + start) * n_kv + g;
     float kr[NS][8];
     float4 vv[NV];
     auto load_kv = [&](int t0) {
@@ -199,7 +201,7 @@ __global__ __launch_bounds__(kThreads) void k_attn(
         }
         __syncthreads();
         if (own_p) {
-            const size_t off = (((size_t)b * max_seq + p) * n_kv + g) * HD;
+            const size_t off = (((size_t)b * kvb + p) * n_kv + g) * HD;
             for (int i = tid; i < HD; i += kThreads) {
                 kc[off + i] = kvp[0][i];
                 vc[off + i] = kvp[1][i];
@@ -342,12 +344,12 @@ __global__ __launch_bounds__(kThreads) void k_attn(
 template <int HD>
 __global__ __launch_bounds__(HD) void k_attn_combine(
     const float* __restrict__ work, int nchunks, int CH, int max_seq, const int* __restrict__ pos,
-    int ctx, const float* __restrict__ gate, int ldg, int ghs, float* __restrict__ out, int ldo,
-    int n_q) {
+    int ctx, int pstep, const float* __restrict__ gate, int ldg, int ghs, float* __restrict__ out,
+    int ldo, int n_q) {
     __shared__ float ms[HD], ls[HD];
     const int h = blockIdx.x, b = blockIdx.y, e = threadIdx.x;
     const float gv = gate ? gate[(size_t)b * ldg + (size_t)h * ghs + HD + e] : 0.0f;
-    const int L = min(pos ? pos[b] + 1 : ctx, max_seq);
+    const int L = min(pos ? pos[b] + 1 : ctx + pstep * b, max_seq);
     const int nc = min(nchunks, (L + CH - 1) / CH);
     const float* base = work + ((size_t)b * n_q + h) * nchunks * (HD + 4);
     float M = -INFINITY, l = 0.0f, o = 0.0f;
@@ -378,12 +380,79 @@ __global__ __launch_bounds__(HD) void k_attn_combine(
     out[(size_t)b * ldo + (size_t)h * HD + e] = r;
 }
 
+// Prefill form of k_attn's PREP phase for T consecutive projection rows
+// (positions p0 + t, one workgroup per row): QK-norm and partial NeoX RoPE of
+// the query heads in place in the row, the same for each k head, and the K/V
+// cache rows p0 + t of one sequence (cache [max_seq, n_kv, HD]). Same
+// arithmetic as the decode prologue (attention.cpp:166-199 per row).
+template <int HD>
+__global__ __launch_bounds__(kThreads) void k_gqa_prep_rows(
+    float* __restrict__ qkv, int ldq, int qhs, const float* __restrict__ qn_w,
+    const float* __restrict__ kn_w, const float* __restrict__ cos_tab,
+    const float* __restrict__ sin_tab, int rot, float* __restrict__ kc, float* __restrict__ vc,
+    int n_q, int n_kv, int p0) {
+    extern __shared__ float rsh[];  // (n_q + n_kv) rows of HD
+    constexpr int EPL = HD / QLM_WAVE;
+    const int t = blockIdx.x, p = p0 + t;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    float* row = qkv + (size_t)t * ldq;
+    const int nr = n_q + n_kv;
+    for (int r = wave; r < nr; r += kNW) {
+        const float* src = r < n_q ? row + (size_t)r * qhs : row + (size_t)n_q * qhs + (size_t)(r - n_q) * HD;
+        const float* w = r < n_q ? qn_w : kn_w;
+        float v[EPL], gn[EPL];
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) {
+            v[j] = src[lane + j * QLM_WAVE];
+            gn[j] = w ? w[lane + j * QLM_WAVE] : 0.0f;
+        }
+        if (w) {
+            float ss = 0.0f;
+#pragma unroll
+            for (int j = 0; j < EPL; ++j) ss = fmaf(v[j], v[j], ss);
+            ss = wave_sum(ss);
+            const float sc = 1.0f / sqrtf(ss / (float)HD + 1e-6f);
+#pragma unroll
+            for (int j = 0; j < EPL; ++j) v[j] = (v[j] * sc) * (1.0f + gn[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) rsh[r * HD + lane + j * QLM_WAVE] = v[j];
+    }
+    __syncthreads();
+    const int half = rot / 2;
+    if (half > 0) {
+        const float* ct = cos_tab + (size_t)p * half;
+        const float* st = sin_tab + (size_t)p * half;
+        for (int i = tid; i < nr * half; i += kThreads) {
+            const int r = i / half, j = i % half;
+            float* v = rsh + r * HD;
+            const float x1 = v[j], x2 = v[j + half];
+            v[j] = nc_mul_sub(x1, ct[j], x2, st[j]);
+            v[j + half] = nc_mul_add2(x2, ct[j], x1, st[j]);
+        }
+    }
+    __syncthreads();
+    for (int i = tid; i < nr * HD; i += kThreads) {
+        const int r = i / HD, e = i % HD;
+        if (r < n_q)
+            row[(size_t)r * qhs + e] = rsh[i];
+        else
+            kc[((size_t)p * n_kv + (r - n_q)) * HD + e] = rsh[i];
+    }
+    for (int i = tid; i < n_kv * HD; i += kThreads) {
+        const int g = i / HD, e = i % HD;
+        vc[((size_t)p * n_kv + g) * HD + e] = row[(size_t)n_q * qhs + (size_t)(n_kv + g) * HD + e];
+    }
+}
+
 // Sub-tile of positions held in registers per workgroup: 64 rows at hd 128,
 // 32 at hd 256 (the K and V rows of a sub-tile are requested together).
 template <int HD>
 constexpr int tile_for() { return HD == 128 ? 64 : 32; }
 constexpr int kNtModel = 1;  // decode step: one sub-tile per chunk (many short chunks)
 constexpr int kNtLong = 4;   // isolated API: contexts up to 32k
+
+constexpr int kPrefillSlice = 256;  // query rows per prefill attention launch
 
 int chunk_len(int hd, int nt) { return (hd == 128 ? 64 : 32) * nt; }
 int nchunks_for(int max_seq, int ch) { return (max_seq + ch - 1) / ch; }
@@ -395,7 +464,8 @@ size_t records_bytes(int B, int n_q, int hd, int max_seq, int nt) {
 template <int HD, int NT, typename KV, bool PREP>
 int launch_g(int G, const float* q, int ldq, int qhs, const float* qn, const float* kn,
              const float* ct, const float* st, int rot, KV* kc, KV* vc, int max_seq, int n_kv,
-             const int* pos, int ctx, float* work, int n_q, int B, hipStream_t s) {
+             const int* pos, int ctx, int pstep, size_t kvb, float* work, int n_q, int B,
+             hipStream_t s) {
     constexpr int T = tile_for<HD>();
     const int nch = nchunks_for(max_seq, T * NT);
     const dim3 grid(nch, n_kv, B);
@@ -403,8 +473,8 @@ int launch_g(int G, const float* q, int ldq, int qhs, const float* qn, const flo
 #define QLM_ATTN_G(GG)                                                                          \
     if (G == GG) {                                                                              \
         hipLaunchKernelGGL((k_attn<HD, GG, T, NT, KV, PREP>), grid, dim3(kThreads), 0, s, q,    \
-                           ldq, qhs, qn, kn, ct, st, rot, kc, vc, max_seq, n_kv, pos, ctx, work, \
-                           nch, n_q, scale);                                                    \
+                           ldq, qhs, qn, kn, ct, st, rot, kc, vc, max_seq, n_kv, pos, ctx,      \
+                           pstep, kvb, work, nch, n_q, scale);                                  \
         return qlm_launch_status();                                                             \
     }
     QLM_ATTN_G(1)
@@ -417,10 +487,10 @@ int launch_g(int G, const float* q, int ldq, int qhs, const float* qn, const flo
 
 template <int HD>
 int launch_combine(const float* work, int nch, int ch, int max_seq, const int* pos, int ctx,
-                   const float* gate, int ldg, int ghs, float* out, int ldo, int n_q, int B,
-                   hipStream_t s) {
+                   int pstep, const float* gate, int ldg, int ghs, float* out, int ldo, int n_q,
+                   int B, hipStream_t s) {
     hipLaunchKernelGGL(k_attn_combine<HD>, dim3(n_q, B), dim3(HD), 0, s, work, nch, ch, max_seq,
-                       pos, ctx, gate, ldg, ghs, out, ldo, n_q);
+                       pos, ctx, pstep, gate, ldg, ghs, out, ldo, n_q);
     return qlm_launch_status();
 }
 
@@ -456,17 +526,17 @@ extern "C" int qlm_gqa_decode(float* qkv, int ldqkv, const float* q_norm, const 
     if (hd == 128) {
         rc = launch_g<128, kNtModel, float, true>(G, qkv, ldqkv, qstride, q_norm, k_norm, cos_tab,
                                                   sin_tab, rot_dim, k_cache, v_cache, max_seq,
-                                                  n_kv, pos, 0, w, n_q, B, st);
+                                                  n_kv, pos, 0, 0, (size_t)max_seq, w, n_q, B, st);
         if (rc != QLM_OK) return rc;
-        return launch_combine<128>(w, nch, ch, max_seq, pos, 0, gate, ldqkv, qstride, out, ldo,
-                                   n_q, B, st);
+        return launch_combine<128>(w, nch, ch, max_seq, pos, 0, 0, gate, ldqkv, qstride, out,
+                                   ldo, n_q, B, st);
     }
     rc = launch_g<256, kNtModel, float, true>(G, qkv, ldqkv, qstride, q_norm, k_norm, cos_tab,
                                               sin_tab, rot_dim, k_cache, v_cache, max_seq, n_kv,
-                                              pos, 0, w, n_q, B, st);
+                                              pos, 0, 0, (size_t)max_seq, w, n_q, B, st);
     if (rc != QLM_OK) return rc;
-    return launch_combine<256>(w, nch, ch, max_seq, pos, 0, gate, ldqkv, qstride, out, ldo, n_q,
-                               B, st);
+    return launch_combine<256>(w, nch, ch, max_seq, pos, 0, 0, gate, ldqkv, qstride, out, ldo,
+                               n_q, B, st);
 }
 
 extern "C" int qlm_attention_decode(const float* q, const void* k_cache, const void* v_cache,
@@ -488,17 +558,78 @@ extern "C" int qlm_attention_decode(const float* q, const void* k_cache, const v
              ? launch_g<HDV, kNtLong, float, false>(                                             \
                    G, q, ldq, hd, nullptr, nullptr, nullptr, nullptr, 0,                         \
                    (float*)const_cast<void*>(k_cache), (float*)const_cast<void*>(v_cache),       \
-                   max_seq, n_kv, nullptr, ctx, w, n_q, B, st)                                   \
+                   max_seq, n_kv, nullptr, ctx, 0, (size_t)max_seq, w, n_q, B, st)               \
              : launch_g<HDV, kNtLong, uint16_t, false>(                                          \
                    G, q, ldq, hd, nullptr, nullptr, nullptr, nullptr, 0,                         \
                    (uint16_t*)const_cast<void*>(k_cache), (uint16_t*)const_cast<void*>(v_cache), \
-                   max_seq, n_kv, nullptr, ctx, w, n_q, B, st);                                  \
+                   max_seq, n_kv, nullptr, ctx, 0, (size_t)max_seq, w, n_q, B, st);              \
     if (rc != QLM_OK) return rc;                                                                 \
-    return launch_combine<HDV>(w, nch, ch, max_seq, nullptr, ctx, nullptr, 0, 0, out, ldq, n_q,  \
-                               B, st);
+    return launch_combine<HDV>(w, nch, ch, max_seq, nullptr, ctx, 0, nullptr, 0, 0, out, ldq,    \
+                               n_q, B, st);
     if (hd == 128) {
         QLM_ISO(128)
     }
     QLM_ISO(256)
 #undef QLM_ISO
+}
+
+extern "C" size_t qlm_gqa_prefill_workspace_bytes(int n_q, int hd, int max_seq) {
+    if (n_q <= 0 || hd <= 0 || max_seq <= 0) return 0;
+    return records_bytes(kPrefillSlice, n_q, hd, max_seq, kNtLong);
+}
+
+extern "C" int qlm_gqa_prefill(float* qkv, int ldqkv, const float* q_norm, const float* k_norm,
+                               const float* cos_tab, const float* sin_tab, int rot_dim,
+                               float* k_cache, float* v_cache, int max_seq, int p0, int T,
+                               float* out, int ldo, int n_q, int n_kv, int hd, int gated,
+                               void* work, void* stream) {
+    if (!qkv || !cos_tab || !sin_tab || !k_cache || !v_cache || !out || !work) return QLM_ERR_ARG;
+    if (T <= 0 || p0 < 0 || n_q <= 0 || n_kv <= 0 || max_seq <= 0) return QLM_ERR_ARG;
+    if (p0 + T > max_seq) return QLM_ERR_SHAPE;
+    if (n_q % n_kv != 0 || (hd != 128 && hd != 256)) return QLM_ERR_SHAPE;
+    if (rot_dim < 0 || rot_dim > hd || rot_dim % 2 != 0) return QLM_ERR_SHAPE;
+    const int G = n_q / n_kv;
+    if (G != 1 && G != 2 && G != 4 && G != 8) return QLM_ERR_SHAPE;
+    const int qstride = gated ? 2 * hd : hd;
+    if (ldqkv < n_q * qstride + 2 * n_kv * hd || ldo < n_q * hd) return QLM_ERR_SHAPE;
+    const size_t lds = (size_t)(n_q + n_kv) * hd * sizeof(float);
+    if (lds > 64 * 1024) return QLM_ERR_SHAPE;
+    hipStream_t st = as_stream(stream);
+    float* w = reinterpret_cast<float*>(work);
+    const int ch = chunk_len(hd, kNtLong);
+    const int nch = nchunks_for(max_seq, ch);
+    if (hd == 128)
+        hipLaunchKernelGGL(k_gqa_prep_rows<128>, dim3(T), dim3(kThreads), lds, st, qkv, ldqkv,
+                           qstride, q_norm, k_norm, cos_tab, sin_tab, rot_dim, k_cache, v_cache,
+                           n_q, n_kv, p0);
+    else
+        hipLaunchKernelGGL(k_gqa_prep_rows<256>, dim3(T), dim3(kThreads), lds, st, qkv, ldqkv,
+                           qstride, q_norm, k_norm, cos_tab, sin_tab, rot_dim, k_cache, v_cache,
+                           n_q, n_kv, p0);
+    int rc = qlm_launch_status();
+    if (rc != QLM_OK) return rc;
+    for (int s0 = 0; s0 < T; s0 += kPrefillSlice) {
+        const int rows = T - s0 < kPrefillSlice ? T - s0 : kPrefillSlice;
+        float* q = qkv + (size_t)s0 * ldqkv;
+        const int ctx = p0 + s0 + 1;  // row s0 sits at position p0 + s0
+        if (hd == 128) {
+            rc = launch_g<128, kNtLong, float, false>(G, q, ldqkv, qstride, nullptr, nullptr,
+                                                      nullptr, nullptr, 0, k_cache, v_cache,
+                                                      max_seq, n_kv, nullptr, ctx, 1, 0, w, n_q,
+                                                      rows, st);
+            if (rc != QLM_OK) return rc;
+            rc = launch_combine<128>(w, nch, ch, max_seq, nullptr, ctx, 1, gated ? q : nullptr,
+                                     ldqkv, qstride, out + (size_t)s0 * ldo, ldo, n_q, rows, st);
+        } else {
+            rc = launch_g<256, kNtLong, float, false>(G, q, ldqkv, qstride, nullptr, nullptr,
+                                                      nullptr, nullptr, 0, k_cache, v_cache,
+                                                      max_seq, n_kv, nullptr, ctx, 1, 0, w, n_q,
+                                                      rows, st);
+            if (rc != QLM_OK) return rc;
+            rc = launch_combine<256>(w, nch, ch, max_seq, nullptr, ctx, 1, gated ? q : nullptr,
+                                     ldqkv, qstride, out + (size_t)s0 * ldo, ldo, n_q, rows, st);
+        }
+        if (rc != QLM_OK) return rc;
+    }
+    return QLM_OK;
 }

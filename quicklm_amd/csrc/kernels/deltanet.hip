@@ -46,7 +46,8 @@ __device__ __forceinline__ void dn_load_state(const float* __restrict__ S,
 }
 
 // Recurrence core. q,k,v in LDS (q already L2-normalised, k too), the state
-// slice in s. Leaves the un-normalised, 1/sqrt(d)-scaled output in sh.vec.
+// slice in s (updated in place; also stored to S unless S is null). Leaves
+// the un-normalised, 1/sqrt(d)-scaled output in sh.vec.
 __device__ __forceinline__ void dn_recurrence(DnShared& sh, float* __restrict__ S,
                                               float4 (&s)[kRowsPer], float dec, float beta) {
     const int tid = threadIdx.x;
@@ -94,7 +95,7 @@ __device__ __forceinline__ void dn_recurrence(DnShared& sh, float* __restrict__ 
         o.y = fmaf(qi, s[r].y, o.y);
         o.z = fmaf(qi, s[r].z, o.z);
         o.w = fmaf(qi, s[r].w, o.w);
-        S4[i * (kD / 4) + jg] = s[r];
+        if (S4) S4[i * (kD / 4) + jg] = s[r];
     }
     __syncthreads();  // everyone has consumed sh.vec (delta)
     reinterpret_cast<float4*>(sh.red[ig])[jg] = o;
@@ -232,6 +233,123 @@ __global__ __launch_bounds__(kThreads) void k_deltanet_decode(
     }
 }
 
+// Prefill of one sequence over T consecutive rows of proj (positions
+// p0 .. p0+T-1), one workgroup per head: the reference processes the rows of
+// a prompt one after another through the same recurrence
+// (Qwen3_5GatedDeltaNet::forward_chunk, attention.cpp:600-758), and so does
+// this kernel, with the decode step's arithmetic (bit-identical to T calls of
+// k_deltanet_decode). The head's state slice and its conv ring live in
+// registers for all T steps and are written back once; each row's operands
+// are requested while the previous row is being processed.
+__global__ __launch_bounds__(kThreads) void k_deltanet_prefill(
+    const float* __restrict__ proj, int ldp, int T, float* __restrict__ conv_state,
+    const float* __restrict__ wt, const float* __restrict__ A_log,
+    const float* __restrict__ dt_bias, const float* __restrict__ norm_w,
+    float* __restrict__ state, int p0, float* __restrict__ out, int ldo, int H) {
+    __shared__ DnShared sh;
+    const int h = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int HD = H * kD;
+    const int C = 3 * HD;
+    float* Sh = state + (size_t)h * kD * kD;
+
+    float4 s[kRowsPer];
+    dn_load_state(Sh, s);
+    const bool conv_t = tid < 3 * kD;
+    const int sec = tid / kD, t = tid % kD;
+    const int ch = sec * HD + h * kD + t;
+    // ring in chronological order: r0 = x[p-3], r1 = x[p-2], r2 = x[p-1]
+    float w4[4] = {0.f, 0.f, 0.f, 0.f}, r0 = 0.f, r1 = 0.f, r2 = 0.f;
+    if (conv_t) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) w4[j] = wt[(size_t)j * C + ch];
+        r0 = conv_state[(size_t)(p0 % 3) * C + ch];
+        r1 = conv_state[(size_t)((p0 + 1) % 3) * C + ch];
+        r2 = conv_state[(size_t)((p0 + 2) % 3) * C + ch];
+    }
+    const bool gate_t = wave == 2 && lane == 0;
+    const float gdt = gate_t ? dt_bias[h] : 0.0f, galog = gate_t ? A_log[h] : 0.0f;
+    const float nwj = tid < kD ? norm_w[tid] : 0.0f;
+
+    float xin = 0.f, ga = 0.f, gb = 0.f, zj = 0.f;
+    auto fetch = [&](int row) {
+        const float* pr = proj + (size_t)row * ldp;
+        if (conv_t) xin = pr[ch];
+        if (gate_t) {
+            ga = pr[4 * HD + H + h];
+            gb = pr[4 * HD + h];
+        }
+        if (tid < kD) zj = pr[3 * HD + h * kD + tid];
+    };
+    fetch(0);
+    for (int r = 0; r < T; ++r) {
+        const float xc = xin, gac = ga, gbc = gb, zc = zj;
+        if (r + 1 < T) fetch(r + 1);
+
+        if (conv_t) {
+            float acc = 0.0f;
+            acc = nc_add_mul(acc, r0, w4[0]);
+            acc = nc_add_mul(acc, r1, w4[1]);
+            acc = nc_add_mul(acc, r2, w4[2]);
+            acc = nc_add_mul(acc, xc, w4[3]);
+            r0 = r1;
+            r1 = r2;
+            r2 = xc;
+            const float y = silu_f(acc);
+            if (sec == 0) sh.q[t] = y;
+            else if (sec == 1) sh.k[t] = y;
+            else sh.v[t] = y;
+        }
+        __syncthreads();
+
+        if (wave < 2) {
+            float* vv = wave == 0 ? sh.q : sh.k;
+            const float a0 = vv[lane], a1 = vv[lane + 64];
+            float ss = fmaf(a0, a0, a1 * a1);
+            ss = wave_sum(ss);
+            const float nrm = sqrtf(ss + 1e-6f);
+            vv[lane] = a0 / nrm;
+            vv[lane + 64] = a1 / nrm;
+        } else if (gate_t) {
+            const float dt = gac + gdt;
+            const float sp = dt > 20.0f ? dt : log1pf(expf(dt));
+            const float alpha = -expf(galog) * sp;
+            sh.scal[0] = expf(alpha);
+            sh.scal[1] = 1.0f / (1.0f + expf(-gbc));
+        }
+        __syncthreads();
+
+        dn_recurrence(sh, nullptr, s, sh.scal[0], sh.scal[1]);
+
+        float o = 0.0f;
+        if (wave < 2) {
+            o = sh.vec[tid];
+            const float ss = wave_sum(o * o);
+            if (lane == 0) sh.scal[2 + wave] = ss;
+        }
+        __syncthreads();
+        if (wave < 2) {
+            const float tot = sh.scal[2] + sh.scal[3];
+            const float sn = 1.0f / sqrtf(tot / (float)kD + 1e-6f);
+            const float rr = (o * sn) * nwj;
+            out[(size_t)r * ldo + h * kD + tid] = rr * silu_f(zc);
+        }
+    }
+
+    // state and ring as the decode step expects them at position p0 + T
+    float4* S4 = reinterpret_cast<float4*>(Sh);
+    const int jg = tid & 31, ig = tid >> 5;
+#pragma unroll
+    for (int rr = 0; rr < kRowsPer; ++rr) S4[(ig * kRowsPer + rr) * (kD / 4) + jg] = s[rr];
+    if (conv_t) {
+        const int p = p0 + T;
+        conv_state[(size_t)(p % 3) * C + ch] = r0;
+        conv_state[(size_t)((p + 1) % 3) * C + ch] = r1;
+        conv_state[(size_t)((p + 2) % 3) * C + ch] = r2;
+    }
+}
+
 }  // namespace
 
 extern "C" int qlm_gated_delta_step(const float* q, const float* k, const float* v,
@@ -256,5 +374,20 @@ extern "C" int qlm_deltanet_decode(const float* proj, int ldp, float* conv_state
     if (ldp < 4 * H * d + 2 * H || ldo < H * d) return QLM_ERR_SHAPE;
     hipLaunchKernelGGL(k_deltanet_decode, dim3(H, B), dim3(kThreads), 0, as_stream(stream), proj,
                        ldp, conv_state, conv_w_t, A_log, dt_bias, norm_w, state, pos, out, ldo, H);
+    return qlm_launch_status();
+}
+
+extern "C" int qlm_deltanet_prefill(const float* proj, int ldp, int T, float* conv_state,
+                                    const float* conv_w_t, const float* A_log,
+                                    const float* dt_bias, const float* norm_w, float* state,
+                                    int p0, float* out, int ldo, int H, int d, void* stream) {
+    if (!proj || !conv_state || !conv_w_t || !A_log || !dt_bias || !norm_w || !state || !out ||
+        T <= 0 || H <= 0 || p0 < 0)
+        return QLM_ERR_ARG;
+    if (d != kD) return QLM_ERR_SHAPE;
+    if (ldp < 4 * H * d + 2 * H || ldo < H * d) return QLM_ERR_SHAPE;
+    hipLaunchKernelGGL(k_deltanet_prefill, dim3(H), dim3(kThreads), 0, as_stream(stream), proj,
+                       ldp, T, conv_state, conv_w_t, A_log, dt_bias, norm_w, state, p0, out, ldo,
+                       H);
     return qlm_launch_status();
 }

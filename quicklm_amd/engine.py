@@ -30,9 +30,9 @@ def lib() -> C.CDLL:
         L.qlm_engine_reset.argtypes = [_vp]
         L.qlm_engine_forward.argtypes = [_vp, _i, _i, _vp]
         L.qlm_engine_generate.argtypes = [_vp, _vp, _i, _i, _i, _vp, C.POINTER(C.c_double),
-                                          C.POINTER(C.c_double), _i]
+                                          C.POINTER(C.c_double), _i, _i]
         L.qlm_engine_last_logits.argtypes = [_vp, _i, _vp]
-        L.qlm_engine_start.argtypes = [_vp, _vp, _i, _i]
+        L.qlm_engine_start.argtypes = [_vp, _vp, _i, _i, _i, C.POINTER(C.c_double)]
         L.qlm_engine_steps.argtypes = [_vp, _i, _i, C.POINTER(C.c_double)]
         L.qlm_engine_tokens.argtypes = [_vp, _i, _i, _i, _vp]
         L.qlm_engine_kernels_per_step.argtypes = [_vp]
@@ -73,20 +73,28 @@ class Engine:
         _check(lib().qlm_engine_forward(self.h, token, pos, lg.ctypes.data))
         return lg
 
-    def generate(self, prompts: np.ndarray, n_new: int, use_graph: bool = True):
-        """prompts [B, n] int32 -> (tokens [B, n_new], prefill_s, decode_s)."""
+    def generate(self, prompts: np.ndarray, n_new: int, use_graph: bool = True,
+                 batched_prefill: bool = True):
+        """prompts [B, n] int32 -> (tokens [B, n_new], prefill_s, decode_s).
+        batched_prefill False forwards each prompt position by a decode step."""
         p = np.ascontiguousarray(np.atleast_2d(prompts), np.int32)
         B, n = p.shape
         out = np.empty((B, n_new), np.int32)
         pre, dec = C.c_double(), C.c_double()
         _check(lib().qlm_engine_generate(self.h, p.ctypes.data, B, n, n_new, out.ctypes.data,
-                                         C.byref(pre), C.byref(dec), 1 if use_graph else 0))
+                                         C.byref(pre), C.byref(dec), 1 if use_graph else 0,
+                                         1 if batched_prefill else 0))
         return out, pre.value, dec.value
 
-    def start(self, prompts: np.ndarray) -> None:
+    def start(self, prompts: np.ndarray, batched_prefill: bool = False) -> float:
+        """Install prompts; with batched_prefill also prefill positions 0..n-2
+        and return its wall time in seconds (the next step forwards n-1)."""
         p = np.ascontiguousarray(np.atleast_2d(prompts), np.int32)
         self._prompts = p
-        _check(lib().qlm_engine_start(self.h, p.ctypes.data, p.shape[0], p.shape[1]))
+        pre = C.c_double()
+        _check(lib().qlm_engine_start(self.h, p.ctypes.data, p.shape[0], p.shape[1],
+                                      1 if batched_prefill else 0, C.byref(pre)))
+        return pre.value
 
     def steps(self, k: int, use_graph: bool = True) -> float:
         """Run k decode steps; returns their GPU time in ms."""

@@ -142,6 +142,63 @@ def test_gemv_exact_integers(hip, orc, rng):
     assert np.array_equal(dy.to_numpy((3, N), np.float32), ref)
 
 
+# ------------------------------------------------------------ A4 matrix cores
+MM_CASES = [  # (M, N, K): batched decode (M <= 64, K % 128 == 0) and prefill tiles
+    (2, 300, 1024), (16, 1000, 2560), (16, 2560, 9728), (33, 517, 1024), (64, 160, 2048),
+    (100, 300, 1056), (300, 1000, 1024), (127, 3584, 1024),
+]
+
+
+@pytest.mark.parametrize("M,N,K", MM_CASES)
+@pytest.mark.parametrize("group", [32, "K"])
+def test_matmul_mfma_parity(hip, orc, rng, M, N, K, group):
+    """bf16 hi/lo split activations, exact int8 weights, fp32 group scaling:
+    within 1e-5 normwise of the fp32 oracle (ragged M and N tiles)."""
+    g = K if group == "K" else 32
+    q, s = _weights(orc, rng, N, K, g)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    ref = orc.matmul_i8(x, q, s, g)
+    ldy = N + 8
+    dy = hip.DeviceBuffer(M * ldy * 4)
+    say("matmul", M, N, K, g)
+    hip.call("qlm_matmul_i8", dev(hip, x), K, dev(hip, q), dev(hip, s), g, dy, ldy, M, N, K, 0,
+             None)
+    y = dy.to_numpy((M, ldy), np.float32)[:, :N]
+    assert rel_err(y, ref) < 1e-5
+
+
+@pytest.mark.parametrize("M,K", [(16, 2560), (200, 1024)])
+@pytest.mark.parametrize("epi", ["resid", "swiglu"])
+def test_matmul_mfma_epilogues(hip, orc, rng, M, K, epi):
+    N = 700
+    rows_w = 2 * N if epi == "swiglu" else N
+    q, s = _weights(orc, rng, rows_w, K, 32)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    y0 = rng.standard_normal((M, N)).astype(np.float32)
+    lg = orc.matmul_i8(x, q, s, 32)
+    ref = y0 + lg if epi == "resid" else orc.silu_mul(lg[:, :N].copy(), lg[:, N:].copy())
+    dy = dev(hip, y0)
+    say("matmul", epi, M, K)
+    hip.call("qlm_matmul_i8", dev(hip, x), K, dev(hip, q), dev(hip, s), 32, dy, N, M, N, K,
+             1 if epi == "resid" else 2, None)
+    assert rel_err(dy.to_numpy((M, N), np.float32), ref) < 1e-5
+
+
+@pytest.mark.parametrize("M", [16, 130])
+def test_matmul_mfma_exact_integers(hip, orc, rng, M):
+    """Small-integer activations are exact in bf16 (lo = 0) and every
+    product and sum is exact, so the matrix-core path is bit-identical."""
+    N, K = 500, 2048
+    q = rng.integers(-127, 128, (N, K), dtype=np.int8)
+    s = (2.0 ** rng.integers(-8, -2, (N, K // 32))).astype(np.float32)
+    x = rng.integers(-16, 17, (M, K)).astype(np.float32)
+    ref = orc.matmul_i8(x, q, s, 32)
+    dy = hip.DeviceBuffer(M * N * 4)
+    hip.call("qlm_matmul_i8", dev(hip, x), K, dev(hip, q), dev(hip, s), 32, dy, N, M, N, K, 0,
+             None)
+    assert np.array_equal(dy.to_numpy((M, N), np.float32), ref)
+
+
 def test_gemv_batched_m(hip, orc, rng):
     """M > 4 runs in slices of four activation rows; strided output rows."""
     N, K, M = 300, 1024, 11
@@ -385,6 +442,81 @@ def test_deltanet_decode_fused(hip, orc, rng):
         assert rel_err(do.to_numpy((B, HD), np.float32), ref) < 1e-4
         assert np.array_equal(dconv.to_numpy(conv.shape, np.float32), np.stack(conv_ref))
         assert rel_err(dS.to_numpy(S.shape, np.float32), np.stack(S_ref)) < 1e-5
+
+
+@pytest.mark.parametrize("p0,T", [(0, 64), (5, 130)])
+def test_deltanet_prefill(hip, orc, rng, p0, T):
+    """Prefill over T rows == the oracle's row-by-row recurrence, and
+    bit-identical to T single decode steps (outputs, conv ring, state)."""
+    H, d = 16, 128
+    HD = H * d
+    ldp = 4 * HD + 2 * H
+    wt = (rng.standard_normal((4, 3 * HD)) * 0.3).astype(np.float32)
+    A_log = np.log(rng.uniform(1, 16, H)).astype(np.float32)
+    dtb = (rng.standard_normal(H) * 0.5 - 4).astype(np.float32)
+    nw = (1 + rng.standard_normal(d) * 0.02).astype(np.float32)
+    conv = (rng.standard_normal((3, 3 * HD)) * (0.5 if p0 else 0.0)).astype(np.float32)
+    S = (rng.standard_normal((H, d, d)) * (0.01 if p0 else 0.0)).astype(np.float32)
+    proj = (rng.standard_normal((T, ldp)) * 0.6).astype(np.float32)
+    conv_ref, S_ref = conv.copy(), S.copy()
+    ref = np.stack([orc.deltanet_core(proj[t], conv_ref, (p0 + t) % 3, wt, A_log, dtb, nw, S_ref,
+                                      H, d) for t in range(T)])
+    dwt, dA, ddt, dnw = dev(hip, wt), dev(hip, A_log), dev(hip, dtb), dev(hip, nw)
+    dconv, dS, dproj = dev(hip, conv), dev(hip, S), dev(hip, proj)
+    do = hip.DeviceBuffer(T * HD * 4)
+    say("deltanet_prefill", p0, T)
+    hip.call("qlm_deltanet_prefill", dproj, ldp, T, dconv, dwt, dA, ddt, dnw, dS, p0, do, HD, H, d,
+             None)
+    out = do.to_numpy((T, HD), np.float32)
+    assert rel_err(out, ref) < 1e-4
+    assert np.array_equal(dconv.to_numpy(conv.shape, np.float32), conv_ref)
+    assert rel_err(dS.to_numpy(S.shape, np.float32), S_ref) < 1e-4
+    # the same rows through the decode kernel, one step at a time
+    dconv2, dS2 = dev(hip, conv), dev(hip, S)
+    do2 = hip.DeviceBuffer(HD * 4)
+    steps = []
+    for t in range(T):
+        hip.call("qlm_deltanet_decode", dev(hip, proj[t:t + 1]), ldp, dconv2, dwt, dA, ddt, dnw,
+                 dS2, dev(hip, np.array([p0 + t], np.int32)), do2, HD, 1, H, d, None)
+        steps.append(do2.to_numpy(HD, np.float32))
+    assert np.array_equal(out, np.stack(steps))
+    assert np.array_equal(dS.to_numpy(S.shape, np.float32), dS2.to_numpy(S.shape, np.float32))
+    assert np.array_equal(dconv.to_numpy(conv.shape, np.float32),
+                          dconv2.to_numpy(conv.shape, np.float32))
+
+
+@pytest.mark.parametrize("n_q,n_kv,hd,rot,gated,p0,T", [(16, 4, 128, 32, 1, 0, 300),
+                                                        (16, 4, 128, 32, 1, 37, 90),
+                                                        (16, 2, 256, 64, 0, 10, 40)])
+def test_gqa_prefill(hip, orc, rng, n_q, n_kv, hd, rot, gated, p0, T):
+    """T prompt rows at positions p0.. (two 256-row slices in the first case)
+    == the oracle row by row: outputs and the cache rows they write."""
+    max_seq, theta = 600, 1e6
+    qs = (2 if gated else 1) * hd
+    ld = n_q * qs + 2 * n_kv * hd
+    qn = (rng.standard_normal(hd) * 0.02).astype(np.float32)
+    kn = (rng.standard_normal(hd) * 0.02).astype(np.float32)
+    cos_t, sin_t = orc.rope_table(theta, rot, max_seq)
+    kc = np.zeros((max_seq, n_kv, hd), np.float32)
+    vc = np.zeros_like(kc)
+    kc[:p0] = rng.standard_normal((p0, n_kv, hd))
+    vc[:p0] = rng.standard_normal((p0, n_kv, hd))
+    dkc, dvc = dev(hip, kc), dev(hip, vc)
+    qkv = rng.standard_normal((T, ld)).astype(np.float32)
+    kref, vref = kc.copy(), vc.copy()
+    ref = np.stack([orc.gqa_core(qkv[t].copy(), qn, kn, theta, rot, kref, vref, p0 + t, n_q, n_kv,
+                                 hd, gated) for t in range(T)])
+    work = hip.DeviceBuffer(hip.lib().qlm_gqa_prefill_workspace_bytes(n_q, hd, max_seq))
+    do = hip.DeviceBuffer(T * n_q * hd * 4)
+    say("gqa_prefill", n_q, n_kv, hd, p0, T)
+    hip.call("qlm_gqa_prefill", dev(hip, qkv), ld, dev(hip, qn), dev(hip, kn), dev(hip, cos_t),
+             dev(hip, sin_t), rot, dkc, dvc, max_seq, p0, T, do, n_q * hd, n_q, n_kv, hd, gated,
+             work, None)
+    assert rel_err(do.to_numpy((T, n_q * hd), np.float32), ref) < 1e-5
+    got_k = dkc.to_numpy(kc.shape, np.float32)
+    assert rel_err(got_k[p0:p0 + T], kref[p0:p0 + T]) < 1e-6
+    assert np.array_equal(got_k[:p0], kc[:p0])
+    assert np.array_equal(dvc.to_numpy(vc.shape, np.float32)[:p0 + T], vref[:p0 + T])
 
 
 # ---------------------------------------------------------------- A8/A9 GQA

@@ -77,8 +77,12 @@ def test_teacher_forced_logits(engine, golden):
     assert worst < 1e-3
 
 
-def test_tiny_greedy_matches_reference(engine, golden):
-    out, pre, dec = engine.generate(golden["prompt"][None, :], 64)
+@pytest.mark.parametrize("batched_prefill", [True, False])
+def test_tiny_greedy_matches_reference(engine, golden, batched_prefill):
+    """The reference's 64-token greedy stream, with the prompt prefilled by
+    the batched prefill kernels or forwarded one decode step per token."""
+    out, pre, dec = engine.generate(golden["prompt"][None, :], 64,
+                                    batched_prefill=batched_prefill)
     toks = golden["tokens"]
     got = out[0]
     diff = np.nonzero(got != toks)[0]
@@ -107,6 +111,22 @@ def test_batch_rows_equal_single(engine, golden):
     s1, _, _ = engine.generate(p1[None, :], 12)
     both, _, _ = engine.generate(np.stack([p0, p1]), 12)
     assert np.array_equal(both[0], s0[0]) and np.array_equal(both[1], s1[0])
+
+
+@pytest.mark.parametrize("n", [128, 1300])
+def test_batched_prefill_equals_stepwise(engine, golden, n):
+    """Batched prefill (matrix-core projections, prefill DeltaNet and
+    attention kernels; 1300 rows span two 1024-row chunks) leaves the model
+    where n-1 decode steps leave it: same tokens, logits within 1e-4."""
+    rng = np.random.default_rng(11)
+    p = golden["prompt"][:n] if n <= 128 else rng.integers(0, 151936, n).astype(np.int32)
+    a, pre_a, _ = engine.generate(p[None, :], 8, batched_prefill=True)
+    la = engine.last_logits(0)
+    b, pre_b, _ = engine.generate(p[None, :], 8, batched_prefill=False)
+    lb = engine.last_logits(0)
+    say(f"n={n}: batched prefill {pre_a:.3f}s, stepwise {pre_b:.3f}s")
+    assert np.array_equal(a, b)
+    assert float(np.abs(la - lb).max() / np.abs(lb).max()) < 1e-4
 
 
 def test_context_overflow_rejected(engine):
