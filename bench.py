@@ -6,12 +6,17 @@ Workload (one "step" = one greedy decode step of every sequence in the batch):
   4B-class hybrid LM, 36 layers (27 Gated DeltaNet + 9 GQA), hidden 2560,
   FFN 9728, vocab 151936, seeded random-init weights quantised to int8 at load
   (Q8_0 group-32 scales, the reference's format), 2048-token uniform random
-  prompts, greedy decode; the whole step is one replayed hipGraph.
+  prompts (batched prefill of positions 0..2046, untimed), greedy decode; the
+  whole step is one replayed hipGraph.
   `value` = batch-1 decode tokens/s over exactly --steps timed steps after
-  the 2047 prompt forwards and --warmup untimed steps; batch 16 is reported
-  beside it. The GEMV section times the config-1 matrices in isolation.
+  --warmup untimed steps; batch 16 is reported beside it. The GEMV section
+  times the config-1 matrices in isolation (M <= 4: GEMV, M > 4: matrix cores).
+  `roofline` is the dominant decode kernel (the fused RMSNorm + gate/up GEMV +
+  SwiGLU, 36 launches per step) timed with HIP events on its own stream.
+  `cpu_baseline` is the reference's own sources built with its release flags
+  on this host's cores, on a bounded sample of the same 4B workload.
 
-Usage: python bench.py [--gpus 1] [--steps 256] [--warmup 8]
+Usage: python bench.py [--gpus 1] [--steps 256] [--warmup 8] [--kernel-only]
 """
 
 from __future__ import annotations
@@ -29,6 +34,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+BF16_PEAK_FLOPS = 2.5e15  # dense bf16 matrix-core peak of MI355X
 METRIC = "decode tokens/sec at batch 1 and 16 (4B int8); int8 GEMV achieved HBM GB/s"
 
 
@@ -61,25 +67,100 @@ def bench_gemv(hip, shapes, Ms, group_kind, iters=100, pool_bytes=2 << 30):
             x = hip.DeviceBuffer.from_numpy(rng.standard_normal((M, K)).astype(np.float32))
             y = hip.DeviceBuffer(M * N * 4)
             n_it = iters if M <= 4 else max(10, iters // 4)
+            # M <= 4: the GEMV; M > 4: the matrix-core matmul (one weight pass)
+            fn = "qlm_gemv_i8" if M <= 4 else "qlm_matmul_i8"
+
+            def launch(i):
+                if M <= 4:
+                    hip.call(fn, x, K, dq[i % ncopy], ds[i % ncopy], group, y, N, M, N, K, st.ptr)
+                else:
+                    hip.call(fn, x, K, dq[i % ncopy], ds[i % ncopy], group, y, N, M, N, K, 0,
+                             st.ptr)
+
             for i in range(ncopy):
-                hip.call("qlm_gemv_i8", x, K, dq[i], ds[i], group, y, N, M, N, K, st.ptr)
+                launch(i)
             e0, e1 = hip.Event(), hip.Event()
             e0.record(st.ptr)
             for i in range(n_it):
-                hip.call("qlm_gemv_i8", x, K, dq[i % ncopy], ds[i % ncopy], group, y, N, M, N, K,
-                         st.ptr)
+                launch(i)
             e1.record(st.ptr)
             us = e0.elapsed_ms(e1) * 1000.0 / n_it
             b = gemv_bytes(N, K, M, group)
-            out.append({"N": N, "K": K, "M": M, "group": group, "us": round(us, 2),
-                        "GBps": round(b / us / 1e3, 1), "bytes": b,
-                        "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4)})
+            r = {"N": N, "K": K, "M": M, "group": group, "kernel": fn, "us": round(us, 2),
+                 "GBps": round(b / us / 1e3, 1), "bytes": b,
+                 "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
+            if M > 4:
+                # algorithmic flops over the dense bf16 matrix-core peak
+                r["mfma_util"] = round(2.0 * M * N * K / (us * 1e-6) / BF16_PEAK_FLOPS, 5)
+            out.append(r)
             log(f"gemv {N}x{K} M={M} G={group}: {us:.1f} us {b / us / 1e3:.0f} GB/s")
             x.free()
             y.free()
         for b_ in dq + ds:
             b_.free()
     return out
+
+
+# The dominant kernel of the batch-1 decode step (about a third of the step):
+# the fused RMSNorm + gate/up projection + SwiGLU GEMV of every layer, 4B
+# shape (F = 9728 outputs from 2F = 19456 int8 rows of K = 2560, group-32
+# scales).
+DOM_F, DOM_K = 9728, 2560
+DOM_NAME = "k_gemv_xs<2, 2, false, 1, 2> (RMSNorm + gate/up GEMV + SwiGLU, 19456x2560 int8 G=32)"
+PMC_FILE = os.path.join(ROOT, "profiles", "gemv_gate_up_4b_pmc.json")
+
+
+def dominant_bytes():
+    """Algorithmic HBM bytes of one launch: int8 weights, group scales, x and
+    the norm gain read once, the F outputs written once."""
+    rows = 2 * DOM_F
+    return rows * DOM_K + 4 * rows * (DOM_K // 32) + 4 * DOM_K + 4 * DOM_K + 4 * DOM_F
+
+
+def measure_dominant(hip, launches=400, pool_bytes=2 << 30):
+    """Average launch duration of the dominant kernel, HIP events recorded on
+    the stream it is launched on, weights cycled over > 2 GiB of copies so
+    every launch streams them from HBM (not the 256 MB last-level cache)."""
+    rng = np.random.default_rng(1)
+    st = hip.Stream()
+    rows, nb = 2 * DOM_F, DOM_K // 32
+    wb = rows * DOM_K + 4 * rows * nb
+    ncopy = int(max(2, min(64, pool_bytes // wb)))
+    q = rng.integers(-127, 128, (rows, DOM_K), dtype=np.int8)
+    s = rng.uniform(0.001, 0.01, (rows, nb)).astype(np.float32)
+    dq = [hip.DeviceBuffer.from_numpy(q) for _ in range(ncopy)]
+    ds = [hip.DeviceBuffer.from_numpy(s) for _ in range(ncopy)]
+    x = hip.DeviceBuffer.from_numpy(rng.standard_normal(DOM_K).astype(np.float32))
+    nw = hip.DeviceBuffer.from_numpy((rng.standard_normal(DOM_K) * 0.02).astype(np.float32))
+    y = hip.DeviceBuffer(DOM_F * 4)
+
+    def launch(i):
+        hip.call("qlm_gemv_i8_swiglu_rmsnorm", x, DOM_K, nw, 1e-6, dq[i % ncopy], ds[i % ncopy],
+                 32, y, DOM_F, 1, DOM_F, DOM_K, st.ptr)
+
+    for i in range(ncopy):
+        launch(i)
+    e0, e1 = hip.Event(), hip.Event()
+    e0.record(st.ptr)
+    for i in range(launches):
+        launch(i)
+    e1.record(st.ptr)
+    us = e0.elapsed_ms(e1) * 1000.0 / launches
+    for b_ in dq + ds + [x, nw, y]:
+        b_.free()
+    return us
+
+
+def copy_calibration(hip, nbytes=256 << 20, reps=4):
+    """A plain device-to-device copy of known size: the reference point for
+    the FETCH_SIZE / WRITE_SIZE counters (profiled with --kernel-only)."""
+    a, b = hip.DeviceBuffer(nbytes), hip.DeviceBuffer(nbytes)
+    a.zero()
+    for _ in range(reps):
+        hip.check(hip.lib().qlm_memcpy_d2d(b.ptr, a.ptr, nbytes, None))
+    hip.sync()
+    a.free()
+    b.free()
 
 
 def run_decode(eng, prompts, warmup, steps, graph=True):
@@ -128,8 +209,11 @@ def main():
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--prompt-len", type=int, default=2048)
     ap.add_argument("--batch", type=int, default=16, help="second batch size (0 to skip)")
-    ap.add_argument("--cpu-prompt", type=int, default=32)
-    ap.add_argument("--cpu-decode", type=int, default=16)
+    ap.add_argument("--cpu-prompt", type=int, default=128)
+    ap.add_argument("--cpu-decode", type=int, default=256)
+    ap.add_argument("--kernel-only", action="store_true",
+                    help="only the dominant-kernel timing and the copy of known size (for "
+                         "rocprofv3 --pmc passes)")
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-gemv", action="store_true")
     ap.add_argument("--model-dir", default=None)
@@ -150,6 +234,14 @@ def main():
         sys.exit(1)
     hip.check(hip.lib().qlm_set_device(0))
     log("device", hip.device_name())
+
+    if args.kernel_only:
+        us = measure_dominant(hip)
+        copy_calibration(hip)
+        b = dominant_bytes()
+        print(json.dumps({"kernel": DOM_NAME, "us_per_launch": round(us, 3), "bytes": b,
+                          "GBps": round(b / us / 1e3, 1)}), flush=True)
+        return
 
     result = {"metric": METRIC}
     gemv = []
@@ -203,9 +295,11 @@ def main():
 
             shutil.rmtree(mdir, ignore_errors=True)
 
+    dom_us = measure_dominant(hip)
+    dom_b = dominant_bytes()
+    log(f"dominant kernel: {dom_us:.2f} us/launch, {dom_b / dom_us / 1e3:.0f} GB/s")
     wbytes = eng.weight_bytes
     step_s = r1["ms_per_step"] / 1000.0
-    lm = [g for g in gemv if g["N"] == 151936 and g["M"] == 1 and g["group"] == 2560]
     result.update({
         "value": round(r1["tok_s"], 2),
         "unit": "tokens/s",
@@ -236,12 +330,18 @@ def main():
                             "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / wbytes, 1)},
         "gemv": gemv,
     })
-    if lm:
-        g = lm[0]
-        result["roofline"] = {"kernel": "k_gemv_i8 (M=1, 151936x2560, per-row scales)",
-                              "bound": "hbm", "achieved": g["GBps"], "peak": HBM_PEAK_GBS,
-                              "unit": "GB/s", "frac": g["frac_hbm"], "traffic": None,
-                              "bytes_per_launch": g["bytes"], "us_per_launch": g["us"]}
+    traffic, traffic_src = None, None
+    if os.path.exists(PMC_FILE):
+        with open(PMC_FILE) as f:
+            pmc = json.load(f)
+        if pmc.get("bytes") == dom_b:
+            traffic, traffic_src = pmc.get("traffic_bytes"), os.path.relpath(PMC_FILE, ROOT)
+    achieved = dom_b / dom_us / 1e3
+    result["roofline"] = {"kernel": DOM_NAME, "bound": "hbm", "achieved": round(achieved, 1),
+                          "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                          "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                          "traffic_source": traffic_src, "bytes_per_launch": dom_b,
+                          "us_per_launch": round(dom_us, 3), "launches_per_step": 36}
     if cpu:
         result["cpu_baseline"] = dict(cpu, sample=(
             f"4B checkpoint, batch 1: prefill of {args.cpu_prompt - 1} prompt ids "
