@@ -94,11 +94,17 @@ int qlm_gemv_i8_config(const float* x, const float* norm_w, float eps, const int
  * math_ops.cpp:845-871). Weights stay exact (int8 in bf16); each activation
  * is split into bf16 hi + lo and the per-group products are scaled in fp32,
  * so results match the fp32 path to ~1e-6 normwise (bit-exact when x holds
- * small integers). epilogue 0: y = x.W^T; 1: y += x.W^T; 2: SwiGLU with
- * weights [2F, K] and N = F outputs (as qlm_gemv_i8_swiglu_rmsnorm, without
- * the norm). Any M >= 1; K a multiple of 32; G = 32 or K. */
-int qlm_matmul_i8(const float* x, int ldx, const int8_t* q, const float* scales, int group,
-                  float* y, int ldy, int M, int N, int K, int epilogue, void* stream);
+ * small integers). norm_w NULL: plain x; else each row of x is first
+ * replaced by rms_norm(x, norm_w, eps) (as qlm_gemv_i8_rmsnorm). epilogue
+ * 0: y = x.W^T; 1: y += x.W^T; 2: SwiGLU with weights [2F, K] and N = F
+ * outputs. Any M >= 1; K a multiple of 32; G = 32 or K. work: device
+ * scratch of qlm_matmul_i8_workspace_bytes(M, N, K, epilogue) bytes (row
+ * scales and K-split partial sums; no initial contents needed; calls that
+ * share it must be ordered on one stream). */
+size_t qlm_matmul_i8_workspace_bytes(int M, int N, int K, int epilogue);
+int qlm_matmul_i8(const float* x, int ldx, const float* norm_w, float eps, const int8_t* q,
+                  const float* scales, int group, float* y, int ldy, int M, int N, int K,
+                  int epilogue, void* work, size_t work_bytes, void* stream);
 
 /* Fused forms used by the decode step (same arithmetic as the unfused
  * reference sequence, one launch instead of two or three):

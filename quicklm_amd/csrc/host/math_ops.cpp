@@ -11,8 +11,8 @@ namespace math {
 
 namespace {
 void* g_stream = nullptr;
-float* g_norm_scratch = nullptr;
-int64_t g_norm_scratch_floats = 0;
+void* g_mm_work = nullptr;
+size_t g_mm_work_bytes = 0;
 
 // Rows from which the matrix-core path replaces the GEMV (which re-reads the
 // weights once per 4 activation rows).
@@ -30,21 +30,23 @@ void check_int8(const Tensor& B) {
 
 void set_stream(void* s) { g_stream = s; }
 void* stream() { return g_stream; }
-void set_norm_scratch(float* p, int64_t floats) {
-    g_norm_scratch = p;
-    g_norm_scratch_floats = floats;
+void set_matmul_workspace(void* p, size_t bytes) {
+    g_mm_work = p;
+    g_mm_work_bytes = bytes;
 }
 
 namespace {
-// rms_norm(A) into the scratch buffer, for the matrix-core path (M rows).
-const float* normed_rows(const Tensor& A, const Tensor& norm_w, float eps) {
+// The matrix-core matmul for M > 4 rows (norm_w null: no RMSNorm prologue).
+void matmul_mfma(const Tensor& A, const float* norm_w, float eps, const Tensor& B, float* C,
+                 int64_t ldc, int64_t N, int epilogue) {
     const int64_t M = A.rows(), K = A.cols();
-    need(g_norm_scratch && g_norm_scratch_floats >= M * K,
-         "matmul_rmsnorm: M > 4 needs set_norm_scratch() of at least M*K floats");
-    need(A.row_stride() == K, "matmul_rmsnorm: M > 4 needs contiguous activation rows");
-    check(qlm_rms_norm(A.data, norm_w.data, g_norm_scratch, (int)M, (int)K, eps, g_stream),
-          "qlm_rms_norm");
-    return g_norm_scratch;
+    const size_t need_b = qlm_matmul_i8_workspace_bytes((int)M, (int)N, (int)K, epilogue);
+    need(g_mm_work && g_mm_work_bytes >= need_b,
+         "matmul: M > 4 needs set_matmul_workspace() of qlm_matmul_i8_workspace_bytes()");
+    check(qlm_matmul_i8(A.data, (int)A.row_stride(), norm_w, eps, B.int8_data, B.int8_scales,
+                        B.int8_group, C, (int)ldc, (int)M, (int)N, (int)K, epilogue, g_mm_work,
+                        g_mm_work_bytes, g_stream),
+          "qlm_matmul_i8");
 }
 }  // namespace
 
@@ -55,9 +57,7 @@ void matmul(const Tensor& A, const Tensor& B, Tensor& C, bool transpose_B) {
     need(B.shape[1] == K, "matmul: K mismatch");
     need(C.cols() >= N || C.row_stride() >= N, "matmul: output too small");
     if (M >= kMfmaMinRows) {
-        check(qlm_matmul_i8(A.data, (int)A.row_stride(), B.int8_data, B.int8_scales, B.int8_group,
-                            C.data, (int)C.row_stride(), (int)M, (int)N, (int)K, 0, g_stream),
-              "qlm_matmul_i8");
+        matmul_mfma(A, nullptr, 0.0f, B, C.data, C.row_stride(), N, 0);
         return;
     }
     check(qlm_gemv_i8(A.data, (int)A.row_stride(), B.int8_data, B.int8_scales, B.int8_group, C.data,
@@ -70,10 +70,7 @@ void matmul_rmsnorm(const Tensor& A, const Tensor& norm_w, float eps, const Tens
     const int64_t K = A.cols(), M = A.rows(), N = B.shape[0];
     need(B.shape[1] == K && norm_w.size() == K, "matmul_rmsnorm: K mismatch");
     if (M >= kMfmaMinRows) {
-        const float* xn = normed_rows(A, norm_w, eps);
-        check(qlm_matmul_i8(xn, (int)K, B.int8_data, B.int8_scales, B.int8_group, C.data,
-                            (int)C.row_stride(), (int)M, (int)N, (int)K, 0, g_stream),
-              "qlm_matmul_i8");
+        matmul_mfma(A, norm_w.data, eps, B, C.data, C.row_stride(), N, 0);
         return;
     }
     check(qlm_gemv_i8_rmsnorm(A.data, (int)A.row_stride(), norm_w.data, eps, B.int8_data,
@@ -87,10 +84,7 @@ void matmul_residual(const Tensor& A, const Tensor& B, Tensor& residual) {
     const int64_t K = A.cols(), M = A.rows(), N = B.shape[0];
     need(B.shape[1] == K && residual.cols() == N, "matmul_residual: shape mismatch");
     if (M >= kMfmaMinRows) {
-        check(qlm_matmul_i8(A.data, (int)A.row_stride(), B.int8_data, B.int8_scales, B.int8_group,
-                            residual.data, (int)residual.row_stride(), (int)M, (int)N, (int)K, 1,
-                            g_stream),
-              "qlm_matmul_i8");
+        matmul_mfma(A, nullptr, 0.0f, B, residual.data, residual.row_stride(), N, 1);
         return;
     }
     check(qlm_gemv_i8_residual(A.data, (int)A.row_stride(), B.int8_data, B.int8_scales,
@@ -105,10 +99,7 @@ void matmul_swiglu_rmsnorm(const Tensor& A, const Tensor& norm_w, float eps, con
     const int64_t K = A.cols(), M = A.rows(), F = B.shape[0] / 2;
     need(B.shape[0] % 2 == 0 && B.shape[1] == K && C.cols() == F, "matmul_swiglu: shape mismatch");
     if (M >= kMfmaMinRows) {
-        const float* xn = normed_rows(A, norm_w, eps);
-        check(qlm_matmul_i8(xn, (int)K, B.int8_data, B.int8_scales, B.int8_group, C.data,
-                            (int)C.row_stride(), (int)M, (int)F, (int)K, 2, g_stream),
-              "qlm_matmul_i8");
+        matmul_mfma(A, norm_w.data, eps, B, C.data, C.row_stride(), F, 2);
         return;
     }
     check(qlm_gemv_i8_swiglu_rmsnorm(A.data, (int)A.row_stride(), norm_w.data, eps, B.int8_data,

@@ -6,6 +6,8 @@
 // error convention); unsupported operand kinds throw instead of falling back.
 #pragma once
 
+#include <cstddef>
+
 #include "tensor.hpp"
 
 namespace qlm {
@@ -18,9 +20,9 @@ void* stream();
 // C = A * B^T with B an int8 (Q8_0) weight operand; A [M, K] fp32, C [M, N]
 // with row stride C.row_stride() (math_ops.hpp:92; math_ops.cpp:820-900).
 void matmul(const Tensor& A, const Tensor& B, Tensor& C, bool transpose_B = true);
-// Device scratch of at least M*K floats for the matrix-core forms with a
-// fused RMSNorm (M > 4): the normalised rows are written there first.
-void set_norm_scratch(float* p, int64_t floats);
+// Device workspace for the matrix-core forms (M > 4): at least
+// qlm_matmul_i8_workspace_bytes() of every call that follows.
+void set_matmul_workspace(void* p, size_t bytes);
 
 // math_ops.hpp:102 / :139-140 / :132.
 void rms_norm(const Tensor& input, const Tensor& weight, Tensor& output, float eps);

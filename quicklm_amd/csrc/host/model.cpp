@@ -32,6 +32,8 @@ std::vector<float> to_f32(const TensorView& t) {
     return out;
 }
 
+constexpr int kPrefillChunk = 1024;  // prompt rows per pass through the layers
+
 double now_s() {
     return std::chrono::duration<double>(std::chrono::steady_clock::now().time_since_epoch()).count();
 }
@@ -224,7 +226,12 @@ void DecoderModel::load(const std::string& dir, int max_seq_len, const std::stri
     proj_.alloc(B * Pmax * sizeof(float));
     core_.alloc(B * CORE_ * sizeof(float));
     act_.alloc(B * F * sizeof(float));
-    norm_scratch_.alloc(B * H * sizeof(float));
+    // one allocation for the whole life of the model: captured decode graphs
+    // hold its address. Batched decode rows and prefill chunks both fit; the
+    // K-split partials of the M <= 64 form grow with M, so M = 64 bounds
+    // every shorter prefill chunk.
+    mm_work_.alloc(std::max({matmul_workspace((int)B), matmul_workspace(64),
+                             matmul_workspace(std::min(kPrefillChunk, max_seq_))}));
     logits_.alloc(B * cfg_.vocab_size * sizeof(float));
     argmax_work_.alloc(qlm_argmax_workspace_bytes((int)B, cfg_.vocab_size));
     tail_work_.alloc(qlm_lm_head_greedy_workspace_bytes());
@@ -262,7 +269,7 @@ int mm_launches(int B, bool norm) {
 
 void DecoderModel::enqueue_step(int B) {
     math::set_stream(stream_);
-    math::set_norm_scratch(norm_scratch_.get<float>(), (int64_t)norm_scratch_.bytes() / 4);
+    math::set_matmul_workspace(mm_work_.get(), mm_work_.bytes());
     const int H = cfg_.hidden_size, F = cfg_.intermediate_size, V = cfg_.vocab_size;
     const int nh = cfg_.linear_num_heads, d = cfg_.linear_head_dim;
     const int nq = cfg_.num_attention_heads, nkv = cfg_.num_key_value_heads, hd = cfg_.head_dim;
@@ -416,9 +423,27 @@ double DecoderModel::start(const int* prompts, int B, int n, bool batched_prefil
     return prefill_s;
 }
 
-namespace {
-constexpr int kPrefillChunk = 1024;  // prompt rows per pass through the layers
-}  // namespace
+// Largest workspace any matrix-core matmul of the model needs at M rows.
+size_t DecoderModel::matmul_workspace(int M) const {
+    const int H = cfg_.hidden_size, F = cfg_.intermediate_size, V = cfg_.vocab_size;
+    const int nq = cfg_.num_attention_heads, hd = cfg_.head_dim;
+    size_t b = 256;
+    auto upd = [&](int N, int K, int epi) {
+        b = std::max(b, qlm_matmul_i8_workspace_bytes(M, N, K, epi));
+    };
+    if (PD_ > 0) {
+        upd(PD_, H, 0);
+        upd(H, HD_, 1);
+    }
+    if (PQ_ > 0) {
+        upd(PQ_, H, 0);
+        upd(H, nq * hd, 1);
+    }
+    upd(F, H, 2);
+    upd(H, F, 1);
+    upd(V, H, 0);
+    return b;
+}
 
 void DecoderModel::ensure_prefill_buffers(int rows) {
     if (rows <= pf_rows_) return;
@@ -428,7 +453,8 @@ void DecoderModel::ensure_prefill_buffers(int rows) {
     proj_pf_.alloc(rows * Pmax * sizeof(float));
     core_pf_.alloc(rows * (size_t)CORE_ * sizeof(float));
     act_pf_.alloc(rows * F * sizeof(float));
-    norm_pf_.alloc(rows * H * sizeof(float));
+    if (matmul_workspace(rows) > mm_work_.bytes())
+        throw std::runtime_error("prefill: matmul workspace smaller than a prefill chunk needs");
     if (QR_ > 0 && gqa_pf_work_.bytes() == 0)
         gqa_pf_work_.alloc(qlm_gqa_prefill_workspace_bytes(cfg_.num_attention_heads,
                                                            cfg_.head_dim, max_seq_));
@@ -446,7 +472,7 @@ void DecoderModel::prefill(int b, int n) {
     const int chunk = std::min(total, kPrefillChunk);
     ensure_prefill_buffers(chunk);
     math::set_stream(stream_);
-    math::set_norm_scratch(norm_pf_.get<float>(), (int64_t)norm_pf_.bytes() / 4);
+    math::set_matmul_workspace(mm_work_.get(), mm_work_.bytes());
     const int H = cfg_.hidden_size, F = cfg_.intermediate_size, V = cfg_.vocab_size;
     const int nh = cfg_.linear_num_heads, d = cfg_.linear_head_dim;
     const int nq = cfg_.num_attention_heads, nkv = cfg_.num_key_value_heads, hd = cfg_.head_dim;

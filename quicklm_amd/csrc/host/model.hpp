@@ -113,6 +113,7 @@ class DecoderModel {
     void enqueue_step(int B);
     void prefill(int b, int n);
     void ensure_prefill_buffers(int rows);
+    size_t matmul_workspace(int M) const;
     void embed_current(int B);
     void* graph_for(int B);
     void quantize_into(LinearI8& lin, int row_off, const std::string& name);
@@ -139,9 +140,9 @@ class DecoderModel {
     int ld_tokens_ = 0;
     // activations
     DeviceBuffer h_, proj_, core_, act_, logits_, argmax_work_, attn_work_, tail_work_;
-    DeviceBuffer norm_scratch_;  // RMSNorm rows for the matrix-core matmuls (M > 4)
+    DeviceBuffer mm_work_;  // workspace of the matrix-core matmuls (M > 4)
     // prefill activations for up to pf_rows_ prompt rows per chunk
-    DeviceBuffer hx_pf_, proj_pf_, core_pf_, act_pf_, norm_pf_, gqa_pf_work_;
+    DeviceBuffer hx_pf_, proj_pf_, core_pf_, act_pf_, gqa_pf_work_;
     int pf_rows_ = 0;
     DeviceBuffer staging_;
 

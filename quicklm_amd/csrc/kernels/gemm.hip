@@ -55,8 +55,49 @@ __device__ __forceinline__ unsigned short i8_bf16(int v) {
     return (unsigned short)(__float_as_uint((float)v) >> 16);
 }
 
-template <int WM, int WN, int WK, int TM, int TN, bool ROWSCALE, int EPI>
+// RMSNorm of a staged activation: (x * s) * (1 + w), the reference's order
+// (math_ops.cpp:1021-1031), s = 1/sqrt(mean(x^2) + eps) of the row.
+__device__ __forceinline__ float4 norm4(float4 v, float s, float4 w) {
+    v.x = (v.x * s) * (1.0f + w.x);
+    v.y = (v.y * s) * (1.0f + w.y);
+    v.z = (v.z * s) * (1.0f + w.z);
+    v.w = (v.w * s) * (1.0f + w.w);
+    return v;
+}
+
+__device__ __forceinline__ void store_hilo(unsigned short* hi, unsigned short* lo, float4 v) {
+    unsigned short h[4], l[4];
+    split_bf16(v.x, h[0], l[0]);
+    split_bf16(v.y, h[1], l[1]);
+    split_bf16(v.z, h[2], l[2]);
+    split_bf16(v.w, h[3], l[3]);
+    *reinterpret_cast<uint2*>(hi) = make_uint2((unsigned)h[0] | ((unsigned)h[1] << 16),
+                                               (unsigned)h[2] | ((unsigned)h[3] << 16));
+    *reinterpret_cast<uint2*>(lo) = make_uint2((unsigned)l[0] | ((unsigned)l[1] << 16),
+                                               (unsigned)l[2] | ((unsigned)l[3] << 16));
+}
+
+// 16 int8 -> 16 bf16 (exact), as two 16-byte LDS stores
+__device__ __forceinline__ void store_w16(unsigned short* dst, int4 w) {
+    const int wv[4] = {w.x, w.y, w.z, w.w};
+    uint4 o[2];
+    unsigned* ow = reinterpret_cast<unsigned*>(o);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const unsigned v = (unsigned)wv[j];
+        const int b0 = (int8_t)(v & 0xffu), b1 = (int8_t)((v >> 8) & 0xffu);
+        const int b2 = (int8_t)((v >> 16) & 0xffu), b3 = (int8_t)(v >> 24);
+        ow[2 * j] = (unsigned)i8_bf16(b0) | ((unsigned)i8_bf16(b1) << 16);
+        ow[2 * j + 1] = (unsigned)i8_bf16(b2) | ((unsigned)i8_bf16(b3) << 16);
+    }
+    reinterpret_cast<uint4*>(dst)[0] = o[0];
+    reinterpret_cast<uint4*>(dst)[1] = o[1];
+}
+
+template <int WM, int WN, int WK, int TM, int TN, bool ROWSCALE, int EPI, bool NORM>
 __global__ __launch_bounds__(kThreads) void k_mm_i8(const float* __restrict__ x, int ldx,
+                                                    const float* __restrict__ rs,
+                                                    const float* __restrict__ nw,
                                                     const int8_t* __restrict__ q,
                                                     const float* __restrict__ sc,
                                                     float* __restrict__ y, int ldy, int M, int N,
@@ -116,6 +157,8 @@ __global__ __launch_bounds__(kThreads) void k_mm_i8(const float* __restrict__ x,
     };
 
     float4 xr[XPT];
+    float4 gr[NORM ? XPT : 1];  // RMSNorm gain of the same columns
+    float rr[NORM ? XPT : 1];   // RMSNorm row scale
     int4 wr[WPT];
     float sr[TN];
     auto load_chunk = [&](int c) {
@@ -127,6 +170,10 @@ __global__ __launch_bounds__(kThreads) void k_mm_i8(const float* __restrict__ x,
                 const int r = i / (KC / 4), c4 = i % (KC / 4);
                 const int m = min(m0 + r, M - 1);
                 xr[u] = *reinterpret_cast<const float4*>(x + (size_t)m * ldx + k0 + c4 * 4);
+                if constexpr (NORM) {
+                    gr[u] = *reinterpret_cast<const float4*>(nw + k0 + c4 * 4);
+                    rr[u] = rs[m];
+                }
             }
         }
 #pragma unroll
@@ -150,11 +197,13 @@ __global__ __launch_bounds__(kThreads) void k_mm_i8(const float* __restrict__ x,
             const int i = tid + u * kThreads;
             if (i < XV) {
                 const int r = i / (KC / 4), c4 = i % (KC / 4);
+                float4 v = xr[u];
+                if constexpr (NORM) v = norm4(v, rr[u], gr[u]);
                 unsigned short h[4], l[4];
-                split_bf16(xr[u].x, h[0], l[0]);
-                split_bf16(xr[u].y, h[1], l[1]);
-                split_bf16(xr[u].z, h[2], l[2]);
-                split_bf16(xr[u].w, h[3], l[3]);
+                split_bf16(v.x, h[0], l[0]);
+                split_bf16(v.y, h[1], l[1]);
+                split_bf16(v.z, h[2], l[2]);
+                split_bf16(v.w, h[3], l[3]);
                 uint2 ph, pl;
                 ph.x = (unsigned)h[0] | ((unsigned)h[1] << 16);
                 ph.y = (unsigned)h[2] | ((unsigned)h[3] << 16);
@@ -289,33 +338,292 @@ __global__ __launch_bounds__(kThreads) void k_mm_i8(const float* __restrict__ x,
         }
 }
 
-template <int WM, int WN, int WK, int TM, int TN, bool RS, int EPI>
-int launch_mm(const float* x, int ldx, const int8_t* q, const float* sc, float* y, int ldy, int M,
-              int N, int K, hipStream_t st) {
+// ---------------------------------------------------------------------------
+// M <= 64 (batched decode): weight streaming with K split across workgroups.
+//
+// A workgroup owns 64 weight rows (wave w: rows 16w..16w+15 as one MFMA
+// n-tile) and 16*TM activation rows, over a K slice of kper columns; per
+// 128-column chunk (4 groups) x [BM, 128] is staged as bf16 hi/lo (with the
+// RMSNorm applied when NORM) and the weights [64, 128] as bf16, the next
+// chunk being loaded into registers meanwhile. Each slice writes its fp32
+// partial tile to part[ks, m, n]; k_mm_reduce sums the slices in order and
+// applies the epilogue. With a single slice and a plain store the partial
+// is the output itself.
+constexpr int kSkRows = 64;
+constexpr int kSkKc = 128;
+
+template <int TM, bool ROWSCALE, bool NORM>
+__global__ __launch_bounds__(kThreads) void k_mm_i8_sk(
+    const float* __restrict__ x, int ldx, const float* __restrict__ rs,
+    const float* __restrict__ nw, const int8_t* __restrict__ q, const float* __restrict__ sc,
+    float* __restrict__ part, int ldp, int M, int NR, int K, int kper) {
+    constexpr int BM = 16 * TM;
+    constexpr int KC = kSkKc;
+    constexpr int XP = KC + 8, WP = KC + 8;
+    constexpr int XV = BM * KC / 4, WV = kSkRows * KC / 16;
+    constexpr int XPT = (XV + kThreads - 1) / kThreads;
+    constexpr int WPT = (WV + kThreads - 1) / kThreads;
+    __shared__ __attribute__((aligned(16))) unsigned short xs_hi[BM * XP];
+    __shared__ __attribute__((aligned(16))) unsigned short xs_lo[BM * XP];
+    __shared__ __attribute__((aligned(16))) unsigned short ws[kSkRows * WP];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n0 = blockIdx.x * kSkRows;
+    const int ks = blockIdx.y;
+    const int m0 = blockIdx.z * BM;
+    const int kb = ks * kper;
+    const int nblk = K >> 5;
+    const int ncol = n0 + wave * 16 + (lane & 15);      // this lane's weight row (output column)
+    const int nrow = ncol < NR ? ncol : NR - 1;
+
+    float4 xr[XPT];
+    float4 gr[NORM ? XPT : 1];
+    float rr[NORM ? XPT : 1];
+    int4 wr[WPT];
+    float4 sr;  // group scales of this lane's row for the chunk's 4 groups
+    auto load_chunk = [&](int c) {
+        const int k0 = kb + c * KC;
+#pragma unroll
+        for (int u = 0; u < XPT; ++u) {
+            const int i = tid + u * kThreads;
+            if (i < XV) {
+                const int r = i / (KC / 4), c4 = i % (KC / 4);
+                const int m = min(m0 + r, M - 1);
+                xr[u] = *reinterpret_cast<const float4*>(x + (size_t)m * ldx + k0 + c4 * 4);
+                if constexpr (NORM) {
+                    gr[u] = *reinterpret_cast<const float4*>(nw + k0 + c4 * 4);
+                    rr[u] = rs[m];
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < WPT; ++u) {
+            const int i = tid + u * kThreads;
+            if (i < WV) {
+                const int r = i / (KC / 16), c16 = i % (KC / 16);
+                const int n = min(n0 + r, NR - 1);
+                wr[u] = *reinterpret_cast<const int4*>(q + (size_t)n * K + k0 + c16 * 16);
+            }
+        }
+        if constexpr (!ROWSCALE)
+            sr = *reinterpret_cast<const float4*>(sc + (size_t)nrow * nblk + (k0 >> 5));
+    };
+    auto store_chunk = [&]() {
+#pragma unroll
+        for (int u = 0; u < XPT; ++u) {
+            const int i = tid + u * kThreads;
+            if (i < XV) {
+                const int r = i / (KC / 4), c4 = i % (KC / 4);
+                float4 v = xr[u];
+                if constexpr (NORM) v = norm4(v, rr[u], gr[u]);
+                store_hilo(&xs_hi[r * XP + c4 * 4], &xs_lo[r * XP + c4 * 4], v);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < WPT; ++u) {
+            const int i = tid + u * kThreads;
+            if (i < WV) {
+                const int r = i / (KC / 16), c16 = i % (KC / 16);
+                store_w16(&ws[r * WP + c16 * 16], wr[u]);
+            }
+        }
+    };
+
+    f32x4 acc[TM];
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm) acc[tm] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int nch = kper / KC;
+    load_chunk(0);
+    for (int c = 0; c < nch; ++c) {
+        const float4 s_cur = sr;
+        __syncthreads();
+        store_chunk();
+        __syncthreads();
+        if (c + 1 < nch) load_chunk(c + 1);
+        const float sg[4] = {s_cur.x, s_cur.y, s_cur.z, s_cur.w};
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int kofs = g * 32 + (lane >> 4) * 8;
+            const bf16x8 bw = *reinterpret_cast<const bf16x8*>(&ws[(wave * 16 + (lane & 15)) * WP + kofs]);
+#pragma unroll
+            for (int tm = 0; tm < TM; ++tm) {
+                const int r = tm * 16 + (lane & 15);
+                const bf16x8 ah = *reinterpret_cast<const bf16x8*>(&xs_hi[r * XP + kofs]);
+                const bf16x8 al = *reinterpret_cast<const bf16x8*>(&xs_lo[r * XP + kofs]);
+                if constexpr (ROWSCALE) {
+                    acc[tm] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bw, acc[tm], 0, 0, 0);
+                    acc[tm] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bw, acc[tm], 0, 0, 0);
+                } else {
+                    f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bw, d, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bw, d, 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) acc[tm][i] = fmaf(d[i], sg[g], acc[tm][i]);
+                }
+            }
+        }
+    }
+    if constexpr (ROWSCALE) {
+        const float s = sc[nrow];
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[tm][i] *= s;
+    }
+    if (ncol < NR) {
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int m = m0 + tm * 16 + (lane >> 4) * 4 + i;
+                if (m < M) part[((size_t)ks * M + m) * ldp + ncol] = acc[tm][i];
+            }
+    }
+}
+
+// y[m, n] (=, +=) sum over slices of part[ks, m, n], or for SwiGLU
+// y[m, n] = silu(gate) * up with gate/up the sums at columns n and F + n.
+template <int EPI>
+__global__ __launch_bounds__(kThreads) void k_mm_reduce(const float* __restrict__ part, int ks,
+                                                        int M, int NR, int N,
+                                                        float* __restrict__ y, int ldy) {
+    const int idx = blockIdx.x * kThreads + threadIdx.x;
+    if (idx >= M * N) return;
+    const int m = idx / N, n = idx % N;
+    float g = 0.0f, u = 0.0f;
+    for (int k = 0; k < ks; ++k) {
+        const float* pr = part + ((size_t)k * M + m) * NR;
+        g += pr[n];
+        if constexpr (EPI == EPI_SWIGLU) u += pr[N + n];
+    }
+    float* dst = y + (size_t)m * ldy + n;
+    if constexpr (EPI == EPI_SWIGLU)
+        *dst = silu_f(g) * u;
+    else if constexpr (EPI == EPI_RESID)
+        *dst += g;
+    else
+        *dst = g;
+}
+
+// RMSNorm row scales rs[m] = 1/sqrt(mean(x[m]^2) + eps): every load of the
+// row is issued before the sum (K <= 4096 per pass of 256 x float4).
+__global__ __launch_bounds__(kThreads) void k_row_rs(const float* __restrict__ x, int ldx, int K,
+                                                     float eps, float* __restrict__ rs) {
+    __shared__ float red[kThreads / QLM_WAVE];
+    const float4* xr = reinterpret_cast<const float4*>(x + (size_t)blockIdx.x * ldx);
+    const int n4 = K >> 2;
+    float ss = 0.0f;
+    for (int b = 0; b < n4; b += 4 * kThreads) {
+        float4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int i = b + u * kThreads + threadIdx.x;
+            v[u] = i < n4 ? xr[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            ss = fmaf(v[u].x, v[u].x, ss);
+            ss = fmaf(v[u].y, v[u].y, ss);
+            ss = fmaf(v[u].z, v[u].z, ss);
+            ss = fmaf(v[u].w, v[u].w, ss);
+        }
+    }
+    ss = block_sum(ss, red);
+    if (threadIdx.x == 0) rs[blockIdx.x] = 1.0f / sqrtf(ss / (float)K + eps);
+}
+
+// K slices for the M <= 64 path: the fewest that give ~1000 workgroups and
+// divide the 128-column chunk count.
+int sk_splits(int NR, int K) {
+    const int nt = (NR + kSkRows - 1) / kSkRows;
+    const int nch = K / kSkKc;
+    const int want = (1024 + nt - 1) / nt;
+    for (int d = 1; d <= nch; ++d)
+        if (nch % d == 0 && d >= want) return d;
+    return nch;
+}
+
+bool use_sk(int M, int K) { return M <= 64 && K % kSkKc == 0; }
+
+size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+size_t mm_workspace(int M, int N, int K, int epi) {
+    size_t b = align256((size_t)M * sizeof(float));  // row scales
+    if (use_sk(M, K)) {
+        const int NR = epi == EPI_SWIGLU ? 2 * N : N;
+        const int ks = sk_splits(NR, K);
+        if (!(ks == 1 && epi == EPI_STORE)) b += (size_t)ks * M * NR * sizeof(float);
+    }
+    return b;
+}
+
+template <int TM, bool RS, bool NORM>
+void launch_sk(const float* x, int ldx, const float* rs, const float* nw, const int8_t* q,
+               const float* sc, float* part, int ldp, int M, int NR, int K, int ks,
+               hipStream_t st) {
+    const dim3 grid((NR + kSkRows - 1) / kSkRows, ks, (M + 16 * TM - 1) / (16 * TM));
+    hipLaunchKernelGGL((k_mm_i8_sk<TM, RS, NORM>), grid, dim3(kThreads), 0, st, x, ldx, rs, nw, q,
+                       sc, part, ldp, M, NR, K, K / ks);
+}
+
+template <int WM, int WN, int WK, int TM, int TN, bool RS, int EPI, bool NORM>
+int launch_mm(const float* x, int ldx, const float* rs, const float* nw, const int8_t* q,
+              const float* sc, float* y, int ldy, int M, int N, int K, hipStream_t st) {
     constexpr int BM = WM * TM * 16;
     constexpr int BN_OUT = WN * (EPI == EPI_SWIGLU ? TN / 2 : TN) * 16;
     const dim3 grid((N + BN_OUT - 1) / BN_OUT, (M + BM - 1) / BM);
-    hipLaunchKernelGGL((k_mm_i8<WM, WN, WK, TM, TN, RS, EPI>), grid, dim3(kThreads), 0, st, x,
-                       ldx, q, sc, y, ldy, M, N, K, N);
+    hipLaunchKernelGGL((k_mm_i8<WM, WN, WK, TM, TN, RS, EPI, NORM>), grid, dim3(kThreads), 0, st,
+                       x, ldx, rs, nw, q, sc, y, ldy, M, N, K, N);
     return qlm_launch_status();
 }
 
-template <bool RS, int EPI>
-int mm_dispatch(const float* x, int ldx, const int8_t* q, const float* sc, float* y, int ldy,
-                int M, int N, int K, hipStream_t st) {
-    constexpr int TNS = EPI == EPI_SWIGLU ? 2 : 1;  // weight tiles per wave, small M
-    if (M <= 64 && K % 128 == 0) {
-        if (M <= 16) return launch_mm<1, 1, 4, 1, TNS, RS, EPI>(x, ldx, q, sc, y, ldy, M, N, K, st);
-        if (M <= 32) return launch_mm<1, 1, 4, 2, TNS, RS, EPI>(x, ldx, q, sc, y, ldy, M, N, K, st);
-        return launch_mm<1, 1, 4, 4, TNS, RS, EPI>(x, ldx, q, sc, y, ldy, M, N, K, st);
+template <bool RS, bool NORM>
+int mm_run(const float* x, int ldx, const float* rs, const float* nw, const int8_t* q,
+           const float* sc, float* y, int ldy, int M, int N, int K, int epi, float* part,
+           hipStream_t st) {
+    if (use_sk(M, K)) {
+        const int NR = epi == EPI_SWIGLU ? 2 * N : N;
+        const int ks = sk_splits(NR, K);
+        const bool direct = ks == 1 && epi == EPI_STORE;
+        float* dst = direct ? y : part;
+        const int ldp = direct ? ldy : NR;
+        if (M <= 16)
+            launch_sk<1, RS, NORM>(x, ldx, rs, nw, q, sc, dst, ldp, M, NR, K, ks, st);
+        else if (M <= 32)
+            launch_sk<2, RS, NORM>(x, ldx, rs, nw, q, sc, dst, ldp, M, NR, K, ks, st);
+        else
+            launch_sk<4, RS, NORM>(x, ldx, rs, nw, q, sc, dst, ldp, M, NR, K, ks, st);
+        int rc = qlm_launch_status();
+        if (rc != QLM_OK || direct) return rc;
+        const int blocks = (M * N + kThreads - 1) / kThreads;
+        if (epi == EPI_STORE)
+            hipLaunchKernelGGL(k_mm_reduce<EPI_STORE>, dim3(blocks), dim3(kThreads), 0, st, part, ks,
+                               M, NR, N, y, ldy);
+        else if (epi == EPI_RESID)
+            hipLaunchKernelGGL(k_mm_reduce<EPI_RESID>, dim3(blocks), dim3(kThreads), 0, st, part, ks,
+                               M, NR, N, y, ldy);
+        else
+            hipLaunchKernelGGL(k_mm_reduce<EPI_SWIGLU>, dim3(blocks), dim3(kThreads), 0, st, part,
+                               ks, M, NR, N, y, ldy);
+        return qlm_launch_status();
     }
-    return launch_mm<2, 2, 1, 4, 4, RS, EPI>(x, ldx, q, sc, y, ldy, M, N, K, st);
+    if (epi == EPI_STORE)
+        return launch_mm<2, 2, 1, 4, 4, RS, EPI_STORE, NORM>(x, ldx, rs, nw, q, sc, y, ldy, M, N, K, st);
+    if (epi == EPI_RESID)
+        return launch_mm<2, 2, 1, 4, 4, RS, EPI_RESID, NORM>(x, ldx, rs, nw, q, sc, y, ldy, M, N, K, st);
+    return launch_mm<2, 2, 1, 4, 4, RS, EPI_SWIGLU, NORM>(x, ldx, rs, nw, q, sc, y, ldy, M, N, K, st);
 }
 
 }  // namespace
 
-extern "C" int qlm_matmul_i8(const float* x, int ldx, const int8_t* q, const float* scales,
-                             int group, float* y, int ldy, int M, int N, int K, int epilogue,
+extern "C" size_t qlm_matmul_i8_workspace_bytes(int M, int N, int K, int epilogue) {
+    if (M <= 0 || N <= 0 || K <= 0 || epilogue < EPI_STORE || epilogue > EPI_SWIGLU) return 0;
+    return mm_workspace(M, N, K, epilogue);
+}
+
+extern "C" int qlm_matmul_i8(const float* x, int ldx, const float* norm_w, float eps,
+                             const int8_t* q, const float* scales, int group, float* y, int ldy,
+                             int M, int N, int K, int epilogue, void* work, size_t work_bytes,
                              void* stream) {
     if (!x || !q || !scales || !y) return QLM_ERR_ARG;
     if (M <= 0 || N <= 0 || K <= 0) return QLM_ERR_ARG;
@@ -324,14 +632,24 @@ extern "C" int qlm_matmul_i8(const float* x, int ldx, const int8_t* q, const flo
     const bool rowscale = (group == K);
     if (!rowscale && group != 32) return QLM_ERR_SHAPE;
     if (ldx < K || ldy < N || ldx % 4 != 0) return QLM_ERR_SHAPE;
-    if (((uintptr_t)x | (uintptr_t)q) & 15u) return QLM_ERR_SHAPE;
+    if (((uintptr_t)x | (uintptr_t)q | (uintptr_t)norm_w | (uintptr_t)scales) & 15u)
+        return QLM_ERR_SHAPE;
+    const size_t need = mm_workspace(M, N, K, epilogue);
+    if (!work || work_bytes < need || ((uintptr_t)work & 15u)) return QLM_ERR_ARG;
     hipStream_t st = as_stream(stream);
-    if (rowscale) {
-        if (epilogue == EPI_STORE) return mm_dispatch<true, EPI_STORE>(x, ldx, q, scales, y, ldy, M, N, K, st);
-        if (epilogue == EPI_RESID) return mm_dispatch<true, EPI_RESID>(x, ldx, q, scales, y, ldy, M, N, K, st);
-        return mm_dispatch<true, EPI_SWIGLU>(x, ldx, q, scales, y, ldy, M, N, K, st);
+    float* rs = reinterpret_cast<float*>(work);
+    float* part = reinterpret_cast<float*>(reinterpret_cast<char*>(work) + align256((size_t)M * 4));
+    if (norm_w) {
+        hipLaunchKernelGGL(k_row_rs, dim3(M), dim3(kThreads), 0, st, x, ldx, K, eps, rs);
+        const int rc = qlm_launch_status();
+        if (rc != QLM_OK) return rc;
+        return rowscale ? mm_run<true, true>(x, ldx, rs, norm_w, q, scales, y, ldy, M, N, K,
+                                             epilogue, part, st)
+                        : mm_run<false, true>(x, ldx, rs, norm_w, q, scales, y, ldy, M, N, K,
+                                              epilogue, part, st);
     }
-    if (epilogue == EPI_STORE) return mm_dispatch<false, EPI_STORE>(x, ldx, q, scales, y, ldy, M, N, K, st);
-    if (epilogue == EPI_RESID) return mm_dispatch<false, EPI_RESID>(x, ldx, q, scales, y, ldy, M, N, K, st);
-    return mm_dispatch<false, EPI_SWIGLU>(x, ldx, q, scales, y, ldy, M, N, K, st);
+    return rowscale ? mm_run<true, false>(x, ldx, nullptr, nullptr, q, scales, y, ldy, M, N, K,
+                                          epilogue, part, st)
+                    : mm_run<false, false>(x, ldx, nullptr, nullptr, q, scales, y, ldy, M, N, K,
+                                           epilogue, part, st);
 }

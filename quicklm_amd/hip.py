@@ -54,7 +54,9 @@ _SIGS = {
     "qlm_gqa_prefill_workspace_bytes": (_sz, [_i, _i, _i]),
     "qlm_gqa_prefill": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _i, _vp, _vp, _i, _i, _i, _vp, _i, _i,
                              _i, _i, _i, _vp, _vp]),
-    "qlm_matmul_i8": (_i, [_vp, _i, _vp, _vp, _i, _vp, _i, _i, _i, _i, _i, _vp]),
+    "qlm_matmul_i8_workspace_bytes": (_sz, [_i, _i, _i, _i]),
+    "qlm_matmul_i8": (_i, [_vp, _i, _vp, _f, _vp, _vp, _i, _vp, _i, _i, _i, _i, _i, _vp, _sz,
+                           _vp]),
     "qlm_gemv_i8_config": (_i, [_vp, _vp, _f, _vp, _vp, _i, _vp, _i, _i, _i, _i, _i, _i, _vp]),
     "qlm_gemv_i8_rmsnorm": (_i, [_vp, _i, _vp, _f, _vp, _vp, _i, _vp, _i, _i, _i, _i, _vp]),
     "qlm_gemv_i8_residual": (_i, [_vp, _i, _vp, _vp, _i, _vp, _i, _i, _i, _i, _vp]),

@@ -161,26 +161,42 @@ def test_matmul_mfma_parity(hip, orc, rng, M, N, K, group):
     ldy = N + 8
     dy = hip.DeviceBuffer(M * ldy * 4)
     say("matmul", M, N, K, g)
-    hip.call("qlm_matmul_i8", dev(hip, x), K, dev(hip, q), dev(hip, s), g, dy, ldy, M, N, K, 0,
-             None)
+    _matmul(hip, dev(hip, x), K, None, 0.0, dev(hip, q), dev(hip, s), g, dy, ldy, M, N, K, 0)
     y = dy.to_numpy((M, ldy), np.float32)[:, :N]
     assert rel_err(y, ref) < 1e-5
 
 
-@pytest.mark.parametrize("M,K", [(16, 2560), (200, 1024)])
-@pytest.mark.parametrize("epi", ["resid", "swiglu"])
+def _matmul(hip, x, ldx, nw, eps, q, s, g, y, ldy, M, N, K, epi):
+    nbytes = hip.lib().qlm_matmul_i8_workspace_bytes(M, N, K, epi)
+    work = hip.DeviceBuffer(nbytes)
+    work.upload(np.full(nbytes, 0xA5, np.uint8))  # no initial contents are required
+    hip.call("qlm_matmul_i8", x, ldx, nw, eps, q, s, g, y, ldy, M, N, K, epi, work, nbytes, None)
+
+
+@pytest.mark.parametrize("M,K", [(16, 2560), (7, 9728), (200, 1024)])
+@pytest.mark.parametrize("epi", ["store_norm", "resid", "swiglu_norm"])
 def test_matmul_mfma_epilogues(hip, orc, rng, M, K, epi):
-    N = 700
-    rows_w = 2 * N if epi == "swiglu" else N
+    """Residual add, SwiGLU and the fused RMSNorm prologue, on the K-split
+    path (M <= 64) and the prefill tiles."""
+    N, eps = 700, 1e-6
+    rows_w = 2 * N if epi.startswith("swiglu") else N
     q, s = _weights(orc, rng, rows_w, K, 32)
     x = rng.standard_normal((M, K)).astype(np.float32)
+    nw = (rng.standard_normal(K) * 0.02).astype(np.float32)
     y0 = rng.standard_normal((M, N)).astype(np.float32)
-    lg = orc.matmul_i8(x, q, s, 32)
-    ref = y0 + lg if epi == "resid" else orc.silu_mul(lg[:, :N].copy(), lg[:, N:].copy())
+    xin = orc.rms_norm(x, nw, eps) if epi.endswith("norm") else x
+    lg = orc.matmul_i8(xin, q, s, 32)
+    if epi == "resid":
+        ref = y0 + lg
+    elif epi == "store_norm":
+        ref = lg
+    else:
+        ref = orc.silu_mul(lg[:, :N].copy(), lg[:, N:].copy())
     dy = dev(hip, y0)
     say("matmul", epi, M, K)
-    hip.call("qlm_matmul_i8", dev(hip, x), K, dev(hip, q), dev(hip, s), 32, dy, N, M, N, K,
-             1 if epi == "resid" else 2, None)
+    code = {"store_norm": 0, "resid": 1, "swiglu_norm": 2}[epi]
+    _matmul(hip, dev(hip, x), K, dev(hip, nw) if epi.endswith("norm") else None, eps,
+            dev(hip, q), dev(hip, s), 32, dy, N, M, N, K, code)
     assert rel_err(dy.to_numpy((M, N), np.float32), ref) < 1e-5
 
 
@@ -194,8 +210,7 @@ def test_matmul_mfma_exact_integers(hip, orc, rng, M):
     x = rng.integers(-16, 17, (M, K)).astype(np.float32)
     ref = orc.matmul_i8(x, q, s, 32)
     dy = hip.DeviceBuffer(M * N * 4)
-    hip.call("qlm_matmul_i8", dev(hip, x), K, dev(hip, q), dev(hip, s), 32, dy, N, M, N, K, 0,
-             None)
+    _matmul(hip, dev(hip, x), K, None, 0.0, dev(hip, q), dev(hip, s), 32, dy, N, M, N, K, 0)
     assert np.array_equal(dy.to_numpy((M, N), np.float32), ref)
 
 
