@@ -46,13 +46,16 @@ int qlm_engine_forward(void* handle, int token, int pos, float* logits);
  * prompt forwards, decode = the n_new steps). use_graph 0 launches eagerly.
  * prefill_mode 1: positions 0..n-2 of each sequence go through the batched
  * prefill (the reference's forward_batch, model.cpp:213-258: every layer
- * over all prompt rows); 0: each is forwarded by its own decode step. */
+ * over all prompt rows) with the DeltaNet recurrence in its chunked form on
+ * the matrix cores; 2: the same with the recurrence row by row (bit-identical
+ * to mode 0's DeltaNet arithmetic); 0: each position is forwarded by its own
+ * decode step. */
 int qlm_engine_generate(void* handle, const int* prompts, int B, int n, int n_new, int* out,
                         double* prefill_s, double* decode_s, int use_graph, int prefill_mode);
 
 /* Stepwise generation for benchmarks: start() resets and installs B prompts
- * of length n (prefill_mode 1 also prefills positions 0..n-2, wall time in
- * *prefill_s, so the first step forwards position n-1); steps() runs k
+ * of length n (prefill_mode 1 or 2 also prefills positions 0..n-2, wall time
+ * in *prefill_s, so the first step forwards position n-1); steps() runs k
  * decode steps (with prefill_mode 0 the prompt forwards come first) as graph
  * replays and reports their GPU time in ms (HIP events on the engine's
  * stream); tokens() copies count tokens of sequence b from position first. */

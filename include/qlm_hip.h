@@ -184,7 +184,20 @@ int qlm_deltanet_prefill(const float* proj, int ldp, int T, float* conv_state,
                          const float* norm_w, float* state, int p0, float* out, int ldo, int H,
                          int d, void* stream);
 
-/* ---- A8/A9: GQA decode attention over a contiguous KV cache/* ---- A8/A9: GQA decode attention over a contiguous KV cache -----------------
+/* The same prefill in the chunked (WY) form: chunks of 64 rows, the
+ * intra-chunk products (K K^T, Q K^T, T V, T K) and the chunk-to-chunk
+ * state products (W = U - Wk S, Q S, K^T W) on the fp32 matrix cores, the
+ * rows of a chunk solved together instead of one after another. Same inputs
+ * and outputs as qlm_deltanet_prefill, within 1e-4 of it (reassociated fp32).
+ * work: device scratch of qlm_deltanet_chunk_workspace_bytes(T, H, d) bytes,
+ * 256-byte aligned, no initial contents needed. */
+size_t qlm_deltanet_chunk_workspace_bytes(int T, int H, int d);
+int qlm_deltanet_prefill_chunked(const float* proj, int ldp, int T, float* conv_state,
+                                 const float* conv_w_t, const float* A_log, const float* dt_bias,
+                                 const float* norm_w, float* state, int p0, float* out, int ldo,
+                                 int H, int d, void* work, size_t work_bytes, void* stream);
+
+/* ---- A8/A9: GQA decode attention over a contiguous KV cache -----------------
  * Qwen3_5Attention::forward steps 2-6 (attention.cpp:160-227) for B
  * sequences at positions pos[b]:
  *   qkv[b] = [q+gate (n_q * 2*hd if gated else n_q*hd) | k (n_kv*hd) | v (n_kv*hd)]
@@ -214,7 +227,7 @@ int qlm_gqa_prefill(float* qkv, int ldqkv, const float* q_norm, const float* k_n
                     float* v_cache, int max_seq, int p0, int T, float* out, int ldo, int n_q,
                     int n_kv, int hd, int gated, void* work, void* stream);
 
-/* Isolated attention core (no norm/RoPE/write)/* Isolated attention core (no norm/RoPE/write): out[b, h] = softmax(q.K^T *
+/* Isolated attention core (no norm/RoPE/write): out[b, h] = softmax(q.K^T *
  * scale) . V over the first ctx positions of a [B, max_seq, n_kv, hd] cache,
  * kv_dtype 0 = fp32, 1 = bf16. q, out are [B, n_q, hd] fp32. */
 int qlm_attention_decode(const float* q, const void* k_cache, const void* v_cache,

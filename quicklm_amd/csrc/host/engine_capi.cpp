@@ -84,7 +84,8 @@ int qlm_engine_generate(void* handle, const int* prompts, int B, int n, int n_ne
     return guarded([&] {
         if (!prompts || !out) throw std::runtime_error("null argument");
         qlm::GenStats st;
-        M(handle)->generate(prompts, B, n, n_new, out, &st, use_graph != 0, prefill_mode != 0);
+        if (prefill_mode < 0 || prefill_mode > 2) throw std::runtime_error("bad prefill_mode");
+        M(handle)->generate(prompts, B, n, n_new, out, &st, use_graph != 0, prefill_mode);
         if (prefill_s) *prefill_s = st.prefill_s;
         if (decode_s) *decode_s = st.decode_s;
     });
@@ -94,7 +95,8 @@ int qlm_engine_start(void* handle, const int* prompts, int B, int n, int prefill
                      double* prefill_s) {
     return guarded([&] {
         if (!prompts) throw std::runtime_error("null prompts");
-        const double s = M(handle)->start(prompts, B, n, prefill_mode != 0);
+        if (prefill_mode < 0 || prefill_mode > 2) throw std::runtime_error("bad prefill_mode");
+        const double s = M(handle)->start(prompts, B, n, prefill_mode);
         if (prefill_s) *prefill_s = s;
     });
 }

@@ -390,7 +390,8 @@ void DecoderModel::last_logits(int b, float* host) const {
     check(qlm_stream_sync(stream_), "sync");
 }
 
-double DecoderModel::start(const int* prompts, int B, int n, bool batched_prefill) {
+double DecoderModel::start(const int* prompts, int B, int n, int prefill_mode) {
+    const bool batched_prefill = prefill_mode != kPrefillSteps;
     if (B <= 0 || B > max_batch_) throw std::runtime_error("generate: batch exceeds max_batch");
     if (n <= 0) throw std::runtime_error("generate: empty prompt");
     if (n > max_seq_)
@@ -409,7 +410,7 @@ double DecoderModel::start(const int* prompts, int B, int n, bool batched_prefil
     if (batched_prefill && n > 1) {
         check(qlm_stream_sync(stream_), "sync");
         const double t0 = now_s();
-        for (int b = 0; b < B; ++b) prefill(b, n);
+        for (int b = 0; b < B; ++b) prefill(b, n, prefill_mode == kPrefillChunked);
         check(qlm_stream_sync(stream_), "sync");
         prefill_s = now_s() - t0;
         std::fill(p.begin(), p.end(), n - 1);
@@ -458,6 +459,9 @@ void DecoderModel::ensure_prefill_buffers(int rows) {
     if (QR_ > 0 && gqa_pf_work_.bytes() == 0)
         gqa_pf_work_.alloc(qlm_gqa_prefill_workspace_bytes(cfg_.num_attention_heads,
                                                            cfg_.head_dim, max_seq_));
+    if (HD_ > 0)
+        dn_pf_work_.alloc(qlm_deltanet_chunk_workspace_bytes(rows, cfg_.linear_num_heads,
+                                                             cfg_.linear_head_dim));
     pf_rows_ = rows;
 }
 
@@ -466,7 +470,7 @@ void DecoderModel::ensure_prefill_buffers(int rows) {
 // model.cpp:213-258, with main.cpp:590-622's convention that the last prompt
 // token is forwarded by the first decode step). Fills the conv rings,
 // DeltaNet states and KV caches of sequence b; no logits are needed.
-void DecoderModel::prefill(int b, int n) {
+void DecoderModel::prefill(int b, int n, bool chunked_deltanet) {
     const int total = n - 1;
     if (total <= 0) return;
     const int chunk = std::min(total, kPrefillChunk);
@@ -493,14 +497,21 @@ void DecoderModel::prefill(int b, int n) {
                 Tensor proj({rows, PD_}, proj_pf_.get<float>());
                 proj.strides = {Pmax, 1};
                 math::matmul_rmsnorm(hx, in_ln, eps, w.dn_in.view(), proj);
-                check(qlm_deltanet_prefill(
-                          proj_pf_.get<float>(), Pmax, rows,
-                          conv_state_[dn_i].get<float>() + (size_t)b * 3 * C,
-                          w.conv_wt.get<float>(), w.A_log.get<float>(), w.dt_bias.get<float>(),
-                          w.dn_norm.get<float>(),
-                          dn_state_[dn_i].get<float>() + (size_t)b * nh * d * d, p0,
-                          core_pf_.get<float>(), CORE_, nh, d, stream_),
-                      "deltanet prefill");
+                float* cs = conv_state_[dn_i].get<float>() + (size_t)b * 3 * C;
+                float* S = dn_state_[dn_i].get<float>() + (size_t)b * nh * d * d;
+                if (chunked_deltanet)
+                    check(qlm_deltanet_prefill_chunked(
+                              proj_pf_.get<float>(), Pmax, rows, cs, w.conv_wt.get<float>(),
+                              w.A_log.get<float>(), w.dt_bias.get<float>(),
+                              w.dn_norm.get<float>(), S, p0, core_pf_.get<float>(), CORE_, nh, d,
+                              dn_pf_work_.get(), dn_pf_work_.bytes(), stream_),
+                          "deltanet prefill");
+                else
+                    check(qlm_deltanet_prefill(proj_pf_.get<float>(), Pmax, rows, cs,
+                                               w.conv_wt.get<float>(), w.A_log.get<float>(),
+                                               w.dt_bias.get<float>(), w.dn_norm.get<float>(), S,
+                                               p0, core_pf_.get<float>(), CORE_, nh, d, stream_),
+                          "deltanet prefill");
                 Tensor core({rows, HD_}, core_pf_.get<float>());
                 core.strides = {CORE_, 1};
                 math::matmul_residual(core, w.dn_out.view(), hx);
@@ -565,14 +576,14 @@ void DecoderModel::tokens(int b, int first, int count, int* out) const {
 }
 
 void DecoderModel::generate(const int* prompts, int B, int n, int n_new, int* out, GenStats* st,
-                            bool use_graph, bool batched_prefill) {
+                            bool use_graph, int prefill_mode) {
     if (n_new < 0) throw std::runtime_error("generate: negative token count");
     if (n + n_new - 1 > max_seq_)
         throw std::runtime_error("context length exceeded max_seq_len (" + std::to_string(max_seq_) +
                                  ")");
     const double t0 = now_s();
-    start(prompts, B, n, batched_prefill);
-    if (!batched_prefill) steps(n - 1, use_graph);
+    start(prompts, B, n, prefill_mode);
+    if (prefill_mode == kPrefillSteps) steps(n - 1, use_graph);
     check(qlm_stream_sync(stream_), "sync");
     const double t1 = now_s();
     steps(n_new, use_graph);

@@ -82,11 +82,14 @@ class DecoderModel {
     // sequences, positions 0..n-2 of the prompt are forwarded as prefill,
     // then n_new steps each forward the newest token and append the argmax.
     // prompts [B, n], out [B, n_new]. use_graph = false launches eagerly.
-    // batched_prefill: positions 0..n-2 go through the prefill kernels (the
-    // reference's forward_batch: every layer over all prompt rows at once);
-    // otherwise each is forwarded by its own decode step.
+    // Prefill of prompt positions 0..n-2: kPrefillSteps forwards each by its
+    // own decode step; the batched modes run every layer over all prompt rows
+    // at once (the reference's forward_batch), with the DeltaNet recurrence
+    // in the chunked matrix-core form or row by row (bit-identical to steps).
+    enum PrefillMode { kPrefillSteps = 0, kPrefillChunked = 1, kPrefillRows = 2 };
+    // prefill_mode (PrefillMode) selects how positions 0..n-2 are forwarded.
     void generate(const int* prompts, int B, int n, int n_new, int* out, GenStats* st,
-                  bool use_graph = true, bool batched_prefill = true);
+                  bool use_graph = true, int prefill_mode = kPrefillChunked);
 
     // Stepwise form of generate() for benchmarking: start() resets the state
     // and installs B prompts of length n (with batched_prefill it also runs
@@ -95,7 +98,7 @@ class DecoderModel {
     // (without batched_prefill the first n-1 are prompt forwards) and returns
     // the GPU time in milliseconds measured with events on the engine stream;
     // tokens() reads back count tokens of sequence b from position first.
-    double start(const int* prompts, int B, int n, bool batched_prefill = false);
+    double start(const int* prompts, int B, int n, int prefill_mode = kPrefillSteps);
     double steps(int k, bool use_graph = true);
     void tokens(int b, int first, int count, int* out) const;
 
@@ -111,7 +114,7 @@ class DecoderModel {
 
    private:
     void enqueue_step(int B);
-    void prefill(int b, int n);
+    void prefill(int b, int n, bool chunked_deltanet);
     void ensure_prefill_buffers(int rows);
     size_t matmul_workspace(int M) const;
     void embed_current(int B);
@@ -142,7 +145,7 @@ class DecoderModel {
     DeviceBuffer h_, proj_, core_, act_, logits_, argmax_work_, attn_work_, tail_work_;
     DeviceBuffer mm_work_;  // workspace of the matrix-core matmuls (M > 4)
     // prefill activations for up to pf_rows_ prompt rows per chunk
-    DeviceBuffer hx_pf_, proj_pf_, core_pf_, act_pf_, gqa_pf_work_;
+    DeviceBuffer hx_pf_, proj_pf_, core_pf_, act_pf_, gqa_pf_work_, dn_pf_work_;
     int pf_rows_ = 0;
     DeviceBuffer staging_;
 

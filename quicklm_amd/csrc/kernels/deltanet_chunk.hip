@@ -1,0 +1,424 @@
+// Chunked prefill of a Gated DeltaNet layer (one sequence, T prompt rows at
+// positions p0 .. p0+T-1). The reference runs the recurrence row by row
+// (Qwen3_5GatedDeltaNet::forward_chunk, attention.cpp:600-758); this is the
+// same recurrence in the chunked "WY" form, with every contraction on the
+// fp32 matrix cores (v_mfma_f32_16x16x4f32).
+//
+// Per head, with the state S [d_k, d_v] before a chunk of C = 64 rows,
+// alpha_t = log-decay, G_t = sum_{s<=t} alpha_s within the chunk,
+// gamma_t = exp(G_t), beta_t the write strength and q, k L2-normalised:
+//   S_t = gamma_t S + sum_{s<=t} (gamma_t/gamma_s) k_s w_s^T, where
+//   (I + A) W = diag(beta) (V - diag(gamma) K S),
+//   A[t][s] = beta_t (gamma_t/gamma_s) (k_t . k_s) for s < t.
+// With T = (I + A)^-1 diag(beta): U = T V, Wk = T diag(gamma) K, W = U - Wk S,
+//   o_t = (gamma_t (Q S)[t] + sum_{s<=t} (gamma_t/gamma_s)(q_t . k_s) w_s) / sqrt(d),
+//   S_next = gamma_end S + K^T diag(gamma_end/gamma) W.
+// Every decay factor is exp of a non-positive number (ratios, never 1/gamma).
+//
+// Kernels (one stream, in order):
+//   k_dn_chunk_prep   per (row, head): conv taps from the prompt rows or the
+//                     ring (positions before p0), SiLU, L2 norms, gates --
+//                     the decode step's arithmetic;
+//   k_dn_chunk_intra  per (chunk, head): K K^T on the matrix cores, the
+//                     triangular solve for T (one column per lane, unrolled),
+//                     U, Wk and the masked, decayed Q K^T on the matrix cores;
+//   k_dn_chunk_inter  per (head, 16 value columns): chunks in order; W, O and
+//                     the state update on the matrix cores, the state slice
+//                     living in the accumulators;
+//   k_dn_chunk_post   per (row, head): head RMSNorm + SiLU(z) gate (decode
+//                     arithmetic) and the conv ring rows of the last positions.
+
+#include "common.hpp"
+
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kD = 128;      // head dim (d_k = d_v)
+constexpr int kC = 64;       // chunk rows
+constexpr int KP = kD + 4;   // padded LDS row of a [64][128] tile
+constexpr int TP = kC + 4;   // padded LDS row of a [64][64] tile
+constexpr int CB = 16;       // value columns per inter-chunk workgroup
+constexpr int SP = CB + 4;   // padded LDS row of a [*][16] tile
+
+// D += A B on a 16x16 tile, K = 4: lane l supplies A[l%16][l/16] and
+// B[l/16][l%16]; it holds D[(l/16)*4 + i][l%16].
+__device__ __forceinline__ f32x4 mma(float a, float b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ size_t rix(int t, int h, int H) { return ((size_t)t * H + h) * kD; }
+
+__global__ __launch_bounds__(3 * kD) void k_dn_chunk_prep(
+    const float* __restrict__ proj, int ldp, int T, const float* __restrict__ conv_state,
+    const float* __restrict__ wt, const float* __restrict__ A_log,
+    const float* __restrict__ dt_bias, int p0, int H, float* __restrict__ qn,
+    float* __restrict__ kn, float* __restrict__ vv, float* __restrict__ alpha,
+    float* __restrict__ beta) {
+    __shared__ float sq[kD], sk[kD];
+    const int t = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int HD = H * kD, C = 3 * HD;
+    const int sec = tid / kD, tt = tid % kD, ch = sec * HD + h * kD + tt;
+    float xs[3];
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+        const int r = t - 3 + j;
+        if (r >= 0) {
+            xs[j] = proj[(size_t)r * ldp + ch];
+        } else {
+            // positions before p0 come from the ring, row (position mod 3), as
+            // the decode step reads it (zero rows on a fresh sequence)
+            const int row = ((p0 + r) % 3 + 3) % 3;
+            xs[j] = conv_state[(size_t)row * C + ch];
+        }
+    }
+    const float x = proj[(size_t)t * ldp + ch];
+    float acc = 0.0f;
+    acc = nc_add_mul(acc, xs[0], wt[ch]);
+    acc = nc_add_mul(acc, xs[1], wt[(size_t)C + ch]);
+    acc = nc_add_mul(acc, xs[2], wt[(size_t)2 * C + ch]);
+    acc = nc_add_mul(acc, x, wt[(size_t)3 * C + ch]);
+    const float y = silu_f(acc);
+    if (sec == 0) sq[tt] = y;
+    else if (sec == 1) sk[tt] = y;
+    else vv[rix(t, h, H) + tt] = y;
+    __syncthreads();
+    if (wave < 2) {
+        const float* v = wave == 0 ? sq : sk;
+        const float a0 = v[lane], a1 = v[lane + 64];
+        float ss = fmaf(a0, a0, a1 * a1);
+        ss = wave_sum(ss);
+        const float nrm = sqrtf(ss + 1e-6f);
+        float* dst = (wave == 0 ? qn : kn) + rix(t, h, H);
+        dst[lane] = a0 / nrm;
+        dst[lane + 64] = a1 / nrm;
+    } else if (wave == 2 && lane == 0) {
+        const float* pr = proj + (size_t)t * ldp;
+        const float dt = pr[4 * HD + H + h] + dt_bias[h];
+        const float sp = dt > 20.0f ? dt : log1pf(expf(dt));
+        alpha[(size_t)t * H + h] = -expf(A_log[h]) * sp;
+        beta[(size_t)t * H + h] = 1.0f / (1.0f + expf(-pr[4 * HD + h]));
+    }
+}
+
+__global__ __launch_bounds__(256) void k_dn_chunk_intra(
+    const float* __restrict__ qn, const float* __restrict__ kn, const float* __restrict__ vv,
+    const float* __restrict__ alpha, const float* __restrict__ beta, int T, int H,
+    float* __restrict__ U, float* __restrict__ Wk, float* __restrict__ Mq,
+    float* __restrict__ Gc) {
+    __shared__ __attribute__((aligned(16))) float Ks[kC * KP];
+    __shared__ float Ts[kC * TP];
+    __shared__ float gs[kC], bs[kC], gam[kC];
+    const int c = blockIdx.x, h = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l16 = lane & 15, l4 = lane >> 4;
+    const int t0 = c * kC;
+    const int nt = min(kC, T - t0);
+
+    for (int i = tid; i < kC * (kD / 4); i += 256) {
+        const int r = i / (kD / 4), c4 = i % (kD / 4);
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (r < nt) v = *reinterpret_cast<const float4*>(kn + rix(t0 + r, h, H) + c4 * 4);
+        *reinterpret_cast<float4*>(&Ks[r * KP + c4 * 4]) = v;
+    }
+    if (tid < kC) {
+        gs[tid] = tid < nt ? alpha[(size_t)(t0 + tid) * H + h] : 0.0f;
+        bs[tid] = tid < nt ? beta[(size_t)(t0 + tid) * H + h] : 0.0f;
+    }
+    __syncthreads();
+    if (tid == 0) {  // cumulative log-decay, in row order
+        float a = 0.0f;
+        for (int t = 0; t < kC; ++t) {
+            a += gs[t];
+            gs[t] = a;
+        }
+    }
+    __syncthreads();
+    if (tid < kC) {
+        gam[tid] = expf(gs[tid]);
+        if (tid < nt) Gc[(size_t)(t0 + tid) * H + h] = gs[tid];
+    }
+
+    // A = beta_t (gamma_t/gamma_s) K K^T, strictly lower; wave w: rows 16w..16w+15
+    {
+        f32x4 acc[4];
+#pragma unroll
+        for (int tc = 0; tc < 4; ++tc) acc[tc] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int k0 = 0; k0 < kD; k0 += 4) {
+            const float a = Ks[(wave * 16 + l16) * KP + k0 + l4];
+#pragma unroll
+            for (int tc = 0; tc < 4; ++tc) acc[tc] = mma(a, Ks[(tc * 16 + l16) * KP + k0 + l4], acc[tc]);
+        }
+#pragma unroll
+        for (int tc = 0; tc < 4; ++tc)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int t = wave * 16 + l4 * 4 + i, s = tc * 16 + l16;
+                Ts[t * TP + s] = s < t ? bs[t] * expf(gs[t] - gs[s]) * acc[tc][i] : 0.0f;
+            }
+    }
+    __syncthreads();
+
+    // T = (I + A)^-1 diag(beta) by forward substitution; lane s < 64 owns
+    // column s (T[t][s] = beta_t [t == s] - sum_{r<t} A[t][r] T[r][s]).
+    float col[kC];
+    if (tid < kC) {
+#pragma unroll
+        for (int t = 0; t < kC; ++t) {
+            float v = t == tid ? bs[t] : 0.0f;
+#pragma unroll
+            for (int r = 0; r < t; ++r) v = fmaf(-Ts[t * TP + r], col[r], v);
+            col[t] = v;
+        }
+    }
+    __syncthreads();  // every read of A is done before T overwrites it
+    if (tid < kC) {
+#pragma unroll
+        for (int t = 0; t < kC; ++t) Ts[t * TP + tid] = col[t];
+    }
+    __syncthreads();
+
+    // Wk = T diag(gamma) K and U = T V: wave w rows 16w.., 8 column tiles
+    {
+        f32x4 wk[8], u[8];
+#pragma unroll
+        for (int ct = 0; ct < 8; ++ct) {
+            wk[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+            u[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+        for (int k0 = 0; k0 < kC; k0 += 4) {
+            const int s = k0 + l4;
+            const float tv = Ts[(wave * 16 + l16) * TP + s];
+            const float tg = tv * gam[s];
+            const float* vrow = vv + rix(t0 + (s < nt ? s : 0), h, H);
+#pragma unroll
+            for (int ct = 0; ct < 8; ++ct) {
+                wk[ct] = mma(tg, Ks[s * KP + ct * 16 + l16], wk[ct]);
+                u[ct] = mma(tv, s < nt ? vrow[ct * 16 + l16] : 0.0f, u[ct]);
+            }
+        }
+#pragma unroll
+        for (int ct = 0; ct < 8; ++ct)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int t = wave * 16 + l4 * 4 + i;
+                if (t < nt) {
+                    Wk[rix(t0 + t, h, H) + ct * 16 + l16] = wk[ct][i];
+                    U[rix(t0 + t, h, H) + ct * 16 + l16] = u[ct][i];
+                }
+            }
+    }
+
+    // Mq[t][s] = (gamma_t/gamma_s) q_t . k_s for s <= t
+    {
+        f32x4 m[4];
+#pragma unroll
+        for (int tc = 0; tc < 4; ++tc) m[tc] = f32x4{0.f, 0.f, 0.f, 0.f};
+        const int tq = wave * 16 + l16;
+        const float* qrow = qn + rix(t0 + (tq < nt ? tq : 0), h, H);
+        for (int k0 = 0; k0 < kD; k0 += 4) {
+            const float a = tq < nt ? qrow[k0 + l4] : 0.0f;
+#pragma unroll
+            for (int tc = 0; tc < 4; ++tc) m[tc] = mma(a, Ks[(tc * 16 + l16) * KP + k0 + l4], m[tc]);
+        }
+        float* mq = Mq + ((size_t)c * H + h) * kC * kC;
+#pragma unroll
+        for (int tc = 0; tc < 4; ++tc)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int t = wave * 16 + l4 * 4 + i, s = tc * 16 + l16;
+                mq[t * kC + s] = (s <= t && t < nt) ? expf(gs[t] - gs[s]) * m[tc][i] : 0.0f;
+            }
+    }
+}
+
+__global__ __launch_bounds__(256) void k_dn_chunk_inter(
+    const float* __restrict__ qn, const float* __restrict__ kn, const float* __restrict__ U,
+    const float* __restrict__ Wk, const float* __restrict__ Mq, const float* __restrict__ Gc,
+    int T, int H, float* __restrict__ state, float* __restrict__ O) {
+    __shared__ float Ss[kD * SP];
+    __shared__ float Ws[kC * SP];
+    __shared__ float gs[kC];
+    const int h = blockIdx.x, jb = blockIdx.y * CB;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l16 = lane & 15, l4 = lane >> 4;
+    float* Sg = state + (size_t)h * kD * kD;
+    const float rsd = 1.0f / sqrtf((float)kD);
+
+    // state rows 32w .. 32w+31 (two 16-row tiles), columns jb .. jb+15
+    f32x4 sacc[2];
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = (2 * wave + tt) * 16 + l4 * 4 + i;
+            sacc[tt][i] = Sg[(size_t)row * kD + jb + l16];
+            Ss[row * SP + l16] = sacc[tt][i];
+        }
+    __syncthreads();
+
+    const int nch = (T + kC - 1) / kC;
+    for (int c = 0; c < nch; ++c) {
+        const int t0 = c * kC;
+        const int nt = min(kC, T - t0);
+        if (tid < kC) gs[tid] = tid < nt ? Gc[(size_t)(t0 + tid) * H + h] : 0.0f;
+        const int tr = wave * 16 + l16;  // A-operand row of this wave's tile
+        const bool tv = tr < nt;
+        // W = U - Wk S: wave w rows 16w..16w+15
+        f32x4 w = f32x4{0.f, 0.f, 0.f, 0.f};
+        {
+            const float* wkr = Wk + rix(t0 + (tv ? tr : 0), h, H);
+            for (int k0 = 0; k0 < kD; k0 += 4)
+                w = mma(tv ? wkr[k0 + l4] : 0.0f, Ss[(k0 + l4) * SP + l16], w);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int t = wave * 16 + l4 * 4 + i;
+            Ws[t * SP + l16] = t < nt ? U[rix(t0 + t, h, H) + jb + l16] - w[i] : 0.0f;
+        }
+        __syncthreads();
+        // O = (gamma_t (Q S) + Mq W) / sqrt(d)
+        {
+            f32x4 qs = f32x4{0.f, 0.f, 0.f, 0.f}, mw = f32x4{0.f, 0.f, 0.f, 0.f};
+            const float* qr = qn + rix(t0 + (tv ? tr : 0), h, H);
+            for (int k0 = 0; k0 < kD; k0 += 4)
+                qs = mma(tv ? qr[k0 + l4] : 0.0f, Ss[(k0 + l4) * SP + l16], qs);
+            const float* mr = Mq + (((size_t)c * H + h) * kC + tr) * kC;
+            for (int k0 = 0; k0 < kC; k0 += 4)
+                mw = mma(tv ? mr[k0 + l4] : 0.0f, Ws[(k0 + l4) * SP + l16], mw);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int t = wave * 16 + l4 * 4 + i;
+                if (t < nt)
+                    O[rix(t0 + t, h, H) + jb + l16] = (expf(gs[t]) * qs[i] + mw[i]) * rsd;
+            }
+        }
+        // S = gamma_end S + K^T diag(gamma_end / gamma) W
+        {
+            const float gend = gs[nt - 1];
+            const float ge = expf(gend);
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) sacc[tt][i] *= ge;
+            for (int k0 = 0; k0 < kC; k0 += 4) {
+                const int t = k0 + l4;
+                const bool ok = t < nt;
+                const float b = ok ? Ws[t * SP + l16] * expf(gend - gs[t]) : 0.0f;
+                const float* kr = kn + rix(t0 + (ok ? t : 0), h, H);
+#pragma unroll
+                for (int tt = 0; tt < 2; ++tt)
+                    sacc[tt] = mma(ok ? kr[(2 * wave + tt) * 16 + l16] : 0.0f, b, sacc[tt]);
+            }
+        }
+        __syncthreads();  // every read of Ss and Ws of this chunk is done
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) Ss[((2 * wave + tt) * 16 + l4 * 4 + i) * SP + l16] = sacc[tt][i];
+        __syncthreads();
+    }
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            Sg[(size_t)((2 * wave + tt) * 16 + l4 * 4 + i) * kD + jb + l16] = sacc[tt][i];
+}
+
+__global__ __launch_bounds__(kD) void k_dn_chunk_post(
+    const float* __restrict__ O, const float* __restrict__ proj, int ldp, int T,
+    const float* __restrict__ norm_w, float* __restrict__ out, int ldo, int H,
+    float* __restrict__ conv_state, int p0) {
+    __shared__ float sc[2];
+    const int t = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int HD = H * kD, C = 3 * HD;
+    const float* pr = proj + (size_t)t * ldp;
+    const float o = O[rix(t, h, H) + tid];
+    const float ss = wave_sum(o * o);
+    if (lane == 0) sc[wave] = ss;
+    __syncthreads();
+    const float tot = sc[0] + sc[1];
+    const float sn = 1.0f / sqrtf(tot / (float)kD + 1e-6f);
+    const float r = (o * sn) * norm_w[tid];
+    out[(size_t)t * ldo + h * kD + tid] = r * silu_f(pr[3 * HD + h * kD + tid]);
+    if (t >= T - 3) {  // ring row of position p0 + t keeps its conv input
+        const int row = (p0 + t) % 3;
+        for (int i = tid; i < 3 * kD; i += kD) {
+            const int ch = (i / kD) * HD + h * kD + i % kD;
+            conv_state[(size_t)row * C + ch] = pr[ch];
+        }
+    }
+}
+
+size_t a256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+struct ChunkWork {
+    float *qn, *kn, *vv, *U, *Wk, *O, *alpha, *beta, *Gc, *Mq;
+    size_t bytes;
+};
+
+ChunkWork carve(void* base, int T, int H) {
+    ChunkWork w{};
+    const size_t rows = a256((size_t)T * H * kD * sizeof(float));
+    const size_t sc = a256((size_t)T * H * sizeof(float));
+    const int nch = (T + kC - 1) / kC;
+    char* p = reinterpret_cast<char*>(base);
+    auto take = [&](size_t b) {
+        float* r = reinterpret_cast<float*>(p);
+        if (p) p += b;
+        return r;
+    };
+    w.qn = take(rows);
+    w.kn = take(rows);
+    w.vv = take(rows);
+    w.U = take(rows);
+    w.Wk = take(rows);
+    w.O = take(rows);
+    w.alpha = take(sc);
+    w.beta = take(sc);
+    w.Gc = take(sc);
+    w.Mq = take(a256((size_t)nch * H * kC * kC * sizeof(float)));
+    w.bytes = 6 * rows + 3 * sc + a256((size_t)nch * H * kC * kC * sizeof(float));
+    return w;
+}
+
+}  // namespace
+
+extern "C" size_t qlm_deltanet_chunk_workspace_bytes(int T, int H, int d) {
+    if (T <= 0 || H <= 0 || d != kD) return 0;
+    return carve(nullptr, T, H).bytes;
+}
+
+extern "C" int qlm_deltanet_prefill_chunked(const float* proj, int ldp, int T, float* conv_state,
+                                            const float* conv_w_t, const float* A_log,
+                                            const float* dt_bias, const float* norm_w,
+                                            float* state, int p0, float* out, int ldo, int H,
+                                            int d, void* work, size_t work_bytes,
+                                            void* stream) {
+    if (!proj || !conv_state || !conv_w_t || !A_log || !dt_bias || !norm_w || !state || !out ||
+        !work || T <= 0 || H <= 0 || p0 < 0)
+        return QLM_ERR_ARG;
+    if (d != kD) return QLM_ERR_SHAPE;
+    if (ldp < 4 * H * d + 2 * H || ldo < H * d) return QLM_ERR_SHAPE;
+    const ChunkWork w = carve(work, T, H);
+    if (work_bytes < w.bytes || ((uintptr_t)work & 255u)) return QLM_ERR_ARG;
+    hipStream_t st = as_stream(stream);
+    const int nch = (T + kC - 1) / kC;
+    hipLaunchKernelGGL(k_dn_chunk_prep, dim3(T, H), dim3(3 * kD), 0, st, proj, ldp, T, conv_state,
+                       conv_w_t, A_log, dt_bias, p0, H, w.qn, w.kn, w.vv, w.alpha, w.beta);
+    int rc = qlm_launch_status();
+    if (rc != QLM_OK) return rc;
+    hipLaunchKernelGGL(k_dn_chunk_intra, dim3(nch, H), dim3(256), 0, st, w.qn, w.kn, w.vv,
+                       w.alpha, w.beta, T, H, w.U, w.Wk, w.Mq, w.Gc);
+    rc = qlm_launch_status();
+    if (rc != QLM_OK) return rc;
+    hipLaunchKernelGGL(k_dn_chunk_inter, dim3(H, kD / CB), dim3(256), 0, st, w.qn, w.kn, w.U,
+                       w.Wk, w.Mq, w.Gc, T, H, state, w.O);
+    rc = qlm_launch_status();
+    if (rc != QLM_OK) return rc;
+    hipLaunchKernelGGL(k_dn_chunk_post, dim3(T, H), dim3(kD), 0, st, w.O, proj, ldp, T, norm_w,
+                       out, ldo, H, conv_state, p0);
+    return qlm_launch_status();
+}

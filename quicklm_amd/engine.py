@@ -73,27 +73,41 @@ class Engine:
         _check(lib().qlm_engine_forward(self.h, token, pos, lg.ctypes.data))
         return lg
 
+    PREFILL_STEPS, PREFILL_CHUNKED, PREFILL_ROWS = 0, 1, 2
+
     def generate(self, prompts: np.ndarray, n_new: int, use_graph: bool = True,
-                 batched_prefill: bool = True):
+                 batched_prefill=True):
         """prompts [B, n] int32 -> (tokens [B, n_new], prefill_s, decode_s).
-        batched_prefill False forwards each prompt position by a decode step."""
+        batched_prefill: True (or PREFILL_CHUNKED) = batched prefill with the
+        chunked DeltaNet form; PREFILL_ROWS = batched with the row-by-row
+        recurrence; False = each prompt position forwarded by a decode step."""
+        mode = self._mode(batched_prefill)
         p = np.ascontiguousarray(np.atleast_2d(prompts), np.int32)
         B, n = p.shape
         out = np.empty((B, n_new), np.int32)
         pre, dec = C.c_double(), C.c_double()
         _check(lib().qlm_engine_generate(self.h, p.ctypes.data, B, n, n_new, out.ctypes.data,
                                          C.byref(pre), C.byref(dec), 1 if use_graph else 0,
-                                         1 if batched_prefill else 0))
+                                         mode))
         return out, pre.value, dec.value
 
-    def start(self, prompts: np.ndarray, batched_prefill: bool = False) -> float:
-        """Install prompts; with batched_prefill also prefill positions 0..n-2
-        and return its wall time in seconds (the next step forwards n-1)."""
+    @staticmethod
+    def _mode(batched_prefill) -> int:
+        if batched_prefill is True:
+            return 1
+        if batched_prefill is False:
+            return 0
+        return int(batched_prefill)
+
+    def start(self, prompts: np.ndarray, batched_prefill=False) -> float:
+        """Install prompts; with batched_prefill (as in generate) also prefill
+        positions 0..n-2 and return its wall time in seconds (the next step
+        forwards n-1)."""
         p = np.ascontiguousarray(np.atleast_2d(prompts), np.int32)
         self._prompts = p
         pre = C.c_double()
         _check(lib().qlm_engine_start(self.h, p.ctypes.data, p.shape[0], p.shape[1],
-                                      1 if batched_prefill else 0, C.byref(pre)))
+                                      self._mode(batched_prefill), C.byref(pre)))
         return pre.value
 
     def steps(self, k: int, use_graph: bool = True) -> float:

@@ -51,6 +51,9 @@ _SIGS = {
     "qlm_gemv_i8": (_i, [_vp, _i, _vp, _vp, _i, _vp, _i, _i, _i, _i, _vp]),
     "qlm_deltanet_prefill": (_i, [_vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp, _i, _i, _i,
                                   _vp]),
+    "qlm_deltanet_chunk_workspace_bytes": (_sz, [_i, _i, _i]),
+    "qlm_deltanet_prefill_chunked": (_i, [_vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp, _i,
+                                          _i, _i, _vp, _sz, _vp]),
     "qlm_gqa_prefill_workspace_bytes": (_sz, [_i, _i, _i]),
     "qlm_gqa_prefill": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _i, _vp, _vp, _i, _i, _i, _vp, _i, _i,
                              _i, _i, _i, _vp, _vp]),

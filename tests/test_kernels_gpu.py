@@ -500,6 +500,45 @@ def test_deltanet_prefill(hip, orc, rng, p0, T):
                           dconv2.to_numpy(conv.shape, np.float32))
 
 
+@pytest.mark.parametrize("p0,T", [(0, 64), (0, 200), (5, 130), (1, 2), (0, 1024)])
+def test_deltanet_prefill_chunked(hip, orc, rng, p0, T):
+    """Chunked (WY, matrix-core) prefill == the row-by-row recurrence: outputs
+    against the oracle, state and conv ring against the sequential kernel
+    (ragged last chunk, continuation from p0 > 0, T < 3)."""
+    H, d = 16, 128
+    HD = H * d
+    ldp = 4 * HD + 2 * H
+    wt = (rng.standard_normal((4, 3 * HD)) * 0.3).astype(np.float32)
+    A_log = np.log(rng.uniform(1, 16, H)).astype(np.float32)
+    dtb = (rng.standard_normal(H) * 0.5 - 4).astype(np.float32)
+    nw = (1 + rng.standard_normal(d) * 0.02).astype(np.float32)
+    conv = (rng.standard_normal((3, 3 * HD)) * (0.5 if p0 else 0.0)).astype(np.float32)
+    S = (rng.standard_normal((H, d, d)) * (0.01 if p0 else 0.0)).astype(np.float32)
+    proj = (rng.standard_normal((T, ldp)) * 0.6).astype(np.float32)
+    dwt, dA, ddt, dnw, dproj = (dev(hip, a) for a in (wt, A_log, dtb, nw, proj))
+    # sequential kernel (bit-identical to decode steps) as the state reference
+    dconv1, dS1, do1 = dev(hip, conv), dev(hip, S), hip.DeviceBuffer(T * HD * 4)
+    hip.call("qlm_deltanet_prefill", dproj, ldp, T, dconv1, dwt, dA, ddt, dnw, dS1, p0, do1, HD,
+             H, d, None)
+    nbytes = hip.lib().qlm_deltanet_chunk_workspace_bytes(T, H, d)
+    work = hip.DeviceBuffer(nbytes)
+    dconv2, dS2, do2 = dev(hip, conv), dev(hip, S), hip.DeviceBuffer(T * HD * 4)
+    say("deltanet_prefill_chunked", p0, T)
+    hip.call("qlm_deltanet_prefill_chunked", dproj, ldp, T, dconv2, dwt, dA, ddt, dnw, dS2, p0,
+             do2, HD, H, d, work, nbytes, None)
+    out_seq = do1.to_numpy((T, HD), np.float32)
+    out = do2.to_numpy((T, HD), np.float32)
+    assert rel_err(out, out_seq) < 1e-4
+    assert rel_err(dS2.to_numpy(S.shape, np.float32), dS1.to_numpy(S.shape, np.float32)) < 1e-4
+    assert np.array_equal(dconv2.to_numpy(conv.shape, np.float32),
+                          dconv1.to_numpy(conv.shape, np.float32))
+    if T <= 200:  # and against the oracle's own recurrence
+        conv_ref, S_ref = conv.copy(), S.copy()
+        ref = np.stack([orc.deltanet_core(proj[t], conv_ref, (p0 + t) % 3, wt, A_log, dtb, nw,
+                                          S_ref, H, d) for t in range(T)])
+        assert rel_err(out, ref) < 1e-4
+
+
 @pytest.mark.parametrize("n_q,n_kv,hd,rot,gated,p0,T", [(16, 4, 128, 32, 1, 0, 300),
                                                         (16, 4, 128, 32, 1, 37, 90),
                                                         (16, 2, 256, 64, 0, 10, 40)])

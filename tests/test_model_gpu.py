@@ -77,10 +77,11 @@ def test_teacher_forced_logits(engine, golden):
     assert worst < 1e-3
 
 
-@pytest.mark.parametrize("batched_prefill", [True, False])
+@pytest.mark.parametrize("batched_prefill", [True, 2, False])
 def test_tiny_greedy_matches_reference(engine, golden, batched_prefill):
     """The reference's 64-token greedy stream, with the prompt prefilled by
-    the batched prefill kernels or forwarded one decode step per token."""
+    the batched prefill (chunked or row-by-row DeltaNet recurrence) or
+    forwarded one decode step per token."""
     out, pre, dec = engine.generate(golden["prompt"][None, :], 64,
                                     batched_prefill=batched_prefill)
     toks = golden["tokens"]
@@ -114,17 +115,19 @@ def test_batch_rows_equal_single(engine, golden):
 
 
 @pytest.mark.parametrize("n", [128, 1300])
-def test_batched_prefill_equals_stepwise(engine, golden, n):
-    """Batched prefill (matrix-core projections, prefill DeltaNet and
-    attention kernels; 1300 rows span two 1024-row chunks) leaves the model
-    where n-1 decode steps leave it: same tokens, logits within 1e-4."""
+@pytest.mark.parametrize("mode", [True, 2])
+def test_batched_prefill_equals_stepwise(engine, golden, n, mode):
+    """Batched prefill (matrix-core projections, chunked or row-by-row
+    DeltaNet, prefill attention; 1300 rows span two 1024-row chunks) leaves
+    the model where n-1 decode steps leave it: same tokens, logits within
+    1e-4."""
     rng = np.random.default_rng(11)
     p = golden["prompt"][:n] if n <= 128 else rng.integers(0, 151936, n).astype(np.int32)
-    a, pre_a, _ = engine.generate(p[None, :], 8, batched_prefill=True)
+    a, pre_a, _ = engine.generate(p[None, :], 8, batched_prefill=mode)
     la = engine.last_logits(0)
     b, pre_b, _ = engine.generate(p[None, :], 8, batched_prefill=False)
     lb = engine.last_logits(0)
-    say(f"n={n}: batched prefill {pre_a:.3f}s, stepwise {pre_b:.3f}s")
+    say(f"n={n} mode={mode}: batched prefill {pre_a:.3f}s, stepwise {pre_b:.3f}s")
     assert np.array_equal(a, b)
     assert float(np.abs(la - lb).max() / np.abs(lb).max()) < 1e-4
 
