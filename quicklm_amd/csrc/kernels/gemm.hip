@@ -351,6 +351,8 @@ __global__ __launch_bounds__(kThreads) void k_mm_i8(const float* __restrict__ x,
 // is the output itself.
 constexpr int kSkRows = 64;
 constexpr int kSkKc = 128;
+// chunks in flight per workgroup (register ring), by activation tiles
+constexpr int sk_ring(int tm) { return tm <= 2 ? 2 : 1; }
 
 template <int TM, bool ROWSCALE, bool NORM>
 __global__ __launch_bounds__(kThreads) void k_mm_i8_sk(
@@ -363,6 +365,7 @@ __global__ __launch_bounds__(kThreads) void k_mm_i8_sk(
     constexpr int XV = BM * KC / 4, WV = kSkRows * KC / 16;
     constexpr int XPT = (XV + kThreads - 1) / kThreads;
     constexpr int WPT = (WV + kThreads - 1) / kThreads;
+    constexpr int CPF = sk_ring(TM);
     __shared__ __attribute__((aligned(16))) unsigned short xs_hi[BM * XP];
     __shared__ __attribute__((aligned(16))) unsigned short xs_lo[BM * XP];
     __shared__ __attribute__((aligned(16))) unsigned short ws[kSkRows * WP];
@@ -376,12 +379,15 @@ __global__ __launch_bounds__(kThreads) void k_mm_i8_sk(
     const int ncol = n0 + wave * 16 + (lane & 15);      // this lane's weight row (output column)
     const int nrow = ncol < NR ? ncol : NR - 1;
 
-    float4 xr[XPT];
-    float4 gr[NORM ? XPT : 1];
-    float rr[NORM ? XPT : 1];
-    int4 wr[WPT];
-    float4 sr;  // group scales of this lane's row for the chunk's 4 groups
-    auto load_chunk = [&](int c) {
+    // a ring of CPF chunk buffers in registers: a chunk's registers are
+    // refilled with chunk c + CPF as soon as chunk c is staged to LDS, so a
+    // workgroup's whole K slice (<= CPF chunks) is requested at once
+    float4 xr[CPF][XPT];
+    float4 gr[CPF][NORM ? XPT : 1];
+    float rr[CPF][NORM ? XPT : 1];
+    int4 wr[CPF][WPT];
+    float4 sr[CPF];  // group scales of this lane's row for a chunk's 4 groups
+    auto load_chunk = [&](int c, int j) {
         const int k0 = kb + c * KC;
 #pragma unroll
         for (int u = 0; u < XPT; ++u) {
@@ -389,10 +395,10 @@ __global__ __launch_bounds__(kThreads) void k_mm_i8_sk(
             if (i < XV) {
                 const int r = i / (KC / 4), c4 = i % (KC / 4);
                 const int m = min(m0 + r, M - 1);
-                xr[u] = *reinterpret_cast<const float4*>(x + (size_t)m * ldx + k0 + c4 * 4);
+                xr[j][u] = *reinterpret_cast<const float4*>(x + (size_t)m * ldx + k0 + c4 * 4);
                 if constexpr (NORM) {
-                    gr[u] = *reinterpret_cast<const float4*>(nw + k0 + c4 * 4);
-                    rr[u] = rs[m];
+                    gr[j][u] = *reinterpret_cast<const float4*>(nw + k0 + c4 * 4);
+                    rr[j][u] = rs[m];
                 }
             }
         }
@@ -402,20 +408,20 @@ __global__ __launch_bounds__(kThreads) void k_mm_i8_sk(
             if (i < WV) {
                 const int r = i / (KC / 16), c16 = i % (KC / 16);
                 const int n = min(n0 + r, NR - 1);
-                wr[u] = *reinterpret_cast<const int4*>(q + (size_t)n * K + k0 + c16 * 16);
+                wr[j][u] = *reinterpret_cast<const int4*>(q + (size_t)n * K + k0 + c16 * 16);
             }
         }
         if constexpr (!ROWSCALE)
-            sr = *reinterpret_cast<const float4*>(sc + (size_t)nrow * nblk + (k0 >> 5));
+            sr[j] = *reinterpret_cast<const float4*>(sc + (size_t)nrow * nblk + (k0 >> 5));
     };
-    auto store_chunk = [&]() {
+    auto store_chunk = [&](int j) {
 #pragma unroll
         for (int u = 0; u < XPT; ++u) {
             const int i = tid + u * kThreads;
             if (i < XV) {
                 const int r = i / (KC / 4), c4 = i % (KC / 4);
-                float4 v = xr[u];
-                if constexpr (NORM) v = norm4(v, rr[u], gr[u]);
+                float4 v = xr[j][u];
+                if constexpr (NORM) v = norm4(v, rr[j][u], gr[j][u]);
                 store_hilo(&xs_hi[r * XP + c4 * 4], &xs_lo[r * XP + c4 * 4], v);
             }
         }
@@ -424,7 +430,7 @@ __global__ __launch_bounds__(kThreads) void k_mm_i8_sk(
             const int i = tid + u * kThreads;
             if (i < WV) {
                 const int r = i / (KC / 16), c16 = i % (KC / 16);
-                store_w16(&ws[r * WP + c16 * 16], wr[u]);
+                store_w16(&ws[r * WP + c16 * 16], wr[j][u]);
             }
         }
     };
@@ -433,13 +439,19 @@ __global__ __launch_bounds__(kThreads) void k_mm_i8_sk(
 #pragma unroll
     for (int tm = 0; tm < TM; ++tm) acc[tm] = f32x4{0.f, 0.f, 0.f, 0.f};
     const int nch = kper / KC;
-    load_chunk(0);
-    for (int c = 0; c < nch; ++c) {
-        const float4 s_cur = sr;
+#pragma unroll
+    for (int j = 0; j < CPF; ++j)
+        if (j < nch) load_chunk(j, j);
+    for (int c0 = 0; c0 < nch; c0 += CPF)
+#pragma unroll
+    for (int j = 0; j < CPF; ++j) {
+        const int c = c0 + j;
+        if (c >= nch) break;  // uniform
+        const float4 s_cur = sr[j];
         __syncthreads();
-        store_chunk();
+        store_chunk(j);
         __syncthreads();
-        if (c + 1 < nch) load_chunk(c + 1);
+        if (c + CPF < nch) load_chunk(c + CPF, j);
         const float sg[4] = {s_cur.x, s_cur.y, s_cur.z, s_cur.w};
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
@@ -490,11 +502,27 @@ __global__ __launch_bounds__(kThreads) void k_mm_reduce(const float* __restrict_
     const int idx = blockIdx.x * kThreads + threadIdx.x;
     if (idx >= M * N) return;
     const int m = idx / N, n = idx % N;
+    // slices summed in order; 8 slices' loads issued together
     float g = 0.0f, u = 0.0f;
-    for (int k = 0; k < ks; ++k) {
-        const float* pr = part + ((size_t)k * M + m) * NR;
-        g += pr[n];
-        if constexpr (EPI == EPI_SWIGLU) u += pr[N + n];
+    const size_t sstride = (size_t)M * NR;
+    const float* pr = part + (size_t)m * NR + n;
+    int k = 0;
+    for (; k + 8 <= ks; k += 8) {
+        float vg[8], vu[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            vg[j] = pr[(k + j) * sstride];
+            vu[j] = EPI == EPI_SWIGLU ? pr[(k + j) * sstride + N] : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            g += vg[j];
+            u += vu[j];
+        }
+    }
+    for (; k < ks; ++k) {
+        g += pr[k * sstride];
+        if constexpr (EPI == EPI_SWIGLU) u += pr[k * sstride + N];
     }
     float* dst = y + (size_t)m * ldy + n;
     if constexpr (EPI == EPI_SWIGLU)
@@ -532,12 +560,16 @@ __global__ __launch_bounds__(kThreads) void k_row_rs(const float* __restrict__ x
     if (threadIdx.x == 0) rs[blockIdx.x] = 1.0f / sqrtf(ss / (float)K + eps);
 }
 
-// K slices for the M <= 64 path: the fewest that give ~1000 workgroups and
-// divide the 128-column chunk count.
+// K slices for the M <= 64 path: the fewest that divide the 128-column
+// chunk count, leave each workgroup at most 4 chunks (one ring) and give at
+// least ~640 workgroups; a tall matrix (>= 1024 row tiles) is one slice.
 int sk_splits(int NR, int K) {
     const int nt = (NR + kSkRows - 1) / kSkRows;
     const int nch = K / kSkKc;
-    const int want = (1024 + nt - 1) / nt;
+    if (nt >= 1024) return 1;
+    const int need_ring = (nch + 3) / 4;
+    const int need_wgs = (640 + nt - 1) / nt;
+    const int want = need_ring > need_wgs ? need_ring : need_wgs;
     for (int d = 1; d <= nch; ++d)
         if (nch % d == 0 && d >= want) return d;
     return nch;
