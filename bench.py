@@ -219,6 +219,8 @@ def main():
                          "rocprofv3 --pmc passes)")
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-gemv", action="store_true")
+    ap.add_argument("--skip-row", action="store_true",
+                    help="skip the batch-1 decode with one scale per output row (int8_row)")
     ap.add_argument("--model-dir", default=None)
     ap.add_argument("--eager", action="store_true",
                     help="launch each step's kernels directly instead of replaying the "
@@ -295,6 +297,16 @@ def main():
                 f"the reference for {match}/{args.cpu_decode} tokens")
             cpu.pop("tokens")
         eng.close()
+
+        rrow = None
+        if not args.skip_row:
+            # the same checkpoint quantised with one fp32 scale per output row
+            erow = Engine(mdir, max_seq_len=max_seq, max_batch=1, precision="int8_row")
+            rrow = run_decode(erow, prompts[:1], args.warmup, args.steps, graph)
+            rrow["weight_bytes"] = erow.weight_bytes
+            erow.close()
+            log(f"batch 1, per-row scales: {rrow['tok_s']:.1f} tok/s "
+                f"({rrow['ms_per_step']:.3f} ms/step), {rrow['weight_bytes'] / 1e9:.3f} GB")
     finally:
         if own_dir:
             import shutil
@@ -336,6 +348,11 @@ def main():
                             "peak": HBM_PEAK_GBS, "unit": "GB/s",
                             "frac": round(wbytes / step_s / 1e9 / HBM_PEAK_GBS, 4),
                             "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / wbytes, 1)},
+        "per_row_scales": None if rrow is None else {
+            "tok_s": round(rrow["tok_s"], 2), "ms_per_step": round(rrow["ms_per_step"], 4),
+            "batch": 1, "scale_group": "row", "weight_bytes": rrow["weight_bytes"],
+            "frac_of_weight_roofline": round(
+                rrow["weight_bytes"] / (rrow["ms_per_step"] / 1000.0) / 1e9 / HBM_PEAK_GBS, 4)},
         "gemv": gemv,
     })
     traffic, traffic_src = None, None

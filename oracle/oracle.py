@@ -351,9 +351,11 @@ class OracleModel:
     modules.hpp:210-241, attention.cpp; fusion off, speculative off).
 
     Weights are read with safetensors' numpy loader and quantised by the
-    oracle quantiser (group 32, the reference's Q8_0)."""
+    oracle quantiser: group 32 (the reference's Q8_0, the default) or
+    group="row" (one scale per output row, G = K)."""
 
-    def __init__(self, model_dir: str, max_seq_len: int = 2048, oracle: Oracle | None = None):
+    def __init__(self, model_dir: str, max_seq_len: int = 2048, oracle: Oracle | None = None,
+                 group=32):
         import json
 
         self.o = oracle or Oracle()
@@ -374,10 +376,16 @@ class OracleModel:
         self.eps = float(c.get("rms_norm_eps", 1e-6))
         self.types = c["layer_types"]
         self.max_seq = max_seq_len
+        self.row = group == "row"
+        if not self.row and group != 32:
+            raise ValueError("group is 32 or 'row'")
         self.q = {}
         self.embed = self._f32("model.embed_tokens.weight")
-        self.lm = self.o.quantize(self.embed, 32)
+        self.lm = self.o.quantize(self.embed, self._g(self.embed.shape[1]))
         self.reset()
+
+    def _g(self, K):
+        return K if self.row else 32
 
     def _f32(self, name):
         a = self.t[name]
@@ -387,7 +395,8 @@ class OracleModel:
 
     def _w(self, name):
         if name not in self.q:
-            self.q[name] = self.o.quantize(np.ascontiguousarray(self.t[name]), 32)
+            w = np.ascontiguousarray(self.t[name])
+            self.q[name] = self.o.quantize(w, self._g(w.shape[1]))
         return self.q[name]
 
     def reset(self):
@@ -404,7 +413,7 @@ class OracleModel:
 
     def _mm(self, x, name):
         q, s = self._w(name)
-        return self.o.matmul_i8(x[None, :], q, s, 32)[0]
+        return self.o.matmul_i8(x[None, :], q, s, self._g(q.shape[1]))[0]
 
     def forward(self, token: int, pos: int) -> np.ndarray:
         o, H = self.o, self.H
@@ -443,7 +452,8 @@ class OracleModel:
             h = (h + m).astype(np.float32)
         self.ring = (self.ring + 1) % 3
         hn = o.rms_norm(h[None, :], self._f32("model.norm.weight"), self.eps)[0]
-        return self.o.matmul_i8(hn[None, :], self.lm[0], self.lm[1], 32)[0]
+        return self.o.matmul_i8(hn[None, :], self.lm[0], self.lm[1],
+                                  self._g(self.H))[0]
 
     def generate(self, prompt, n_new: int, keep_logits: bool = False):
         """main.cpp:574-690 convention: prefill prompt[:-1], then n_new steps."""

@@ -348,8 +348,9 @@ __global__ __launch_bounds__(kThreads) void k_gemv_xs(
     auto out_row = [&](int rb, int r) -> int {
         return rb * out_per_block + grp * OUT_PER_GRP + ((EPI == EPI_SWIGLU) ? (r % (R / 2)) : r);
     };
-    // Weight chunks and group scales of block rb; for EPI_RESID also the
-    // residual values the block adds to (read long before they are needed).
+    // Weight chunks and group scales (row scale in sv[r][0] when ROWSCALE) of
+    // block rb; for EPI_RESID also the residual values the block adds to
+    // (read long before they are needed).
     auto load = [&](int rb, int4 (&w)[R][SLOTS], float (&sv)[R][SLOTS],
                     float (&res)[OUT_PER_GRP]) {
 #pragma unroll
@@ -364,6 +365,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_xs(
                 w[r][s] = *reinterpret_cast<const int4*>(rp + soff[s]);
                 if constexpr (!ROWSCALE) sv[r][s] = sp[coff[s]];
             }
+            if constexpr (ROWSCALE) sv[r][0] = sc[o];  // the row's one scale
         }
         if constexpr (EPI == EPI_RESID) {
 #pragma unroll
@@ -470,12 +472,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_xs(
         }
         if constexpr (ROWSCALE) {
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
-                int o = min(out_row(rb, r), N - 1);
-                if constexpr (EPI == EPI_SWIGLU)
-                    if (r >= R / 2) o += F;
-                acc[r] *= sc[o];
-            }
+            for (int r = 0; r < R; ++r) acc[r] *= sv[r][0];
         }
         // epilogue: lane li == r of each row group stores output r
         const int o0 = rb * out_per_block + grp * OUT_PER_GRP;

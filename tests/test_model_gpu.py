@@ -139,3 +139,27 @@ def test_context_overflow_rejected(engine):
         engine.generate(np.zeros((1, 2000), np.int32), 100)
     with pytest.raises(EngineError):
         engine.forward(1, 5000)
+
+
+def test_micro_per_row_scales_match_oracle(hip, tmp_path):
+    """precision "int8_row" (one fp32 scale per output row, G = K, the scheme
+    of an isolated per-row int8 matmul): the engine's greedy stream equals the
+    oracle model quantised the same way."""
+    from oracle.oracle import Oracle, OracleModel
+    from quicklm_amd import synth
+    from quicklm_amd.engine import Engine
+
+    d = str(tmp_path)
+    synth.write_model(d, "micro")
+    prompt = synth.prompt_tokens(24, seed=5, vocab=4096)[0]
+    eng = Engine(d, max_seq_len=64, max_batch=1, precision="int8_row")
+    try:
+        got, _, _ = eng.generate(prompt[None, :], 16)
+        lg = eng.last_logits(0)
+    finally:
+        eng.close()
+    want, wlg = OracleModel(d, 64, Oracle(), group="row").generate(prompt, 16, keep_logits=True)
+    err = float(np.abs(lg - wlg[-1]).max() / np.abs(wlg[-1]).max())
+    say("int8_row micro: last-step logit rel err", err)
+    assert np.array_equal(got[0], want)
+    assert err < 1e-3

@@ -201,6 +201,25 @@ def test_quantizer_per_row_group(orc, rng):
     assert np.abs(q.astype(np.float32) * s - w).max() <= s.max() / 2 * 1.0001
 
 
+def test_oracle_model_per_row_scales(orc, tmp_path):
+    """group="row" quantises every matrix (lm_head included) with one scale
+    per output row; its logits stay within quantisation noise of group 32."""
+    from quicklm_amd import synth
+
+    d = str(tmp_path)
+    synth.write_model(d, "micro")
+    prompt = synth.prompt_tokens(20, seed=3, vocab=4096)[0]
+    _, la = OracleModel(d, 64, orc).generate(prompt, 4, keep_logits=True)
+    m = OracleModel(d, 64, orc, group="row")
+    _, lb = m.generate(prompt, 4, keep_logits=True)
+    assert all(s.shape == (q.shape[0], 1) for q, s in m.q.values()) and len(m.q) > 10
+    assert m.lm[1].shape == (m.embed.shape[0], 1)
+    rel = np.abs(la - lb).max(1) / np.abs(la).max(1)
+    assert (rel > 0).all() and (rel < 0.1).all()
+    with pytest.raises(ValueError):
+        OracleModel(d, 64, orc, group=64)
+
+
 def test_matmul_exact_on_integers(orc, rng):
     """Integer activations, int8 weights, power-of-two scales: every partial
     sum is an exact integer multiple of the scale, so the result equals the
