@@ -90,6 +90,44 @@ int qlm_gemv_i8_config(const float* x, const float* norm_w, float eps, const int
                        const float* scales, int group, float* y, int N, int K, int epilogue,
                        int lanes_per_row, int rows, int grid, void* stream);
 
+/* Tile-major weight layout of the matrix-core M = 1 GEMV below: each half of
+ * the rows (halves = 2 for the [gate; up] SwiGLU matrix; rows = rows per
+ * half) is padded with zero rows to 16-row tiles, and every 16-row x
+ * 64-column block is stored as one contiguous 1 KB matrix-core operand in
+ * lane order, so a wave streams HBM linearly. Group-32 scales are reordered
+ * alike (32 floats per block); per-row scales (group = K) keep their layout
+ * and s_bytes is 0. No counterpart in the reference (its weights stay
+ * row-major in host memory). K a multiple of 64. */
+int qlm_mx_layout_bytes(int rows, int K, int group, int halves, size_t* q_bytes,
+                        size_t* s_bytes);
+int qlm_mx_swizzle(const int8_t* q, const float* scales, int group, int rows, int K, int halves,
+                   int8_t* q_out, float* s_out, void* stream);
+
+/* M = 1 on the int8 matrix cores with tile-major weights (q and scales from
+ * qlm_mx_swizzle; per-row scales as quantised), explicit launch shape.
+ * x (after the RMSNorm prologue when norm_w is given) is written as four
+ * int8 digit vectors with one power-of-two scale, x = 2^E (d0 + d1/2^7 +
+ * d2/2^14 + d3/2^21) to within 2^-27 max|x|, and every weight group's dot
+ * products with the digits are exact int32 sums (v_mfma_i32_16x16x64_i8);
+ * results match the fp32 path to ~1e-7 normwise. norm_w and epilogue as
+ * qlm_gemv_i8_config. waves in {4, 8, 16} per workgroup and ring = ceil(K /
+ * 64 / waves) blocks per wave, one of the instantiated pairs (4,1) (4,2)
+ * (4,4) (4,8) (4,10) (8,4) (8,5) (8,8) (16,2) (16,4) (16,10) (16,12); K a
+ * multiple of 64, at most 3072 (waves 4), 10240 (8) or 12288 (16); grid =
+ * workgroups (grid-stride over 16-row tiles). */
+int qlm_gemv_i8_mx_config(const float* x, const float* norm_w, float eps, const int8_t* q,
+                          const float* scales, int group, float* y, int N, int K, int epilogue,
+                          int waves, int ring, int grid, void* stream);
+
+/* The same with the launch shape picked from N, K and the epilogue (the
+ * batch-1 decode projections: math::matmul / matmul_rmsnorm /
+ * matmul_residual / SwiGLU with M = 1, math_ops.cpp:820-900). Returns
+ * QLM_ERR_SHAPE when no instantiated shape fits K; the row-major GEMV
+ * serves such weights. */
+int qlm_gemv_i8_mx(const float* x, const float* norm_w, float eps, const int8_t* q_tiles,
+                   const float* s_tiles, int group, float* y, int N, int K, int epilogue,
+                   void* stream);
+
 /* A4: the same matmul for M > 1 on the matrix cores (batched decode, prefill;
  * math_ops.cpp:845-871). Weights stay exact (int8 in bf16); each activation
  * is split into bf16 hi + lo and the per-group products are scaled in fp32,
@@ -262,6 +300,14 @@ int qlm_lm_head_greedy(const float* x, const float* norm_w, float eps, const int
                        const float* scales, int group, float* logits, int V, int K, void* work,
                        int* tokens, int ld_tokens, int* pos, const int* prompt_len,
                        const float* embed, int H, float* h_next, void* stream);
+/* qlm_lm_head_greedy with the lm_head in the tile-major layout (q_tiles,
+ * s_tiles from qlm_mx_swizzle; per-row scales as quantised), on the matrix
+ * cores; same workspace and semantics. */
+int qlm_lm_head_greedy_mx(const float* x, const float* norm_w, float eps, const int8_t* q_tiles,
+                          const float* s_tiles, int group, float* logits, int V, int K,
+                          void* work, int* tokens, int ld_tokens, int* pos,
+                          const int* prompt_len, const float* embed, int H, float* h_next,
+                          void* stream);
 
 /* Embedding gather (model.cpp:157-164, F32 table): out[b] = table[tokens[b,
  * pos[b]]] for a [vocab, H] fp32 table (pos NULL: tokens[b, 0]). */

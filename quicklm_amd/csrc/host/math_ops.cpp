@@ -36,6 +36,19 @@ void set_matmul_workspace(void* p, size_t bytes) {
 }
 
 namespace {
+// One activation row on the matrix cores over the tile-major copy of the
+// weight (qlm_gemv_i8_mx); false when the weight has no such copy or no
+// launch shape fits K, and the row-major GEMV takes the row.
+bool gemv_tiles(const Tensor& A, const float* norm_w, float eps, const Tensor& B, float* C,
+                int64_t N, int epilogue) {
+    if (A.rows() != 1 || !B.int8_tiles) return false;
+    const int rc = qlm_gemv_i8_mx(A.data, norm_w, eps, B.int8_tiles, B.int8_tile_scales,
+                                  B.int8_group, C, (int)N, (int)A.cols(), epilogue, g_stream);
+    if (rc == QLM_ERR_SHAPE) return false;
+    check(rc, "qlm_gemv_i8_mx");
+    return true;
+}
+
 // The matrix-core matmul for M > 4 rows (norm_w null: no RMSNorm prologue).
 void matmul_mfma(const Tensor& A, const float* norm_w, float eps, const Tensor& B, float* C,
                  int64_t ldc, int64_t N, int epilogue) {
@@ -60,6 +73,7 @@ void matmul(const Tensor& A, const Tensor& B, Tensor& C, bool transpose_B) {
         matmul_mfma(A, nullptr, 0.0f, B, C.data, C.row_stride(), N, 0);
         return;
     }
+    if (gemv_tiles(A, nullptr, 0.0f, B, C.data, N, 0)) return;
     check(qlm_gemv_i8(A.data, (int)A.row_stride(), B.int8_data, B.int8_scales, B.int8_group, C.data,
                       (int)C.row_stride(), (int)M, (int)N, (int)K, g_stream),
           "qlm_gemv_i8");
@@ -73,6 +87,7 @@ void matmul_rmsnorm(const Tensor& A, const Tensor& norm_w, float eps, const Tens
         matmul_mfma(A, norm_w.data, eps, B, C.data, C.row_stride(), N, 0);
         return;
     }
+    if (gemv_tiles(A, norm_w.data, eps, B, C.data, N, 0)) return;
     check(qlm_gemv_i8_rmsnorm(A.data, (int)A.row_stride(), norm_w.data, eps, B.int8_data,
                               B.int8_scales, B.int8_group, C.data, (int)C.row_stride(), (int)M,
                               (int)N, (int)K, g_stream),
@@ -87,6 +102,7 @@ void matmul_residual(const Tensor& A, const Tensor& B, Tensor& residual) {
         matmul_mfma(A, nullptr, 0.0f, B, residual.data, residual.row_stride(), N, 1);
         return;
     }
+    if (gemv_tiles(A, nullptr, 0.0f, B, residual.data, N, 1)) return;
     check(qlm_gemv_i8_residual(A.data, (int)A.row_stride(), B.int8_data, B.int8_scales,
                                B.int8_group, residual.data, (int)residual.row_stride(), (int)M,
                                (int)N, (int)K, g_stream),
@@ -102,6 +118,7 @@ void matmul_swiglu_rmsnorm(const Tensor& A, const Tensor& norm_w, float eps, con
         matmul_mfma(A, norm_w.data, eps, B, C.data, C.row_stride(), F, 2);
         return;
     }
+    if (gemv_tiles(A, norm_w.data, eps, B, C.data, F, 2)) return;
     check(qlm_gemv_i8_swiglu_rmsnorm(A.data, (int)A.row_stride(), norm_w.data, eps, B.int8_data,
                                      B.int8_scales, B.int8_group, C.data, (int)C.row_stride(),
                                      (int)M, (int)F, (int)K, g_stream),

@@ -80,6 +80,21 @@ void DecoderModel::quantize_into(LinearI8& lin, int row_off, const std::string& 
               "quantize");
 }
 
+// The tile-major copy the one-row GEMV streams (qlm_mx_swizzle); skipped
+// where K is not a multiple of 64 (the row-major GEMV serves those).
+void DecoderModel::tile_linear(LinearI8& lin, int halves) {
+    size_t qb = 0, sb = 0;
+    if (lin.K % 64 != 0 || lin.N % halves != 0) return;
+    const int rows = lin.N / halves;
+    check(qlm_mx_layout_bytes(rows, lin.K, lin.group, halves, &qb, &sb), "tile layout");
+    lin.halves = halves;
+    lin.qz.alloc(qb);
+    if (sb) lin.sz.alloc(sb);
+    check(qlm_mx_swizzle(lin.q.get<int8_t>(), lin.s.get<float>(), lin.group, rows, lin.K, halves,
+                         lin.qz.get<int8_t>(), sb ? lin.sz.get<float>() : nullptr, stream_),
+          "tile swizzle");
+}
+
 void DecoderModel::upload_f32(DeviceBuffer& dst, const std::string& name, int64_t expect) {
     TensorView t = ws_->get(name);
     if (expect >= 0 && t.numel() != expect)
@@ -132,8 +147,10 @@ void DecoderModel::load(const std::string& dir, int max_seq_len, const std::stri
             quantize_into(w.dn_in, 3 * HD_, p + "linear_attn.in_proj_z.weight");
             quantize_into(w.dn_in, 4 * HD_, p + "linear_attn.in_proj_b.weight");
             quantize_into(w.dn_in, 4 * HD_ + nh, p + "linear_attn.in_proj_a.weight");
+            tile_linear(w.dn_in, 1);
             alloc_linear(w.dn_out, H, HD_);
             quantize_into(w.dn_out, 0, p + "linear_attn.out_proj.weight");
+            tile_linear(w.dn_out, 1);
             // conv1d.weight [3HD, 1, ks] -> tap-major [ks, 3HD]
             TensorView cw = ws_->get(p + "linear_attn.conv1d.weight");
             const int C = 3 * HD_;
@@ -160,8 +177,10 @@ void DecoderModel::load(const std::string& dir, int max_seq_len, const std::stri
             quantize_into(w.at_qkv, 0, p + "self_attn.q_proj.weight");
             quantize_into(w.at_qkv, qr, p + "self_attn.k_proj.weight");
             quantize_into(w.at_qkv, qr + nkv * hd, p + "self_attn.v_proj.weight");
+            tile_linear(w.at_qkv, 1);
             alloc_linear(w.at_o, H, nq * hd);
             quantize_into(w.at_o, 0, p + "self_attn.o_proj.weight");
+            tile_linear(w.at_o, 1);
             if (ws_->has(p + "self_attn.q_norm.weight")) {
                 upload_f32(w.q_norm, p + "self_attn.q_norm.weight", hd);
                 upload_f32(w.k_norm, p + "self_attn.k_norm.weight", hd);
@@ -170,8 +189,10 @@ void DecoderModel::load(const std::string& dir, int max_seq_len, const std::stri
         alloc_linear(w.gate_up, 2 * F, H);
         quantize_into(w.gate_up, 0, p + "mlp.gate_proj.weight");
         quantize_into(w.gate_up, F, p + "mlp.up_proj.weight");
+        tile_linear(w.gate_up, 2);
         alloc_linear(w.down, H, F);
         quantize_into(w.down, 0, p + "mlp.down_proj.weight");
+        tile_linear(w.down, 1);
     }
     upload_f32(final_norm_, "model.norm.weight", H);
     // Embedding gathered as fp32 (model.cpp:157-164); tied lm_head is the
@@ -190,6 +211,7 @@ void DecoderModel::load(const std::string& dir, int max_seq_len, const std::stri
                                   lm_head_.s.get<float>(), stream_),
               "quantize lm_head");
     }
+    tile_linear(lm_head_, 1);
     cfg_.vocab_size = lm_head_.N;  // model.cpp:123
     check(qlm_stream_sync(stream_), "sync");
     staging_.release();
@@ -321,12 +343,22 @@ void DecoderModel::enqueue_step(int B) {
     // embedding of the token now at pos (the next step's input, or the next
     // prompt token) -- model.cpp:193-199, :263-274, :157-164.
     if (B == 1) {
-        check(qlm_lm_head_greedy(h_.get<float>(), final_norm_.get<float>(), eps,
-                                 lm_head_.q.get<int8_t>(), lm_head_.s.get<float>(), lm_head_.group,
-                                 logits_.get<float>(), V, H, tail_work_.get(), tokens_.get<int>(),
-                                 ld_tokens_, pos_.get<int>(), prompt_len_.get<int>(),
-                                 embed_.get<float>(), H, h_.get<float>(), stream_),
-              "lm_head");
+        const Tensor lm = lm_head_.view();
+        int rc = QLM_ERR_SHAPE;
+        if (lm.int8_tiles)
+            rc = qlm_lm_head_greedy_mx(h_.get<float>(), final_norm_.get<float>(), eps, lm.int8_tiles,
+                                       lm.int8_tile_scales, lm_head_.group, logits_.get<float>(), V,
+                                       H, tail_work_.get(), tokens_.get<int>(), ld_tokens_,
+                                       pos_.get<int>(), prompt_len_.get<int>(), embed_.get<float>(),
+                                       H, h_.get<float>(), stream_);
+        if (rc == QLM_ERR_SHAPE)
+            rc = qlm_lm_head_greedy(h_.get<float>(), final_norm_.get<float>(), eps,
+                                    lm_head_.q.get<int8_t>(), lm_head_.s.get<float>(),
+                                    lm_head_.group, logits_.get<float>(), V, H, tail_work_.get(),
+                                    tokens_.get<int>(), ld_tokens_, pos_.get<int>(),
+                                    prompt_len_.get<int>(), embed_.get<float>(), H, h_.get<float>(),
+                                    stream_);
+        check(rc, "lm_head");
         n += 2;
     } else {
         Tensor fn({H}, final_norm_.get<float>());

@@ -31,8 +31,17 @@ namespace qlm {
 struct LinearI8 {
     DeviceBuffer q, s;
     int N = 0, K = 0, group = 32;
+    // tile-major copy for the one-row GEMV (halves = 2: [gate; up] rows);
+    // sz stays empty with per-row scales, which keep their layout
+    DeviceBuffer qz, sz;
+    int halves = 1;
     Tensor view() const {
-        return Tensor::int8(q.get<int8_t>(), s.get<float>(), N, K, group);
+        Tensor t = Tensor::int8(q.get<int8_t>(), s.get<float>(), N, K, group);
+        if (qz.bytes()) {
+            t.int8_tiles = qz.get<int8_t>();
+            t.int8_tile_scales = sz.bytes() ? sz.get<float>() : s.get<float>();
+        }
+        return t;
     }
     int blocks_per_row() const { return group >= K ? 1 : K / group; }
 };
@@ -122,6 +131,7 @@ class DecoderModel {
     void quantize_into(LinearI8& lin, int row_off, const std::string& name);
     void upload_f32(DeviceBuffer& dst, const std::string& name, int64_t expect);
     void alloc_linear(LinearI8& lin, int N, int K);
+    void tile_linear(LinearI8& lin, int halves);
 
     ModelConfig cfg_;
     std::unique_ptr<WeightStore> ws_;

@@ -20,6 +20,10 @@ struct Tensor {
     const int8_t* int8_data = nullptr;     // int8 weight operand
     const float* int8_scales = nullptr;
     int int8_group = 32;
+    // The same weight in the matrix-core tile-major layout (qlm_mx_swizzle),
+    // streamed by the one-row GEMV; null where the model keeps no such copy.
+    const int8_t* int8_tiles = nullptr;
+    const float* int8_tile_scales = nullptr;
 
     Tensor() = default;
     Tensor(std::vector<int64_t> shp, float* d) : shape(std::move(shp)), data(d) { compute_strides(); }

@@ -43,6 +43,9 @@ enum { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_ARGMAX = 3 };
 // invalidates its XCD's L2, ~0.3 us apiece over a 2048-workgroup grid).
 // One 64-bit key slot per workgroup of the logits GEMV (grid <= kMaxXsGrid).
 constexpr int kMaxXsGrid = 2048;
+// float4 of the activation each thread of the matrix-core M = 1 kernel
+// holds through its prologue (so K <= 4 * 64 * NW * mx_xmax(NW)).
+__host__ __device__ constexpr int mx_xmax(int nw) { return nw == 8 ? 5 : 3; }
 
 struct GreedyTail {
     unsigned long long* keys;
@@ -567,6 +570,366 @@ __global__ __launch_bounds__(kThreads) void k_greedy_finish(GreedyTail tail, int
     for (int i = tid; i < tail.H; i += kThreads) tail.h[i] = src[i];
 }
 
+// ---------------------------------------------------------------------------
+// M = 1 on the int8 matrix cores (v_mfma_i32_16x16x64_i8), weights in the
+// tile-major layout below.
+//
+// The activation is written as four int8 digit vectors: with E chosen from
+// max|x| so that |x| / 2^E < 64,
+//     x = 2^E * (d0 + d1 2^-7 + d2 2^-14 + d3 2^-21) + e,   |e| <= 2^-27 max|x|,
+// every |d| <= 64. A weight group's dot products with the four digit vectors
+// are exact int32 sums on the matrix cores, so per 1024 weights a wave spends
+// one MFMA and about six VALU operations (two shift-adds, two conversions,
+// two FMAs) instead of a conversion and an FMA per weight.
+//
+// Operands of one K = 64 block b of a tile of 16 weight rows (lane l,
+// n = l & 15, q = l >> 4):
+//   B (weights) lane l: row n, bytes 64b + 16q .. +15. The tile-major layout
+//               stores these 64 fragments as one contiguous 1 KB span, so a
+//               wave's load is a linear 1 KB read (row-major rows would make
+//               it 16 scattered 64-byte pieces, which streams ~30% slower).
+//   A (digits)  lane l: A row n, elements 64b + 16q .. +15. With group-32
+//               scales A row 4h + d holds digit d of the elements of group
+//               2b + h (zero for the other group, and rows 8..15 are zero);
+//               with one scale per row, A rows 0..3 hold digits 0..3 of all
+//               64 elements.
+//   D           lane l: D[4q + i][n], i = 0..3. Group-32: lanes q = 0, 1 hold
+//               the four digit sums of row n over group 2b + q, combined as
+//               P = (D0 << 7) + D1, Q = (D2 << 7) + D3 (exact int32) and
+//               accumulated as (P + Q 2^-14) * s[n][2b + q] in fp32. Per-row
+//               scales: the int32 digit sums accumulate across blocks.
+//
+// A workgroup of NW waves owns one tile at a time (grid-stride over tiles);
+// wave w takes the P = ceil(K / 64 / NW) blocks w, w + NW, ... of every tile.
+// All P blocks of a wave (and their scales) are requested at once, before the
+// prologue, and each slot is refilled with the next tile's block as soon as
+// it is consumed; the activation and gain are requested before them, so the
+// prologue (RMSNorm sum of squares and max, digits into LDS) overlaps the
+// first weight fetches. At the end of a tile the waves' partial sums meet in
+// LDS (one barrier per tile) and wave 0 applies 2^E, the epilogue and the
+// stores.
+
+// Tile-major weight layout: the rows are cut into halves (2 for the
+// [gate; up] matrix of SwiGLU) of `rows` rows each, each half padded with
+// zero rows to 16-row tiles; fragment (tile g, block b) is the 1 KB B operand
+// above in lane order (lane l = 16q + n: row 16t + n, bytes 64b + 16q .. +15).
+// Group-32 scales of the fragment follow as 32 floats [h][n] (group 2b + h of
+// row n). One thread per 16 bytes.
+__global__ __launch_bounds__(256) void k_mx_swizzle(const int8_t* __restrict__ q,
+                                                    const float* __restrict__ sc, int rows,
+                                                    int K, int tiles, int halves,
+                                                    int8_t* __restrict__ qz,
+                                                    float* __restrict__ sz) {
+    const int nblk = K >> 6, nsb = K >> 5;
+    const size_t total = (size_t)halves * tiles * nblk * QLM_WAVE;
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total;
+         i += (size_t)gridDim.x * blockDim.x) {
+        const int lane = (int)(i % QLM_WAVE);
+        const size_t fb = i / QLM_WAVE;
+        const int b = (int)(fb % nblk);
+        const int g = (int)(fb / nblk);
+        const int half = g / tiles, t = g % tiles;
+        const int n = lane & 15, qd = lane >> 4;
+        const int rh = t * 16 + n;  // row within the half
+        int4 v = make_int4(0, 0, 0, 0);
+        if (rh < rows)
+            v = *reinterpret_cast<const int4*>(q + ((size_t)half * rows + rh) * K + b * 64 +
+                                               qd * 16);
+        reinterpret_cast<int4*>(qz)[i] = v;
+        if (sz && lane < 32) {
+            const int h = lane >> 4;
+            sz[fb * 32 + lane] =
+                rh < rows ? sc[((size_t)half * rows + rh) * nsb + 2 * b + h] : 0.0f;
+        }
+    }
+}
+
+template <int NW, int T, int P, bool ROWSCALE, int PRO, int EPI>
+__global__ __launch_bounds__(NW * QLM_WAVE) void k_gemv_mx(
+    const float* __restrict__ x, const float* __restrict__ nw, float eps,
+    const int8_t* __restrict__ q, const float* __restrict__ sc, float* __restrict__ y, int N,
+    int K, int F, int ntiles, GreedyTail tail) {
+    constexpr int NT = NW * QLM_WAVE;
+    constexpr int XMAX = mx_xmax(NW);  // float4 of x per thread
+    typedef int v4i __attribute__((ext_vector_type(4)));
+    extern __shared__ __align__(16) unsigned char mx_lds[];  // 4 digit planes, then 16 zero bytes
+    __shared__ int red[2][NW][T][16][ROWSCALE ? 4 : 1];
+    __shared__ float rsum[NW], rmax[NW];
+
+    const int tid = threadIdx.x, lane = tid & (QLM_WAVE - 1);
+    const int w = __builtin_amdgcn_readfirstlane(tid / QLM_WAVE);
+    const int n = lane & 15, qd = lane >> 4;
+    const int nblk = K >> 6;
+    const int PS = K + 64;   // digit plane stride (bytes)
+    const int zoff = 4 * PS; // 16 zero bytes
+
+    // ---- activation (and gain) requests first: they return before the ring
+    const int nx4 = K >> 2;
+    float4 xr[XMAX], gr[XMAX];
+#pragma unroll
+    for (int i = 0; i < XMAX; ++i) {
+        const int idx = tid + i * NT;
+        if (idx < nx4) {
+            xr[i] = reinterpret_cast<const float4*>(x)[idx];
+            if constexpr (PRO == PRO_RMSNORM) gr[i] = reinterpret_cast<const float4*>(nw)[idx];
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    auto row_of = [&](int tile, int tt) {
+        int r = min(tile * 16 + n, N - 1);
+        if constexpr (EPI == EPI_SWIGLU)
+            if (tt == 1) r += F;
+        return r;
+    };
+    // Epilogue operands (residual, row scales) of the first tile, requested
+    // by every lane before the ring (row clamped, unconditional). Later tiles
+    // read theirs in the epilogue, after their ring loads have drained: a
+    // load issued behind the ring could only be waited for by draining it
+    // (loads retire in order).
+    float res0 = 0.0f, rsc0[T];
+    if constexpr (EPI == EPI_RESID) res0 = y[min((int)blockIdx.x * 16 + n, N - 1)];
+#pragma unroll
+    for (int tt = 0; tt < T; ++tt) rsc0[tt] = ROWSCALE ? sc[row_of(blockIdx.x, tt)] : 1.0f;
+
+    // ---- weight ring: slot u holds block w + NW*u of the current tile.
+    // P = ceil(blocks / NW), so a wave's last slot may lie past K: it then
+    // repeats the wave's last block (a cache hit) and meets zero digits. The
+    // next tile's slot u is requested as soon as slot u is consumed.
+    const int blast = nblk - 1 - ((nblk - 1 - w) % NW);  // this wave's last block
+    int4 wb[P][T];
+    float sb[P][T];
+    auto issue = [&](int tile, int u) {
+        const int b = min(w + NW * u, blast);
+#pragma unroll
+        for (int tt = 0; tt < T; ++tt) {
+            // fragment (tile of half tt, block b): 1 KB in lane order
+            const size_t fb = (size_t)(tile + tt * ntiles) * nblk + b;
+            wb[u][tt] = reinterpret_cast<const int4*>(q)[fb * QLM_WAVE + lane];
+            if constexpr (!ROWSCALE) sb[u][tt] = sc[fb * 32 + (qd & 1) * 16 + n];
+        }
+    };
+#pragma unroll
+    for (int u = 0; u < P; ++u) issue(blockIdx.x, u);
+
+    // ---- prologue: RMSNorm sum of squares and max|x|, then digits -> LDS
+    float ss = 0.0f, mx = 0.0f;
+#pragma unroll
+    for (int i = 0; i < XMAX; ++i) {
+        const int idx = tid + i * NT;
+        if (idx < nx4) {
+            float4 v = xr[i];
+            if constexpr (PRO == PRO_RMSNORM) {
+                ss = fmaf(v.x, v.x, ss);
+                ss = fmaf(v.y, v.y, ss);
+                ss = fmaf(v.z, v.z, ss);
+                ss = fmaf(v.w, v.w, ss);
+                const float4 g = gr[i];
+                v.x *= 1.0f + g.x;
+                v.y *= 1.0f + g.y;
+                v.z *= 1.0f + g.z;
+                v.w *= 1.0f + g.w;
+                xr[i] = v;
+            }
+            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        }
+    }
+    if constexpr (PRO == PRO_RMSNORM) ss = wave_sum(ss);
+    mx = wave_max(mx);
+    if (lane == 0) {
+        rsum[w] = ss;
+        rmax[w] = mx;
+    }
+    if (tid < 4) reinterpret_cast<unsigned*>(mx_lds + zoff)[tid] = 0u;
+    __syncthreads();
+    float tot = rsum[0], m = rmax[0];
+#pragma unroll
+    for (int i = 1; i < NW; ++i) {
+        tot += rsum[i];
+        m = fmaxf(m, rmax[i]);
+    }
+    const float rs = (PRO == PRO_RMSNORM) ? 1.0f / sqrtf(tot / (float)K + eps) : 1.0f;
+    int e2 = 0;
+    frexpf(m * rs, &e2);
+    const int E = e2 - 6;  // max|x| / 2^E < 64 (one rounding of slack: digits <= 64)
+#pragma unroll
+    for (int i = 0; i < XMAX; ++i) {
+        const int idx = tid + i * NT;
+        if (idx < nx4) {
+            const float vv[4] = {xr[i].x, xr[i].y, xr[i].z, xr[i].w};
+            unsigned pk[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const float u = ldexpf(PRO == PRO_RMSNORM ? vv[c] * rs : vv[c], -E);
+                const float d0 = rintf(u);
+                float t = (u - d0) * 128.0f;
+                const float d1 = rintf(t);
+                t = (t - d1) * 128.0f;
+                const float d2 = rintf(t);
+                t = (t - d2) * 128.0f;
+                const float d3 = rintf(t);
+                pk[0] |= ((unsigned)(int)d0 & 0xffu) << (8 * c);
+                pk[1] |= ((unsigned)(int)d1 & 0xffu) << (8 * c);
+                pk[2] |= ((unsigned)(int)d2 & 0xffu) << (8 * c);
+                pk[3] |= ((unsigned)(int)d3 & 0xffu) << (8 * c);
+            }
+#pragma unroll
+            for (int d = 0; d < 4; ++d)
+                *reinterpret_cast<unsigned*>(mx_lds + d * PS + idx * 4) = pk[d];
+        }
+    }
+    __syncthreads();
+
+    // A-fragment address of this lane (the zero bytes for rows that carry
+    // nothing, and for every row of a slot past K)
+    bool active;
+    int dpl;
+    if constexpr (ROWSCALE) {
+        active = n < 4;
+        dpl = n;
+    } else {
+        active = n < 8 && (n >> 2) == (qd >> 1);
+        dpl = n & 3;
+    }
+    const int abase = active ? dpl * PS + qd * 16 : zoff;
+    const int astep = active ? 64 : 0;
+
+    float accf[T];
+    v4i acci[T];
+#pragma unroll
+    for (int tt = 0; tt < T; ++tt) {
+        accf[tt] = 0.0f;
+        acci[tt] = v4i{0, 0, 0, 0};
+    }
+    auto consume = [&](int u) {
+        const int b = w + NW * u;
+        const int aoff = b < nblk ? abase + b * astep : zoff;
+        const v4i a = *reinterpret_cast<const v4i*>(mx_lds + aoff);
+#pragma unroll
+        for (int tt = 0; tt < T; ++tt) {
+            const v4i bw = v4i{wb[u][tt].x, wb[u][tt].y, wb[u][tt].z, wb[u][tt].w};
+            if constexpr (ROWSCALE) {
+                acci[tt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, bw, acci[tt], 0, 0, 0);
+            } else {
+                const v4i d =
+                    __builtin_amdgcn_mfma_i32_16x16x64_i8(a, bw, v4i{0, 0, 0, 0}, 0, 0, 0);
+                const int pp = (d[0] << 7) + d[1];
+                const int qq = (d[2] << 7) + d[3];
+                const float v = fmaf((float)qq, 0x1p-14f, (float)pp);
+                accf[tt] = fmaf(v, sb[u][tt], accf[tt]);
+            }
+        }
+    };
+
+    float best_v = -INFINITY;
+    int best_i = 0x7fffffff;
+    int par = 0;
+    // Partial sums of the waves meet in LDS (double-buffered by tile parity:
+    // a buffer is rewritten two tiles later, after a barrier wave 0 reaches
+    // only once it has read it); wave 0 reduces them in wave order, applies
+    // 2^E, the epilogue and the stores.
+    auto tile_end = [&](int tile) {
+#pragma unroll
+        for (int tt = 0; tt < T; ++tt) {
+            if constexpr (ROWSCALE) {
+                if (qd == 0) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) red[par][w][tt][n][i] = acci[tt][i];
+                }
+                acci[tt] = v4i{0, 0, 0, 0};
+            } else {
+                const float p = accf[tt] + __shfl_xor(accf[tt], 16, QLM_WAVE);
+                if (qd == 0) red[par][w][tt][n][0] = __float_as_int(p);
+                accf[tt] = 0.0f;
+            }
+        }
+        __syncthreads();
+        if (w == 0 && qd == 0) {
+            const int o = tile * 16 + n;
+            const bool first = tile == (int)blockIdx.x;
+            float val[T];
+#pragma unroll
+            for (int tt = 0; tt < T; ++tt) {
+                if constexpr (ROWSCALE) {
+                    int s4[4] = {0, 0, 0, 0};
+                    for (int ww = 0; ww < NW; ++ww)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) s4[i] += red[par][ww][tt][n][i];
+                    const float v = fmaf((float)s4[3], 0x1p-21f,
+                                         fmaf((float)s4[2], 0x1p-14f,
+                                              fmaf((float)s4[1], 0x1p-7f, (float)s4[0])));
+                    val[tt] = ldexpf(v, E) * (first ? rsc0[tt] : sc[row_of(tile, tt)]);
+                } else {
+                    float v = __int_as_float(red[par][0][tt][n][0]);
+                    for (int ww = 1; ww < NW; ++ww) v += __int_as_float(red[par][ww][tt][n][0]);
+                    val[tt] = ldexpf(v, E - 7);
+                }
+            }
+            if (o < N) {
+                if constexpr (EPI == EPI_SWIGLU)
+                    y[o] = silu_f(val[0]) * val[1];
+                else if constexpr (EPI == EPI_RESID)
+                    y[o] = (first ? res0 : y[o]) + val[0];
+                else
+                    y[o] = val[0];
+                if constexpr (EPI == EPI_ARGMAX) {
+                    if (val[0] > best_v || (val[0] == best_v && o < best_i)) {
+                        best_v = val[0];
+                        best_i = o;
+                    }
+                }
+            }
+        }
+        par ^= 1;
+    };
+
+    // ---- tiles: consume the P slots in order (each refilled with the next
+    // tile's block when there is one), then the cross-wave epilogue
+    for (int tile = blockIdx.x;; tile += gridDim.x) {
+        const int next = tile + (int)gridDim.x;
+        if (next < ntiles) {
+#pragma unroll
+            for (int u = 0; u < P; ++u) {
+                consume(u);
+                issue(next, u);
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < P; ++u) consume(u);
+        }
+        tile_end(tile);
+        if (next >= ntiles) break;
+    }
+
+    if constexpr (EPI == EPI_ARGMAX) {
+        if (w == 0) {
+            unsigned long long k = argmax_key(best_v, best_i);
+            if (best_i == 0x7fffffff) k = 0ull;
+#pragma unroll
+            for (int mm = 32; mm >= 1; mm >>= 1) {
+                const unsigned long long o = __shfl_xor(k, mm, QLM_WAVE);
+                k = o > k ? o : k;
+            }
+            if (lane == 0) tail.keys[blockIdx.x] = k;
+        }
+    }
+}
+
+GreedyTail greedy_tail(void* work, int* tokens, int ld_tokens, int* pos, const int* prompt_len,
+                       const float* embed, int H, int V, float* h_next) {
+    GreedyTail t;
+    t.keys = reinterpret_cast<unsigned long long*>(work);
+    t.tokens = tokens;
+    t.ld_tokens = ld_tokens;
+    t.pos = pos;
+    t.prompt_len = prompt_len;
+    t.embed = embed;
+    t.H = H;
+    t.vocab = V;
+    t.h = h_next;
+    return t;
+}
+
 // Dynamic LDS of the M = 1 kernel: x, plus the RMSNorm gain.
 size_t xs_lds_bytes(int K, int pro) {
     return (size_t)K * sizeof(float) * (pro == PRO_RMSNORM ? 2 : 1);
@@ -732,6 +1095,121 @@ int xs_dispatch(int pro, int epi, XsConfig c, const float* x, const float* nw, f
 #undef QLM_XS_CALL
 }
 
+// ---- matrix-core M = 1 launches (tile-major weights) ----
+struct MxConfig {
+    int nw, ring, grid;
+};
+
+// Dynamic LDS of k_gemv_mx: four digit planes of K + 64 bytes, 16 zero bytes.
+size_t mx_lds_bytes(int K) { return 4 * (size_t)(K + 64) + 16; }
+
+// Instantiated (waves per workgroup, slots per wave) pairs; slots =
+// ceil(K / 64 / waves), so each pair serves a range of K.
+constexpr int kMxPairs[][2] = {{4, 1}, {4, 2},  {4, 4},  {4, 8},   {4, 10},  {8, 4},
+                               {8, 5}, {8, 8},  {16, 2}, {16, 4}, {16, 10}, {16, 12}};
+
+// Whether k_gemv_mx<nw, *, ring> runs this K: whole 64-element blocks, the
+// activation fits its prologue registers, ring = ceil(blocks / nw), and the
+// pair is instantiated.
+bool mx_fits(int K, int nw, int ring) {
+    if (K <= 0 || K % 64 != 0 || K > 4 * QLM_WAVE * nw * mx_xmax(nw)) return false;
+    if (ring != (K / 64 + nw - 1) / nw) return false;
+    for (const auto& pr : kMxPairs)
+        if (pr[0] == nw && pr[1] == ring) return true;
+    return false;
+}
+
+// Measured launch shapes of the 4B hybrid's decode projections (N, K,
+// epilogue -> waves per workgroup, ring depth, grid), graph replays on MI355X.
+struct MxTuned {
+    int N, K, epi, nw, ring, grid;
+};
+constexpr MxTuned kMxTuned[] = {
+    {9728, 2560, EPI_SWIGLU, 8, 5, 256},     // gate/up
+    {2560, 9728, EPI_RESID, 16, 10, 160},    // down
+    {8224, 2560, EPI_STORE, 8, 5, 512},      // DeltaNet in_proj [qkv|z|b|a]
+    {5120, 2560, EPI_STORE, 8, 5, 256},      // GQA q(+gate)/k/v
+    {2560, 2048, EPI_RESID, 16, 2, 160},     // out_proj / o_proj
+    {151936, 2560, EPI_STORE, 8, 5, 2048},   // lm_head (also its greedy form)
+};
+
+// Launch shape: the tuned table, else the fewest waves per workgroup that
+// give >= 2048 waves in all (each a K-slice of a tile) among the
+// instantiated pairs, and one tile per workgroup up to the greedy tail's key
+// slots. nw = 0 when no pair fits K.
+MxConfig mx_config(int N, int K, int epi) {
+    const int e = epi == EPI_ARGMAX ? EPI_STORE : epi;
+    for (const MxTuned& t : kMxTuned)
+        if (t.N == N && t.K == K && t.epi == e) return MxConfig{t.nw, t.ring, t.grid};
+    const int tiles = (N + 15) / 16, nblk = K / 64;
+    MxConfig c{0, 0, tiles < kMaxXsGrid ? tiles : kMaxXsGrid};
+    for (int nw = 4; nw <= 16; nw *= 2) {
+        const int ring = (nblk + nw - 1) / nw;
+        if (!mx_fits(K, nw, ring)) continue;
+        c.nw = nw;
+        c.ring = ring;
+        if (tiles * nw >= 2048) break;
+    }
+    return c;
+}
+
+template <int NW, int P, bool ROWSCALE, int PRO, int EPI>
+int launch_mx(const MxConfig& c, const float* x, const float* nw, float eps, const int8_t* q,
+              const float* sc, float* y, int N, int K, int F, hipStream_t st,
+              const GreedyTail& tail) {
+    constexpr int T = EPI == EPI_SWIGLU ? 2 : 1;
+    const int ntiles = (N + 15) / 16;
+    int grid = c.grid < ntiles ? c.grid : ntiles;
+    if (grid < 1) grid = 1;
+    hipLaunchKernelGGL((k_gemv_mx<NW, T, P, ROWSCALE, PRO, EPI>), dim3(grid),
+                       dim3(NW * QLM_WAVE), mx_lds_bytes(K), st, x, nw, eps, q, sc, y, N, K, F,
+                       ntiles, tail);
+    if constexpr (EPI == EPI_ARGMAX) {
+        const int rc = qlm_launch_status();
+        if (rc != QLM_OK) return rc;
+        hipLaunchKernelGGL(k_greedy_finish, dim3(1), dim3(kThreads), 0, st, tail, grid, N);
+    }
+    return qlm_launch_status();
+}
+
+template <bool ROWSCALE, int PRO, int EPI>
+int launch_mx_np(const MxConfig& c, const float* x, const float* nw, float eps, const int8_t* q,
+                 const float* sc, float* y, int N, int K, int F, hipStream_t st,
+                 const GreedyTail& tail) {
+#define QLM_MX(W, PP)                                                                      \
+    if (c.nw == W && c.ring == PP)                                                          \
+        return launch_mx<W, PP, ROWSCALE, PRO, EPI>(c, x, nw, eps, q, sc, y, N, K, F, st, tail);
+    QLM_MX(4, 1) QLM_MX(4, 2) QLM_MX(4, 4) QLM_MX(4, 8) QLM_MX(4, 10) QLM_MX(8, 4)
+    QLM_MX(8, 5) QLM_MX(8, 8) QLM_MX(16, 2) QLM_MX(16, 4) QLM_MX(16, 10) QLM_MX(16, 12)
+#undef QLM_MX
+    return QLM_ERR_SHAPE;
+}
+
+int mx_dispatch(int pro, int epi, const MxConfig& c, const float* x, const float* nw, float eps,
+                const int8_t* q, const float* sc, bool rowscale, float* y, int N, int K,
+                hipStream_t st, const GreedyTail& tail = GreedyTail{}) {
+    if (!mx_fits(K, c.nw, c.ring) || c.grid < 1) return QLM_ERR_SHAPE;
+    if (epi == EPI_ARGMAX && c.grid > kMaxXsGrid) return QLM_ERR_SHAPE;
+    const int F = N;
+#define QLM_MX_CALL(RS, P, E) \
+    return launch_mx_np<RS, P, E>(c, x, nw, eps, q, sc, y, N, K, F, st, tail)
+    if (epi == EPI_ARGMAX) {
+        if (rowscale) QLM_MX_CALL(true, PRO_RMSNORM, EPI_ARGMAX);
+        QLM_MX_CALL(false, PRO_RMSNORM, EPI_ARGMAX);
+    }
+    if (rowscale) {
+        if (pro == PRO_NONE && epi == EPI_STORE) QLM_MX_CALL(true, PRO_NONE, EPI_STORE);
+        if (pro == PRO_RMSNORM && epi == EPI_STORE) QLM_MX_CALL(true, PRO_RMSNORM, EPI_STORE);
+        if (pro == PRO_NONE && epi == EPI_RESID) QLM_MX_CALL(true, PRO_NONE, EPI_RESID);
+        QLM_MX_CALL(true, PRO_RMSNORM, EPI_SWIGLU);
+    }
+    if (pro == PRO_NONE && epi == EPI_STORE) QLM_MX_CALL(false, PRO_NONE, EPI_STORE);
+    if (pro == PRO_RMSNORM && epi == EPI_STORE) QLM_MX_CALL(false, PRO_RMSNORM, EPI_STORE);
+    if (pro == PRO_NONE && epi == EPI_RESID) QLM_MX_CALL(false, PRO_NONE, EPI_RESID);
+    QLM_MX_CALL(false, PRO_RMSNORM, EPI_SWIGLU);
+#undef QLM_MX_CALL
+}
+
 template <int R, int M, bool ROWSCALE, int PRO, int EPI, bool XLDS>
 int launch_one(const float* x, int ldx, int mr, const float* nw, float eps, const int8_t* q,
                const float* sc, float* y, int ldy, int N, int K, int F, hipStream_t st) {
@@ -860,6 +1338,50 @@ extern "C" int qlm_gemv_i8_config(const float* x, const float* norm_w, float eps
                        as_stream(stream));
 }
 
+extern "C" int qlm_mx_layout_bytes(int rows, int K, int group, int halves, size_t* q_bytes,
+                                   size_t* s_bytes) {
+    if (rows <= 0 || K <= 0 || K % 64 != 0 || (halves != 1 && halves != 2) || !q_bytes ||
+        !s_bytes)
+        return QLM_ERR_ARG;
+    if (group != 32 && group != K) return QLM_ERR_SHAPE;
+    const size_t tiles = (size_t)(rows + 15) / 16;
+    *q_bytes = halves * tiles * 16 * (size_t)K;
+    *s_bytes = group == 32 ? halves * tiles * (size_t)(K / 64) * 32 * sizeof(float) : 0;
+    return QLM_OK;
+}
+
+extern "C" int qlm_mx_swizzle(const int8_t* q, const float* scales, int group, int rows, int K,
+                              int halves, int8_t* q_out, float* s_out, void* stream) {
+    size_t qb = 0, sb = 0;
+    const int rc = qlm_mx_layout_bytes(rows, K, group, halves, &qb, &sb);
+    if (rc != QLM_OK) return rc;
+    if (!q || !q_out || (sb && (!scales || !s_out))) return QLM_ERR_ARG;
+    if (((uintptr_t)q | (uintptr_t)q_out) & 15u) return QLM_ERR_SHAPE;
+    const int tiles = (rows + 15) / 16;
+    const size_t chunks = qb / 16;
+    const int grid = (int)((chunks + 255) / 256 < 65536 ? (chunks + 255) / 256 : 65536);
+    hipLaunchKernelGGL(k_mx_swizzle, dim3(grid), dim3(256), 0, as_stream(stream), q,
+                       sb ? scales : nullptr, rows, K, tiles, halves, q_out,
+                       sb ? s_out : nullptr);
+    return qlm_launch_status();
+}
+
+extern "C" int qlm_gemv_i8_mx_config(const float* x, const float* norm_w, float eps,
+                                     const int8_t* q, const float* scales, int group, float* y,
+                                     int N, int K, int epilogue, int waves, int ring, int grid,
+                                     void* stream) {
+    if (!x || !q || !scales || !y || N <= 0 || K <= 0 || grid <= 0) return QLM_ERR_ARG;
+    if (epilogue < EPI_STORE || epilogue > EPI_SWIGLU) return QLM_ERR_ARG;
+    const bool rowscale = (group == K);
+    if (!rowscale && group != 32) return QLM_ERR_SHAPE;
+    if (((uintptr_t)x | (uintptr_t)q | (uintptr_t)norm_w) & 15u) return QLM_ERR_SHAPE;
+    const int pro = norm_w ? PRO_RMSNORM : PRO_NONE;
+    if (epilogue == EPI_SWIGLU && !norm_w) return QLM_ERR_ARG;  // only the fused-norm form exists
+    if (epilogue == EPI_RESID && pro == PRO_RMSNORM) return QLM_ERR_ARG;
+    return mx_dispatch(pro, epilogue, MxConfig{waves, ring, grid}, x, norm_w, eps, q, scales,
+                       rowscale, y, N, K, as_stream(stream));
+}
+
 extern "C" size_t qlm_lm_head_greedy_workspace_bytes(void) {
     return (size_t)kMaxXsGrid * sizeof(unsigned long long);
 }
@@ -879,18 +1401,45 @@ extern "C" int qlm_lm_head_greedy(const float* x, const float* norm_w, float eps
         return QLM_ERR_SHAPE;
     const XsConfig c = xs_config(V, K, EPI_STORE);
     if (c.grid > kMaxXsGrid || xs_lds_bytes(K, PRO_RMSNORM) > kXsLdsMax) return QLM_ERR_SHAPE;
-    GreedyTail t;
-    t.keys = reinterpret_cast<unsigned long long*>(work);
-    t.tokens = tokens;
-    t.ld_tokens = ld_tokens;
-    t.pos = pos;
-    t.prompt_len = prompt_len;
-    t.embed = embed;
-    t.H = H;
-    t.vocab = V;
-    t.h = h_next;
     return xs_dispatch(PRO_RMSNORM, EPI_ARGMAX, c, x, norm_w, eps, q, scales, rowscale, logits, V,
-                       K, as_stream(stream), t);
+                       K, as_stream(stream),
+                       greedy_tail(work, tokens, ld_tokens, pos, prompt_len, embed, H, V, h_next));
+}
+
+extern "C" int qlm_lm_head_greedy_mx(const float* x, const float* norm_w, float eps,
+                                     const int8_t* q_tiles, const float* s_tiles, int group,
+                                     float* logits, int V, int K, void* work, int* tokens,
+                                     int ld_tokens, int* pos, const int* prompt_len,
+                                     const float* embed, int H, float* h_next, void* stream) {
+    if (!x || !norm_w || !q_tiles || !s_tiles || !logits || !work || !tokens || !pos ||
+        !prompt_len || !embed || !h_next || V <= 0 || K <= 0 || H <= 0 || ld_tokens <= 0)
+        return QLM_ERR_ARG;
+    const bool rowscale = (group == K);
+    if (!rowscale && group != 32) return QLM_ERR_SHAPE;
+    if (((uintptr_t)x | (uintptr_t)q_tiles | (uintptr_t)norm_w | (uintptr_t)work) & 15u)
+        return QLM_ERR_SHAPE;
+    const MxConfig c = mx_config(V, K, EPI_ARGMAX);
+    if (c.nw == 0) return QLM_ERR_SHAPE;
+    return mx_dispatch(PRO_RMSNORM, EPI_ARGMAX, c, x, norm_w, eps, q_tiles, s_tiles, rowscale,
+                       logits, V, K, as_stream(stream),
+                       greedy_tail(work, tokens, ld_tokens, pos, prompt_len, embed, H, V, h_next));
+}
+
+extern "C" int qlm_gemv_i8_mx(const float* x, const float* norm_w, float eps,
+                              const int8_t* q_tiles, const float* s_tiles, int group, float* y,
+                              int N, int K, int epilogue, void* stream) {
+    if (!x || !q_tiles || !s_tiles || !y || N <= 0 || K <= 0) return QLM_ERR_ARG;
+    if (epilogue < EPI_STORE || epilogue > EPI_SWIGLU) return QLM_ERR_ARG;
+    const bool rowscale = (group == K);
+    if (!rowscale && group != 32) return QLM_ERR_SHAPE;
+    if (((uintptr_t)x | (uintptr_t)q_tiles | (uintptr_t)norm_w) & 15u) return QLM_ERR_SHAPE;
+    const int pro = norm_w ? PRO_RMSNORM : PRO_NONE;
+    if (epilogue == EPI_SWIGLU && !norm_w) return QLM_ERR_ARG;
+    if (epilogue == EPI_RESID && pro == PRO_RMSNORM) return QLM_ERR_ARG;
+    const MxConfig c = mx_config(N, K, epilogue);
+    if (c.nw == 0) return QLM_ERR_SHAPE;
+    return mx_dispatch(pro, epilogue, c, x, norm_w, eps, q_tiles, s_tiles, rowscale, y, N, K,
+                       as_stream(stream));
 }
 
 extern "C" int qlm_gemv_i8_rmsnorm(const float* x, int ldx, const float* norm_w, float eps,

@@ -61,6 +61,11 @@ _SIGS = {
     "qlm_matmul_i8": (_i, [_vp, _i, _vp, _f, _vp, _vp, _i, _vp, _i, _i, _i, _i, _i, _vp, _sz,
                            _vp]),
     "qlm_gemv_i8_config": (_i, [_vp, _vp, _f, _vp, _vp, _i, _vp, _i, _i, _i, _i, _i, _i, _vp]),
+    "qlm_gemv_i8_mx_config": (_i, [_vp, _vp, _f, _vp, _vp, _i, _vp, _i, _i, _i, _i, _i, _i,
+                                   _vp]),
+    "qlm_mx_layout_bytes": (_i, [_i, _i, _i, _i, C.POINTER(_sz), C.POINTER(_sz)]),
+    "qlm_gemv_i8_mx": (_i, [_vp, _vp, _f, _vp, _vp, _i, _vp, _i, _i, _i, _vp]),
+    "qlm_mx_swizzle": (_i, [_vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp]),
     "qlm_gemv_i8_rmsnorm": (_i, [_vp, _i, _vp, _f, _vp, _vp, _i, _vp, _i, _i, _i, _i, _vp]),
     "qlm_gemv_i8_residual": (_i, [_vp, _i, _vp, _vp, _i, _vp, _i, _i, _i, _i, _vp]),
     "qlm_gemv_i8_swiglu_rmsnorm": (_i, [_vp, _i, _vp, _f, _vp, _vp, _i, _vp, _i, _i, _i, _i,
@@ -82,6 +87,8 @@ _SIGS = {
     "qlm_greedy_advance": (_i, [_vp, _i, _i, _i, _vp, _vp, _i, _vp, _vp, _vp]),
     "qlm_lm_head_greedy_workspace_bytes": (_sz, []),
     "qlm_lm_head_greedy": (_i, [_vp, _vp, _f, _vp, _vp, _i, _vp, _i, _i, _vp, _vp, _i, _vp, _vp,
+                                _vp, _i, _vp, _vp]),
+    "qlm_lm_head_greedy_mx": (_i, [_vp, _vp, _f, _vp, _vp, _i, _vp, _i, _i, _vp, _vp, _i, _vp, _vp,
                                 _vp, _i, _vp, _vp]),
     "qlm_embed_tokens": (_i, [_vp, _i, _i, _vp, _i, _vp, _vp, _i, _i, _vp]),
 }

@@ -6,6 +6,8 @@ evaluates exactly the reference's per-element arithmetic (conv1d tap sums,
 RoPE from the reference's own cos/sin table), the bar is bit-exactness.
 """
 
+import ctypes as C
+
 import numpy as np
 import pytest
 
@@ -127,6 +129,151 @@ def test_gemv_config_fused(hip, orc, rng, epi):
                          g, dy, N, K, code, lpr, rows, grid, None)
                 err = rel_err(dy.to_numpy((1, N), np.float32), ref)
                 assert err < 1e-5, (epi, lpr, rows, grid, err)
+
+
+MX_CASES = [  # (N, K, waves, ring, grid): ragged last tile, several tiles per workgroup
+    (1000, 2560, 4, 10, None), (1000, 2560, 8, 5, 7), (300, 2048, 16, 2, None),
+    (517, 4096, 8, 8, 3), (160, 9728, 16, 10, None), (37, 12288, 16, 12, 1),
+    (2000, 2048, 4, 8, 5), (77, 2048, 8, 4, None), (300, 256, 4, 1, None), (129, 512, 4, 2, 4),
+    (700, 1024, 4, 4, None),
+]
+
+
+def _mx_layout(hip, q, s, g, rows, K, halves):
+    """Weights and scales on the device in the tile-major layout."""
+    dq, ds = dev(hip, q), dev(hip, s)
+    qb, sb = C.c_size_t(), C.c_size_t()
+    hip.check(hip.lib().qlm_mx_layout_bytes(rows, K, g, halves, C.byref(qb), C.byref(sb)))
+    qz = hip.DeviceBuffer(qb.value)
+    sz = hip.DeviceBuffer(max(sb.value, 16))
+    hip.call("qlm_mx_swizzle", dq, ds, g, rows, K, halves, qz, sz if sb.value else None, None)
+    return qz, (sz if sb.value else ds), (dq, ds, qz, sz)
+
+
+def test_mx_swizzle_layout(hip, orc, rng):
+    """Tile-major layout: fragment (tile, block) holds, in lane order l = 16q
+    + n, bytes 64b + 16q .. +15 of row 16t + n of its half; rows past the
+    half are zero; scales follow as [h][n] = s[row n, group 2b + h]."""
+    rows, K, halves = 37, 192, 2
+    q, s = _weights(orc, rng, halves * rows, K, 32)
+    dq, ds, keep = _mx_layout(hip, q, s, 32, rows, K, halves)
+    tiles, nblk = (rows + 15) // 16, K // 64
+    qz = dq.to_numpy((halves * tiles, nblk, 64, 16), np.int8)
+    sz = ds.to_numpy((halves * tiles, nblk, 2, 16), np.float32)
+    for g in range(halves * tiles):
+        half, t = divmod(g, tiles)
+        for b in range(nblk):
+            for lane in range(64):
+                n, qd = lane & 15, lane >> 4
+                r = t * 16 + n
+                want = q[half * rows + r, 64 * b + 16 * qd:64 * b + 16 * qd + 16] if r < rows \
+                    else np.zeros(16, np.int8)
+                assert np.array_equal(qz[g, b, lane], want), (g, b, lane)
+            for h in range(2):
+                for n in range(16):
+                    r = t * 16 + n
+                    want = s[half * rows + r, 2 * b + h] if r < rows else 0.0
+                    assert sz[g, b, h, n] == want
+
+
+@pytest.mark.parametrize("epi", ["store", "norm", "resid", "swiglu"])
+@pytest.mark.parametrize("group", [32, "K"])
+def test_gemv_mx(hip, orc, rng, epi, group):
+    """The matrix-core M = 1 GEMV (int8 digits of x on v_mfma_i32_16x16x64_i8,
+    tile-major weights) under every instantiated launch pair: within 1e-5
+    normwise of the fp32 oracle (the fp32 GEMV's own bar), fused prologue and
+    epilogues included."""
+    eps = 1e-6
+    code = {"store": 0, "norm": 0, "resid": 1, "swiglu": 2}[epi]
+    for N, K, waves, ring, grid in MX_CASES:
+        g = K if group == "K" else 32
+        rows_w = 2 * N if epi == "swiglu" else N
+        q, s = _weights(orc, rng, rows_w, K, g)
+        x = rng.standard_normal((1, K)).astype(np.float32)
+        nw = (rng.standard_normal(K) * 0.02).astype(np.float32)
+        y0 = rng.standard_normal((1, N)).astype(np.float32)
+        if epi == "store":
+            ref = orc.matmul_i8(x, q, s, g)
+        elif epi == "resid":
+            ref = y0 + orc.matmul_i8(x, q, s, g)
+        else:
+            lg = orc.matmul_i8(orc.rms_norm(x, nw, eps), q, s, g)
+            ref = lg if epi == "norm" else orc.silu_mul(lg[:, :N].copy(), lg[:, N:].copy())
+        dy = dev(hip, y0)
+        tiles = (N + 15) // 16
+        say("gemv_mx", epi, g, N, K, waves, ring, grid)
+        dq, ds, keep = _mx_layout(hip, q, s, g, N, K, 2 if epi == "swiglu" else 1)
+        hip.call("qlm_gemv_i8_mx_config", dev(hip, x),
+                 dev(hip, nw) if epi in ("norm", "swiglu") else None, eps, dq, ds, g, dy, N, K,
+                 code, waves, ring, grid or tiles, None)
+        err = rel_err(dy.to_numpy((1, N), np.float32), ref)
+        assert err < 1e-5, (epi, g, N, K, waves, ring, grid, err)
+
+
+@pytest.mark.parametrize("N,K,epi", [(9728, 2560, "swiglu"), (2560, 9728, "resid"),
+                                     (8224, 2560, "norm"), (2560, 2048, "resid"),
+                                     (3584, 1024, "swiglu"), (1024, 3584, "resid"),
+                                     (300, 4160, "norm")])
+def test_gemv_mx_auto(hip, orc, rng, N, K, epi):
+    """qlm_gemv_i8_mx picks its launch shape (tuned table for the 4B decode
+    projections, rule elsewhere) and matches the oracle; a K no instantiated
+    shape fits (4160 = 65 blocks) is refused with QLM_ERR_SHAPE."""
+    g, eps = 32, 1e-6
+    code = {"norm": 0, "resid": 1, "swiglu": 2}[epi]
+    rows_w = 2 * N if epi == "swiglu" else N
+    q, s = _weights(orc, rng, rows_w, K, g)
+    x = rng.standard_normal((1, K)).astype(np.float32)
+    nw = (rng.standard_normal(K) * 0.02).astype(np.float32)
+    y0 = rng.standard_normal((1, N)).astype(np.float32)
+    if epi == "resid":
+        ref = y0 + orc.matmul_i8(x, q, s, g)
+    else:
+        lg = orc.matmul_i8(orc.rms_norm(x, nw, eps), q, s, g)
+        ref = lg if epi == "norm" else orc.silu_mul(lg[:, :N].copy(), lg[:, N:].copy())
+    dq, ds, keep = _mx_layout(hip, q, s, g, N, K, 2 if epi == "swiglu" else 1)
+    dy, dx, dnw = dev(hip, y0), dev(hip, x), dev(hip, nw)
+    rc = hip.lib().qlm_gemv_i8_mx(dx.ptr, None if epi == "resid" else dnw.ptr, C.c_float(eps),
+                                  dq.ptr, ds.ptr, g, dy.ptr, N, K, code, None)
+    if K == 4160:
+        assert rc == -2
+        return
+    hip.check(rc)
+    assert rel_err(dy.to_numpy((1, N), np.float32), ref) < 1e-5
+
+
+def test_gemv_mx_dynamic_range(hip, orc, rng):
+    """Activations spanning 1e-6 .. 1e3 (one power-of-two scale for all
+    digits), a zero activation (exact zeros out) and a one-hot activation."""
+    N, K = 500, 2560
+    q, s = _weights(orc, rng, N, K, 32)
+    dq, ds, keep = _mx_layout(hip, q, s, 32, N, K, 1)
+    dy = hip.DeviceBuffer(N * 4)
+    mags = 10.0 ** rng.uniform(-6, 3, K)
+    cases = {"wide": (rng.standard_normal(K) * mags).astype(np.float32),
+             "zero": np.zeros(K, np.float32),
+             "onehot": np.eye(1, K, 1234, dtype=np.float32)[0] * 3.0}
+    for name, xv in cases.items():
+        x = xv[None, :]
+        ref = orc.matmul_i8(x, q, s, 32)
+        hip.call("qlm_gemv_i8_mx_config", dev(hip, x), None, 0.0, dq, ds, 32, dy, N, K, 0, 4,
+                 10, 32, None)
+        y = dy.to_numpy((1, N), np.float32)
+        if name == "zero":
+            assert not y.any()
+        else:
+            assert rel_err(y, ref) < 1e-5, name
+
+
+def test_gemv_mx_rejects_bad_shapes(hip, orc, rng):
+    """Launch pairs that are not instantiated or do not match K are refused
+    before any launch."""
+    q, s = _weights(orc, rng, 64, 4096, 32)
+    x = dev(hip, rng.standard_normal((1, 4096)).astype(np.float32))
+    dq, ds = dev(hip, q), dev(hip, s)
+    dy = hip.DeviceBuffer(64 * 4)
+    for waves, ring, K in ((4, 5, 2560), (16, 3, 2560), (4, 10, 2560 + 32), (4, 13, 3328)):
+        assert hip.lib().qlm_gemv_i8_mx_config(x.ptr, None, 0.0, dq.ptr, ds.ptr, 32, dy.ptr,
+                                               64, K, 0, waves, ring, 4, None) != 0
 
 
 def test_gemv_exact_integers(hip, orc, rng):
@@ -368,9 +515,11 @@ def test_greedy_advance_and_embed(hip, rng):
 
 
 @pytest.mark.parametrize("group", [32, "K"])
-def test_lm_head_greedy_fused(hip, orc, rng, group):
+@pytest.mark.parametrize("tiles", [False, True])
+def test_lm_head_greedy_fused(hip, orc, rng, group, tiles):
     """Final norm + lm_head + argmax + advance + next embedding (two launches),
-    three calls in a row (prompt position, then two generated tokens)."""
+    three calls in a row (prompt position, then two generated tokens); with
+    row-major weights and, on the matrix cores, tile-major ones."""
     V, K, L = 151936, 1024, 16
     g = K if group == "K" else 32
     q, s = _weights(orc, rng, V, K, g)
@@ -383,14 +532,18 @@ def test_lm_head_greedy_fused(hip, orc, rng, group):
     nwork = hip.lib().qlm_lm_head_greedy_workspace_bytes()
     work = hip.DeviceBuffer(nwork)
     work.upload(np.full(nwork, 0xA5, np.uint8))  # no initial contents are required
-    dq, ds, dnw, dtab = dev(hip, q), dev(hip, s), dev(hip, nw), dev(hip, table)
+    if tiles:
+        dq, ds, keep = _mx_layout(hip, q, s, g, V, K, 1)
+    else:
+        dq, ds = dev(hip, q), dev(hip, s)
+    dnw, dtab = dev(hip, nw), dev(hip, table)
     dlg, dh = hip.DeviceBuffer(V * 4), hip.DeviceBuffer(K * 4)
     p = 1
     for step in range(3):
         x = (rng.standard_normal((1, K)) * 2).astype(np.float32)
         lg_ref = orc.matmul_i8(orc.rms_norm(x, nw, 1e-6), q, s, g)[0]
-        hip.call("qlm_lm_head_greedy", dev(hip, x), dnw, 1e-6, dq, ds, g, dlg, V, K, work, dtok, L,
-                 dpos, dplen, dtab, K, dh, None)
+        hip.call("qlm_lm_head_greedy_mx" if tiles else "qlm_lm_head_greedy", dev(hip, x), dnw,
+                 1e-6, dq, ds, g, dlg, V, K, work, dtok, L, dpos, dplen, dtab, K, dh, None)
         lg = dlg.to_numpy(V, np.float32)
         assert rel_err(lg, lg_ref) < 1e-5
         want = int(np.argmax(lg))  # first maximum of the GPU's own logits
