@@ -63,6 +63,7 @@ def bench_gemv(hip, shapes, Ms, group_kind, iters=100, pool_bytes=2 << 30):
         s = rng.uniform(0.001, 0.01, (N, nb)).astype(np.float32)
         dq = [hip.DeviceBuffer.from_numpy(q) for _ in range(ncopy)]
         ds = [hip.DeviceBuffer.from_numpy(s) for _ in range(ncopy)]
+        dz = _tile_major(hip, dq, ds, group, N, K, 1)
         for M in Ms:
             x = hip.DeviceBuffer.from_numpy(rng.standard_normal((M, K)).astype(np.float32))
             y = hip.DeviceBuffer(M * N * 4)
@@ -96,20 +97,59 @@ def bench_gemv(hip, shapes, Ms, group_kind, iters=100, pool_bytes=2 << 30):
                 r["mfma_util"] = round(2.0 * M * N * K / (us * 1e-6) / BF16_PEAK_FLOPS, 5)
             out.append(r)
             log(f"gemv {N}x{K} M={M} G={group}: {us:.1f} us {b / us / 1e3:.0f} GB/s")
+            if M == 1 and dz:
+                # the same product on the matrix cores over tile-major weights
+                def launch_mx(i):
+                    qz, sz = dz[i % ncopy]
+                    hip.call("qlm_gemv_i8_mx", x, None, 0.0, qz, sz, group, y, N, K, 0, st.ptr)
+
+                for i in range(ncopy):
+                    launch_mx(i)
+                e0, e1 = hip.Event(), hip.Event()
+                e0.record(st.ptr)
+                for i in range(n_it):
+                    launch_mx(i)
+                e1.record(st.ptr)
+                us = e0.elapsed_ms(e1) * 1000.0 / n_it
+                out.append({"N": N, "K": K, "M": M, "group": group, "kernel": "qlm_gemv_i8_mx",
+                            "layout": "tile-major", "us": round(us, 2),
+                            "GBps": round(b / us / 1e3, 1), "bytes": b,
+                            "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4)})
+                log(f"gemv_mx {N}x{K} M=1 G={group}: {us:.1f} us {b / us / 1e3:.0f} GB/s")
             x.free()
             y.free()
             work.free()
-        for b_ in dq + ds:
+        for b_ in dq + ds + [t for pair in dz for t in pair if t not in ds]:
             b_.free()
+    return out
+
+
+def _tile_major(hip, dq, ds, group, rows, K, halves):
+    """Tile-major copies (qlm_mx_swizzle) of each weight copy; [] when K has
+    no matrix-core launch shape. Per-row scales keep their layout."""
+    import ctypes as C
+
+    qb, sb = C.c_size_t(), C.c_size_t()
+    if hip.lib().qlm_mx_layout_bytes(rows, K, group, halves, C.byref(qb), C.byref(sb)) != 0:
+        return []
+    out = []
+    for q_, s_ in zip(dq, ds):
+        qz = hip.DeviceBuffer(qb.value)
+        sz = hip.DeviceBuffer(sb.value) if sb.value else s_
+        hip.call("qlm_mx_swizzle", q_, s_, group, rows, K, halves, qz,
+                 sz if sb.value else None, None)
+        out.append((qz, sz))
+    hip.sync()
     return out
 
 
 # The dominant kernel of the batch-1 decode step (about a third of the step):
 # the fused RMSNorm + gate/up projection + SwiGLU GEMV of every layer, 4B
 # shape (F = 9728 outputs from 2F = 19456 int8 rows of K = 2560, group-32
-# scales).
+# scales), on the int8 matrix cores over tile-major weights.
 DOM_F, DOM_K = 9728, 2560
-DOM_NAME = "k_gemv_xs<2, 2, false, 1, 2> (RMSNorm + gate/up GEMV + SwiGLU, 19456x2560 int8 G=32)"
+DOM_NAME = ("k_gemv_mx<8, 2, 5, false, 1, 2> (RMSNorm + gate/up GEMV + SwiGLU on the int8 "
+            "matrix cores, 19456x2560 int8 G=32, tile-major)")
 PMC_FILE = os.path.join(ROOT, "profiles", "gemv_gate_up_4b_pmc.json")
 
 
@@ -122,8 +162,9 @@ def dominant_bytes():
 
 def measure_dominant(hip, launches=400, pool_bytes=2 << 30):
     """Average launch duration of the dominant kernel, HIP events recorded on
-    the stream it is launched on, weights cycled over > 2 GiB of copies so
-    every launch streams them from HBM (not the 256 MB last-level cache)."""
+    the stream it is launched on (around graph replays of back-to-back
+    launches), weights cycled over > 2 GiB of copies so every launch streams
+    them from HBM (not the 256 MB last-level cache)."""
     rng = np.random.default_rng(1)
     st = hip.Stream()
     rows, nb = 2 * DOM_F, DOM_K // 32
@@ -131,25 +172,49 @@ def measure_dominant(hip, launches=400, pool_bytes=2 << 30):
     ncopy = int(max(2, min(64, pool_bytes // wb)))
     q = rng.integers(-127, 128, (rows, DOM_K), dtype=np.int8)
     s = rng.uniform(0.001, 0.01, (rows, nb)).astype(np.float32)
-    dq = [hip.DeviceBuffer.from_numpy(q) for _ in range(ncopy)]
-    ds = [hip.DeviceBuffer.from_numpy(s) for _ in range(ncopy)]
+    dq1 = [hip.DeviceBuffer.from_numpy(q)]
+    ds1 = [hip.DeviceBuffer.from_numpy(s)]
+    z = _tile_major(hip, dq1, ds1, 32, DOM_F, DOM_K, 2)[0]
+    dq1[0].free()
+    ds1[0].free()
+    # ncopy tile-major copies: the first swizzled, the rest device copies of it
+    dz = [z] + [(hip.DeviceBuffer(z[0].nbytes), hip.DeviceBuffer(z[1].nbytes))
+                for _ in range(ncopy - 1)]
+    for qz, sz in dz[1:]:
+        hip.check(hip.lib().qlm_memcpy_d2d(qz.ptr, z[0].ptr, z[0].nbytes, None))
+        hip.check(hip.lib().qlm_memcpy_d2d(sz.ptr, z[1].ptr, z[1].nbytes, None))
+    hip.sync()
     x = hip.DeviceBuffer.from_numpy(rng.standard_normal(DOM_K).astype(np.float32))
     nw = hip.DeviceBuffer.from_numpy((rng.standard_normal(DOM_K) * 0.02).astype(np.float32))
     y = hip.DeviceBuffer(DOM_F * 4)
 
     def launch(i):
-        hip.call("qlm_gemv_i8_swiglu_rmsnorm", x, DOM_K, nw, 1e-6, dq[i % ncopy], ds[i % ncopy],
-                 32, y, DOM_F, 1, DOM_F, DOM_K, st.ptr)
+        qz, sz = dz[i % ncopy]
+        hip.call("qlm_gemv_i8_mx", x, nw, 1e-6, qz, sz, 32, y, DOM_F, DOM_K, 2, st.ptr)
 
+    # launched as in the decode step: back-to-back kernels replayed from one
+    # captured graph (no host launch gaps between them)
+    import ctypes as C
+
+    lib = hip.lib()
     for i in range(ncopy):
         launch(i)
+    per = 4 * ncopy
+    hip.check(lib.qlm_graph_begin(st.ptr))
+    for i in range(per):
+        launch(i)
+    g = C.c_void_p()
+    hip.check(lib.qlm_graph_end(st.ptr, C.byref(g)))
+    hip.check(lib.qlm_graph_launch(g, st.ptr))
+    reps = max(1, launches // per)
     e0, e1 = hip.Event(), hip.Event()
     e0.record(st.ptr)
-    for i in range(launches):
-        launch(i)
+    for _ in range(reps):
+        hip.check(lib.qlm_graph_launch(g, st.ptr))
     e1.record(st.ptr)
-    us = e0.elapsed_ms(e1) * 1000.0 / launches
-    for b_ in dq + ds + [x, nw, y]:
+    us = e0.elapsed_ms(e1) * 1000.0 / (reps * per)
+    hip.check(lib.qlm_graph_destroy(g))
+    for b_ in [t for pair in dz for t in pair] + [x, nw, y]:
         b_.free()
     return us
 
