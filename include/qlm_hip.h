@@ -127,6 +127,9 @@ int qlm_gemv_i8_mx_config(const float* x, const float* norm_w, float eps, const 
 int qlm_gemv_i8_mx(const float* x, const float* norm_w, float eps, const int8_t* q_tiles,
                    const float* s_tiles, int group, float* y, int N, int K, int epilogue,
                    void* stream);
+/* The launch shape qlm_gemv_i8_mx picks (waves per workgroup, blocks per
+ * wave, workgroups), or QLM_ERR_SHAPE. Host only. */
+int qlm_gemv_i8_mx_shape(int N, int K, int epilogue, int* waves, int* ring, int* grid);
 
 /* A4: the same matmul for M > 1 on the matrix cores (batched decode, prefill;
  * math_ops.cpp:845-871). Weights stay exact (int8 in bf16); each activation
@@ -140,9 +143,31 @@ int qlm_gemv_i8_mx(const float* x, const float* norm_w, float eps, const int8_t*
  * scales and K-split partial sums; no initial contents needed; calls that
  * share it must be ordered on one stream). */
 size_t qlm_matmul_i8_workspace_bytes(int M, int N, int K, int epilogue);
+
 int qlm_matmul_i8(const float* x, int ldx, const float* norm_w, float eps, const int8_t* q,
                   const float* scales, int group, float* y, int ldy, int M, int N, int K,
                   int epilogue, void* work, size_t work_bytes, void* stream);
+
+/* Batched decode (2 <= M <= 16 activation rows) on the int8 matrix cores
+ * over the tile-major weights of qlm_mx_swizzle (per-row scales as
+ * quantised): a first launch writes each row's (optionally RMSNormed)
+ * int8 digit vectors into `work`, the second streams the weights once with
+ * one v_mfma_i32_16x16x64_i8 per pair of rows and 64-column block, the
+ * whole K inside each workgroup (no partial sums). Same semantics, epilogues
+ * and accuracy (~1e-7 normwise) as qlm_matmul_i8. K a multiple of 64, at
+ * most 3584 or from 8256 to 10240; QLM_ERR_SHAPE otherwise (and for
+ * M > 16), where qlm_matmul_i8 serves. work: device scratch of
+ * qlm_matmul_i8_mx_workspace_bytes(M, K), 256-byte aligned, no initial
+ * contents needed; calls sharing it must be ordered on one stream. */
+size_t qlm_matmul_i8_mx_workspace_bytes(int M, int K);
+/* The launch shape qlm_matmul_i8_mx picks (waves per workgroup, blocks per
+ * wave and tile, ring slots, workgroups), or QLM_ERR_SHAPE. Host only. */
+int qlm_matmul_i8_mx_shape(int M, int N, int K, int epilogue, int* waves, int* blocks, int* ring,
+                           int* grid);
+int qlm_matmul_i8_mx(const float* x, int ldx, const float* norm_w, float eps,
+                     const int8_t* q_tiles, const float* s_tiles, int group, float* y, int ldy,
+                     int M, int N, int K, int epilogue, void* work, size_t work_bytes,
+                     void* stream);
 
 /* Fused forms used by the decode step (same arithmetic as the unfused
  * reference sequence, one launch instead of two or three):

@@ -14,9 +14,9 @@ void* g_stream = nullptr;
 void* g_mm_work = nullptr;
 size_t g_mm_work_bytes = 0;
 
-// Rows from which the matrix-core path replaces the GEMV (which re-reads the
-// weights once per 4 activation rows).
-constexpr int64_t kMfmaMinRows = 5;
+// Rows from which the matrix-core paths replace the row-major GEMV (which
+// re-reads the weights once per 4 activation rows).
+constexpr int64_t kMfmaMinRows = 2;
 
 void need(bool ok, const char* what) {
     if (!ok) throw std::runtime_error(std::string("math: ") + what);
@@ -27,6 +27,17 @@ void check_int8(const Tensor& B) {
     need(B.shape.size() == 2, "int8 weight must be [N, K]");
 }
 }  // namespace
+
+bool use_tiles_batched(int64_t M, int64_t N, int64_t K) {
+    return M >= 2 && M <= 8 && (N >= 4096 || K <= 2048);
+}
+
+int matmul_launches(int64_t M, int64_t N, int64_t K, bool norm) {
+    if (M == 1) return 1;
+    if (use_tiles_batched(M, N, K)) return 2;  // digits + matmul
+    if (M < kMfmaMinRows) return (int)((M + 3) / 4);
+    return norm ? 3 : 2;  // [row norms +] split-K matmul + ordered reduction
+}
 
 void set_stream(void* s) { g_stream = s; }
 void* stream() { return g_stream; }
@@ -49,13 +60,34 @@ bool gemv_tiles(const Tensor& A, const float* norm_w, float eps, const Tensor& B
     return true;
 }
 
-// The matrix-core matmul for M > 4 rows (norm_w null: no RMSNorm prologue).
+// 2..8 activation rows on the int8 matrix cores over the tile-major copy
+// (qlm_matmul_i8_mx): measured faster than the split-K bf16 form for wide
+// matrices (N >= 4096) and short K (<= 2048); the 2560-row, 9728-column down
+// projection keeps the split-K form, which spreads its few 16-row tiles over
+// more workgroups. false when not taken.
+bool gemm_tiles(const Tensor& A, const float* norm_w, float eps, const Tensor& B, float* C,
+                int64_t ldc, int64_t N, int epilogue) {
+    const int64_t M = A.rows(), K = A.cols();
+    if (!use_tiles_batched(M, N, K) || !B.int8_tiles) return false;
+    const size_t need_b = qlm_matmul_i8_mx_workspace_bytes((int)M, (int)K);
+    need(g_mm_work && g_mm_work_bytes >= need_b,
+         "matmul: batched rows need set_matmul_workspace() of qlm_matmul_i8_mx_workspace_bytes()");
+    const int rc = qlm_matmul_i8_mx(A.data, (int)A.row_stride(), norm_w, eps, B.int8_tiles,
+                                    B.int8_tile_scales, B.int8_group, C, (int)ldc, (int)M, (int)N,
+                                    (int)K, epilogue, g_mm_work, g_mm_work_bytes, g_stream);
+    if (rc == QLM_ERR_SHAPE) return false;
+    check(rc, "qlm_matmul_i8_mx");
+    return true;
+}
+
+// The split-K bf16 matrix-core matmul for M > 1 rows (norm_w null: no
+// RMSNorm prologue).
 void matmul_mfma(const Tensor& A, const float* norm_w, float eps, const Tensor& B, float* C,
                  int64_t ldc, int64_t N, int epilogue) {
     const int64_t M = A.rows(), K = A.cols();
     const size_t need_b = qlm_matmul_i8_workspace_bytes((int)M, (int)N, (int)K, epilogue);
     need(g_mm_work && g_mm_work_bytes >= need_b,
-         "matmul: M > 4 needs set_matmul_workspace() of qlm_matmul_i8_workspace_bytes()");
+         "matmul: M > 1 needs set_matmul_workspace() of qlm_matmul_i8_workspace_bytes()");
     check(qlm_matmul_i8(A.data, (int)A.row_stride(), norm_w, eps, B.int8_data, B.int8_scales,
                         B.int8_group, C, (int)ldc, (int)M, (int)N, (int)K, epilogue, g_mm_work,
                         g_mm_work_bytes, g_stream),
@@ -69,6 +101,7 @@ void matmul(const Tensor& A, const Tensor& B, Tensor& C, bool transpose_B) {
     const int64_t K = A.cols(), M = A.rows(), N = B.shape[0];
     need(B.shape[1] == K, "matmul: K mismatch");
     need(C.cols() >= N || C.row_stride() >= N, "matmul: output too small");
+    if (gemm_tiles(A, nullptr, 0.0f, B, C.data, C.row_stride(), N, 0)) return;
     if (M >= kMfmaMinRows) {
         matmul_mfma(A, nullptr, 0.0f, B, C.data, C.row_stride(), N, 0);
         return;
@@ -83,6 +116,7 @@ void matmul_rmsnorm(const Tensor& A, const Tensor& norm_w, float eps, const Tens
     check_int8(B);
     const int64_t K = A.cols(), M = A.rows(), N = B.shape[0];
     need(B.shape[1] == K && norm_w.size() == K, "matmul_rmsnorm: K mismatch");
+    if (gemm_tiles(A, norm_w.data, eps, B, C.data, C.row_stride(), N, 0)) return;
     if (M >= kMfmaMinRows) {
         matmul_mfma(A, norm_w.data, eps, B, C.data, C.row_stride(), N, 0);
         return;
@@ -98,6 +132,7 @@ void matmul_residual(const Tensor& A, const Tensor& B, Tensor& residual) {
     check_int8(B);
     const int64_t K = A.cols(), M = A.rows(), N = B.shape[0];
     need(B.shape[1] == K && residual.cols() == N, "matmul_residual: shape mismatch");
+    if (gemm_tiles(A, nullptr, 0.0f, B, residual.data, residual.row_stride(), N, 1)) return;
     if (M >= kMfmaMinRows) {
         matmul_mfma(A, nullptr, 0.0f, B, residual.data, residual.row_stride(), N, 1);
         return;
@@ -114,6 +149,7 @@ void matmul_swiglu_rmsnorm(const Tensor& A, const Tensor& norm_w, float eps, con
     check_int8(B);
     const int64_t K = A.cols(), M = A.rows(), F = B.shape[0] / 2;
     need(B.shape[0] % 2 == 0 && B.shape[1] == K && C.cols() == F, "matmul_swiglu: shape mismatch");
+    if (gemm_tiles(A, norm_w.data, eps, B, C.data, C.row_stride(), F, 2)) return;
     if (M >= kMfmaMinRows) {
         matmul_mfma(A, norm_w.data, eps, B, C.data, C.row_stride(), F, 2);
         return;

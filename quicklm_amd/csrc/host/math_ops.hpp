@@ -20,9 +20,15 @@ void* stream();
 // C = A * B^T with B an int8 (Q8_0) weight operand; A [M, K] fp32, C [M, N]
 // with row stride C.row_stride() (math_ops.hpp:92; math_ops.cpp:820-900).
 void matmul(const Tensor& A, const Tensor& B, Tensor& C, bool transpose_B = true);
-// Device workspace for the matrix-core forms (M > 4): at least
-// qlm_matmul_i8_workspace_bytes() of every call that follows.
+// Device workspace for the matrix-core forms (M > 1): at least
+// qlm_matmul_i8_workspace_bytes() and qlm_matmul_i8_mx_workspace_bytes() of
+// every call that follows.
 void set_matmul_workspace(void* p, size_t bytes);
+// Whether M activation rows against an [N, K] weight with a tile-major copy
+// take the int8 matrix-core batched form, and the kernel launches one
+// matmul call makes (for launch counts).
+bool use_tiles_batched(int64_t M, int64_t N, int64_t K);
+int matmul_launches(int64_t M, int64_t N, int64_t K, bool norm);
 
 // math_ops.hpp:102 / :139-140 / :132.
 void rms_norm(const Tensor& input, const Tensor& weight, Tensor& output, float eps);

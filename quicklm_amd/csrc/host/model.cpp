@@ -278,16 +278,6 @@ void DecoderModel::reset_states() {
 // One decode step for sequences [0, B): the forward of DecoderModel::forward
 // (model.cpp:151-199) with every layer's elementwise work fused into the
 // projections, followed by greedy sampling and the position advance.
-namespace {
-// Launches of one math::matmul* call over B rows: the M = 1 GEMV, the GEMV
-// in slices of 4 rows, or (B > 4) the matrix-core matmul after a separate
-// RMSNorm when the norm is fused.
-int mm_launches(int B, bool norm) {
-    if (B == 1) return 1;
-    if (B > 4) return norm ? 2 : 1;
-    return (B + 3) / 4;
-}
-}  // namespace
 
 void DecoderModel::enqueue_step(int B) {
     math::set_stream(stream_);
@@ -316,7 +306,8 @@ void DecoderModel::enqueue_step(int B) {
             core.strides = {CORE_, 1};
             math::matmul_residual(core, w.dn_out.view(), hx);
             ++dn_i;
-            n += mm_launches(B, true) + 1 + mm_launches(B, false);
+            n += math::matmul_launches(B, PD_, H, true) + 1 +
+                 math::matmul_launches(B, H, HD_, false);
         } else {
             Tensor proj({B, PQ_}, proj_.get<float>());
             proj.strides = {Pmax, 1};
@@ -332,12 +323,13 @@ void DecoderModel::enqueue_step(int B) {
             core.strides = {CORE_, 1};
             math::matmul_residual(core, w.at_o.view(), hx);
             ++at_i;
-            n += mm_launches(B, true) + 2 + mm_launches(B, false);  // + attention, combine
+            n += math::matmul_launches(B, PQ_, H, true) + 2 +  // + attention, combine
+                 math::matmul_launches(B, H, nq * hd, false);
         }
         Tensor act({B, F}, act_.get<float>());
         math::matmul_swiglu_rmsnorm(hx, post_ln, eps, w.gate_up.view(), act);
         math::matmul_residual(act, w.down.view(), hx);
-        n += mm_launches(B, true) + mm_launches(B, false);
+        n += math::matmul_launches(B, F, H, true) + math::matmul_launches(B, H, F, false);
     }
     // Step tail: final norm + lm_head + greedy sample + advance, then the
     // embedding of the token now at pos (the next step's input, or the next
@@ -369,7 +361,7 @@ void DecoderModel::enqueue_step(int B) {
                                  prompt_len_.get<int>(), stream_),
               "argmax");
         embed_current(B);
-        n += mm_launches(B, true) + 3;  // + argmax (two passes with advance), embedding
+        n += math::matmul_launches(B, V, H, true) + 3;  // + argmax (two passes), embedding
     }
     kernels_per_step_ = n;
 }
@@ -463,6 +455,7 @@ size_t DecoderModel::matmul_workspace(int M) const {
     size_t b = 256;
     auto upd = [&](int N, int K, int epi) {
         b = std::max(b, qlm_matmul_i8_workspace_bytes(M, N, K, epi));
+        if (M <= 16) b = std::max(b, qlm_matmul_i8_mx_workspace_bytes(M, K));
     };
     if (PD_ > 0) {
         upd(PD_, H, 0);

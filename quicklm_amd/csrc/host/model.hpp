@@ -153,7 +153,7 @@ class DecoderModel {
     int ld_tokens_ = 0;
     // activations
     DeviceBuffer h_, proj_, core_, act_, logits_, argmax_work_, attn_work_, tail_work_;
-    DeviceBuffer mm_work_;  // workspace of the matrix-core matmuls (M > 4)
+    DeviceBuffer mm_work_;  // workspace of the matrix-core matmuls (M > 1)
     // prefill activations for up to pf_rows_ prompt rows per chunk
     DeviceBuffer hx_pf_, proj_pf_, core_pf_, act_pf_, gqa_pf_work_, dn_pf_work_;
     int pf_rows_ = 0;

@@ -696,7 +696,9 @@ __global__ __launch_bounds__(NW * QLM_WAVE) void k_gemv_mx(
     // P = ceil(blocks / NW), so a wave's last slot may lie past K: it then
     // repeats the wave's last block (a cache hit) and meets zero digits. The
     // next tile's slot u is requested as soon as slot u is consumed.
-    const int blast = nblk - 1 - ((nblk - 1 - w) % NW);  // this wave's last block
+    // this wave's last block (a wave past the last block reads block nblk-1,
+    // which then meets zero digits)
+    const int blast = w < nblk ? nblk - 1 - ((nblk - 1 - w) % NW) : nblk - 1;
     int4 wb[P][T];
     float sb[P][T];
     auto issue = [&](int tile, int u) {
@@ -1113,6 +1115,7 @@ constexpr int kMxPairs[][2] = {{4, 1}, {4, 2},  {4, 4},  {4, 8},   {4, 10},  {8,
 // pair is instantiated.
 bool mx_fits(int K, int nw, int ring) {
     if (K <= 0 || K % 64 != 0 || K > 4 * QLM_WAVE * nw * mx_xmax(nw)) return false;
+    if (K / 64 < nw) return false;  // every wave has a block
     if (ring != (K / 64 + nw - 1) / nw) return false;
     for (const auto& pr : kMxPairs)
         if (pr[0] == nw && pr[1] == ring) return true;
@@ -1423,6 +1426,17 @@ extern "C" int qlm_lm_head_greedy_mx(const float* x, const float* norm_w, float 
     return mx_dispatch(PRO_RMSNORM, EPI_ARGMAX, c, x, norm_w, eps, q_tiles, s_tiles, rowscale,
                        logits, V, K, as_stream(stream),
                        greedy_tail(work, tokens, ld_tokens, pos, prompt_len, embed, H, V, h_next));
+}
+
+extern "C" int qlm_gemv_i8_mx_shape(int N, int K, int epilogue, int* waves, int* ring,
+                                    int* grid) {
+    if (N <= 0 || K <= 0 || !waves || !ring || !grid) return QLM_ERR_ARG;
+    const MxConfig c = mx_config(N, K, epilogue);
+    if (c.nw == 0 || !mx_fits(K, c.nw, c.ring)) return QLM_ERR_SHAPE;
+    *waves = c.nw;
+    *ring = c.ring;
+    *grid = c.grid;
+    return QLM_OK;
 }
 
 extern "C" int qlm_gemv_i8_mx(const float* x, const float* norm_w, float eps,

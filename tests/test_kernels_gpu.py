@@ -347,6 +347,62 @@ def test_matmul_mfma_epilogues(hip, orc, rng, M, K, epi):
     assert rel_err(dy.to_numpy((M, N), np.float32), ref) < 1e-5
 
 
+MMX_CASES = [  # (M, N, K): batched decode rows over every K range the tile-major form serves
+    (2, 300, 1024), (3, 517, 2560), (5, 1000, 2048), (8, 160, 9728), (16, 2560, 9728),
+    (16, 1000, 2560), (16, 77, 3584), (7, 300, 512), (12, 130, 2560),
+]
+
+
+@pytest.mark.parametrize("M,N,K", MMX_CASES)
+@pytest.mark.parametrize("epi", ["store", "store_norm", "resid", "swiglu_norm"])
+@pytest.mark.parametrize("group", [32, "K"])
+def test_matmul_mx(hip, orc, rng, M, N, K, epi, group):
+    """Batched decode on the int8 matrix cores over tile-major weights
+    (per-row digits, one MFMA per row pair, K inside the workgroup): within
+    1e-5 normwise of the fp32 oracle, strided output rows, every epilogue."""
+    g, eps = (K if group == "K" else 32), 1e-6
+    rows_w = 2 * N if epi.startswith("swiglu") else N
+    q, s = _weights(orc, rng, rows_w, K, g)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    nw = (rng.standard_normal(K) * 0.02).astype(np.float32)
+    ldy = N + 5
+    y0 = rng.standard_normal((M, ldy)).astype(np.float32)
+    xin = orc.rms_norm(x, nw, eps) if epi.endswith("norm") else x
+    lg = orc.matmul_i8(xin, q, s, g)
+    if epi == "resid":
+        ref = y0[:, :N] + lg
+    elif epi.startswith("store"):
+        ref = lg
+    else:
+        ref = orc.silu_mul(lg[:, :N].copy(), lg[:, N:].copy())
+    dq, ds, keep = _mx_layout(hip, q, s, g, N, K, 2 if epi.startswith("swiglu") else 1)
+    nwork = hip.lib().qlm_matmul_i8_mx_workspace_bytes(M, K)
+    work = hip.DeviceBuffer(nwork)
+    work.upload(np.full(nwork, 0x5A, np.uint8))  # no initial contents are required
+    dy = dev(hip, y0)
+    code = {"store": 0, "store_norm": 0, "resid": 1, "swiglu_norm": 2}[epi]
+    say("matmul_mx", epi, g, M, N, K)
+    hip.call("qlm_matmul_i8_mx", dev(hip, x), K, dev(hip, nw) if epi.endswith("norm") else None,
+             eps, dq, ds, g, dy, ldy, M, N, K, code, work, nwork, None)
+    y = dy.to_numpy((M, ldy), np.float32)
+    assert rel_err(y[:, :N], ref) < 1e-5
+    assert np.array_equal(y[:, N:], y0[:, N:])  # the stride gap is untouched
+
+
+def test_matmul_mx_refuses(hip, orc, rng):
+    """M > 16 and K outside the served ranges return QLM_ERR_SHAPE before
+    any launch."""
+    lib = hip.lib()
+    q, s = _weights(orc, rng, 64, 4096, 32)
+    dq, ds = dev(hip, q), dev(hip, s)
+    x = dev(hip, rng.standard_normal((17, 4096)).astype(np.float32))
+    y = hip.DeviceBuffer(17 * 64 * 4)
+    work = hip.DeviceBuffer(1 << 20)
+    for M, K in ((17, 2560), (4, 6144), (4, 8192), (4, 2560 + 32)):
+        assert lib.qlm_matmul_i8_mx(x.ptr, K, None, C.c_float(0.0), dq.ptr, ds.ptr, 32, y.ptr, 64,
+                                    M, 64, K, 0, work.ptr, C.c_size_t(1 << 20), None) != 0
+
+
 @pytest.mark.parametrize("M", [16, 130])
 def test_matmul_mfma_exact_integers(hip, orc, rng, M):
     """Small-integer activations are exact in bf16 (lo = 0) and every
