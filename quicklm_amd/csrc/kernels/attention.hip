@@ -126,13 +126,16 @@ __global__ __launch_bounds__(kThreads) void k_attn(
             vv[u] = load4<KV>(vc + (row0 + (size_t)pl * n_kv) * HD + c4 * 4);
         }
     };
-    load_kv(0);
-
-    // ---- query rows (+ QK-norm, RoPE, k_p/v_p when PREP) ----
+    // ---- prologue operands first: loads complete in order, so operands
+    // requested after the K/V rows could only be used once those arrived ----
+    float qv[RPW][EPL], gq[EPL], gk[EPL], kp[EPL], vp[EPL];
+    float cj = 0.0f, sj = 0.0f;
+    const bool k_wave = own_p && wave == kNW - 1;
+    const int half = rot / 2;
+    const int rj = half > 0 ? tid % half : 0;
     if constexpr (PREP) {
         // wave w normalises query rows w, w + kNW, ...; the last wave also
-        // takes k_p when this chunk owns p. All operands load at once.
-        float qv[RPW][EPL], gq[EPL], gk[EPL], kp[EPL], vp[EPL];
+        // takes k_p when this chunk owns p
 #pragma unroll
         for (int i = 0; i < RPW; ++i) {
             const int r = wave + i * kNW;
@@ -140,7 +143,6 @@ __global__ __launch_bounds__(kThreads) void k_attn(
             for (int j = 0; j < EPL; ++j)
                 qv[i][j] = r < G ? qrow[(size_t)(g * G + r) * qhs + lane + j * QLM_WAVE] : 0.0f;
         }
-        const bool k_wave = own_p && wave == kNW - 1;
 #pragma unroll
         for (int j = 0; j < EPL; ++j) {
             const int e = lane + j * QLM_WAVE;
@@ -149,11 +151,14 @@ __global__ __launch_bounds__(kThreads) void k_attn(
             kp[j] = k_wave ? qrow[(size_t)n_q * qhs + (size_t)g * HD + e] : 0.0f;
             vp[j] = k_wave ? qrow[(size_t)n_q * qhs + (size_t)(n_kv + g) * HD + e] : 0.0f;
         }
-        const int half = rot / 2;
-        const int rj = half > 0 ? tid % half : 0;
-        const float cj = half > 0 ? cos_tab[(size_t)p * half + rj] : 0.0f;
-        const float sj = half > 0 ? sin_tab[(size_t)p * half + rj] : 0.0f;
+        cj = half > 0 ? cos_tab[(size_t)p * half + rj] : 0.0f;
+        sj = half > 0 ? sin_tab[(size_t)p * half + rj] : 0.0f;
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    load_kv(0);
 
+    // ---- query rows (+ QK-norm, RoPE, k_p/v_p when PREP) ----
+    if constexpr (PREP) {
 #pragma unroll
         for (int i = 0; i < RPW; ++i) {
             const int r = wave + i * kNW;
@@ -338,46 +343,94 @@ __global__ __launch_bounds__(kThreads) void k_attn(
     }
 }
 
-// Merge of the chunk records of one (query head, sequence), in tiles of HD
-// chunks with a running maximum, then the optional sigmoid output gate
-// (attention.cpp:216-227): gate[b*ldg + h*ghs + HD + e].
+// Merge of the chunk records of one (query head, sequence), then the
+// optional sigmoid output gate (attention.cpp:216-227): gate[b*ldg + h*ghs +
+// HD + e]. 256 threads: the chunks' (m, l) go to LDS first, every thread
+// then takes the weights exp(m_c - M) of the chunks c = cg, cg + 8, ... of
+// one float4 column and requests all their records at once; the 8 chunk
+// groups meet in LDS. Up to kCombineTile chunks per pass (a running maximum
+// rescales across passes).
+constexpr int kCombineThreads = 256;
+constexpr int kCombineTile = 256;
+
 template <int HD>
-__global__ __launch_bounds__(HD) void k_attn_combine(
+__global__ __launch_bounds__(kCombineThreads) void k_attn_combine(
     const float* __restrict__ work, int nchunks, int CH, int max_seq, const int* __restrict__ pos,
     int ctx, int pstep, const float* __restrict__ gate, int ldg, int ghs, float* __restrict__ out,
     int ldo, int n_q) {
-    __shared__ float ms[HD], ls[HD];
-    const int h = blockIdx.x, b = blockIdx.y, e = threadIdx.x;
-    const float gv = gate ? gate[(size_t)b * ldg + (size_t)h * ghs + HD + e] : 0.0f;
+    constexpr int C4 = HD / 4;                    // float4 columns
+    constexpr int NG = kCombineThreads / C4;      // chunk groups
+    __shared__ float fs[kCombineTile], ls_[kCombineTile];
+    __shared__ float4 part[NG][C4];
+    __shared__ float red[kCombineThreads / QLM_WAVE];
+    const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+    const int c4 = tid % C4, cg = tid / C4;
     const int L = min(pos ? pos[b] + 1 : ctx + pstep * b, max_seq);
     const int nc = min(nchunks, (L + CH - 1) / CH);
     const float* base = work + ((size_t)b * n_q + h) * nchunks * (HD + 4);
-    float M = -INFINITY, l = 0.0f, o = 0.0f;
-    for (int c0 = 0; c0 < nc; c0 += HD) {
-        const int nt = min(HD, nc - c0);
-        if (e < nt) {
-            ms[e] = base[(size_t)(c0 + e) * (HD + 4)];
-            ls[e] = base[(size_t)(c0 + e) * (HD + 4) + 1];
+    float M = -INFINITY, lsum = 0.0f;
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int c0 = 0; c0 < nc; c0 += kCombineTile) {
+        const int nt = min(kCombineTile, nc - c0);
+        float mc = -INFINITY, lc = 0.0f;
+        if (tid < nt) {
+            mc = base[(size_t)(c0 + tid) * (HD + 4)];
+            lc = base[(size_t)(c0 + tid) * (HD + 4) + 1];
         }
+        // tile maximum
+        float mt = wave_max(mc);
+        if ((tid & (QLM_WAVE - 1)) == 0) red[tid / QLM_WAVE] = mt;
         __syncthreads();
-        float mt = -INFINITY;
-        for (int c = 0; c < nt; ++c) mt = fmaxf(mt, ms[c]);
+        mt = red[0];
+#pragma unroll
+        for (int w = 1; w < kCombineThreads / QLM_WAVE; ++w) mt = fmaxf(mt, red[w]);
         const float Mn = fmaxf(M, mt);
-        const float f0 = expf(M - Mn);  // 0 on the first tile
-        l *= f0;
-        o *= f0;
-#pragma unroll 8
-        for (int c = 0; c < nt; ++c) {
-            const float f = expf(ms[c] - Mn);
-            l = fmaf(f, ls[c], l);
-            o = fmaf(f, base[(size_t)(c0 + c) * (HD + 4) + 4 + e], o);
+        if (tid < nt) {
+            fs[tid] = expf(mc - Mn);
+            ls_[tid] = lc;
         }
-        M = Mn;
         __syncthreads();
+        const float f0 = expf(M - Mn);  // 0 on the first pass
+        lsum *= f0;
+        o.x *= f0;
+        o.y *= f0;
+        o.z *= f0;
+        o.w *= f0;
+        for (int c = cg; c < nt; c += NG) {
+            const float f = fs[c];
+            const float4 v = reinterpret_cast<const float4*>(base + (size_t)(c0 + c) * (HD + 4) + 4)[c4];
+            o.x = fmaf(f, v.x, o.x);
+            o.y = fmaf(f, v.y, o.y);
+            o.z = fmaf(f, v.z, o.z);
+            o.w = fmaf(f, v.w, o.w);
+        }
+        if (cg == 0)
+            for (int c = 0; c < nt; ++c) lsum = fmaf(fs[c], ls_[c], lsum);
+        M = Mn;
+        __syncthreads();  // fs/ls_/red are rewritten by the next pass
     }
-    float r = o / l;
-    if (gate) r *= 1.0f / (1.0f + expf(-gv));
-    out[(size_t)b * ldo + (size_t)h * HD + e] = r;
+    part[cg][c4] = o;
+    __syncthreads();
+    if (cg == 0) {
+        float4 t = part[0][c4];
+#pragma unroll
+        for (int g2 = 1; g2 < NG; ++g2) {
+            const float4 u = part[g2][c4];
+            t.x += u.x;
+            t.y += u.y;
+            t.z += u.z;
+            t.w += u.w;
+        }
+        float r[4] = {t.x / lsum, t.y / lsum, t.z / lsum, t.w / lsum};
+        if (gate) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                r[i] *= 1.0f / (1.0f + expf(-gate[(size_t)b * ldg + (size_t)h * ghs + HD + c4 * 4 + i]));
+        }
+        float* dst = out + (size_t)b * ldo + (size_t)h * HD + c4 * 4;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dst[i] = r[i];
+    }
 }
 
 // Prefill form of k_attn's PREP phase for T consecutive projection rows
@@ -489,7 +542,8 @@ template <int HD>
 int launch_combine(const float* work, int nch, int ch, int max_seq, const int* pos, int ctx,
                    int pstep, const float* gate, int ldg, int ghs, float* out, int ldo, int n_q,
                    int B, hipStream_t s) {
-    hipLaunchKernelGGL(k_attn_combine<HD>, dim3(n_q, B), dim3(HD), 0, s, work, nch, ch, max_seq,
+    hipLaunchKernelGGL(k_attn_combine<HD>, dim3(n_q, B), dim3(kCombineThreads), 0, s, work, nch,
+                       ch, max_seq,
                        pos, ctx, pstep, gate, ldg, ghs, out, ldo, n_q);
     return qlm_launch_status();
 }
