@@ -127,32 +127,41 @@ __global__ __launch_bounds__(kThreads) void k_attn(
         }
     };
     // ---- prologue operands first: loads complete in order, so operands
-    // requested after the K/V rows could only be used once those arrived ----
-    float qv[RPW][EPL], gq[EPL], gk[EPL], kp[EPL], vp[EPL];
-    float cj = 0.0f, sj = 0.0f;
+    // requested after the K/V rows could only be used once those arrived.
+    // Every load is unconditional (clamped or substitute address; unused
+    // values are dropped later): a load under a branch makes the compiler
+    // wait for it where the branch ends, ahead of the K/V requests.
+    constexpr int RI = ((G + 1) * (HD / 2) + kThreads - 1) / kThreads;  // RoPE items per thread
+    float qv[RPW][EPL], gq[EPL], gk[EPL], kp[EPL], vp[EPL], cr[RI], sr[RI];
     const bool k_wave = own_p && wave == kNW - 1;
     const int half = rot / 2;
-    const int rj = half > 0 ? tid % half : 0;
     if constexpr (PREP) {
         // wave w normalises query rows w, w + kNW, ...; the last wave also
         // takes k_p when this chunk owns p
+        const float* gqp = qn_w ? qn_w : qrow;
+        const float* gkp = kn_w ? kn_w : qrow;
 #pragma unroll
         for (int i = 0; i < RPW; ++i) {
-            const int r = wave + i * kNW;
+            const int r = min(wave + i * kNW, G - 1);
 #pragma unroll
             for (int j = 0; j < EPL; ++j)
-                qv[i][j] = r < G ? qrow[(size_t)(g * G + r) * qhs + lane + j * QLM_WAVE] : 0.0f;
+                qv[i][j] = qrow[(size_t)(g * G + r) * qhs + lane + j * QLM_WAVE];
         }
 #pragma unroll
         for (int j = 0; j < EPL; ++j) {
             const int e = lane + j * QLM_WAVE;
-            gq[j] = qn_w ? qn_w[e] : 0.0f;
-            gk[j] = (k_wave && kn_w) ? kn_w[e] : 0.0f;
-            kp[j] = k_wave ? qrow[(size_t)n_q * qhs + (size_t)g * HD + e] : 0.0f;
-            vp[j] = k_wave ? qrow[(size_t)n_q * qhs + (size_t)(n_kv + g) * HD + e] : 0.0f;
+            gq[j] = gqp[e];
+            gk[j] = gkp[e];
+            kp[j] = qrow[(size_t)n_q * qhs + (size_t)g * HD + e];
+            vp[j] = qrow[(size_t)n_q * qhs + (size_t)(n_kv + g) * HD + e];
         }
-        cj = half > 0 ? cos_tab[(size_t)p * half + rj] : 0.0f;
-        sj = half > 0 ? sin_tab[(size_t)p * half + rj] : 0.0f;
+        // cos/sin of this thread's RoPE items i = tid + k*kThreads (column i % half)
+#pragma unroll
+        for (int k = 0; k < RI; ++k) {
+            const size_t o = half > 0 ? (size_t)p * half + (tid + k * kThreads) % half : 0;
+            cr[k] = (half > 0 ? cos_tab : qrow)[o];
+            sr[k] = (half > 0 ? sin_tab : qrow)[o];
+        }
     }
     __builtin_amdgcn_sched_barrier(0);
     load_kv(0);
@@ -195,14 +204,16 @@ __global__ __launch_bounds__(kThreads) void k_attn(
         __syncthreads();
         // NeoX rotation of the first `rot` dims (attention.cpp:181-188)
         const int nrows = G + (own_p ? 1 : 0);
-        for (int i = tid; i < nrows * half; i += kThreads) {
-            const int r = i / half, j = i % half;
-            const float c = (j == rj) ? cj : cos_tab[(size_t)p * half + j];
-            const float sn = (j == rj) ? sj : sin_tab[(size_t)p * half + j];
-            float* v = r < G ? qs[r] : kvp[0];
-            const float x1 = v[j], x2 = v[j + half];
-            v[j] = nc_mul_sub(x1, c, x2, sn);
-            v[j + half] = nc_mul_add2(x2, c, x1, sn);
+#pragma unroll
+        for (int k = 0; k < RI; ++k) {
+            const int i = tid + k * kThreads;
+            if (i < nrows * half) {
+                const int r = i / half, j = i % half;
+                float* v = r < G ? qs[r] : kvp[0];
+                const float x1 = v[j], x2 = v[j + half];
+                v[j] = nc_mul_sub(x1, cr[k], x2, sr[k]);
+                v[j + half] = nc_mul_add2(x2, cr[k], x1, sr[k]);
+            }
         }
         __syncthreads();
         if (own_p) {
@@ -345,11 +356,13 @@ __global__ __launch_bounds__(kThreads) void k_attn(
 
 // Merge of the chunk records of one (query head, sequence), then the
 // optional sigmoid output gate (attention.cpp:216-227): gate[b*ldg + h*ghs +
-// HD + e]. 256 threads: the chunks' (m, l) go to LDS first, every thread
-// then takes the weights exp(m_c - M) of the chunks c = cg, cg + 8, ... of
-// one float4 column and requests all their records at once; the 8 chunk
-// groups meet in LDS. Up to kCombineTile chunks per pass (a running maximum
-// rescales across passes).
+// HD + e]. 256 threads: thread (cg, c4) takes float4 column c4 of the
+// chunks c = cg, cg + NG, ...; the chunks' (m, l) meet in LDS, and the 8 (4
+// at hd 256) chunk groups meet in LDS at the end. Everything the first pass
+// needs -- (m, l) of chunk tid, the first KB records of the thread's chunks
+// and the gate -- is requested at kernel start with clamped, unconditional
+// loads, so a short context costs one memory round trip. Up to kCombineTile
+// chunks per pass (a running maximum rescales across passes).
 constexpr int kCombineThreads = 256;
 constexpr int kCombineTile = 256;
 
@@ -360,6 +373,8 @@ __global__ __launch_bounds__(kCombineThreads) void k_attn_combine(
     int ldo, int n_q) {
     constexpr int C4 = HD / 4;                    // float4 columns
     constexpr int NG = kCombineThreads / C4;      // chunk groups
+    constexpr int KB = 8;                         // records per thread per request batch
+    constexpr int RS = HD + 4;                    // record stride (floats)
     __shared__ float fs[kCombineTile], ls_[kCombineTile];
     __shared__ float4 part[NG][C4];
     __shared__ float red[kCombineThreads / QLM_WAVE];
@@ -367,15 +382,32 @@ __global__ __launch_bounds__(kCombineThreads) void k_attn_combine(
     const int c4 = tid % C4, cg = tid / C4;
     const int L = min(pos ? pos[b] + 1 : ctx + pstep * b, max_seq);
     const int nc = min(nchunks, (L + CH - 1) / CH);
-    const float* base = work + ((size_t)b * n_q + h) * nchunks * (HD + 4);
+    const int last = max(nc, 1) - 1;  // clamp target of the unconditional loads
+    const float* base = work + ((size_t)b * n_q + h) * nchunks * RS;
+
+    // ---- first-pass operands, all requested before any is used ----
+    auto rec4 = [&](int c) {  // float4 column c4 of record c (clamped into the context)
+        return reinterpret_cast<const float4*>(base + (size_t)min(c, last) * RS + 4)[c4];
+    };
+    float mc = base[(size_t)min(tid, last) * RS];
+    float lc = base[(size_t)min(tid, last) * RS + 1];
+    float4 ov[KB];
+#pragma unroll
+    for (int k = 0; k < KB; ++k) ov[k] = rec4(cg + NG * k);
+    const float* gp = (gate ? gate + (size_t)b * ldg + (size_t)h * ghs + HD : base + 4) + c4 * 4;
+    const float gg[4] = {gp[0], gp[1], gp[2], gp[3]};
+
     float M = -INFINITY, lsum = 0.0f;
     float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int c0 = 0; c0 < nc; c0 += kCombineTile) {
         const int nt = min(kCombineTile, nc - c0);
-        float mc = -INFINITY, lc = 0.0f;
-        if (tid < nt) {
-            mc = base[(size_t)(c0 + tid) * (HD + 4)];
-            lc = base[(size_t)(c0 + tid) * (HD + 4) + 1];
+        if (c0 > 0) {
+            mc = base[(size_t)(c0 + min(tid, nt - 1)) * RS];
+            lc = base[(size_t)(c0 + min(tid, nt - 1)) * RS + 1];
+        }
+        if (tid >= nt) {
+            mc = -INFINITY;
+            lc = 0.0f;
         }
         // tile maximum
         float mt = wave_max(mc);
@@ -396,13 +428,20 @@ __global__ __launch_bounds__(kCombineThreads) void k_attn_combine(
         o.y *= f0;
         o.z *= f0;
         o.w *= f0;
-        for (int c = cg; c < nt; c += NG) {
-            const float f = fs[c];
-            const float4 v = reinterpret_cast<const float4*>(base + (size_t)(c0 + c) * (HD + 4) + 4)[c4];
-            o.x = fmaf(f, v.x, o.x);
-            o.y = fmaf(f, v.y, o.y);
-            o.z = fmaf(f, v.z, o.z);
-            o.w = fmaf(f, v.w, o.w);
+        for (int k0 = 0; k0 * NG < nt; k0 += KB) {
+            if (c0 > 0 || k0 > 0) {
+#pragma unroll
+                for (int k = 0; k < KB; ++k) ov[k] = rec4(c0 + cg + NG * (k0 + k));
+            }
+#pragma unroll
+            for (int k = 0; k < KB; ++k) {
+                const int c = cg + NG * (k0 + k);
+                const float f = c < nt ? fs[c] : 0.0f;
+                o.x = fmaf(f, ov[k].x, o.x);
+                o.y = fmaf(f, ov[k].y, o.y);
+                o.z = fmaf(f, ov[k].z, o.z);
+                o.w = fmaf(f, ov[k].w, o.w);
+            }
         }
         if (cg == 0)
             for (int c = 0; c < nt; ++c) lsum = fmaf(fs[c], ls_[c], lsum);
@@ -424,8 +463,7 @@ __global__ __launch_bounds__(kCombineThreads) void k_attn_combine(
         float r[4] = {t.x / lsum, t.y / lsum, t.z / lsum, t.w / lsum};
         if (gate) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                r[i] *= 1.0f / (1.0f + expf(-gate[(size_t)b * ldg + (size_t)h * ghs + HD + c4 * 4 + i]));
+            for (int i = 0; i < 4; ++i) r[i] *= 1.0f / (1.0f + expf(-gg[i]));
         }
         float* dst = out + (size_t)b * ldo + (size_t)h * HD + c4 * 4;
 #pragma unroll

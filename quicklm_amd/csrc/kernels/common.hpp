@@ -15,25 +15,47 @@ static inline int qlm_launch_status() { return qlm_status(hipGetLastError()); }
 
 static inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
-// Butterfly sum over the full wave (64 lanes); every lane gets the total.
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, QLM_WAVE);
-    return v;
+// Cross-lane reductions. Within a row of 16 lanes they run on DPP (a VALU
+// operand modifier, no LDS round trip): xor 1 and xor 2 as quad permutes;
+// once every lane of a quad holds the same value, the row half-mirror
+// (lane i <-> 7-i) and mirror (i <-> 15-i) pair quads and half-rows exactly
+// as xor 4 and xor 8 would. Across rows, xor 16 and 32 are lane shuffles.
+// Callers keep every lane of the wave active (the reductions read all of
+// them).
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1, 0, 3, 2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2, 3, 0, 1]
+constexpr int kDppHalfMirror = 0x141;  // row_half_mirror
+constexpr int kDppMirror = 0x140;      // row_mirror
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
 }
 
-// Butterfly sum over aligned groups of `width` lanes (width a power of two <= 64).
+// Sum over aligned groups of `width` lanes (a power of two, 2..64); every
+// lane of a group gets the group total.
 template <int width>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-    for (int m = width / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, QLM_WAVE);
+    static_assert(width >= 2 && width <= QLM_WAVE && (width & (width - 1)) == 0, "group width");
+    v += dpp_mov<kDppXor1>(v);
+    if constexpr (width >= 4) v += dpp_mov<kDppXor2>(v);
+    if constexpr (width >= 8) v += dpp_mov<kDppHalfMirror>(v);
+    if constexpr (width >= 16) v += dpp_mov<kDppMirror>(v);
+    if constexpr (width >= 32) v += __shfl_xor(v, 16, QLM_WAVE);
+    if constexpr (width >= 64) v += __shfl_xor(v, 32, QLM_WAVE);
     return v;
 }
 
+// Sum over the full wave (64 lanes); every lane gets the total.
+__device__ __forceinline__ float wave_sum(float v) { return group_sum<QLM_WAVE>(v); }
+
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, QLM_WAVE));
-    return v;
+    v = fmaxf(v, dpp_mov<kDppXor1>(v));
+    v = fmaxf(v, dpp_mov<kDppXor2>(v));
+    v = fmaxf(v, dpp_mov<kDppHalfMirror>(v));
+    v = fmaxf(v, dpp_mov<kDppMirror>(v));
+    v = fmaxf(v, __shfl_xor(v, 16, QLM_WAVE));
+    return fmaxf(v, __shfl_xor(v, 32, QLM_WAVE));
 }
 
 // Block-wide sum for blockDim.x a multiple of 64 (<= 1024). `red` is LDS

@@ -43,9 +43,6 @@ enum { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_ARGMAX = 3 };
 // invalidates its XCD's L2, ~0.3 us apiece over a 2048-workgroup grid).
 // One 64-bit key slot per workgroup of the logits GEMV (grid <= kMaxXsGrid).
 constexpr int kMaxXsGrid = 2048;
-// float4 of the activation each thread of the matrix-core M = 1 kernel
-// holds through its prologue (so K <= 4 * 64 * NW * mx_xmax(NW)).
-__host__ __device__ constexpr int mx_xmax(int nw) { return nw == 8 ? 5 : 3; }
 
 struct GreedyTail {
     unsigned long long* keys;
@@ -574,8 +571,9 @@ __global__ __launch_bounds__(kThreads) void k_greedy_finish(GreedyTail tail, int
 // M = 1 on the int8 matrix cores (v_mfma_i32_16x16x64_i8), weights in the
 // tile-major layout below.
 //
-// The activation is written as four int8 digit vectors: with E chosen from
-// max|x| so that |x| / 2^E < 64,
+// The activation is written as four int8 digit vectors, with one exponent
+// per wave over the elements that wave multiplies (its K blocks): with E
+// chosen from their max|x| so that |x| / 2^E < 64,
 //     x = 2^E * (d0 + d1 2^-7 + d2 2^-14 + d3 2^-21) + e,   |e| <= 2^-27 max|x|,
 // every |d| <= 64. A weight group's dot products with the four digit vectors
 // are exact int32 sums on the matrix cores, so per 1024 weights a wave spends
@@ -588,26 +586,30 @@ __global__ __launch_bounds__(kThreads) void k_greedy_finish(GreedyTail tail, int
 //               stores these 64 fragments as one contiguous 1 KB span, so a
 //               wave's load is a linear 1 KB read (row-major rows would make
 //               it 16 scattered 64-byte pieces, which streams ~30% slower).
-//   A (digits)  lane l: A row n, elements 64b + 16q .. +15. With group-32
-//               scales A row 4h + d holds digit d of the elements of group
-//               2b + h (zero for the other group, and rows 8..15 are zero);
-//               with one scale per row, A rows 0..3 hold digits 0..3 of all
-//               64 elements.
-//   D           lane l: D[4q + i][n], i = 0..3. Group-32: lanes q = 0, 1 hold
-//               the four digit sums of row n over group 2b + q, combined as
+//   A (digits)  lane l: A row n, elements 64b + 16q .. +15. A row 4h + d
+//               holds digit d of the elements of group 2b + h (zero for the
+//               other group; rows 8..15 are zero).
+//   D           lane l: D[4q + i][n], i = 0..3. Lanes q = 0, 1 hold the four
+//               digit sums of row n over group 2b + q, combined as
 //               P = (D0 << 7) + D1, Q = (D2 << 7) + D3 (exact int32) and
-//               accumulated as (P + Q 2^-14) * s[n][2b + q] in fp32. Per-row
-//               scales: the int32 digit sums accumulate across blocks.
+//               accumulated as (P + Q 2^-14) * s[n][2b + q] in fp32; the
+//               wave's sum is then scaled by 2^(E - 7) (with one scale per
+//               row, s = 1 there and the row scale multiplies the result).
 //
 // A workgroup of NW waves owns one tile at a time (grid-stride over tiles);
 // wave w takes the P = ceil(K / 64 / NW) blocks w, w + NW, ... of every tile.
-// All P blocks of a wave (and their scales) are requested at once, before the
-// prologue, and each slot is refilled with the next tile's block as soon as
-// it is consumed; the activation and gain are requested before them, so the
-// prologue (RMSNorm sum of squares and max, digits into LDS) overlaps the
-// first weight fetches. At the end of a tile the waves' partial sums meet in
-// LDS (one barrier per tile) and wave 0 applies 2^E, the epilogue and the
-// stores.
+// A wave requests the activation (and gain) of its own blocks first, then all
+// P weight blocks of its first tile (and their scales); each slot is refilled
+// with the next tile's block as soon as it is consumed. A wave's digits
+// depend only on its own blocks, so it starts on its weights as soon as its
+// own activation has arrived, with no workgroup barrier before the first
+// MFMA (an exponent shared by the workgroup would wait for the whole vector,
+// whose loads queue behind the flood of weight loads: measured, that wait
+// was the largest part of a launch). RMSNorm is linear in 1/rms, so the
+// digits are taken of x * (1 + w) and 1/rms multiplies the finished sums;
+// the waves' sums of squares meet at the first tile end. At the end of a tile the waves' partial
+// sums meet in LDS (one barrier per tile) and wave 0 applies the epilogue and
+// the stores.
 
 // Tile-major weight layout: the rows are cut into halves (2 for the
 // [gate; up] matrix of SwiGLU) of `rows` rows each, each half padded with
@@ -649,30 +651,29 @@ __global__ __launch_bounds__(NW * QLM_WAVE) void k_gemv_mx(
     const float* __restrict__ x, const float* __restrict__ nw, float eps,
     const int8_t* __restrict__ q, const float* __restrict__ sc, float* __restrict__ y, int N,
     int K, int F, int ntiles, GreedyTail tail) {
-    constexpr int NT = NW * QLM_WAVE;
-    constexpr int XMAX = mx_xmax(NW);  // float4 of x per thread
+    constexpr int XL = (P + 3) / 4;  // activation float4 per lane (16 lanes per block)
     typedef int v4i __attribute__((ext_vector_type(4)));
-    extern __shared__ __align__(16) unsigned char mx_lds[];  // 4 digit planes, then 16 zero bytes
-    __shared__ int red[2][NW][T][16][ROWSCALE ? 4 : 1];
-    __shared__ float rsum[NW], rmax[NW];
+    extern __shared__ __align__(16) unsigned char mx_lds[];  // [wave][slot][digit][64 B]
+    __shared__ int red[2][NW][T][16];
+    __shared__ float rsum[NW];
 
     const int tid = threadIdx.x, lane = tid & (QLM_WAVE - 1);
     const int w = __builtin_amdgcn_readfirstlane(tid / QLM_WAVE);
     const int n = lane & 15, qd = lane >> 4;
     const int nblk = K >> 6;
-    const int PS = K + 64;   // digit plane stride (bytes)
-    const int zoff = 4 * PS; // 16 zero bytes
+    unsigned char* dig = mx_lds + (size_t)w * P * 256;
 
-    // ---- activation (and gain) requests first: they return before the ring
-    const int nx4 = K >> 2;
-    float4 xr[XMAX], gr[XMAX];
+    // ---- this wave's activation (and gain) first: load i of lane l is
+    // elements 4n .. 4n+3 of slot u = 4i + q (block w + NW*u). The loads are
+    // unconditional (block clamped into K; lanes past the wave's blocks are
+    // zeroed once the values are used): a load under a branch makes the
+    // compiler wait for it at the branch's end, before the weight loads.
+    float4 xr[XL], gr[XL];
 #pragma unroll
-    for (int i = 0; i < XMAX; ++i) {
-        const int idx = tid + i * NT;
-        if (idx < nx4) {
-            xr[i] = reinterpret_cast<const float4*>(x)[idx];
-            if constexpr (PRO == PRO_RMSNORM) gr[i] = reinterpret_cast<const float4*>(nw)[idx];
-        }
+    for (int i = 0; i < XL; ++i) {
+        const int b = min(w + NW * (4 * i + qd), nblk - 1);
+        xr[i] = reinterpret_cast<const float4*>(x)[b * 16 + n];
+        if constexpr (PRO == PRO_RMSNORM) gr[i] = reinterpret_cast<const float4*>(nw)[b * 16 + n];
     }
     __builtin_amdgcn_sched_barrier(0);
 
@@ -714,112 +715,83 @@ __global__ __launch_bounds__(NW * QLM_WAVE) void k_gemv_mx(
 #pragma unroll
     for (int u = 0; u < P; ++u) issue(blockIdx.x, u);
 
-    // ---- prologue: RMSNorm sum of squares and max|x|, then digits -> LDS
-    float ss = 0.0f, mx = 0.0f;
+    // ---- digits of this wave's blocks, one exponent per wave
+    float ss = 0.0f, m = 0.0f;
 #pragma unroll
-    for (int i = 0; i < XMAX; ++i) {
-        const int idx = tid + i * NT;
-        if (idx < nx4) {
-            float4 v = xr[i];
-            if constexpr (PRO == PRO_RMSNORM) {
-                ss = fmaf(v.x, v.x, ss);
-                ss = fmaf(v.y, v.y, ss);
-                ss = fmaf(v.z, v.z, ss);
-                ss = fmaf(v.w, v.w, ss);
-                const float4 g = gr[i];
-                v.x *= 1.0f + g.x;
-                v.y *= 1.0f + g.y;
-                v.z *= 1.0f + g.z;
-                v.w *= 1.0f + g.w;
-                xr[i] = v;
-            }
-            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    for (int i = 0; i < XL; ++i) {
+        float4& v = xr[i];
+        const int u = 4 * i + qd;
+        if (u >= P || w + NW * u >= nblk) v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if constexpr (PRO == PRO_RMSNORM) {
+            ss = fmaf(v.x, v.x, ss);
+            ss = fmaf(v.y, v.y, ss);
+            ss = fmaf(v.z, v.z, ss);
+            ss = fmaf(v.w, v.w, ss);
+            const float4 g = gr[i];
+            v.x *= 1.0f + g.x;
+            v.y *= 1.0f + g.y;
+            v.z *= 1.0f + g.z;
+            v.w *= 1.0f + g.w;
         }
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
     }
-    if constexpr (PRO == PRO_RMSNORM) ss = wave_sum(ss);
-    mx = wave_max(mx);
-    if (lane == 0) {
-        rsum[w] = ss;
-        rmax[w] = mx;
-    }
-    if (tid < 4) reinterpret_cast<unsigned*>(mx_lds + zoff)[tid] = 0u;
-    __syncthreads();
-    float tot = rsum[0], m = rmax[0];
-#pragma unroll
-    for (int i = 1; i < NW; ++i) {
-        tot += rsum[i];
-        m = fmaxf(m, rmax[i]);
-    }
-    const float rs = (PRO == PRO_RMSNORM) ? 1.0f / sqrtf(tot / (float)K + eps) : 1.0f;
     int e2 = 0;
-    frexpf(m * rs, &e2);
-    const int E = e2 - 6;  // max|x| / 2^E < 64 (one rounding of slack: digits <= 64)
+    frexpf(wave_max(m), &e2);
+    const int E = __builtin_amdgcn_readfirstlane(e2 - 6);  // max|x| / 2^E < 64 (digits <= 64)
+    const float fx = ldexpf(1.0f, E - 7);  // 2^(E - 7): multiplies the wave's sums
 #pragma unroll
-    for (int i = 0; i < XMAX; ++i) {
-        const int idx = tid + i * NT;
-        if (idx < nx4) {
-            const float vv[4] = {xr[i].x, xr[i].y, xr[i].z, xr[i].w};
-            unsigned pk[4] = {0u, 0u, 0u, 0u};
+    for (int i = 0; i < XL; ++i) {
+        const float vv[4] = {xr[i].x, xr[i].y, xr[i].z, xr[i].w};
+        unsigned pk[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const float u = ldexpf(PRO == PRO_RMSNORM ? vv[c] * rs : vv[c], -E);
-                const float d0 = rintf(u);
-                float t = (u - d0) * 128.0f;
-                const float d1 = rintf(t);
-                t = (t - d1) * 128.0f;
-                const float d2 = rintf(t);
-                t = (t - d2) * 128.0f;
-                const float d3 = rintf(t);
-                pk[0] |= ((unsigned)(int)d0 & 0xffu) << (8 * c);
-                pk[1] |= ((unsigned)(int)d1 & 0xffu) << (8 * c);
-                pk[2] |= ((unsigned)(int)d2 & 0xffu) << (8 * c);
-                pk[3] |= ((unsigned)(int)d3 & 0xffu) << (8 * c);
-            }
+        for (int c = 0; c < 4; ++c) {
+            const float s0 = ldexpf(vv[c], -E);
+            const float d0 = rintf(s0);
+            float t = (s0 - d0) * 128.0f;
+            const float d1 = rintf(t);
+            t = (t - d1) * 128.0f;
+            const float d2 = rintf(t);
+            t = (t - d2) * 128.0f;
+            const float d3 = rintf(t);
+            pk[0] |= ((unsigned)(int)d0 & 0xffu) << (8 * c);
+            pk[1] |= ((unsigned)(int)d1 & 0xffu) << (8 * c);
+            pk[2] |= ((unsigned)(int)d2 & 0xffu) << (8 * c);
+            pk[3] |= ((unsigned)(int)d3 & 0xffu) << (8 * c);
+        }
+        const int u = 4 * i + qd;
+        if (u < P) {
 #pragma unroll
             for (int d = 0; d < 4; ++d)
-                *reinterpret_cast<unsigned*>(mx_lds + d * PS + idx * 4) = pk[d];
+                *reinterpret_cast<unsigned*>(dig + (u * 4 + d) * 64 + n * 4) = pk[d];
         }
     }
-    __syncthreads();
-
-    // A-fragment address of this lane (the zero bytes for rows that carry
-    // nothing, and for every row of a slot past K)
-    bool active;
-    int dpl;
-    if constexpr (ROWSCALE) {
-        active = n < 4;
-        dpl = n;
-    } else {
-        active = n < 8 && (n >> 2) == (qd >> 1);
-        dpl = n & 3;
+    if constexpr (PRO == PRO_RMSNORM) {
+        ss = wave_sum(ss);
+        if (lane == 0) rsum[w] = ss;
     }
-    const int abase = active ? dpl * PS + qd * 16 : zoff;
-    const int astep = active ? 64 : 0;
+    // the wave's own digit stores complete before its lanes read them back
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    __builtin_amdgcn_wave_barrier();
+
+    // A fragment of this lane: digit n & 3 of elements 16q .. 16q+15 when
+    // A row n carries group q >> 1, zero otherwise
+    const bool active = n < 8 && (n >> 2) == (qd >> 1);
+    int aoff = (n & 3) * 64 + qd * 16;
 
     float accf[T];
-    v4i acci[T];
 #pragma unroll
-    for (int tt = 0; tt < T; ++tt) {
-        accf[tt] = 0.0f;
-        acci[tt] = v4i{0, 0, 0, 0};
-    }
+    for (int tt = 0; tt < T; ++tt) accf[tt] = 0.0f;
     auto consume = [&](int u) {
-        const int b = w + NW * u;
-        const int aoff = b < nblk ? abase + b * astep : zoff;
-        const v4i a = *reinterpret_cast<const v4i*>(mx_lds + aoff);
+        v4i a = v4i{0, 0, 0, 0};
+        if (active) a = *reinterpret_cast<const v4i*>(dig + u * 256 + aoff);
 #pragma unroll
         for (int tt = 0; tt < T; ++tt) {
             const v4i bw = v4i{wb[u][tt].x, wb[u][tt].y, wb[u][tt].z, wb[u][tt].w};
-            if constexpr (ROWSCALE) {
-                acci[tt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, bw, acci[tt], 0, 0, 0);
-            } else {
-                const v4i d =
-                    __builtin_amdgcn_mfma_i32_16x16x64_i8(a, bw, v4i{0, 0, 0, 0}, 0, 0, 0);
-                const int pp = (d[0] << 7) + d[1];
-                const int qq = (d[2] << 7) + d[3];
-                const float v = fmaf((float)qq, 0x1p-14f, (float)pp);
-                accf[tt] = fmaf(v, sb[u][tt], accf[tt]);
-            }
+            const v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, bw, v4i{0, 0, 0, 0}, 0, 0, 0);
+            const int pp = (d[0] << 7) + d[1];
+            const int qq = (d[2] << 7) + d[3];
+            const float v = fmaf((float)qq, 0x1p-14f, (float)pp);
+            accf[tt] = ROWSCALE ? accf[tt] + v : fmaf(v, sb[u][tt], accf[tt]);
         }
     };
 
@@ -829,43 +801,33 @@ __global__ __launch_bounds__(NW * QLM_WAVE) void k_gemv_mx(
     // Partial sums of the waves meet in LDS (double-buffered by tile parity:
     // a buffer is rewritten two tiles later, after a barrier wave 0 reaches
     // only once it has read it); wave 0 reduces them in wave order, applies
-    // 2^E, the epilogue and the stores.
+    // 1/rms, the row scale, the epilogue and the stores.
     auto tile_end = [&](int tile) {
 #pragma unroll
         for (int tt = 0; tt < T; ++tt) {
-            if constexpr (ROWSCALE) {
-                if (qd == 0) {
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) red[par][w][tt][n][i] = acci[tt][i];
-                }
-                acci[tt] = v4i{0, 0, 0, 0};
-            } else {
-                const float p = accf[tt] + __shfl_xor(accf[tt], 16, QLM_WAVE);
-                if (qd == 0) red[par][w][tt][n][0] = __float_as_int(p);
-                accf[tt] = 0.0f;
-            }
+            const float p = (accf[tt] + __shfl_xor(accf[tt], 16, QLM_WAVE)) * fx;
+            if (qd == 0) red[par][w][tt][n] = __float_as_int(p);
+            accf[tt] = 0.0f;
         }
         __syncthreads();
         if (w == 0 && qd == 0) {
             const int o = tile * 16 + n;
             const bool first = tile == (int)blockIdx.x;
+            float rs = 1.0f;
+            if constexpr (PRO == PRO_RMSNORM) {
+                float tot = rsum[0];
+#pragma unroll
+                for (int i = 1; i < NW; ++i) tot += rsum[i];
+                rs = 1.0f / sqrtf(tot / (float)K + eps);
+            }
             float val[T];
 #pragma unroll
             for (int tt = 0; tt < T; ++tt) {
-                if constexpr (ROWSCALE) {
-                    int s4[4] = {0, 0, 0, 0};
-                    for (int ww = 0; ww < NW; ++ww)
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) s4[i] += red[par][ww][tt][n][i];
-                    const float v = fmaf((float)s4[3], 0x1p-21f,
-                                         fmaf((float)s4[2], 0x1p-14f,
-                                              fmaf((float)s4[1], 0x1p-7f, (float)s4[0])));
-                    val[tt] = ldexpf(v, E) * (first ? rsc0[tt] : sc[row_of(tile, tt)]);
-                } else {
-                    float v = __int_as_float(red[par][0][tt][n][0]);
-                    for (int ww = 1; ww < NW; ++ww) v += __int_as_float(red[par][ww][tt][n][0]);
-                    val[tt] = ldexpf(v, E - 7);
-                }
+                float v = __int_as_float(red[par][0][tt][n]);
+                for (int ww = 1; ww < NW; ++ww) v += __int_as_float(red[par][ww][tt][n]);
+                if constexpr (PRO == PRO_RMSNORM) v *= rs;
+                if constexpr (ROWSCALE) v *= first ? rsc0[tt] : sc[row_of(tile, tt)];
+                val[tt] = v;
             }
             if (o < N) {
                 if constexpr (EPI == EPI_SWIGLU)
@@ -889,6 +851,9 @@ __global__ __launch_bounds__(NW * QLM_WAVE) void k_gemv_mx(
     // tile's block when there is one), then the cross-wave epilogue
     for (int tile = blockIdx.x;; tile += gridDim.x) {
         const int next = tile + (int)gridDim.x;
+        // the digit reads stay in the loop (hoisted, P fragments would stay
+        // live across it)
+        asm volatile("" : "+v"(aoff));
         if (next < ntiles) {
 #pragma unroll
             for (int u = 0; u < P; ++u) {
@@ -1102,19 +1067,18 @@ struct MxConfig {
     int nw, ring, grid;
 };
 
-// Dynamic LDS of k_gemv_mx: four digit planes of K + 64 bytes, 16 zero bytes.
-size_t mx_lds_bytes(int K) { return 4 * (size_t)(K + 64) + 16; }
+// Dynamic LDS of k_gemv_mx: per wave and slot, four 64-byte digit planes.
+size_t mx_lds_bytes(int nw, int ring) { return (size_t)nw * ring * 256; }
 
 // Instantiated (waves per workgroup, slots per wave) pairs; slots =
 // ceil(K / 64 / waves), so each pair serves a range of K.
 constexpr int kMxPairs[][2] = {{4, 1}, {4, 2},  {4, 4},  {4, 8},   {4, 10},  {8, 4},
                                {8, 5}, {8, 8},  {16, 2}, {16, 4}, {16, 10}, {16, 12}};
 
-// Whether k_gemv_mx<nw, *, ring> runs this K: whole 64-element blocks, the
-// activation fits its prologue registers, ring = ceil(blocks / nw), and the
-// pair is instantiated.
+// Whether k_gemv_mx<nw, *, ring> runs this K: whole 64-element blocks,
+// ring = ceil(blocks / nw), and the pair is instantiated.
 bool mx_fits(int K, int nw, int ring) {
-    if (K <= 0 || K % 64 != 0 || K > 4 * QLM_WAVE * nw * mx_xmax(nw)) return false;
+    if (K <= 0 || K % 64 != 0) return false;
     if (K / 64 < nw) return false;  // every wave has a block
     if (ring != (K / 64 + nw - 1) / nw) return false;
     for (const auto& pr : kMxPairs)
@@ -1128,12 +1092,12 @@ struct MxTuned {
     int N, K, epi, nw, ring, grid;
 };
 constexpr MxTuned kMxTuned[] = {
-    {9728, 2560, EPI_SWIGLU, 8, 5, 256},     // gate/up
+    {9728, 2560, EPI_SWIGLU, 8, 5, 203},     // gate/up (3 tiles per workgroup)
     {2560, 9728, EPI_RESID, 16, 10, 160},    // down
     {8224, 2560, EPI_STORE, 8, 5, 512},      // DeltaNet in_proj [qkv|z|b|a]
-    {5120, 2560, EPI_STORE, 8, 5, 256},      // GQA q(+gate)/k/v
-    {2560, 2048, EPI_RESID, 16, 2, 160},     // out_proj / o_proj
-    {151936, 2560, EPI_STORE, 8, 5, 2048},   // lm_head (also its greedy form)
+    {5120, 2560, EPI_STORE, 8, 5, 320},      // GQA q(+gate)/k/v
+    {2560, 2048, EPI_RESID, 8, 4, 160},      // out_proj / o_proj
+    {151936, 2560, EPI_STORE, 8, 5, 256},    // lm_head (also its greedy form)
 };
 
 // Launch shape: the tuned table, else the fewest waves per workgroup that
@@ -1165,7 +1129,7 @@ int launch_mx(const MxConfig& c, const float* x, const float* nw, float eps, con
     int grid = c.grid < ntiles ? c.grid : ntiles;
     if (grid < 1) grid = 1;
     hipLaunchKernelGGL((k_gemv_mx<NW, T, P, ROWSCALE, PRO, EPI>), dim3(grid),
-                       dim3(NW * QLM_WAVE), mx_lds_bytes(K), st, x, nw, eps, q, sc, y, N, K, F,
+                       dim3(NW * QLM_WAVE), mx_lds_bytes(NW, P), st, x, nw, eps, q, sc, y, N, K, F,
                        ntiles, tail);
     if constexpr (EPI == EPI_ARGMAX) {
         const int rc = qlm_launch_status();
