@@ -284,6 +284,8 @@ def main():
                          "rocprofv3 --pmc passes)")
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-gemv", action="store_true")
+    ap.add_argument("--skip-int4", action="store_true",
+                    help="skip the batch-1 decode at --precision int4")
     ap.add_argument("--skip-row", action="store_true",
                     help="skip the batch-1 decode with one scale per output row (int8_row)")
     ap.add_argument("--model-dir", default=None)
@@ -372,6 +374,16 @@ def main():
             erow.close()
             log(f"batch 1, per-row scales: {rrow['tok_s']:.1f} tok/s "
                 f"({rrow['ms_per_step']:.3f} ms/step), {rrow['weight_bytes'] / 1e9:.3f} GB")
+
+        r4 = None
+        if not args.skip_int4:
+            # the same checkpoint at --precision int4 (Q4_0 weights, lm_head included)
+            e4 = Engine(mdir, max_seq_len=max_seq, max_batch=1, precision="int4")
+            r4 = run_decode(e4, prompts[:1], args.warmup, args.steps, graph)
+            r4["weight_bytes"] = e4.weight_bytes
+            e4.close()
+            log(f"batch 1, int4 weights: {r4['tok_s']:.1f} tok/s "
+                f"({r4['ms_per_step']:.3f} ms/step), {r4['weight_bytes'] / 1e9:.3f} GB")
     finally:
         if own_dir:
             import shutil
@@ -418,6 +430,12 @@ def main():
             "batch": 1, "scale_group": "row", "weight_bytes": rrow["weight_bytes"],
             "frac_of_weight_roofline": round(
                 rrow["weight_bytes"] / (rrow["ms_per_step"] / 1000.0) / 1e9 / HBM_PEAK_GBS, 4)},
+        "int4": None if r4 is None else {
+            "tok_s": round(r4["tok_s"], 2), "ms_per_step": round(r4["ms_per_step"], 4),
+            "batch": 1, "precision": "int4 (Q4_0, group 32)", "weight_bytes": r4["weight_bytes"],
+            "frac_of_weight_roofline": round(
+                r4["weight_bytes"] / (r4["ms_per_step"] / 1000.0) / 1e9 / HBM_PEAK_GBS, 4),
+            "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / r4["weight_bytes"], 1)},
         "gemv": gemv,
     })
     traffic, traffic_src = None, None

@@ -106,14 +106,14 @@ int qlm_mx_swizzle(const int8_t* q, const float* scales, int group, int rows, in
 /* M = 1 on the int8 matrix cores with tile-major weights (q and scales from
  * qlm_mx_swizzle; per-row scales as quantised), explicit launch shape.
  * x (after the RMSNorm prologue when norm_w is given) is written as four
- * int8 digit vectors with one power-of-two scale, x = 2^E (d0 + d1/2^7 +
- * d2/2^14 + d3/2^21) to within 2^-27 max|x|, and every weight group's dot
- * products with the digits are exact int32 sums (v_mfma_i32_16x16x64_i8);
- * results match the fp32 path to ~1e-7 normwise. norm_w and epilogue as
- * qlm_gemv_i8_config. waves in {4, 8, 16} per workgroup and ring = ceil(K /
- * 64 / waves) blocks per wave, one of the instantiated pairs (4,1) (4,2)
- * (4,4) (4,8) (4,10) (8,4) (8,5) (8,8) (16,2) (16,4) (16,10) (16,12); K a
- * multiple of 64, at most 3072 (waves 4), 10240 (8) or 12288 (16); grid =
+ * int8 digit vectors with a power-of-two scale per wave (over the K blocks
+ * that wave multiplies), x = 2^E (d0 + d1/2^7 + d2/2^14 + d3/2^21) to within
+ * 2^-27 max|x|, and every weight group's dot products with the digits are
+ * exact int32 sums (v_mfma_i32_16x16x64_i8); results match the fp32 path to
+ * ~1e-7 normwise. norm_w and epilogue as qlm_gemv_i8_config. waves in
+ * {4, 8, 16} per workgroup and ring = ceil(K / 64 / waves) blocks per wave,
+ * one of the instantiated pairs (4,1) (4,2) (4,4) (4,8) (4,10) (8,4) (8,5)
+ * (8,8) (16,2) (16,4) (16,10) (16,12); K a multiple of 64; grid =
  * workgroups (grid-stride over 16-row tiles). */
 int qlm_gemv_i8_mx_config(const float* x, const float* norm_w, float eps, const int8_t* q,
                           const float* scales, int group, float* y, int N, int K, int epilogue,
@@ -338,6 +338,47 @@ int qlm_lm_head_greedy_mx(const float* x, const float* norm_w, float eps, const 
  * pos[b]]] for a [vocab, H] fp32 table (pos NULL: tokens[b, 0]). */
 int qlm_embed_tokens(const float* table, int vocab, int H, const int* tokens, int ld_tokens,
                      const int* pos, float* out, int ldo, int B, void* stream);
+
+/* ---- int4 (Q4_0) weights (reference --precision int4) ----------------------
+ * Replaces SafetensorsLoader::get_tensor_keep_int4 (safetensors.cpp:587-656,
+ * st_quantize_row_f32_int4 / _bf16_int4 :393-515) and the int4 branch of
+ * math::matmul (math_ops.cpp:820-900, int4_gemv_range :768-800). */
+
+/* Load-time quantiser, bit-exact with the reference's IEEE semantics: per
+ * 32 columns m = max|x|, s = m > 0 ? m/8 : 1, q = clamp(rne(x * (1/s)),
+ * -8, 7); q4 is [rows, K/2] bytes holding the nibble q + 8 (low
+ * nibble = even column), scales [rows, K/32]. q8 (optional, may be NULL)
+ * receives the signed values as int8 [rows, K]: with the same scales they
+ * are an int8 weight for every qlm_*_i8 entry point, whose results then
+ * equal the int4 matmul's (the reference's int4 dot is its int8 dot over
+ * the unpacked values, math_ops.cpp:604-700). K a multiple of 32; q4, q8
+ * 16-byte aligned. */
+int qlm_quantize_q4_f32(const float* w, int rows, int K, uint8_t* q4, float* scales, int8_t* q8,
+                        void* stream);
+int qlm_quantize_q4_bf16(const uint16_t* w, int rows, int K, uint8_t* q4, float* scales,
+                         int8_t* q8, void* stream);
+
+/* int4 tile-major copy for the one-row GEMV: the fragments of the int8
+ * tile-major layout at 8 bytes a lane (512 B a fragment), nibbles value + 8
+ * (padded rows value 0); scales as qlm_mx_swizzle's. K a multiple of 64. */
+int qlm_mx4_layout_bytes(int rows, int K, int halves, size_t* q_bytes, size_t* s_bytes);
+int qlm_mx4_swizzle(const uint8_t* q4, const float* scales, int rows, int K, int halves,
+                    uint8_t* q_out, float* s_out, void* stream);
+
+/* qlm_gemv_i8_mx / _config / qlm_lm_head_greedy_mx over int4 tile-major
+ * weights (group 32): each lane widens its 16 nibbles to int8 in registers
+ * and the matrix-core arithmetic is the int8 path's, at half the weight
+ * bytes. Same arguments, launch shapes and semantics. */
+int qlm_gemv_i4_mx_config(const float* x, const float* norm_w, float eps, const uint8_t* q_tiles,
+                          const float* s_tiles, float* y, int N, int K, int epilogue, int waves,
+                          int ring, int grid, void* stream);
+int qlm_gemv_i4_mx(const float* x, const float* norm_w, float eps, const uint8_t* q_tiles,
+                   const float* s_tiles, float* y, int N, int K, int epilogue, void* stream);
+int qlm_lm_head_greedy_mx4(const float* x, const float* norm_w, float eps,
+                           const uint8_t* q_tiles, const float* s_tiles, float* logits, int V,
+                           int K, void* work, int* tokens, int ld_tokens, int* pos,
+                           const int* prompt_len, const float* embed, int H, float* h_next,
+                           void* stream);
 
 #ifdef __cplusplus
 }

@@ -78,6 +78,29 @@ class Oracle:
         self.lib.orc_matmul_i8(_p(A), _i(M), _i(K), _p(q), _p(s), _i(group), _i(N), _p(out), _i(N))
         return out
 
+    def quantize_q4(self, w: np.ndarray):
+        """Packed int4 rows [rows, (K+1)//2] (low nibble = even column) and
+        scales [rows, ceil(K/32)]."""
+        rows, K = w.shape
+        q = np.empty((rows, (K + 1) // 2), np.uint8)
+        s = np.empty((rows, (K + 31) // 32), np.float32)
+        fn = {np.float32: "orc_quantize_rows_q4_f32", np.uint16: "orc_quantize_rows_q4_bf16"}
+        getattr(self.lib, fn[w.dtype.type])(_p(w), _i(rows), _i(K), _p(q), _p(s))
+        return q, s
+
+    def unpack_q4(self, p: np.ndarray, K: int) -> np.ndarray:
+        rows = p.shape[0]
+        q = np.empty((rows, K), np.int8)
+        self.lib.orc_unpack_q4(_p(np.ascontiguousarray(p)), _i(rows), _i(K), _p(q))
+        return q
+
+    def matmul_i4(self, A: np.ndarray, p: np.ndarray, s: np.ndarray) -> np.ndarray:
+        M, K = A.shape
+        N = p.shape[0]
+        out = np.empty((M, N), np.float32)
+        self.lib.orc_matmul_i4(_p(A), _i(M), _i(K), _p(p), _p(s), _i(N), _p(out), _i(N))
+        return out
+
     def sumsq(self, x: np.ndarray) -> float:
         return float(self.lib.orc_sumsq(_p(x), _i(x.size)))
 
@@ -208,6 +231,21 @@ class Reference:
         N = q.shape[0]
         out = np.empty((M, N), np.float32)
         self.lib.qref_matmul_i8(_p(A), _i(M), _i(K), _p(q), _p(s), _i(N), _p(out), _i(N))
+        return out
+
+    def quantize_q4(self, w: np.ndarray):
+        rows, K = w.shape
+        q = np.empty((rows, (K + 1) // 2), np.uint8)
+        s = np.empty((rows, (K + 31) // 32), np.float32)
+        fn = "qref_quantize_rows_f32_int4" if w.dtype == np.float32 else "qref_quantize_rows_bf16_int4"
+        getattr(self.lib, fn)(_p(w), _i(rows), _i(K), _p(q), _p(s))
+        return q, s
+
+    def matmul_i4(self, A, p, s):
+        M, K = A.shape
+        N = p.shape[0]
+        out = np.empty((M, N), np.float32)
+        self.lib.qref_matmul_i4(_p(A), _i(M), _i(K), _p(p), _p(s), _i(N), _p(out), _i(N))
         return out
 
     def sumsq(self, x):

@@ -116,6 +116,94 @@ void orc_matmul_i8(const float* A, int M, int K, const int8_t* q, const float* s
     }
 }
 
+/* ---- int4 (Q4_0) weights: st_quantize_row_f32_int4 / _bf16_int4
+ * (safetensors.cpp:393-515) and the int4 branch of math::matmul
+ * (math_ops.cpp:581-818). Per 32-block: scale = max|x|/8 (1 if zero),
+ * inv = 1/scale, q = clamp(round(x*inv), -8, 7) stored as the nibble q+8,
+ * two columns per byte, low nibble = even column (:397-455). The 8-wide
+ * vector part rounds half-to-even (_mm256_round_ps, :426-435); a ragged
+ * block tail (fewer than 8 left) uses lround and packs pairs, with nibble 8
+ * (value 0) above an odd K's last column (:438-455). */
+static int clamp8(int q) { return q < -8 ? -8 : (q > 7 ? 7 : q); }
+
+static void quant4_row(const float* row, int K, uint8_t* out, float* s) {
+    const int nb = (K + 31) / 32;
+    for (int b = 0; b < nb; ++b) {
+        const int k0 = b * 32, k1 = k0 + 32 < K ? k0 + 32 : K;
+        float m = 0.0f;
+        for (int k = k0; k < k1; ++k) m = fmaxf(m, fabsf(row[k]));
+        const float scale = (m > 0.0f) ? (m / 8.0f) : 1.0f;
+        s[b] = scale;
+        const float inv = 1.0f / scale;
+        const int nv = k0 + ((k1 - k0) / 8) * 8;
+        for (int k = k0; k < nv; k += 2) {
+            const int q0 = clamp8((int)rintf(row[k] * inv));
+            const int q1 = clamp8((int)rintf(row[k + 1] * inv));
+            out[k / 2] = (uint8_t)(((q1 + 8) << 4) | ((q0 + 8) & 0x0F));
+        }
+        for (int k = nv; k < k1; k += 2) {
+            const int q0 = clamp8((int)lroundf(row[k] * inv));
+            const int n1 = k + 1 < k1 ? clamp8((int)lroundf(row[k + 1] * inv)) + 8 : 8;
+            out[k / 2] = (uint8_t)((n1 << 4) | ((q0 + 8) & 0x0F));
+        }
+    }
+}
+
+void orc_quantize_rows_q4_f32(const float* w, int rows, int K, uint8_t* q, float* s) {
+    const int nb = (K + 31) / 32, pb = (K + 1) / 2;
+#pragma omp parallel for schedule(static) num_threads(g_threads)
+    for (int r = 0; r < rows; ++r)
+        quant4_row(w + (size_t)r * K, K, q + (size_t)r * pb, s + (size_t)r * nb);
+}
+
+void orc_quantize_rows_q4_bf16(const uint16_t* w, int rows, int K, uint8_t* q, float* s) {
+    const int nb = (K + 31) / 32, pb = (K + 1) / 2;
+#pragma omp parallel num_threads(g_threads)
+    {
+        float* tmp = (float*)malloc((size_t)K * sizeof(float));
+#pragma omp for schedule(static)
+        for (int r = 0; r < rows; ++r) {
+            for (int k = 0; k < K; ++k) {
+                uint32_t bits = (uint32_t)w[(size_t)r * K + k] << 16;
+                memcpy(&tmp[k], &bits, 4);
+            }
+            quant4_row(tmp, K, q + (size_t)r * pb, s + (size_t)r * nb);
+        }
+        free(tmp);
+    }
+}
+
+/* Signed values of packed rows: (nibble - 8), Tensor's int4 contract
+ * (tensor.hpp:45-56). */
+void orc_unpack_q4(const uint8_t* p, int rows, int K, int8_t* q) {
+    const int pb = (K + 1) / 2;
+    for (int r = 0; r < rows; ++r)
+        for (int k = 0; k < K; ++k)
+            q[(size_t)r * K + k] =
+                (int8_t)(((p[(size_t)r * pb + k / 2] >> ((k & 1) * 4)) & 0x0F) - 8);
+}
+
+/* dot_avx2_int4 / dot8_avx2_int4 (math_ops.cpp:604-700) unpack each block
+ * and then run dot_avx2_int8's arithmetic unchanged (four 8-lane products,
+ * (p0+p1)+(p2+p3), fma with the block scale, hsum8, scaled scalar tail), so
+ * the int4 matmul is the int8 one over the unpacked values. */
+void orc_matmul_i4(const float* A, int M, int K, const uint8_t* p, const float* s, int N,
+                   float* C, int ldc) {
+    const int nb = (K + 31) / 32, pb = (K + 1) / 2;
+    for (int m = 0; m < M; ++m) {
+#pragma omp parallel num_threads(g_threads)
+        {
+            int8_t* row = (int8_t*)malloc((size_t)K);
+#pragma omp for schedule(static)
+            for (int n = 0; n < N; ++n) {
+                orc_unpack_q4(p + (size_t)n * pb, 1, K, row);
+                C[(size_t)m * ldc + n] = dot_q8(A + (size_t)m * K, row, s + (size_t)n * nb, K, 0);
+            }
+            free(row);
+        }
+    }
+}
+
 /* ---- A5/A6: norms (math_ops.cpp:990-1072, :1133-1172) --------------------- */
 
 float orc_sumsq(const float* x, int n) {

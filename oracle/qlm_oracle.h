@@ -26,6 +26,15 @@ extern "C" {
 void orc_quantize_rows_f32(const float* w, int rows, int K, int group, int8_t* q, float* s);
 void orc_quantize_rows_bf16(const uint16_t* w, int rows, int K, int group, int8_t* q, float* s);
 
+/* int4 (Q4_0) quantiser (safetensors.cpp:393-515): packed rows of (K+1)/2
+ * bytes (low nibble = even column), one scale per 32 columns; unpacking to
+ * the signed values; int4 matmul (math_ops.cpp:581-818). C is [M, ldc]. */
+void orc_quantize_rows_q4_f32(const float* w, int rows, int K, uint8_t* q, float* s);
+void orc_quantize_rows_q4_bf16(const uint16_t* w, int rows, int K, uint8_t* q, float* s);
+void orc_unpack_q4(const uint8_t* p, int rows, int K, int8_t* q);
+void orc_matmul_i4(const float* A, int M, int K, const uint8_t* p, const float* s, int N,
+                   float* C, int ldc);
+
 /* A3/A4 int8 matmul (math_ops.cpp:405-579, :820-900). C is [M, ldc]. */
 void orc_matmul_i8(const float* A, int M, int K, const int8_t* q, const float* s, int group,
                    int N, float* C, int ldc);

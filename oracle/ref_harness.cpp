@@ -44,6 +44,18 @@ Tensor int8_weight(const int8_t* q, const float* s, int N, int K) {
     return t;
 }
 
+Tensor int4_weight(const uint8_t* q, const float* s, int N, int K) {
+    Tensor t;
+    t.shape = {N, K};
+    t.compute_strides();
+    int nb = (K + Tensor::INT4_BLOCK_SIZE - 1) / Tensor::INT4_BLOCK_SIZE;
+    int pb = (K + 1) / 2;
+    t.int4_owner = std::make_shared<std::vector<uint8_t>>(q, q + (size_t)N * pb);
+    t.int4_scales = std::make_shared<std::vector<float>>(s, s + (size_t)N * nb);
+    t.int4_data = t.int4_owner->data();
+    return t;
+}
+
 Tensor owned_f32(const float* p, std::vector<int> shape) {
     Tensor t(shape);
     std::memcpy(t.data, p, (size_t)t.size() * sizeof(float));
@@ -68,6 +80,30 @@ void qref_quantize_rows_bf16(const uint16_t* w, int rows, int K, int8_t* q, floa
     int nb = (K + Tensor::INT8_BLOCK_SIZE - 1) / Tensor::INT8_BLOCK_SIZE;
     for (int r = 0; r < rows; ++r)
         st_quantize_row_bf16(w + (size_t)r * K, K, q + (size_t)r * K, s + (size_t)r * nb);
+}
+
+// int4 (Q4_0) load-time quantiser (safetensors.cpp:393-515): packed rows of
+// (K+1)/2 bytes, one scale per 32 columns.
+void qref_quantize_rows_f32_int4(const float* w, int rows, int K, uint8_t* q, float* s) {
+    int nb = (K + Tensor::INT4_BLOCK_SIZE - 1) / Tensor::INT4_BLOCK_SIZE, pb = (K + 1) / 2;
+    for (int r = 0; r < rows; ++r)
+        st_quantize_row_f32_int4(w + (size_t)r * K, K, q + (size_t)r * pb, s + (size_t)r * nb);
+}
+
+void qref_quantize_rows_bf16_int4(const uint16_t* w, int rows, int K, uint8_t* q, float* s) {
+    int nb = (K + Tensor::INT4_BLOCK_SIZE - 1) / Tensor::INT4_BLOCK_SIZE, pb = (K + 1) / 2;
+    for (int r = 0; r < rows; ++r)
+        st_quantize_row_bf16_int4(w + (size_t)r * K, K, q + (size_t)r * pb, s + (size_t)r * nb);
+}
+
+// math::matmul int4 branch (math_ops.cpp:820-900 via int4_gemv_range :768-800).
+void qref_matmul_i4(const float* A, int M, int K, const uint8_t* q, const float* s, int N,
+                    float* C, int ldc) {
+    Tensor a({M, K}, const_cast<float*>(A));
+    Tensor b = int4_weight(q, s, N, K);
+    Tensor c({M, N}, C);
+    c.strides = {ldc, 1};
+    math::matmul(a, b, c, true);
 }
 
 // A3/A4: math::matmul int8 branch (math_ops.cpp:820-900). C is [M, ldc].

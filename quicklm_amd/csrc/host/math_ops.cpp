@@ -53,8 +53,12 @@ namespace {
 bool gemv_tiles(const Tensor& A, const float* norm_w, float eps, const Tensor& B, float* C,
                 int64_t N, int epilogue) {
     if (A.rows() != 1 || !B.int8_tiles) return false;
-    const int rc = qlm_gemv_i8_mx(A.data, norm_w, eps, B.int8_tiles, B.int8_tile_scales,
-                                  B.int8_group, C, (int)N, (int)A.cols(), epilogue, g_stream);
+    const int rc =
+        B.int4_tiles
+            ? qlm_gemv_i4_mx(A.data, norm_w, eps, B.int4_tiles, B.int8_tile_scales, C, (int)N,
+                             (int)A.cols(), epilogue, g_stream)
+            : qlm_gemv_i8_mx(A.data, norm_w, eps, B.int8_tiles, B.int8_tile_scales,
+                             B.int8_group, C, (int)N, (int)A.cols(), epilogue, g_stream);
     if (rc == QLM_ERR_SHAPE) return false;
     check(rc, "qlm_gemv_i8_mx");
     return true;

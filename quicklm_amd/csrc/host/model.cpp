@@ -51,7 +51,14 @@ void DecoderModel::alloc_linear(LinearI8& lin, int N, int K) {
     lin.group = (group_ == 0) ? K : group_;
     lin.q.alloc((size_t)N * K);
     lin.s.alloc((size_t)N * lin.blocks_per_row() * sizeof(float));
-    weight_bytes_ += (size_t)N * K + (size_t)N * lin.blocks_per_row() * sizeof(float);
+    // bytes a one-row step streams: int8 values, or the int4 copy
+    const size_t scale_bytes = (size_t)N * lin.blocks_per_row() * sizeof(float);
+    if (int4_) {
+        lin.q4.alloc((size_t)N * K / 2);
+        weight_bytes_ += (size_t)N * K / 2 + scale_bytes;
+    } else {
+        weight_bytes_ += (size_t)N * K + scale_bytes;
+    }
 }
 
 // Device-side equivalent of get_weight -> get_tensor_keep_int8
@@ -72,6 +79,16 @@ void DecoderModel::quantize_into(LinearI8& lin, int row_off, const std::string& 
     const int rows = (int)t.shape[0];
     int8_t* q = lin.q.get<int8_t>() + (size_t)row_off * lin.K;
     float* s = lin.s.get<float>() + (size_t)row_off * lin.blocks_per_row();
+    if (int4_) {  // get_tensor_keep_int4 (safetensors.cpp:587-656)
+        uint8_t* q4 = lin.q4.get<uint8_t>() + (size_t)row_off * lin.K / 2;
+        if (t.dtype == "F32")
+            check(qlm_quantize_q4_f32(staging_.get<float>(), rows, lin.K, q4, s, q, stream_),
+                  "quantize");
+        else
+            check(qlm_quantize_q4_bf16(staging_.get<uint16_t>(), rows, lin.K, q4, s, q, stream_),
+                  "quantize");
+        return;
+    }
     if (t.dtype == "F32")
         check(qlm_quantize_q8_f32(staging_.get<float>(), rows, lin.K, lin.group, q, s, stream_),
               "quantize");
@@ -93,6 +110,13 @@ void DecoderModel::tile_linear(LinearI8& lin, int halves) {
     check(qlm_mx_swizzle(lin.q.get<int8_t>(), lin.s.get<float>(), lin.group, rows, lin.K, halves,
                          lin.qz.get<int8_t>(), sb ? lin.sz.get<float>() : nullptr, stream_),
           "tile swizzle");
+    if (int4_) {  // the int4 copy; its scales are the ones just written to sz
+        check(qlm_mx4_layout_bytes(rows, lin.K, halves, &qb, &sb), "int4 tile layout");
+        lin.qz4.alloc(qb);
+        check(qlm_mx4_swizzle(lin.q4.get<uint8_t>(), lin.s.get<float>(), rows, lin.K, halves,
+                              lin.qz4.get<uint8_t>(), lin.sz.get<float>(), stream_),
+              "int4 tile swizzle");
+    }
 }
 
 void DecoderModel::upload_f32(DeviceBuffer& dst, const std::string& name, int64_t expect) {
@@ -109,9 +133,12 @@ void DecoderModel::upload_f32(DeviceBuffer& dst, const std::string& name, int64_
 void DecoderModel::load(const std::string& dir, int max_seq_len, const std::string& precision,
                         int max_batch) {
     if (max_seq_len <= 0 || max_batch <= 0) throw std::runtime_error("load: bad sizes");
-    if (precision == "int8") group_ = 32;
+    int4_ = precision == "int4";
+    if (precision == "int8" || int4_) group_ = 32;
     else if (precision == "int8_row") group_ = 0;  // resolved per matrix to K
-    else throw std::runtime_error("load: precision must be int8 or int8_row, got " + precision);
+    else
+        throw std::runtime_error("load: precision must be int8, int8_row or int4, got " +
+                                 precision);
     cfg_ = parse_model_config(dir);
     ws_ = std::make_unique<WeightStore>(dir);
     max_seq_ = max_seq_len;
@@ -207,9 +234,14 @@ void DecoderModel::load(const std::string& dir, int max_seq_len, const std::stri
         quantize_into(lm_head_, 0, "lm_head.weight");
     } else {
         alloc_linear(lm_head_, V, H);
-        check(qlm_quantize_q8_f32(embed_.get<float>(), V, H, lm_head_.group, lm_head_.q.get<int8_t>(),
-                                  lm_head_.s.get<float>(), stream_),
-              "quantize lm_head");
+        if (int4_)
+            check(qlm_quantize_q4_f32(embed_.get<float>(), V, H, lm_head_.q4.get<uint8_t>(),
+                                      lm_head_.s.get<float>(), lm_head_.q.get<int8_t>(), stream_),
+                  "quantize lm_head");
+        else
+            check(qlm_quantize_q8_f32(embed_.get<float>(), V, H, lm_head_.group,
+                                      lm_head_.q.get<int8_t>(), lm_head_.s.get<float>(), stream_),
+                  "quantize lm_head");
     }
     tile_linear(lm_head_, 1);
     cfg_.vocab_size = lm_head_.N;  // model.cpp:123
@@ -337,7 +369,13 @@ void DecoderModel::enqueue_step(int B) {
     if (B == 1) {
         const Tensor lm = lm_head_.view();
         int rc = QLM_ERR_SHAPE;
-        if (lm.int8_tiles)
+        if (lm.int4_tiles)
+            rc = qlm_lm_head_greedy_mx4(h_.get<float>(), final_norm_.get<float>(), eps,
+                                        lm.int4_tiles, lm.int8_tile_scales, logits_.get<float>(),
+                                        V, H, tail_work_.get(), tokens_.get<int>(), ld_tokens_,
+                                        pos_.get<int>(), prompt_len_.get<int>(),
+                                        embed_.get<float>(), H, h_.get<float>(), stream_);
+        else if (lm.int8_tiles)
             rc = qlm_lm_head_greedy_mx(h_.get<float>(), final_norm_.get<float>(), eps, lm.int8_tiles,
                                        lm.int8_tile_scales, lm_head_.group, logits_.get<float>(), V,
                                        H, tail_work_.get(), tokens_.get<int>(), ld_tokens_,

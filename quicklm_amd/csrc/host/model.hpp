@@ -35,12 +35,16 @@ struct LinearI8 {
     // sz stays empty with per-row scales, which keep their layout
     DeviceBuffer qz, sz;
     int halves = 1;
+    // int4 models: packed rows [N, K/2] as quantised (q then holds their
+    // unpacked values) and the int4 tile-major copy (scales: sz)
+    DeviceBuffer q4, qz4;
     Tensor view() const {
         Tensor t = Tensor::int8(q.get<int8_t>(), s.get<float>(), N, K, group);
         if (qz.bytes()) {
             t.int8_tiles = qz.get<int8_t>();
             t.int8_tile_scales = sz.bytes() ? sz.get<float>() : s.get<float>();
         }
+        if (qz4.bytes()) t.int4_tiles = qz4.get<uint8_t>();
         return t;
     }
     int blocks_per_row() const { return group >= K ? 1 : K / group; }
@@ -136,6 +140,7 @@ class DecoderModel {
     ModelConfig cfg_;
     std::unique_ptr<WeightStore> ws_;
     int max_seq_ = 0, max_batch_ = 0, group_ = 32;
+    bool int4_ = false;  // --precision int4: Q4_0 weights (lm_head included)
     int HD_ = 0, PD_ = 0, QR_ = 0, PQ_ = 0, CORE_ = 0;
     size_t weight_bytes_ = 0;
     int kernels_per_step_ = 0;

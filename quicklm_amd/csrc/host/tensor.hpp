@@ -24,6 +24,11 @@ struct Tensor {
     // streamed by the one-row GEMV; null where the model keeps no such copy.
     const int8_t* int8_tiles = nullptr;
     const float* int8_tile_scales = nullptr;
+    // int4 (Q4_0) weights: the int8 fields then hold the unpacked values
+    // (same scales; the reference's int4 dot is its int8 dot over them) and
+    // this is their int4 tile-major copy (qlm_mx4_swizzle, scales as above),
+    // which the one-row GEMV streams at half the bytes.
+    const uint8_t* int4_tiles = nullptr;
 
     Tensor() = default;
     Tensor(std::vector<int64_t> shp, float* d) : shape(std::move(shp)), data(d) { compute_strides(); }

@@ -21,6 +21,8 @@
 //   - Fused prologue (RMSNorm with zero-centred gain) and epilogues (residual
 //     add, SiLU(gate)*up) remove separate elementwise launches.
 
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace {
@@ -646,7 +648,70 @@ __global__ __launch_bounds__(256) void k_mx_swizzle(const int8_t* __restrict__ q
     }
 }
 
-template <int NW, int T, int P, bool ROWSCALE, int PRO, int EPI>
+// int4 tile-major layout: the same fragments as the int8 one (lane l = 16q +
+// n: row 16t + n, columns 64b + 16q .. +15) at 8 bytes a lane, 512 B a
+// fragment, each column as the nibble value + 8 (8 for padded rows): byte i
+// of the lane's first word holds columns i (low nibble) and 4 + i (high),
+// of its second word columns 8 + i and 12 + i. Scales as in the int8 layout.
+__global__ __launch_bounds__(256) void k_mx4_swizzle(const uint8_t* __restrict__ q4,
+                                                     const float* __restrict__ sc, int rows,
+                                                     int K, int tiles, int halves,
+                                                     uint8_t* __restrict__ qz,
+                                                     float* __restrict__ sz) {
+    const int nblk = K >> 6, nsb = K >> 5;
+    const size_t total = (size_t)halves * tiles * nblk * QLM_WAVE;
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total;
+         i += (size_t)gridDim.x * blockDim.x) {
+        const int lane = (int)(i % QLM_WAVE);
+        const size_t fb = i / QLM_WAVE;
+        const int b = (int)(fb % nblk);
+        const int g = (int)(fb / nblk);
+        const int half = g / tiles, t = g % tiles;
+        const int n = lane & 15, qd = lane >> 4;
+        const int rh = t * 16 + n;  // row within the half
+        unsigned wa = 0x88888888u, wb = 0x88888888u;
+        if (rh < rows) {
+            // columns 64b + 16q .. +15: 8 packed bytes (low nibble = even column)
+            const uint2 src = *reinterpret_cast<const uint2*>(
+                q4 + ((size_t)half * rows + rh) * (K / 2) + 32 * b + 8 * qd);
+            unsigned v[16];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const unsigned byte = ((j < 4 ? src.x : src.y) >> (8 * (j % 4))) & 0xffu;
+                v[2 * j] = byte & 15u;
+                v[2 * j + 1] = byte >> 4;
+            }
+            wa = 0u;
+            wb = 0u;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                wa |= (v[j] | (v[4 + j] << 4)) << (8 * j);
+                wb |= (v[8 + j] | (v[12 + j] << 4)) << (8 * j);
+            }
+        }
+        reinterpret_cast<uint2*>(qz)[i] = make_uint2(wa, wb);
+        if (lane < 32) {
+            const int h = lane >> 4;
+            sz[fb * 32 + lane] =
+                rh < rows ? sc[((size_t)half * rows + rh) * nsb + 2 * b + h] : 0.0f;
+        }
+    }
+}
+
+// A lane's 16 int4 weights (int4 tile-major layout) as the int8 B operand:
+// nibbles to bytes, then value = nibble - 8 per byte without borrows
+// ((x | 0x80) - 8 stays >= 0x78; the xor restores the sign).
+__device__ __forceinline__ int unbias4(unsigned w) {
+    return (int)(((w | 0x80808080u) - 0x08080808u) ^ 0x80808080u);
+}
+typedef int v4i_w4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ v4i_w4 unpack_w4(int2 w) {
+    const unsigned a = (unsigned)w.x, b = (unsigned)w.y;
+    return v4i_w4{unbias4(a & 0x0F0F0F0Fu), unbias4((a >> 4) & 0x0F0F0F0Fu),
+                  unbias4(b & 0x0F0F0F0Fu), unbias4((b >> 4) & 0x0F0F0F0Fu)};
+}
+
+template <int NW, int T, int P, bool ROWSCALE, int PRO, int EPI, bool W4>
 __global__ __launch_bounds__(NW * QLM_WAVE) void k_gemv_mx(
     const float* __restrict__ x, const float* __restrict__ nw, float eps,
     const int8_t* __restrict__ q, const float* __restrict__ sc, float* __restrict__ y, int N,
@@ -700,15 +765,16 @@ __global__ __launch_bounds__(NW * QLM_WAVE) void k_gemv_mx(
     // this wave's last block (a wave past the last block reads block nblk-1,
     // which then meets zero digits)
     const int blast = w < nblk ? nblk - 1 - ((nblk - 1 - w) % NW) : nblk - 1;
-    int4 wb[P][T];
+    using WT = typename std::conditional<W4, int2, int4>::type;  // a lane's 16 weights
+    WT wb[P][T];
     float sb[P][T];
     auto issue = [&](int tile, int u) {
         const int b = min(w + NW * u, blast);
 #pragma unroll
         for (int tt = 0; tt < T; ++tt) {
-            // fragment (tile of half tt, block b): 1 KB in lane order
+            // fragment (tile of half tt, block b): 1 KB (512 B at int4) in lane order
             const size_t fb = (size_t)(tile + tt * ntiles) * nblk + b;
-            wb[u][tt] = reinterpret_cast<const int4*>(q)[fb * QLM_WAVE + lane];
+            wb[u][tt] = reinterpret_cast<const WT*>(q)[fb * QLM_WAVE + lane];
             if constexpr (!ROWSCALE) sb[u][tt] = sc[fb * 32 + (qd & 1) * 16 + n];
         }
     };
@@ -786,7 +852,12 @@ __global__ __launch_bounds__(NW * QLM_WAVE) void k_gemv_mx(
         if (active) a = *reinterpret_cast<const v4i*>(dig + u * 256 + aoff);
 #pragma unroll
         for (int tt = 0; tt < T; ++tt) {
-            const v4i bw = v4i{wb[u][tt].x, wb[u][tt].y, wb[u][tt].z, wb[u][tt].w};
+            v4i bw;
+            if constexpr (W4) {
+                bw = unpack_w4(wb[u][tt]);
+            } else {
+                bw = v4i{wb[u][tt].x, wb[u][tt].y, wb[u][tt].z, wb[u][tt].w};
+            }
             const v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, bw, v4i{0, 0, 0, 0}, 0, 0, 0);
             const int pp = (d[0] << 7) + d[1];
             const int qq = (d[2] << 7) + d[3];
@@ -1100,12 +1171,20 @@ constexpr MxTuned kMxTuned[] = {
     {151936, 2560, EPI_STORE, 8, 5, 256},    // lm_head (also its greedy form)
 };
 
-// Launch shape: the tuned table, else the fewest waves per workgroup that
-// give >= 2048 waves in all (each a K-slice of a tile) among the
-// instantiated pairs, and one tile per workgroup up to the greedy tail's key
-// slots. nw = 0 when no pair fits K.
-MxConfig mx_config(int N, int K, int epi) {
+// Where int4 weights (half the bytes) measured a different best shape.
+constexpr MxTuned kMx4Tuned[] = {
+    {151936, 2560, EPI_STORE, 8, 5, 512},    // lm_head
+};
+
+// Launch shape: the tuned table (int4 overrides first), else the fewest
+// waves per workgroup that give >= 2048 waves in all (each a K-slice of a
+// tile) among the instantiated pairs, and one tile per workgroup up to the
+// greedy tail's key slots. nw = 0 when no pair fits K.
+MxConfig mx_config(int N, int K, int epi, bool w4 = false) {
     const int e = epi == EPI_ARGMAX ? EPI_STORE : epi;
+    if (w4)
+        for (const MxTuned& t : kMx4Tuned)
+            if (t.N == N && t.K == K && t.epi == e) return MxConfig{t.nw, t.ring, t.grid};
     for (const MxTuned& t : kMxTuned)
         if (t.N == N && t.K == K && t.epi == e) return MxConfig{t.nw, t.ring, t.grid};
     const int tiles = (N + 15) / 16, nblk = K / 64;
@@ -1120,7 +1199,7 @@ MxConfig mx_config(int N, int K, int epi) {
     return c;
 }
 
-template <int NW, int P, bool ROWSCALE, int PRO, int EPI>
+template <int NW, int P, bool ROWSCALE, int PRO, int EPI, bool W4>
 int launch_mx(const MxConfig& c, const float* x, const float* nw, float eps, const int8_t* q,
               const float* sc, float* y, int N, int K, int F, hipStream_t st,
               const GreedyTail& tail) {
@@ -1128,7 +1207,7 @@ int launch_mx(const MxConfig& c, const float* x, const float* nw, float eps, con
     const int ntiles = (N + 15) / 16;
     int grid = c.grid < ntiles ? c.grid : ntiles;
     if (grid < 1) grid = 1;
-    hipLaunchKernelGGL((k_gemv_mx<NW, T, P, ROWSCALE, PRO, EPI>), dim3(grid),
+    hipLaunchKernelGGL((k_gemv_mx<NW, T, P, ROWSCALE, PRO, EPI, W4>), dim3(grid),
                        dim3(NW * QLM_WAVE), mx_lds_bytes(NW, P), st, x, nw, eps, q, sc, y, N, K, F,
                        ntiles, tail);
     if constexpr (EPI == EPI_ARGMAX) {
@@ -1139,13 +1218,13 @@ int launch_mx(const MxConfig& c, const float* x, const float* nw, float eps, con
     return qlm_launch_status();
 }
 
-template <bool ROWSCALE, int PRO, int EPI>
+template <bool ROWSCALE, int PRO, int EPI, bool W4>
 int launch_mx_np(const MxConfig& c, const float* x, const float* nw, float eps, const int8_t* q,
                  const float* sc, float* y, int N, int K, int F, hipStream_t st,
                  const GreedyTail& tail) {
 #define QLM_MX(W, PP)                                                                      \
     if (c.nw == W && c.ring == PP)                                                          \
-        return launch_mx<W, PP, ROWSCALE, PRO, EPI>(c, x, nw, eps, q, sc, y, N, K, F, st, tail);
+        return launch_mx<W, PP, ROWSCALE, PRO, EPI, W4>(c, x, nw, eps, q, sc, y, N, K, F, st, tail);
     QLM_MX(4, 1) QLM_MX(4, 2) QLM_MX(4, 4) QLM_MX(4, 8) QLM_MX(4, 10) QLM_MX(8, 4)
     QLM_MX(8, 5) QLM_MX(8, 8) QLM_MX(16, 2) QLM_MX(16, 4) QLM_MX(16, 10) QLM_MX(16, 12)
 #undef QLM_MX
@@ -1154,26 +1233,34 @@ int launch_mx_np(const MxConfig& c, const float* x, const float* nw, float eps, 
 
 int mx_dispatch(int pro, int epi, const MxConfig& c, const float* x, const float* nw, float eps,
                 const int8_t* q, const float* sc, bool rowscale, float* y, int N, int K,
-                hipStream_t st, const GreedyTail& tail = GreedyTail{}) {
+                hipStream_t st, const GreedyTail& tail = GreedyTail{}, bool w4 = false) {
     if (!mx_fits(K, c.nw, c.ring) || c.grid < 1) return QLM_ERR_SHAPE;
     if (epi == EPI_ARGMAX && c.grid > kMaxXsGrid) return QLM_ERR_SHAPE;
     const int F = N;
-#define QLM_MX_CALL(RS, P, E) \
-    return launch_mx_np<RS, P, E>(c, x, nw, eps, q, sc, y, N, K, F, st, tail)
+#define QLM_MX_CALL(RS, P, E, W) \
+    return launch_mx_np<RS, P, E, W>(c, x, nw, eps, q, sc, y, N, K, F, st, tail)
+    if (w4) {  // int4 weights: group-32 scales only (the reference's Q4_0)
+        if (rowscale) return QLM_ERR_SHAPE;
+        if (epi == EPI_ARGMAX) QLM_MX_CALL(false, PRO_RMSNORM, EPI_ARGMAX, true);
+        if (pro == PRO_NONE && epi == EPI_STORE) QLM_MX_CALL(false, PRO_NONE, EPI_STORE, true);
+        if (pro == PRO_RMSNORM && epi == EPI_STORE) QLM_MX_CALL(false, PRO_RMSNORM, EPI_STORE, true);
+        if (pro == PRO_NONE && epi == EPI_RESID) QLM_MX_CALL(false, PRO_NONE, EPI_RESID, true);
+        QLM_MX_CALL(false, PRO_RMSNORM, EPI_SWIGLU, true);
+    }
     if (epi == EPI_ARGMAX) {
-        if (rowscale) QLM_MX_CALL(true, PRO_RMSNORM, EPI_ARGMAX);
-        QLM_MX_CALL(false, PRO_RMSNORM, EPI_ARGMAX);
+        if (rowscale) QLM_MX_CALL(true, PRO_RMSNORM, EPI_ARGMAX, false);
+        QLM_MX_CALL(false, PRO_RMSNORM, EPI_ARGMAX, false);
     }
     if (rowscale) {
-        if (pro == PRO_NONE && epi == EPI_STORE) QLM_MX_CALL(true, PRO_NONE, EPI_STORE);
-        if (pro == PRO_RMSNORM && epi == EPI_STORE) QLM_MX_CALL(true, PRO_RMSNORM, EPI_STORE);
-        if (pro == PRO_NONE && epi == EPI_RESID) QLM_MX_CALL(true, PRO_NONE, EPI_RESID);
-        QLM_MX_CALL(true, PRO_RMSNORM, EPI_SWIGLU);
+        if (pro == PRO_NONE && epi == EPI_STORE) QLM_MX_CALL(true, PRO_NONE, EPI_STORE, false);
+        if (pro == PRO_RMSNORM && epi == EPI_STORE) QLM_MX_CALL(true, PRO_RMSNORM, EPI_STORE, false);
+        if (pro == PRO_NONE && epi == EPI_RESID) QLM_MX_CALL(true, PRO_NONE, EPI_RESID, false);
+        QLM_MX_CALL(true, PRO_RMSNORM, EPI_SWIGLU, false);
     }
-    if (pro == PRO_NONE && epi == EPI_STORE) QLM_MX_CALL(false, PRO_NONE, EPI_STORE);
-    if (pro == PRO_RMSNORM && epi == EPI_STORE) QLM_MX_CALL(false, PRO_RMSNORM, EPI_STORE);
-    if (pro == PRO_NONE && epi == EPI_RESID) QLM_MX_CALL(false, PRO_NONE, EPI_RESID);
-    QLM_MX_CALL(false, PRO_RMSNORM, EPI_SWIGLU);
+    if (pro == PRO_NONE && epi == EPI_STORE) QLM_MX_CALL(false, PRO_NONE, EPI_STORE, false);
+    if (pro == PRO_RMSNORM && epi == EPI_STORE) QLM_MX_CALL(false, PRO_RMSNORM, EPI_STORE, false);
+    if (pro == PRO_NONE && epi == EPI_RESID) QLM_MX_CALL(false, PRO_NONE, EPI_RESID, false);
+    QLM_MX_CALL(false, PRO_RMSNORM, EPI_SWIGLU, false);
 #undef QLM_MX_CALL
 }
 
@@ -1440,4 +1527,74 @@ extern "C" int qlm_gemv_i8_swiglu_rmsnorm(const float* x, int ldx, const float* 
                                           void* stream) {
     return gemv_dispatch(PRO_RMSNORM, EPI_SWIGLU, x, ldx, norm_w, eps, q, scales, group, y, ldy,
                          M, F, K, stream);
+}
+
+// ---- int4 (Q4_0) weights on the matrix cores ----
+
+extern "C" int qlm_mx4_layout_bytes(int rows, int K, int halves, size_t* q_bytes,
+                                    size_t* s_bytes) {
+    size_t qb = 0;
+    const int rc = qlm_mx_layout_bytes(rows, K, 32, halves, &qb, s_bytes);
+    if (rc != QLM_OK) return rc;
+    *q_bytes = qb / 2;
+    return QLM_OK;
+}
+
+extern "C" int qlm_mx4_swizzle(const uint8_t* q4, const float* scales, int rows, int K,
+                               int halves, uint8_t* q_out, float* s_out, void* stream) {
+    size_t qb = 0, sb = 0;
+    const int rc = qlm_mx4_layout_bytes(rows, K, halves, &qb, &sb);
+    if (rc != QLM_OK) return rc;
+    if (!q4 || !scales || !q_out || !s_out) return QLM_ERR_ARG;
+    if (((uintptr_t)q4 | (uintptr_t)q_out) & 7u) return QLM_ERR_SHAPE;
+    const int tiles = (rows + 15) / 16;
+    const size_t lanes = qb / 8;
+    const int grid = (int)((lanes + 255) / 256 < 65536 ? (lanes + 255) / 256 : 65536);
+    hipLaunchKernelGGL(k_mx4_swizzle, dim3(grid), dim3(256), 0, as_stream(stream), q4, scales,
+                       rows, K, tiles, halves, q_out, s_out);
+    return qlm_launch_status();
+}
+
+extern "C" int qlm_gemv_i4_mx_config(const float* x, const float* norm_w, float eps,
+                                     const uint8_t* q_tiles, const float* s_tiles, float* y,
+                                     int N, int K, int epilogue, int waves, int ring, int grid,
+                                     void* stream) {
+    if (!x || !q_tiles || !s_tiles || !y || N <= 0 || K <= 0 || grid <= 0) return QLM_ERR_ARG;
+    if (epilogue < EPI_STORE || epilogue > EPI_SWIGLU) return QLM_ERR_ARG;
+    if (((uintptr_t)x | (uintptr_t)q_tiles | (uintptr_t)norm_w) & 15u) return QLM_ERR_SHAPE;
+    const int pro = norm_w ? PRO_RMSNORM : PRO_NONE;
+    if (epilogue == EPI_SWIGLU && !norm_w) return QLM_ERR_ARG;
+    if (epilogue == EPI_RESID && pro == PRO_RMSNORM) return QLM_ERR_ARG;
+    return mx_dispatch(pro, epilogue, MxConfig{waves, ring, grid}, x, norm_w, eps,
+                       reinterpret_cast<const int8_t*>(q_tiles), s_tiles, false, y, N, K,
+                       as_stream(stream), GreedyTail{}, true);
+}
+
+extern "C" int qlm_gemv_i4_mx(const float* x, const float* norm_w, float eps,
+                              const uint8_t* q_tiles, const float* s_tiles, float* y, int N,
+                              int K, int epilogue, void* stream) {
+    if (N <= 0 || K <= 0) return QLM_ERR_ARG;
+    const MxConfig c = mx_config(N, K, epilogue, true);
+    if (c.nw == 0) return QLM_ERR_SHAPE;
+    return qlm_gemv_i4_mx_config(x, norm_w, eps, q_tiles, s_tiles, y, N, K, epilogue, c.nw,
+                                 c.ring, c.grid, stream);
+}
+
+extern "C" int qlm_lm_head_greedy_mx4(const float* x, const float* norm_w, float eps,
+                                      const uint8_t* q_tiles, const float* s_tiles, float* logits,
+                                      int V, int K, void* work, int* tokens, int ld_tokens,
+                                      int* pos, const int* prompt_len, const float* embed, int H,
+                                      float* h_next, void* stream) {
+    if (!x || !norm_w || !q_tiles || !s_tiles || !logits || !work || !tokens || !pos ||
+        !prompt_len || !embed || !h_next || V <= 0 || K <= 0 || H <= 0 || ld_tokens <= 0)
+        return QLM_ERR_ARG;
+    if (((uintptr_t)x | (uintptr_t)q_tiles | (uintptr_t)norm_w | (uintptr_t)work) & 15u)
+        return QLM_ERR_SHAPE;
+    const MxConfig c = mx_config(V, K, EPI_ARGMAX, true);
+    if (c.nw == 0) return QLM_ERR_SHAPE;
+    return mx_dispatch(PRO_RMSNORM, EPI_ARGMAX, c, x, norm_w, eps,
+                       reinterpret_cast<const int8_t*>(q_tiles), s_tiles, false, logits, V, K,
+                       as_stream(stream),
+                       greedy_tail(work, tokens, ld_tokens, pos, prompt_len, embed, H, V, h_next),
+                       true);
 }

@@ -97,6 +97,14 @@ _SIGS = {
     "qlm_lm_head_greedy_mx": (_i, [_vp, _vp, _f, _vp, _vp, _i, _vp, _i, _i, _vp, _vp, _i, _vp, _vp,
                                 _vp, _i, _vp, _vp]),
     "qlm_embed_tokens": (_i, [_vp, _i, _i, _vp, _i, _vp, _vp, _i, _i, _vp]),
+    "qlm_quantize_q4_f32": (_i, [_vp, _i, _i, _vp, _vp, _vp, _vp]),
+    "qlm_quantize_q4_bf16": (_i, [_vp, _i, _i, _vp, _vp, _vp, _vp]),
+    "qlm_mx4_layout_bytes": (_i, [_i, _i, _i, C.POINTER(_sz), C.POINTER(_sz)]),
+    "qlm_mx4_swizzle": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp]),
+    "qlm_gemv_i4_mx_config": (_i, [_vp, _vp, _f, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp]),
+    "qlm_gemv_i4_mx": (_i, [_vp, _vp, _f, _vp, _vp, _vp, _i, _i, _i, _vp]),
+    "qlm_lm_head_greedy_mx4": (_i, [_vp, _vp, _f, _vp, _vp, _vp, _i, _i, _vp, _vp, _i, _vp, _vp,
+                                    _vp, _i, _vp, _vp]),
 }
 
 

@@ -12,7 +12,10 @@ prompt[0..126], 64 decode steps, no EOS stop) and stores:
   tensor_sha                     sha256 of a few synthetic tensors (pins the
                                  generator across hosts)
 plus the same stream from the reference's own -O3 -ffast-math build
-(tokens_fast) for the record. Usage: python tests/golden/make_golden.py
+(tokens_fast) for the record; and tiny_greedy_int4.npz, the IEEE build's
+run of the same prompt at --precision int4 (prompt, tokens, top_idx,
+top_val, margin, logits0_head). Usage: python tests/golden/make_golden.py
+[--int4 (the int4 fixture only)]
 """
 import hashlib
 import os
@@ -39,7 +42,30 @@ def tensor_sha(model_dir):
     return {n: hashlib.sha256(t[n].tobytes()).hexdigest() for n in SHA_TENSORS}
 
 
+def int4_stream(d, prompt):
+    """The same run at --precision int4 (Q4_0 weights, lm_head included),
+    IEEE build only: tiny_greedy_int4.npz."""
+    out = os.path.join(os.path.dirname(os.path.abspath(__file__)), "tiny_greedy_int4.npz")
+    ref = Reference("ieee")
+    ref.init_threads(os.cpu_count() or 1)
+    m = ref.load_model(d, 2048, "int4")
+    toks, pre, dec, lg = m.generate(prompt, 64, keep_logits=True)
+    print(f"int4 ieee: prefill {pre:.2f}s decode {dec:.2f}s tokens {toks[:8]}...", flush=True)
+    order = np.argsort(-lg, axis=1, kind="stable")[:, :32]
+    top_val = np.take_along_axis(lg, order, axis=1)
+    np.savez_compressed(
+        out, prompt=prompt.astype(np.int32), tokens=toks.astype(np.int32),
+        top_idx=order.astype(np.int32), top_val=top_val.astype(np.float32),
+        margin=(top_val[:, 0] - top_val[:, 1]), logits0_head=lg[0, :4096].copy())
+    print("wrote", out)
+
+
 def main():
+    if "--int4" in sys.argv:  # only the int4 fixture
+        with tempfile.TemporaryDirectory() as d:
+            synth.write_model(d, "tiny")
+            int4_stream(d, synth.prompt_tokens(128, seed=0)[0])
+        return
     out = os.path.join(os.path.dirname(os.path.abspath(__file__)), "tiny_greedy.npz")
     with tempfile.TemporaryDirectory() as d:
         synth.write_model(d, "tiny")
@@ -65,6 +91,7 @@ def main():
             logits0_head=lg[0, :4096].copy(), logits63_head=lg[63, :4096].copy(),
             tensor_names=np.array(SHA_TENSORS), tensor_sha=np.array(
                 [tensor_sha(d)[n] for n in SHA_TENSORS]))
+        int4_stream(d, prompt)
     print("wrote", out, "fast==ieee tokens:", bool(np.array_equal(res["fast"][0], toks)))
 
 

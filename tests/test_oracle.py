@@ -173,7 +173,72 @@ def test_micro_model_vs_reference(orc, ref, tmp_path):
     assert np.array_equal(bits(m.forward_batch(prompt[:8], 0)), bits(seq))
 
 
+@needs_ref
+@pytest.mark.parametrize("K", [1024, 2560, 1000, 40, 33])
+def test_q4_quantizer_vs_reference(orc, ref, rng, K):
+    """int4 (Q4_0) quantiser, f32 and bf16 rows, including an all-zero row,
+    tiny values, ragged block tails and an odd K."""
+    w = (rng.standard_normal((33, K)) * 0.02).astype(np.float32)
+    w[1] = 0
+    w[2, :16] = 1e-30
+    w[3, :min(K, 32)] = (np.arange(32, dtype=np.float32) * np.float32(0.125) - 2)[:min(K, 32)]
+    for src in (w, (w.view(np.uint32) >> 16).astype(np.uint16)):
+        q1, s1 = orc.quantize_q4(src)
+        q2, s2 = ref.quantize_q4(src)
+        assert q1.shape == (33, (K + 1) // 2)
+        assert np.array_equal(q1, q2) and np.array_equal(bits(s1), bits(s2))
+
+
+@needs_ref
+@pytest.mark.parametrize("M,K", [(1, 2560), (3, 1024), (2, 1000), (1, 3584)])
+def test_q4_matmul_vs_reference(orc, ref, rng, M, K):
+    """The int4 matmul, and the reference's own int4 matmul equals its int8
+    matmul over the unpacked values (the identity the device path builds on)."""
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    p, s = ref.quantize_q4((rng.standard_normal((67, K)) * 0.02).astype(np.float32))
+    got = ref.matmul_i4(A, p, s)
+    assert np.array_equal(bits(orc.matmul_i4(A, p, s)), bits(got))
+    assert np.array_equal(bits(ref.matmul_i8(A, orc.unpack_q4(p, K), s)), bits(got))
+
+
 # ------------------------------------------------------------ 2. mathematics
+def test_q4_quantizer_known_answers(orc):
+    """Scale = max|x|/8 (1 for an all-zero block); exact multiples of the
+    scale map to those integers, the positive maximum (8 scales) clamps to 7;
+    exact halves round half to even in the 8-wide part and half away from
+    zero in a block's ragged tail; nibble = value + 8, low nibble = even
+    column, an odd K's last byte carries value 0 above its last column."""
+    s = np.float32(0.01)
+    row = np.zeros((1, 64), np.float32)
+    row[0, :8] = np.array([8, -8, 3, -3, 7, 0.5, 1.5, -2.5], np.float32) * s
+    p, sc = orc.quantize_q4(row)
+    assert sc[0, 0] == np.float32(8 * s) / np.float32(8) and sc[0, 1] == 1.0
+    v = orc.unpack_q4(p, 64)[0]
+    inv = np.float32(1) / sc[0, 0]
+    expect = np.clip(np.rint(row[0, :8] * inv), -8, 7).astype(np.int8)
+    assert list(expect[[0, 1, 5, 6, 7]]) == [7, -8, 0, 2, -2]
+    assert np.array_equal(v[:8], expect) and not v[8:].any()
+    assert np.all(p[0, 16:] == 0x88)  # zero block: value 0 in both nibbles
+    # ragged tail (K = 36: block 1 holds 4 columns, all past the 8-wide part)
+    t = np.zeros((1, 36), np.float32)
+    t[0, 32:36] = np.array([8, 0.5, -0.5, 2.5], np.float32)  # scale 1: lround
+    pt, st = orc.quantize_q4(t)
+    assert st[0, 1] == 1.0 and list(orc.unpack_q4(pt, 36)[0, 32:]) == [7, 1, -1, 3]
+    # odd K: the high nibble of the last byte is 8 (value 0)
+    po, _ = orc.quantize_q4(np.array([[0.08, -0.08, 0.04]], np.float32))
+    assert po.shape == (1, 2) and po[0, 1] >> 4 == 8
+    assert list(orc.unpack_q4(po, 3)[0]) == [7, -8, 4]
+
+
+def test_q4_unpack_layout(orc, rng):
+    p = rng.integers(0, 256, (3, 50), dtype=np.uint8)
+    q = orc.unpack_q4(p, 99)
+    lo = (p & 15).astype(np.int16) - 8
+    hi = (p >> 4).astype(np.int16) - 8
+    want = np.stack([lo, hi], axis=2).reshape(3, 100)[:, :99]
+    assert np.array_equal(q, want.astype(np.int8))
+
+
 def test_quantizer_known_answers(orc):
     """Scale = max|x|/127; values at exact multiples of the scale map to those
     integers; ties at .5 round half to even; an all-zero group has scale 1."""
