@@ -148,7 +148,7 @@ def _tile_major(hip, dq, ds, group, rows, K, halves):
 # shape (F = 9728 outputs from 2F = 19456 int8 rows of K = 2560, group-32
 # scales), on the int8 matrix cores over tile-major weights.
 DOM_F, DOM_K = 9728, 2560
-DOM_NAME = ("k_gemv_mx<8, 2, 5, false, 1, 2> (RMSNorm + gate/up GEMV + SwiGLU on the int8 "
+DOM_NAME = ("k_gemv_mx<8, 2, 5, false, 1, 2, false> (RMSNorm + gate/up GEMV + SwiGLU on the int8 "
             "matrix cores, 19456x2560 int8 G=32, tile-major)")
 PMC_FILE = os.path.join(ROOT, "profiles", "gemv_gate_up_4b_pmc.json")
 
