@@ -354,7 +354,10 @@ constexpr int kSkKc = 128;
 // chunks in flight per workgroup (register ring), by activation tiles
 constexpr int sk_ring(int tm) { return tm <= 2 ? 2 : 1; }
 
-template <int TM, bool ROWSCALE, bool NORM>
+// DEFER (with NORM): the activation is staged as x * (1 + w) and the row's
+// 1/rms multiplies the reduced sums instead (k_mm_reduce<..., true>), so no
+// separate row-scale launch precedes the matmul.
+template <int TM, bool ROWSCALE, bool NORM, bool DEFER>
 __global__ __launch_bounds__(kThreads) void k_mm_i8_sk(
     const float* __restrict__ x, int ldx, const float* __restrict__ rs,
     const float* __restrict__ nw, const int8_t* __restrict__ q, const float* __restrict__ sc,
@@ -398,7 +401,7 @@ __global__ __launch_bounds__(kThreads) void k_mm_i8_sk(
                 xr[j][u] = *reinterpret_cast<const float4*>(x + (size_t)m * ldx + k0 + c4 * 4);
                 if constexpr (NORM) {
                     gr[j][u] = *reinterpret_cast<const float4*>(nw + k0 + c4 * 4);
-                    rr[j][u] = rs[m];
+                    rr[j][u] = DEFER ? 1.0f : rs[m];
                 }
             }
         }
@@ -495,13 +498,31 @@ __global__ __launch_bounds__(kThreads) void k_mm_i8_sk(
 
 // y[m, n] (=, +=) sum over slices of part[ks, m, n], or for SwiGLU
 // y[m, n] = silu(gate) * up with gate/up the sums at columns n and F + n.
-template <int EPI>
+// Workgroup (bx, m) takes columns bx*256.. of row m. NORM: the slices hold
+// (x * (1 + w)) . W and the row's RMSNorm factor 1/sqrt(mean(x^2) + eps) is
+// computed here from x and multiplies the sums.
+template <int EPI, bool NORM>
 __global__ __launch_bounds__(kThreads) void k_mm_reduce(const float* __restrict__ part, int ks,
                                                         int M, int NR, int N,
-                                                        float* __restrict__ y, int ldy) {
-    const int idx = blockIdx.x * kThreads + threadIdx.x;
-    if (idx >= M * N) return;
-    const int m = idx / N, n = idx % N;
+                                                        float* __restrict__ y, int ldy,
+                                                        const float* __restrict__ x, int ldx,
+                                                        int K, float eps) {
+    const int m = blockIdx.y, n = blockIdx.x * kThreads + threadIdx.x;
+    float rsv = 1.0f;
+    if constexpr (NORM) {
+        __shared__ float red[kThreads / QLM_WAVE];
+        const float4* xr = reinterpret_cast<const float4*>(x + (size_t)m * ldx);
+        float ss = 0.0f;
+        for (int i = threadIdx.x; i < (K >> 2); i += kThreads) {
+            const float4 v = xr[i];
+            ss = fmaf(v.x, v.x, ss);
+            ss = fmaf(v.y, v.y, ss);
+            ss = fmaf(v.z, v.z, ss);
+            ss = fmaf(v.w, v.w, ss);
+        }
+        rsv = 1.0f / sqrtf(block_sum(ss, red) / (float)K + eps);
+    }
+    if (n >= N) return;
     // slices summed in order; 8 slices' loads issued together
     float g = 0.0f, u = 0.0f;
     const size_t sstride = (size_t)M * NR;
@@ -523,6 +544,10 @@ __global__ __launch_bounds__(kThreads) void k_mm_reduce(const float* __restrict_
     for (; k < ks; ++k) {
         g += pr[k * sstride];
         if constexpr (EPI == EPI_SWIGLU) u += pr[k * sstride + N];
+    }
+    if constexpr (NORM) {
+        g *= rsv;
+        u *= rsv;
     }
     float* dst = y + (size_t)m * ldy + n;
     if constexpr (EPI == EPI_SWIGLU)
@@ -589,13 +614,33 @@ size_t mm_workspace(int M, int N, int K, int epi) {
     return b;
 }
 
-template <int TM, bool RS, bool NORM>
+template <int TM, bool RS, bool NORM, bool DEFER>
 void launch_sk(const float* x, int ldx, const float* rs, const float* nw, const int8_t* q,
                const float* sc, float* part, int ldp, int M, int NR, int K, int ks,
                hipStream_t st) {
     const dim3 grid((NR + kSkRows - 1) / kSkRows, ks, (M + 16 * TM - 1) / (16 * TM));
-    hipLaunchKernelGGL((k_mm_i8_sk<TM, RS, NORM>), grid, dim3(kThreads), 0, st, x, ldx, rs, nw, q,
-                       sc, part, ldp, M, NR, K, K / ks);
+    hipLaunchKernelGGL((k_mm_i8_sk<TM, RS, NORM, DEFER>), grid, dim3(kThreads), 0, st, x, ldx, rs,
+                       nw, q, sc, part, ldp, M, NR, K, K / ks);
+}
+
+template <bool RS, bool NORM, bool DEFER>
+void launch_sk_tm(const float* x, int ldx, const float* rs, const float* nw, const int8_t* q,
+                  const float* sc, float* part, int ldp, int M, int NR, int K, int ks,
+                  hipStream_t st) {
+    if (M <= 16)
+        launch_sk<1, RS, NORM, DEFER>(x, ldx, rs, nw, q, sc, part, ldp, M, NR, K, ks, st);
+    else if (M <= 32)
+        launch_sk<2, RS, NORM, DEFER>(x, ldx, rs, nw, q, sc, part, ldp, M, NR, K, ks, st);
+    else
+        launch_sk<4, RS, NORM, DEFER>(x, ldx, rs, nw, q, sc, part, ldp, M, NR, K, ks, st);
+}
+
+template <int EPI, bool NORM>
+void launch_reduce(const float* part, int ks, int M, int NR, int N, float* y, int ldy,
+                   const float* x, int ldx, int K, float eps, hipStream_t st) {
+    const dim3 grid((N + kThreads - 1) / kThreads, M);
+    hipLaunchKernelGGL((k_mm_reduce<EPI, NORM>), grid, dim3(kThreads), 0, st, part, ks, M, NR, N,
+                       y, ldy, x, ldx, K, eps);
 }
 
 template <int WM, int WN, int WK, int TM, int TN, bool RS, int EPI, bool NORM>
@@ -610,7 +655,7 @@ int launch_mm(const float* x, int ldx, const float* rs, const float* nw, const i
 }
 
 template <bool RS, bool NORM>
-int mm_run(const float* x, int ldx, const float* rs, const float* nw, const int8_t* q,
+int mm_run(const float* x, int ldx, float* rs, const float* nw, float eps, const int8_t* q,
            const float* sc, float* y, int ldy, int M, int N, int K, int epi, float* part,
            hipStream_t st) {
     if (use_sk(M, K)) {
@@ -619,25 +664,31 @@ int mm_run(const float* x, int ldx, const float* rs, const float* nw, const int8
         const bool direct = ks == 1 && epi == EPI_STORE;
         float* dst = direct ? y : part;
         const int ldp = direct ? ldy : NR;
-        if (M <= 16)
-            launch_sk<1, RS, NORM>(x, ldx, rs, nw, q, sc, dst, ldp, M, NR, K, ks, st);
-        else if (M <= 32)
-            launch_sk<2, RS, NORM>(x, ldx, rs, nw, q, sc, dst, ldp, M, NR, K, ks, st);
-        else
-            launch_sk<4, RS, NORM>(x, ldx, rs, nw, q, sc, dst, ldp, M, NR, K, ks, st);
+        if (direct) {  // the matmul writes y itself: row scales first
+            if constexpr (NORM) {
+                hipLaunchKernelGGL(k_row_rs, dim3(M), dim3(kThreads), 0, st, x, ldx, K, eps, rs);
+                const int rc = qlm_launch_status();
+                if (rc != QLM_OK) return rc;
+            }
+            launch_sk_tm<RS, NORM, false>(x, ldx, rs, nw, q, sc, dst, ldp, M, NR, K, ks, st);
+            return qlm_launch_status();
+        }
+        // row scales folded into the reduction (no separate launch)
+        launch_sk_tm<RS, NORM, NORM>(x, ldx, rs, nw, q, sc, dst, ldp, M, NR, K, ks, st);
         int rc = qlm_launch_status();
-        if (rc != QLM_OK || direct) return rc;
-        const int blocks = (M * N + kThreads - 1) / kThreads;
+        if (rc != QLM_OK) return rc;
         if (epi == EPI_STORE)
-            hipLaunchKernelGGL(k_mm_reduce<EPI_STORE>, dim3(blocks), dim3(kThreads), 0, st, part, ks,
-                               M, NR, N, y, ldy);
+            launch_reduce<EPI_STORE, NORM>(part, ks, M, NR, N, y, ldy, x, ldx, K, eps, st);
         else if (epi == EPI_RESID)
-            hipLaunchKernelGGL(k_mm_reduce<EPI_RESID>, dim3(blocks), dim3(kThreads), 0, st, part, ks,
-                               M, NR, N, y, ldy);
+            launch_reduce<EPI_RESID, false>(part, ks, M, NR, N, y, ldy, x, ldx, K, eps, st);
         else
-            hipLaunchKernelGGL(k_mm_reduce<EPI_SWIGLU>, dim3(blocks), dim3(kThreads), 0, st, part,
-                               ks, M, NR, N, y, ldy);
+            launch_reduce<EPI_SWIGLU, NORM>(part, ks, M, NR, N, y, ldy, x, ldx, K, eps, st);
         return qlm_launch_status();
+    }
+    if constexpr (NORM) {
+        hipLaunchKernelGGL(k_row_rs, dim3(M), dim3(kThreads), 0, st, x, ldx, K, eps, rs);
+        const int rc = qlm_launch_status();
+        if (rc != QLM_OK) return rc;
     }
     if (epi == EPI_STORE)
         return launch_mm<2, 2, 1, 4, 4, RS, EPI_STORE, NORM>(x, ldx, rs, nw, q, sc, y, ldy, M, N, K, st);
@@ -671,17 +722,13 @@ extern "C" int qlm_matmul_i8(const float* x, int ldx, const float* norm_w, float
     hipStream_t st = as_stream(stream);
     float* rs = reinterpret_cast<float*>(work);
     float* part = reinterpret_cast<float*>(reinterpret_cast<char*>(work) + align256((size_t)M * 4));
-    if (norm_w) {
-        hipLaunchKernelGGL(k_row_rs, dim3(M), dim3(kThreads), 0, st, x, ldx, K, eps, rs);
-        const int rc = qlm_launch_status();
-        if (rc != QLM_OK) return rc;
-        return rowscale ? mm_run<true, true>(x, ldx, rs, norm_w, q, scales, y, ldy, M, N, K,
+    if (norm_w)
+        return rowscale ? mm_run<true, true>(x, ldx, rs, norm_w, eps, q, scales, y, ldy, M, N, K,
                                              epilogue, part, st)
-                        : mm_run<false, true>(x, ldx, rs, norm_w, q, scales, y, ldy, M, N, K,
-                                              epilogue, part, st);
-    }
-    return rowscale ? mm_run<true, false>(x, ldx, nullptr, nullptr, q, scales, y, ldy, M, N, K,
-                                          epilogue, part, st)
-                    : mm_run<false, false>(x, ldx, nullptr, nullptr, q, scales, y, ldy, M, N, K,
-                                           epilogue, part, st);
+                        : mm_run<false, true>(x, ldx, rs, norm_w, eps, q, scales, y, ldy, M, N,
+                                              K, epilogue, part, st);
+    return rowscale ? mm_run<true, false>(x, ldx, nullptr, nullptr, eps, q, scales, y, ldy, M, N,
+                                          K, epilogue, part, st)
+                    : mm_run<false, false>(x, ldx, nullptr, nullptr, eps, q, scales, y, ldy, M, N,
+                                           K, epilogue, part, st);
 }
