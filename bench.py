@@ -286,6 +286,8 @@ def main():
     ap.add_argument("--skip-gemv", action="store_true")
     ap.add_argument("--skip-int4", action="store_true",
                     help="skip the batch-1 decode at --precision int4")
+    ap.add_argument("--skip-native", action="store_true",
+                    help="skip the batch-1 decode at --precision bf16 (weights as stored)")
     ap.add_argument("--skip-row", action="store_true",
                     help="skip the batch-1 decode with one scale per output row (int8_row)")
     ap.add_argument("--model-dir", default=None)
@@ -384,6 +386,16 @@ def main():
             e4.close()
             log(f"batch 1, int4 weights: {r4['tok_s']:.1f} tok/s "
                 f"({r4['ms_per_step']:.3f} ms/step), {r4['weight_bytes'] / 1e9:.3f} GB")
+        rn = None
+        if not args.skip_native:
+            # the same checkpoint at --precision bf16, the reference's default:
+            # linears as stored (bf16), tied lm_head = the fp32 embedding table
+            en = Engine(mdir, max_seq_len=max_seq, max_batch=1, precision="bf16")
+            rn = run_decode(en, prompts[:1], args.warmup, args.steps, graph)
+            rn["weight_bytes"] = en.weight_bytes
+            en.close()
+            log(f"batch 1, native weights: {rn['tok_s']:.1f} tok/s "
+                f"({rn['ms_per_step']:.3f} ms/step), {rn['weight_bytes'] / 1e9:.3f} GB")
     finally:
         if own_dir:
             import shutil
@@ -436,6 +448,13 @@ def main():
             "frac_of_weight_roofline": round(
                 r4["weight_bytes"] / (r4["ms_per_step"] / 1000.0) / 1e9 / HBM_PEAK_GBS, 4),
             "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / r4["weight_bytes"], 1)},
+        "native": None if rn is None else {
+            "tok_s": round(rn["tok_s"], 2), "ms_per_step": round(rn["ms_per_step"], 4),
+            "batch": 1, "precision": "bf16 (weights as stored: bf16 linears, fp32 tied lm_head)",
+            "weight_bytes": rn["weight_bytes"],
+            "frac_of_weight_roofline": round(
+                rn["weight_bytes"] / (rn["ms_per_step"] / 1000.0) / 1e9 / HBM_PEAK_GBS, 4),
+            "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / rn["weight_bytes"], 1)},
         "gemv": gemv,
     })
     traffic, traffic_src = None, None

@@ -380,6 +380,24 @@ int qlm_lm_head_greedy_mx4(const float* x, const float* norm_w, float eps,
                            const int* prompt_len, const float* embed, int H, float* h_next,
                            void* stream);
 
+/* ---- native (unquantised) weights (reference --precision bf16) -------------
+ * The reference keeps each weight in its checkpoint dtype under its default
+ * precision (get_tensor_keep_bf16, safetensors.cpp:248-273): bf16 rows for
+ * BF16 tensors, fp32 rows for F32 ones, and math::matmul takes fp32 dot
+ * products against them (dot_avx2 / bf16_gemv_range, math_ops.cpp:209-400,
+ * :820-900). Replaces those branches: y = x . W^T on the fp32 matrix cores
+ * (bf16 widened exactly), fp32 accumulation. W [N, K] row-major fp32
+ * (w_bf16 = 0) or bf16 bits (w_bf16 = 1); x [M, ldx], y [M, ldy], any M (16
+ * rows per launch). norm_w / epilogue as qlm_matmul_i8 (RMSNorm prologue:
+ * the row scale multiplies the finished sums; SwiGLU: W is [2N, K], gate
+ * rows then up rows; it needs norm_w); work holds
+ * qlm_matmul_w_workspace_bytes(K) bytes when norm_w is given. K a multiple
+ * of 16; x, W, norm_w 16-byte aligned. */
+size_t qlm_matmul_w_workspace_bytes(int K);
+int qlm_matmul_w(const float* x, int ldx, const float* norm_w, float eps, const void* w,
+                 int w_bf16, float* y, int ldy, int M, int N, int K, int epilogue, void* work,
+                 size_t work_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -101,6 +101,15 @@ class Oracle:
         self.lib.orc_matmul_i4(_p(A), _i(M), _i(K), _p(p), _p(s), _i(N), _p(out), _i(N))
         return out
 
+    def matmul_w(self, A: np.ndarray, W: np.ndarray) -> np.ndarray:
+        """Native weights W [N, K]: float32, or uint16 bf16 bits."""
+        M, K = A.shape
+        N = W.shape[0]
+        out = np.empty((M, N), np.float32)
+        self.lib.orc_matmul_w(_p(A), _i(M), _i(K), _p(np.ascontiguousarray(W)),
+                              _i(1 if W.dtype == np.uint16 else 0), _i(N), _p(out), _i(N))
+        return out
+
     def sumsq(self, x: np.ndarray) -> float:
         return float(self.lib.orc_sumsq(_p(x), _i(x.size)))
 
@@ -246,6 +255,14 @@ class Reference:
         N = p.shape[0]
         out = np.empty((M, N), np.float32)
         self.lib.qref_matmul_i4(_p(A), _i(M), _i(K), _p(p), _p(s), _i(N), _p(out), _i(N))
+        return out
+
+    def matmul_w(self, A, W):
+        M, K = A.shape
+        N = W.shape[0]
+        out = np.empty((M, N), np.float32)
+        self.lib.qref_matmul_w(_p(A), _i(M), _i(K), _p(np.ascontiguousarray(W)),
+                               _i(1 if W.dtype == np.uint16 else 0), _i(N), _p(out), _i(N))
         return out
 
     def sumsq(self, x):

@@ -204,6 +204,68 @@ void orc_matmul_i4(const float* A, int M, int K, const uint8_t* p, const float* 
     }
 }
 
+/* ---- native weights (--precision bf16: checkpoint dtype kept) ------------
+ * fp32 rows: dot_avx2 (math_ops.cpp:209-240), four 8-lane FMA accumulators
+ * over 32-column steps, whole 8-column chunks into the first, then
+ * (a0+a1)+(a2+a3), hsum8, and a scalar multiply-add tail.
+ * bf16 rows: dot_avx2_bf16 / dot8 / dot4 (:245-400, bit-identical per row),
+ * two accumulators over 16-column steps (exact bf16 -> fp32 upcast), whole 8-
+ * column chunks into the first, a0+a1, hsum8, scalar tail. */
+static float bf16_f(uint16_t b) {
+    const uint32_t bits = (uint32_t)b << 16;
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+static float dot_f32w(const float* a, const float* b, int K) {
+    float acc[4][8];
+    memset(acc, 0, sizeof(acc));
+    int k = 0;
+    for (; k + 32 <= K; k += 32)
+        for (int c = 0; c < 4; ++c)
+            for (int l = 0; l < 8; ++l)
+                acc[c][l] = fmaf(a[k + 8 * c + l], b[k + 8 * c + l], acc[c][l]);
+    for (; k + 8 <= K; k += 8)
+        for (int l = 0; l < 8; ++l) acc[0][l] = fmaf(a[k + l], b[k + l], acc[0][l]);
+    float s[8];
+    for (int l = 0; l < 8; ++l) s[l] = (acc[0][l] + acc[1][l]) + (acc[2][l] + acc[3][l]);
+    float r = hsum8(s);
+    for (; k < K; ++k) r += a[k] * b[k];
+    return r;
+}
+
+static float dot_bf16w(const float* a, const uint16_t* b, int K) {
+    float lo[8], hi[8];
+    memset(lo, 0, sizeof(lo));
+    memset(hi, 0, sizeof(hi));
+    int k = 0;
+    for (; k + 16 <= K; k += 16)
+        for (int l = 0; l < 8; ++l) {
+            lo[l] = fmaf(a[k + l], bf16_f(b[k + l]), lo[l]);
+            hi[l] = fmaf(a[k + 8 + l], bf16_f(b[k + 8 + l]), hi[l]);
+        }
+    for (; k + 8 <= K; k += 8)
+        for (int l = 0; l < 8; ++l) lo[l] = fmaf(a[k + l], bf16_f(b[k + l]), lo[l]);
+    float s[8];
+    for (int l = 0; l < 8; ++l) s[l] = lo[l] + hi[l];
+    float r = hsum8(s);
+    for (; k < K; ++k) r += a[k] * bf16_f(b[k]);
+    return r;
+}
+
+/* C[m, n] = dot(A[m], W[n]); W fp32 (bf16 = 0) or bf16 bits (bf16 = 1). */
+void orc_matmul_w(const float* A, int M, int K, const void* W, int bf16, int N, float* C,
+                  int ldc) {
+    for (int m = 0; m < M; ++m) {
+#pragma omp parallel for schedule(static) num_threads(g_threads)
+        for (int n = 0; n < N; ++n)
+            C[(size_t)m * ldc + n] =
+                bf16 ? dot_bf16w(A + (size_t)m * K, (const uint16_t*)W + (size_t)n * K, K)
+                     : dot_f32w(A + (size_t)m * K, (const float*)W + (size_t)n * K, K);
+    }
+}
+
 /* ---- A5/A6: norms (math_ops.cpp:990-1072, :1133-1172) --------------------- */
 
 float orc_sumsq(const float* x, int n) {

@@ -35,6 +35,12 @@ void orc_unpack_q4(const uint8_t* p, int rows, int K, int8_t* q);
 void orc_matmul_i4(const float* A, int M, int K, const uint8_t* p, const float* s, int N,
                    float* C, int ldc);
 
+/* Native (unquantised) weights, the reference's --precision bf16: fp32 rows
+ * (dot_avx2, math_ops.cpp:209-240) or bf16 rows (dot_avx2_bf16, :245-400).
+ * W is [N, K]; bf16 = 1 for bf16 bits. C is [M, ldc]. */
+void orc_matmul_w(const float* A, int M, int K, const void* W, int bf16, int N, float* C,
+                  int ldc);
+
 /* A3/A4 int8 matmul (math_ops.cpp:405-579, :820-900). C is [M, ldc]. */
 void orc_matmul_i8(const float* A, int M, int K, const int8_t* q, const float* s, int group,
                    int N, float* C, int ldc);

@@ -106,6 +106,23 @@ void qref_matmul_i4(const float* A, int M, int K, const uint8_t* q, const float*
     math::matmul(a, b, c, true);
 }
 
+// math::matmul over native weights (math_ops.cpp:820-900): fp32 rows
+// (dot_avx2) or bf16 rows (bf16_gemv_range). C is [M, ldc].
+void qref_matmul_w(const float* A, int M, int K, const void* W, int bf16, int N, float* C,
+                   int ldc) {
+    Tensor a({M, K}, const_cast<float*>(A));
+    Tensor b;
+    b.shape = {N, K};
+    b.compute_strides();
+    if (bf16)
+        b.bf16_data = static_cast<const uint16_t*>(W);
+    else
+        b.data = const_cast<float*>(static_cast<const float*>(W));
+    Tensor c({M, N}, C);
+    c.strides = {ldc, 1};
+    math::matmul(a, b, c, true);
+}
+
 // A3/A4: math::matmul int8 branch (math_ops.cpp:820-900). C is [M, ldc].
 void qref_matmul_i8(const float* A, int M, int K, const int8_t* q, const float* s, int N,
                     float* C, int ldc) {

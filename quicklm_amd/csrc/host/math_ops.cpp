@@ -23,8 +23,17 @@ void need(bool ok, const char* what) {
 }
 
 void check_int8(const Tensor& B) {
-    need(B.is_int8(), "weight operand must be int8 on the device (bf16/int4 forms are not built)");
+    need(B.is_int8(), "weight operand must be int8 (or int4 unpacked) on the device");
     need(B.shape.size() == 2, "int8 weight must be [N, K]");
+}
+
+// Native (fp32 / bf16) weights: qlm_matmul_w for every M and epilogue.
+void matmul_native(const Tensor& A, const float* norm_w, float eps, const Tensor& B, float* C,
+                   int64_t ldc, int64_t N, int epilogue) {
+    check(qlm_matmul_w(A.data, (int)A.row_stride(), norm_w, eps, B.native_data,
+                       B.native_bf16 ? 1 : 0, C, (int)ldc, (int)A.rows(), (int)N, (int)A.cols(),
+                       epilogue, g_mm_work, g_mm_work_bytes, g_stream),
+          "qlm_matmul_w");
 }
 }  // namespace
 
@@ -32,7 +41,8 @@ bool use_tiles_batched(int64_t M, int64_t N, int64_t K) {
     return M >= 2 && M <= 8 && (N >= 4096 || K <= 2048);
 }
 
-int matmul_launches(int64_t M, int64_t N, int64_t K, bool norm) {
+int matmul_launches(int64_t M, int64_t N, int64_t K, bool norm, bool native) {
+    if (native) return (int)((M + 15) / 16) * (norm ? 2 : 1);  // row prep + matmul per 16 rows
     if (M == 1) return 1;
     if (use_tiles_batched(M, N, K)) return 2;  // digits + matmul
     if (M < kMfmaMinRows) return (int)((M + 3) / 4);
@@ -102,10 +112,11 @@ void matmul_mfma(const Tensor& A, const float* norm_w, float eps, const Tensor& 
 
 void matmul(const Tensor& A, const Tensor& B, Tensor& C, bool transpose_B) {
     need(transpose_B, "only the x * W^T form exists on the device");
-    check_int8(B);
     const int64_t K = A.cols(), M = A.rows(), N = B.shape[0];
     need(B.shape[1] == K, "matmul: K mismatch");
     need(C.cols() >= N || C.row_stride() >= N, "matmul: output too small");
+    if (B.is_native()) return matmul_native(A, nullptr, 0.0f, B, C.data, C.row_stride(), N, 0);
+    check_int8(B);
     if (gemm_tiles(A, nullptr, 0.0f, B, C.data, C.row_stride(), N, 0)) return;
     if (M >= kMfmaMinRows) {
         matmul_mfma(A, nullptr, 0.0f, B, C.data, C.row_stride(), N, 0);
@@ -118,9 +129,10 @@ void matmul(const Tensor& A, const Tensor& B, Tensor& C, bool transpose_B) {
 }
 
 void matmul_rmsnorm(const Tensor& A, const Tensor& norm_w, float eps, const Tensor& B, Tensor& C) {
-    check_int8(B);
     const int64_t K = A.cols(), M = A.rows(), N = B.shape[0];
     need(B.shape[1] == K && norm_w.size() == K, "matmul_rmsnorm: K mismatch");
+    if (B.is_native()) return matmul_native(A, norm_w.data, eps, B, C.data, C.row_stride(), N, 0);
+    check_int8(B);
     if (gemm_tiles(A, norm_w.data, eps, B, C.data, C.row_stride(), N, 0)) return;
     if (M >= kMfmaMinRows) {
         matmul_mfma(A, norm_w.data, eps, B, C.data, C.row_stride(), N, 0);
@@ -134,9 +146,11 @@ void matmul_rmsnorm(const Tensor& A, const Tensor& norm_w, float eps, const Tens
 }
 
 void matmul_residual(const Tensor& A, const Tensor& B, Tensor& residual) {
-    check_int8(B);
     const int64_t K = A.cols(), M = A.rows(), N = B.shape[0];
     need(B.shape[1] == K && residual.cols() == N, "matmul_residual: shape mismatch");
+    if (B.is_native())
+        return matmul_native(A, nullptr, 0.0f, B, residual.data, residual.row_stride(), N, 1);
+    check_int8(B);
     if (gemm_tiles(A, nullptr, 0.0f, B, residual.data, residual.row_stride(), N, 1)) return;
     if (M >= kMfmaMinRows) {
         matmul_mfma(A, nullptr, 0.0f, B, residual.data, residual.row_stride(), N, 1);
@@ -151,9 +165,10 @@ void matmul_residual(const Tensor& A, const Tensor& B, Tensor& residual) {
 
 void matmul_swiglu_rmsnorm(const Tensor& A, const Tensor& norm_w, float eps, const Tensor& B,
                            Tensor& C) {
-    check_int8(B);
     const int64_t K = A.cols(), M = A.rows(), F = B.shape[0] / 2;
     need(B.shape[0] % 2 == 0 && B.shape[1] == K && C.cols() == F, "matmul_swiglu: shape mismatch");
+    if (B.is_native()) return matmul_native(A, norm_w.data, eps, B, C.data, C.row_stride(), F, 2);
+    check_int8(B);
     if (gemm_tiles(A, norm_w.data, eps, B, C.data, C.row_stride(), F, 2)) return;
     if (M >= kMfmaMinRows) {
         matmul_mfma(A, norm_w.data, eps, B, C.data, C.row_stride(), F, 2);

@@ -28,7 +28,7 @@ void set_matmul_workspace(void* p, size_t bytes);
 // take the int8 matrix-core batched form, and the kernel launches one
 // matmul call makes (for launch counts).
 bool use_tiles_batched(int64_t M, int64_t N, int64_t K);
-int matmul_launches(int64_t M, int64_t N, int64_t K, bool norm);
+int matmul_launches(int64_t M, int64_t N, int64_t K, bool norm, bool native = false);
 
 // math_ops.hpp:102 / :139-140 / :132.
 void rms_norm(const Tensor& input, const Tensor& weight, Tensor& output, float eps);

@@ -49,6 +49,7 @@ void DecoderModel::alloc_linear(LinearI8& lin, int N, int K) {
     lin.N = N;
     lin.K = K;
     lin.group = (group_ == 0) ? K : group_;
+    if (native_) return;  // sized by the first tensor's dtype (quantize_into)
     lin.q.alloc((size_t)N * K);
     lin.s.alloc((size_t)N * lin.blocks_per_row() * sizeof(float));
     // bytes a one-row step streams: int8 values, or the int4 copy
@@ -71,6 +72,23 @@ void DecoderModel::quantize_into(LinearI8& lin, int row_off, const std::string& 
     if (t.dtype != "F32" && t.dtype != "BF16")
         throw std::runtime_error("Unsupported tensor datatype for '" + name + "': " + t.dtype +
                                  " (only F32 and BF16 supported for int8 quantization)");
+    if (native_) {  // get_tensor_keep_bf16 / get_tensor (safetensors.cpp:248-273): dtype kept
+        const int dt = t.dtype == "BF16" ? 2 : 1;
+        const size_t elt = dt == 2 ? 2 : 4;
+        if (!lin.wdtype) {
+            lin.wdtype = dt;
+            lin.w.alloc((size_t)lin.N * lin.K * elt);
+            weight_bytes_ += (size_t)lin.N * lin.K * elt;
+        } else if (lin.wdtype != dt) {
+            throw std::runtime_error("weight '" + name + "' mixes F32 and BF16 with the rows it "
+                                     "is stacked with");
+        }
+        check(qlm_memcpy_h2d(static_cast<char*>(lin.w.get()) + (size_t)row_off * lin.K * elt,
+                             t.data, t.nbytes, stream_),
+              "upload");
+        check(qlm_stream_sync(stream_), "sync");  // the mapped source may be unmapped later
+        return;
+    }
     if (staging_.bytes() < t.nbytes) {
         check(qlm_stream_sync(stream_), "sync");
         staging_.alloc(t.nbytes);
@@ -101,6 +119,7 @@ void DecoderModel::quantize_into(LinearI8& lin, int row_off, const std::string& 
 // where K is not a multiple of 64 (the row-major GEMV serves those).
 void DecoderModel::tile_linear(LinearI8& lin, int halves) {
     size_t qb = 0, sb = 0;
+    if (native_) return;
     if (lin.K % 64 != 0 || lin.N % halves != 0) return;
     const int rows = lin.N / halves;
     check(qlm_mx_layout_bytes(rows, lin.K, lin.group, halves, &qb, &sb), "tile layout");
@@ -134,10 +153,11 @@ void DecoderModel::load(const std::string& dir, int max_seq_len, const std::stri
                         int max_batch) {
     if (max_seq_len <= 0 || max_batch <= 0) throw std::runtime_error("load: bad sizes");
     int4_ = precision == "int4";
-    if (precision == "int8" || int4_) group_ = 32;
+    native_ = precision == "bf16";  // the reference's default: weights as stored
+    if (precision == "int8" || int4_ || native_) group_ = 32;
     else if (precision == "int8_row") group_ = 0;  // resolved per matrix to K
     else
-        throw std::runtime_error("load: precision must be int8, int8_row or int4, got " +
+        throw std::runtime_error("load: precision must be int8, int8_row, int4 or bf16, got " +
                                  precision);
     cfg_ = parse_model_config(dir);
     ws_ = std::make_unique<WeightStore>(dir);
@@ -234,7 +254,9 @@ void DecoderModel::load(const std::string& dir, int max_seq_len, const std::stri
         quantize_into(lm_head_, 0, "lm_head.weight");
     } else {
         alloc_linear(lm_head_, V, H);
-        if (int4_)
+        if (native_)  // tied: the embedding table itself, in its stored dtype
+            quantize_into(lm_head_, 0, "model.embed_tokens.weight");
+        else if (int4_)
             check(qlm_quantize_q4_f32(embed_.get<float>(), V, H, lm_head_.q4.get<uint8_t>(),
                                       lm_head_.s.get<float>(), lm_head_.q.get<int8_t>(), stream_),
                   "quantize lm_head");
@@ -338,8 +360,8 @@ void DecoderModel::enqueue_step(int B) {
             core.strides = {CORE_, 1};
             math::matmul_residual(core, w.dn_out.view(), hx);
             ++dn_i;
-            n += math::matmul_launches(B, PD_, H, true) + 1 +
-                 math::matmul_launches(B, H, HD_, false);
+            n += math::matmul_launches(B, PD_, H, true, native_) + 1 +
+                 math::matmul_launches(B, H, HD_, false, native_);
         } else {
             Tensor proj({B, PQ_}, proj_.get<float>());
             proj.strides = {Pmax, 1};
@@ -355,18 +377,19 @@ void DecoderModel::enqueue_step(int B) {
             core.strides = {CORE_, 1};
             math::matmul_residual(core, w.at_o.view(), hx);
             ++at_i;
-            n += math::matmul_launches(B, PQ_, H, true) + 2 +  // + attention, combine
-                 math::matmul_launches(B, H, nq * hd, false);
+            n += math::matmul_launches(B, PQ_, H, true, native_) + 2 +  // + attention, combine
+                 math::matmul_launches(B, H, nq * hd, false, native_);
         }
         Tensor act({B, F}, act_.get<float>());
         math::matmul_swiglu_rmsnorm(hx, post_ln, eps, w.gate_up.view(), act);
         math::matmul_residual(act, w.down.view(), hx);
-        n += math::matmul_launches(B, F, H, true) + math::matmul_launches(B, H, F, false);
+        n += math::matmul_launches(B, F, H, true, native_) +
+             math::matmul_launches(B, H, F, false, native_);
     }
     // Step tail: final norm + lm_head + greedy sample + advance, then the
     // embedding of the token now at pos (the next step's input, or the next
     // prompt token) -- model.cpp:193-199, :263-274, :157-164.
-    if (B == 1) {
+    if (B == 1 && !native_) {
         const Tensor lm = lm_head_.view();
         int rc = QLM_ERR_SHAPE;
         if (lm.int4_tiles)
@@ -399,7 +422,7 @@ void DecoderModel::enqueue_step(int B) {
                                  prompt_len_.get<int>(), stream_),
               "argmax");
         embed_current(B);
-        n += math::matmul_launches(B, V, H, true) + 3;  // + argmax (two passes), embedding
+        n += math::matmul_launches(B, V, H, true, native_) + 3;  // + argmax (two passes), embedding
     }
     kernels_per_step_ = n;
 }
@@ -494,6 +517,7 @@ size_t DecoderModel::matmul_workspace(int M) const {
     auto upd = [&](int N, int K, int epi) {
         b = std::max(b, qlm_matmul_i8_workspace_bytes(M, N, K, epi));
         if (M <= 16) b = std::max(b, qlm_matmul_i8_mx_workspace_bytes(M, K));
+        b = std::max(b, qlm_matmul_w_workspace_bytes(K));
     };
     if (PD_ > 0) {
         upd(PD_, H, 0);

@@ -38,7 +38,18 @@ struct LinearI8 {
     // int4 models: packed rows [N, K/2] as quantised (q then holds their
     // unpacked values) and the int4 tile-major copy (scales: sz)
     DeviceBuffer q4, qz4;
+    // native-precision models: the rows as stored (fp32 or bf16), no int8
+    DeviceBuffer w;
+    int wdtype = 0;  // 0 int8 forms, 1 fp32, 2 bf16
     Tensor view() const {
+        if (wdtype) {
+            Tensor t;
+            t.shape = {N, K};
+            t.compute_strides();
+            t.native_data = w.get();
+            t.native_bf16 = wdtype == 2;
+            return t;
+        }
         Tensor t = Tensor::int8(q.get<int8_t>(), s.get<float>(), N, K, group);
         if (qz.bytes()) {
             t.int8_tiles = qz.get<int8_t>();
@@ -141,6 +152,7 @@ class DecoderModel {
     std::unique_ptr<WeightStore> ws_;
     int max_seq_ = 0, max_batch_ = 0, group_ = 32;
     bool int4_ = false;  // --precision int4: Q4_0 weights (lm_head included)
+    bool native_ = false;  // --precision bf16: weights kept in the checkpoint dtype
     int HD_ = 0, PD_ = 0, QR_ = 0, PQ_ = 0, CORE_ = 0;
     size_t weight_bytes_ = 0;
     int kernels_per_step_ = 0;

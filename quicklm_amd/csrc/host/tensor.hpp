@@ -29,6 +29,10 @@ struct Tensor {
     // this is their int4 tile-major copy (qlm_mx4_swizzle, scales as above),
     // which the one-row GEMV streams at half the bytes.
     const uint8_t* int4_tiles = nullptr;
+    // Native (unquantised) weights, the reference's --precision bf16: fp32
+    // rows (F32 checkpoint tensors) or bf16 rows (BF16 ones); no int8 form.
+    const void* native_data = nullptr;
+    bool native_bf16 = false;
 
     Tensor() = default;
     Tensor(std::vector<int64_t> shp, float* d) : shape(std::move(shp)), data(d) { compute_strides(); }
@@ -44,6 +48,7 @@ struct Tensor {
     }
 
     bool is_int8() const { return int8_data != nullptr; }
+    bool is_native() const { return native_data != nullptr; }
 
     void compute_strides() {
         strides.assign(shape.size(), 1);

@@ -15,7 +15,9 @@ plus the same stream from the reference's own -O3 -ffast-math build
 (tokens_fast) for the record; and tiny_greedy_int4.npz, the IEEE build's
 run of the same prompt at --precision int4 (prompt, tokens, top_idx,
 top_val, margin, logits0_head). Usage: python tests/golden/make_golden.py
-[--int4 (the int4 fixture only)]
+[--int4 | --native (those fixtures only)]; tiny_greedy_native.npz and
+micro_greedy_native.npz are the --precision bf16 runs (weights in their
+checkpoint dtype: fp32 for the tiny model, bf16 for the micro one).
 """
 import hashlib
 import os
@@ -60,7 +62,39 @@ def int4_stream(d, prompt):
     print("wrote", out)
 
 
+def native_streams():
+    """--precision bf16 (the reference's default: weights in their checkpoint
+    dtype), IEEE build: the tiny model (F32 linears: fp32 weights) ->
+    tiny_greedy_native.npz; the micro model (BF16 linears: bf16 weights) ->
+    micro_greedy_native.npz."""
+    here = os.path.dirname(os.path.abspath(__file__))
+    for cfg, n_prompt, n_new, vocab in (("tiny", 128, 64, None), ("micro", 24, 32, 4096)):
+        with tempfile.TemporaryDirectory() as d:
+            synth.write_model(d, cfg)
+            prompt = (synth.prompt_tokens(n_prompt, seed=0)[0] if vocab is None else
+                      synth.prompt_tokens(n_prompt, seed=0, vocab=vocab)[0])
+            ref = Reference("ieee")
+            ref.init_threads(os.cpu_count() or 1)
+            m = ref.load_model(d, 2048, "bf16")
+            toks, pre, dec, lg = m.generate(prompt, n_new, keep_logits=True)
+            print(f"{cfg} native ieee: prefill {pre:.2f}s decode {dec:.2f}s tokens {toks[:8]}...",
+                  flush=True)
+            order = np.argsort(-lg, axis=1, kind="stable")[:, :32]
+            top_val = np.take_along_axis(lg, order, axis=1)
+            out = os.path.join(here, f"{cfg}_greedy_native.npz")
+            np.savez_compressed(
+                out, prompt=prompt.astype(np.int32), tokens=toks.astype(np.int32),
+                top_idx=order.astype(np.int32), top_val=top_val.astype(np.float32),
+                margin=(top_val[:, 0] - top_val[:, 1]),
+                logits0_head=lg[0, :4096].copy())
+            print("wrote", out)
+            del m
+
+
 def main():
+    if "--native" in sys.argv:  # only the native-precision fixtures
+        native_streams()
+        return
     if "--int4" in sys.argv:  # only the int4 fixture
         with tempfile.TemporaryDirectory() as d:
             synth.write_model(d, "tiny")
@@ -92,6 +126,7 @@ def main():
             tensor_names=np.array(SHA_TENSORS), tensor_sha=np.array(
                 [tensor_sha(d)[n] for n in SHA_TENSORS]))
         int4_stream(d, prompt)
+    native_streams()
     print("wrote", out, "fast==ieee tokens:", bool(np.array_equal(res["fast"][0], toks)))
 
 

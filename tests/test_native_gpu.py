@@ -1,0 +1,100 @@
+"""Native (unquantised) weights on the GPU (reference --precision bf16).
+
+qlm_matmul_w against the oracle's fp32 dot products over fp32 or bf16 rows
+(orc_matmul_w, itself bit-exact with the reference's dot_avx2 /
+dot_avx2_bf16, tests/test_oracle.py). The summation order differs (matrix
+cores, 16-row tiles split over waves), so the bar is fp32 rounding: 1e-5
+normwise per call.
+"""
+
+import numpy as np
+import pytest
+
+from tests.util import bf16_bits, rel_err, say
+
+pytestmark = pytest.mark.gpu
+
+EPI = {"store": 0, "norm": 0, "resid": 1, "swiglu": 2}
+TOL = 1e-5
+
+
+def dev(hip, a):
+    return hip.DeviceBuffer.from_numpy(np.ascontiguousarray(a))
+
+
+def _ref(orc, epi, x, w, nw, y0, N, eps):
+    if epi == "store":
+        return orc.matmul_w(x, w)
+    if epi == "resid":
+        return y0 + orc.matmul_w(x, w)
+    lg = orc.matmul_w(orc.rms_norm(x, nw, eps), w)
+    return lg if epi == "norm" else orc.silu_mul(lg[:, :N].copy(), lg[:, N:].copy())
+
+
+def _run(hip, epi, x, ldx, w, nw, y0, ldy, M, N, K, eps):
+    """x [M, ldx] and y [M, ldy] padded rows; returns y's first N columns."""
+    xp = np.zeros((M, ldx), np.float32)
+    xp[:, :K] = x
+    yp = np.full((M, ldy), 7.0, np.float32)
+    yp[:, :N] = y0
+    dx, dy, dw = dev(hip, xp), dev(hip, yp), dev(hip, w)
+    dnw = dev(hip, nw) if epi in ("norm", "swiglu") else None
+    wb = hip.lib().qlm_matmul_w_workspace_bytes(K)
+    work = hip.DeviceBuffer(wb) if dnw is not None else None
+    hip.call("qlm_matmul_w", dx, ldx, dnw, eps, dw, 1 if w.dtype == np.uint16 else 0, dy, ldy,
+             M, N, K, EPI[epi], work, wb if work is not None else 0, None)
+    got = dy.to_numpy((M, ldy), np.float32)
+    assert np.all(got[:, N:] == 7.0), "wrote past N"
+    return got[:, :N]
+
+
+CASES = [  # (M, N, K)
+    (1, 100, 256), (3, 37, 48), (16, 513, 1040), (20, 200, 2560), (1, 2560, 9728),
+    (5, 16, 16), (17, 1000, 512),
+]
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("epi", ["store", "norm", "resid", "swiglu"])
+def test_matmul_w(hip, orc, rng, dtype, epi):
+    eps = 1e-6
+    for M, N, K in CASES:
+        rows_w = 2 * N if epi == "swiglu" else N
+        w32 = (rng.standard_normal((rows_w, K)) * 0.02).astype(np.float32)
+        w = bf16_bits(w32) if dtype == "bf16" else w32
+        x = rng.standard_normal((M, K)).astype(np.float32)
+        nw = (rng.standard_normal(K) * 0.02).astype(np.float32)
+        y0 = rng.standard_normal((M, N)).astype(np.float32)
+        ldx, ldy = K + (4 if M > 1 else 0), N + (3 if M > 1 else 0)
+        say("matmul_w", dtype, epi, M, N, K)
+        got = _run(hip, epi, x, ldx, w, nw, y0, ldy, M, N, K, eps)
+        ref = _ref(orc, epi, x, w, nw, y0, N, eps)
+        for m in range(M):  # each activation row on its own scale
+            err = rel_err(got[m], ref[m])
+            assert err < TOL, (dtype, epi, M, N, K, m, err)
+
+
+def test_matmul_w_4b_shapes(hip, orc, rng):
+    """The 4B model's one-row projections with bf16 rows."""
+    for N, K, epi in [(9728, 2560, "swiglu"), (2560, 9728, "resid"), (8224, 2560, "norm")]:
+        rows_w = 2 * N if epi == "swiglu" else N
+        w = bf16_bits((rng.standard_normal((rows_w, K)) * 0.02).astype(np.float32))
+        x = rng.standard_normal((1, K)).astype(np.float32)
+        nw = (rng.standard_normal(K) * 0.02).astype(np.float32)
+        y0 = rng.standard_normal((1, N)).astype(np.float32)
+        say("matmul_w 4b", N, K, epi)
+        got = _run(hip, epi, x, K, w, nw, y0, N, 1, N, K, 1e-6)
+        assert rel_err(got, _ref(orc, epi, x, w, nw, y0, N, 1e-6)) < TOL
+
+
+def test_matmul_w_rejects_bad_args(hip):
+    d = hip.DeviceBuffer(1 << 16)
+    wb = hip.lib().qlm_matmul_w_workspace_bytes(64)
+    with pytest.raises(hip.HipError):  # K not a multiple of 16
+        hip.call("qlm_matmul_w", d, 40, None, 1e-6, d, 0, d, 8, 1, 8, 40, 0, None, 0, None)
+    with pytest.raises(hip.HipError):  # SwiGLU needs the fused norm
+        hip.call("qlm_matmul_w", d, 64, None, 1e-6, d, 0, d, 8, 1, 8, 64, 2, None, 0, None)
+    with pytest.raises(hip.HipError):  # norm without a workspace
+        hip.call("qlm_matmul_w", d, 64, d, 1e-6, d, 0, d, 8, 1, 8, 64, 0, None, 0, None)
+    with pytest.raises(hip.HipError):  # workspace too small
+        hip.call("qlm_matmul_w", d, 64, d, 1e-6, d, 0, d, 8, 1, 8, 64, 0, d, wb - 4, None)

@@ -201,7 +201,37 @@ def test_q4_matmul_vs_reference(orc, ref, rng, M, K):
     assert np.array_equal(bits(ref.matmul_i8(A, orc.unpack_q4(p, K), s)), bits(got))
 
 
+@needs_ref
+@pytest.mark.parametrize("M,K", [(1, 2560), (3, 1024), (2, 1000), (1, 3584), (2, 45)])
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_native_matmul_vs_reference(orc, ref, rng, M, K, dtype):
+    """Native (unquantised) weights: fp32 rows (dot_avx2) and bf16 rows
+    (dot_avx2_bf16), ragged K included."""
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    W = (rng.standard_normal((67, K)) * 0.02).astype(np.float32)
+    if dtype == "bf16":
+        W = (W.view(np.uint32) >> 16).astype(np.uint16)
+    assert np.array_equal(bits(orc.matmul_w(A, W)), bits(ref.matmul_w(A, W)))
+
+
 # ------------------------------------------------------------ 2. mathematics
+def test_native_matmul_exact_and_close(orc, rng):
+    """Integer activations and weights: every partial sum is exact, so fp32
+    and bf16 rows give the float64 product exactly; random inputs within
+    fp32 accumulation error of float64."""
+    K = 1000
+    x = rng.integers(-16, 17, (2, K)).astype(np.float32)
+    w = rng.integers(-100, 101, (30, K)).astype(np.float32)
+    want = x.astype(np.float64) @ w.astype(np.float64).T
+    assert np.array_equal(orc.matmul_w(x, w).astype(np.float64), want)
+    wb = (w.view(np.uint32) >> 16).astype(np.uint16)  # small integers are exact in bf16
+    assert np.array_equal(orc.matmul_w(x, wb).astype(np.float64), want)
+    xr = rng.standard_normal((2, K)).astype(np.float32)
+    wr = rng.standard_normal((30, K)).astype(np.float32)
+    ref = xr.astype(np.float64) @ wr.astype(np.float64).T
+    assert np.abs(orc.matmul_w(xr, wr) - ref).max() / np.abs(ref).max() < 1e-5
+
+
 def test_q4_quantizer_known_answers(orc):
     """Scale = max|x|/8 (1 for an all-zero block); exact multiples of the
     scale map to those integers, the positive maximum (8 scales) clamps to 7;
