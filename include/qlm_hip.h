@@ -397,6 +397,18 @@ size_t qlm_matmul_w_workspace_bytes(int K);
 int qlm_matmul_w(const float* x, int ldx, const float* norm_w, float eps, const void* w,
                  int w_bf16, float* y, int ldy, int M, int N, int K, int epilogue, void* work,
                  size_t work_bytes, void* stream);
+/* One activation row (M = 1) on the vector ALUs, which qlm_matmul_w uses for
+ * M = 1: x staged once per workgroup in LDS (times 1 + norm_w, with 1/rms,
+ * when norm_w is given; no workspace), each wave streaming 16-byte loads of
+ * rows_per_wave rows (both halves for SwiGLU) through a ring of `ring`
+ * items, the columns split over k_phases waves. Built shapes (waves,
+ * rows_per_wave, k_phases, ring): (4,1,1,4) (8,1,1,4) (4,2,1,3) (8,2,1,3)
+ * (4,4,1,2) (8,2,4,3) (8,1,4,4) (16,1,8,4); others return QLM_ERR_ARG.
+ * grid <= 0: one workgroup per tile. QLM_ERR_SHAPE when K is too long for
+ * the staged x (more than 20 columns per thread or 64 KiB of LDS). */
+int qlm_gemv_w_config(const float* x, const float* norm_w, float eps, const void* w, int w_bf16,
+                      float* y, int N, int K, int epilogue, int waves, int rows_per_wave,
+                      int k_phases, int ring, int grid, void* stream);
 
 #ifdef __cplusplus
 }

@@ -188,6 +188,231 @@ __global__ __launch_bounds__(NW * QLM_WAVE) void k_gemv_w(
     }
 }
 
+// One activation row on the vector ALUs (the matrix-core form above would
+// spend 15 of its 16 activation columns on nothing and cost about as much
+// time as the weight stream). The workgroup stages x (times 1 + gain for the
+// RMSNorm prologue, whose 1/rms it also computes) in LDS once. A tile is
+// RT = G * RG rows (G = NW / KS row groups): wave w owns row group w % G (RG
+// rows, both halves for SwiGLU) and the column chunks (w / G) + KS * j of
+// every tile it visits, so one x chunk read from LDS serves RG * T weight
+// loads. Chunk c of a row is
+// the 64 lanes' 16-byte loads, columns c * CW + EL * lane .. + EL - 1. Work
+// items (tile, chunk) stream through a ring of R register slots as in
+// k_gemv_w; a finished tile's partial sums meet in LDS (KS > 1) or are
+// reduced inside the wave (KS == 1), and lanes of the first wave write the
+// epilogue. Columns past K (a ragged last chunk) read an in-row clamped
+// address and multiply staged zeros.
+template <typename WT, int NW, int RG, int KS, int R, int EPI, bool NORM, int XL>
+__global__ __launch_bounds__(NW * QLM_WAVE) void k_gemv_wv(
+    const float* __restrict__ x, const float* __restrict__ gain, float eps,
+    const WT* __restrict__ W, float* __restrict__ y, int N, int K, int F, int ntiles) {
+    constexpr int T = EPI == EPI_SWIGLU ? 2 : 1;
+    constexpr int G = NW / KS;           // row groups per tile
+    constexpr int RT = G * RG;           // rows per tile
+    constexpr int EL = 16 / sizeof(WT);  // weights per 16-byte load
+    constexpr int XV = EL / 4;           // float4 of x per load
+    constexpr int CW = QLM_WAVE * EL;    // columns per chunk
+    constexpr int NT = NW * QLM_WAVE;
+    static_assert(NW % KS == 0, "KS must divide the wave count");
+    static_assert(R >= 2, "the x prefetch needs two ring slots");
+    // x chunks, each as XV planes of 64 float4, then one chunk of zeros that
+    // masked items read
+    extern __shared__ float4 xs4[];
+    __shared__ float red[KS > 1 ? 2 : 1][KS > 1 ? KS : 1][T][RT][4];
+    __shared__ float bred[NW];
+
+    const int tid = threadIdx.x, lane = tid & (QLM_WAVE - 1);
+    const int w = __builtin_amdgcn_readfirstlane(tid / QLM_WAVE);
+    const int rg = w % G, ph = w / G;
+    const int nch = (K + CW - 1) / CW;
+    const int per = (nch + KS - 1) / KS;  // items per tile and wave
+    const int clast = ph < nch ? ph + KS * ((nch - 1 - ph) / KS) : nch - 1;
+    const int K4 = K >> 2, KP4 = (nch + 1) * (CW / 4);
+
+    // x and gain: loads first (clamped, unconditional, their values used
+    // unconditionally so that none is sunk behind the ring's loads)
+    float4 xr[XL], gr[XL];
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+    const float4* g4 = reinterpret_cast<const float4*>(gain);
+#pragma unroll
+    for (int u = 0; u < XL; ++u) {
+        const int i = min(tid + u * NT, K4 - 1);
+        xr[u] = x4[i];
+        if constexpr (NORM) gr[u] = g4[i];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // work item s of this wave: tile blockIdx.x + (s / per) * gridDim.x, chunk
+    // ph + KS * (s % per); items past the wave's last chunk or last tile
+    // reload a clamped chunk and read the zero chunk of x
+    uint4 wb[R][T][RG];
+    auto issue = [&](int s, int sl) {
+        const int tile = min((int)blockIdx.x + (s / per) * (int)gridDim.x, ntiles - 1);
+        const int c = min(ph + KS * (s % per), clast);
+        const int col = min(c * CW + lane * EL, K - EL);
+#pragma unroll
+        for (int tt = 0; tt < T; ++tt)
+#pragma unroll
+            for (int i = 0; i < RG; ++i) {
+                const int row = min(tile * RT + rg * RG + i, N - 1) + tt * F;
+                wb[sl][tt][i] = *reinterpret_cast<const uint4*>(W + (size_t)row * K + col);
+            }
+    };
+#pragma unroll
+    for (int r = 0; r < R; ++r) issue(r, r);
+
+    float ss = 0.0f;
+#pragma unroll
+    for (int u = 0; u < XL; ++u) {
+        const int i = tid + u * NT;  // float4 index in the staged x
+        float4 v = xr[u];
+        if (i >= K4) v = make_float4(0.f, 0.f, 0.f, 0.f);
+        ss = fmaf(v.x, v.x, ss);
+        ss = fmaf(v.y, v.y, ss);
+        ss = fmaf(v.z, v.z, ss);
+        ss = fmaf(v.w, v.w, ss);
+        if constexpr (NORM) {
+            const float4 g = gr[u];
+            v = make_float4(v.x * (1.0f + g.x), v.y * (1.0f + g.y), v.z * (1.0f + g.z),
+                            v.w * (1.0f + g.w));
+        }
+        // lane l's float4 p (< XV) of chunk c sits at plane p, slot l
+        const int c = i / (CW / 4), o = i % (CW / 4);
+        if (i < KP4) xs4[c * (CW / 4) + (o % XV) * QLM_WAVE + o / XV] = v;
+    }
+    float rs = 1.0f;
+    if constexpr (NORM) {
+        ss = block_sum(ss, bred);  // also the barrier that publishes xs4
+        rs = 1.0f / sqrtf(ss / (float)K + eps);
+    } else {
+        __syncthreads();
+    }
+
+    float acc[T][RG];
+#pragma unroll
+    for (int tt = 0; tt < T; ++tt)
+#pragma unroll
+        for (int i = 0; i < RG; ++i) acc[tt][i] = 0.0f;
+
+    // x of an item is read from LDS one item ahead of its use
+    float4 xq[R][XV];
+    auto xread = [&](int s, int sl, int items) {
+        const bool real = (ph + KS * (s % per) < nch) && s < items;
+        const int c = real ? ph + KS * (s % per) : nch;
+#pragma unroll
+        for (int p = 0; p < XV; ++p) xq[sl][p] = xs4[c * (CW / 4) + p * QLM_WAVE + lane];
+    };
+
+    auto consume = [&](int sl) {
+        float xe[EL];
+#pragma unroll
+        for (int p = 0; p < XV; ++p) {
+            xe[4 * p] = xq[sl][p].x;
+            xe[4 * p + 1] = xq[sl][p].y;
+            xe[4 * p + 2] = xq[sl][p].z;
+            xe[4 * p + 3] = xq[sl][p].w;
+        }
+#pragma unroll
+        for (int tt = 0; tt < T; ++tt)
+#pragma unroll
+            for (int i = 0; i < RG; ++i) {
+                const uint4 q = wb[sl][tt][i];
+                const uint32_t u4[4] = {q.x, q.y, q.z, q.w};
+                float a = acc[tt][i];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    if constexpr (sizeof(WT) == 2) {
+                        a = fmaf(__uint_as_float(u4[e] << 16), xe[2 * e], a);
+                        a = fmaf(__uint_as_float(u4[e] & 0xffff0000u), xe[2 * e + 1], a);
+                    } else {
+                        a = fmaf(__uint_as_float(u4[e]), xe[e], a);
+                    }
+                }
+                acc[tt][i] = a;
+            }
+    };
+
+    auto epilogue = [&](int row, const float* v) {
+        float* dst = y + row;
+        if constexpr (EPI == EPI_SWIGLU)
+            *dst = silu_f(v[0] * rs) * (v[1] * rs);
+        else if constexpr (EPI == EPI_RESID)
+            *dst += v[0] * rs;
+        else
+            *dst = v[0] * rs;
+    };
+
+    int par = 0;
+    auto tile_end = [&](int tile) {
+        if constexpr (KS == 1) {
+            // whole rows in this wave: reduce inside it, lane i writes row i
+            float tot[T][RG];
+#pragma unroll
+            for (int tt = 0; tt < T; ++tt)
+#pragma unroll
+                for (int i = 0; i < RG; ++i) {
+                    tot[tt][i] = wave_sum(acc[tt][i]);
+                    acc[tt][i] = 0.0f;
+                }
+#pragma unroll
+            for (int i = 0; i < RG; ++i) {
+                const int row = tile * RT + rg * RG + i;
+                if (lane == i && row < N) {
+                    float v[T];
+#pragma unroll
+                    for (int tt = 0; tt < T; ++tt) v[tt] = tot[tt][i];
+                    epilogue(row, v);
+                }
+            }
+        } else {
+            // 16-lane sums meet in LDS: [parity][phase][half][tile row][lane group]
+#pragma unroll
+            for (int tt = 0; tt < T; ++tt)
+#pragma unroll
+                for (int i = 0; i < RG; ++i) {
+                    const float v = group_sum<16>(acc[tt][i]);
+                    acc[tt][i] = 0.0f;
+                    if ((lane & 15) == 0) red[par][ph][tt][rg * RG + i][lane >> 4] = v;
+                }
+            __syncthreads();
+            if (tid < RT) {
+                const int row = tile * RT + tid;
+                if (row < N) {
+                    float v[T];
+#pragma unroll
+                    for (int tt = 0; tt < T; ++tt) {
+                        float s = 0.0f;
+#pragma unroll
+                        for (int p = 0; p < KS; ++p) {
+                            const float* r4 = red[par][p][tt][tid];
+                            s += (r4[0] + r4[1]) + (r4[2] + r4[3]);
+                        }
+                        v[tt] = s;
+                    }
+                    epilogue(row, v);
+                }
+            }
+            par ^= 1;  // a buffer is rewritten two tiles later, after another barrier
+        }
+    };
+
+    const int my_tiles = (ntiles - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
+    const int items = my_tiles * per;
+    xread(0, 0, items);
+#pragma unroll 1
+    for (int s0 = 0; s0 < items; s0 += R) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int s = s0 + r;
+            xread(s + 1, (r + 1) % R, items);
+            consume(r);
+            issue(s + R, r);
+            if (s < items && s % per == per - 1)
+                tile_end((int)blockIdx.x + (s / per) * (int)gridDim.x);
+        }
+    }
+}
+
 struct WConfig {
     int nw, r, grid;
 };
@@ -244,7 +469,122 @@ int w_dispatch(const float* x, int ldx, const float* norm_w, float eps, const WT
     return QLM_OK;
 }
 
+// ---- one-row launch shapes ---------------------------------------------------
+struct WvConfig {
+    int nw, rg, ks, r, grid;
+};
+
+// x staged by XL float4 loads per thread: 2 or 5 (up to 8 or 20 columns of
+// the padded x per thread), 0 if K needs more (the matrix-core kernel then
+// serves).
+int wv_xl(int K, int elt, int nw) {
+    const int cw = QLM_WAVE * (16 / elt);
+    const int kp4 = ((K + cw - 1) / cw + 1) * (cw / 4);  // chunks + the zero chunk
+    const int nt = nw * QLM_WAVE;
+    return kp4 <= 2 * nt ? 2 : kp4 <= 5 * nt ? 5 : 0;
+}
+
+template <typename WT, int NW, int RG, int KS, int R, int EPI, bool NORM>
+int launch_wv_e(const WvConfig& c, int xl, const float* x, const float* gain, float eps,
+                const WT* W, float* y, int N, int K, hipStream_t st) {
+    constexpr int RT = NW / KS * RG;
+    const int ntiles = (N + RT - 1) / RT;
+    const int grid = c.grid > 0 && c.grid < ntiles ? c.grid : ntiles;
+    constexpr int CW = QLM_WAVE * (16 / (int)sizeof(WT));
+    const size_t lds = (size_t)((K + CW - 1) / CW + 1) * CW * sizeof(float);
+    if (xl == 2)
+        hipLaunchKernelGGL((k_gemv_wv<WT, NW, RG, KS, R, EPI, NORM, 2>), dim3(grid),
+                           dim3(NW * QLM_WAVE), lds, st, x, gain, eps, W, y, N, K, N, ntiles);
+    else
+        hipLaunchKernelGGL((k_gemv_wv<WT, NW, RG, KS, R, EPI, NORM, 5>), dim3(grid),
+                           dim3(NW * QLM_WAVE), lds, st, x, gain, eps, W, y, N, K, N, ntiles);
+    return qlm_launch_status();
+}
+
+template <typename WT, int NW, int RG, int KS, int R>
+int launch_wv_t(const WvConfig& c, const float* x, const float* gain, float eps, const WT* W,
+                float* y, int N, int K, int epi, hipStream_t st) {
+    const int xl = wv_xl(K, (int)sizeof(WT), NW);
+    constexpr int CW = QLM_WAVE * (16 / (int)sizeof(WT));
+    if (!xl || ((size_t)K + 2 * CW) * sizeof(float) > 65536) return QLM_ERR_SHAPE;
+    if (epi == EPI_SWIGLU)
+        return launch_wv_e<WT, NW, RG, KS, R, EPI_SWIGLU, true>(c, xl, x, gain, eps, W, y, N, K,
+                                                                 st);
+    if (epi == EPI_RESID)
+        return launch_wv_e<WT, NW, RG, KS, R, EPI_RESID, false>(c, xl, x, gain, eps, W, y, N, K,
+                                                                 st);
+    if (gain)
+        return launch_wv_e<WT, NW, RG, KS, R, EPI_STORE, true>(c, xl, x, gain, eps, W, y, N, K,
+                                                                st);
+    return launch_wv_e<WT, NW, RG, KS, R, EPI_STORE, false>(c, xl, x, gain, eps, W, y, N, K, st);
+}
+
+// The built shapes (waves, rows per wave, K phases, ring).
+template <typename WT>
+int launch_wv(const WvConfig& c, const float* x, const float* gain, float eps, const WT* W,
+              float* y, int N, int K, int epi, hipStream_t st) {
+#define QLM_WV(NW_, RG_, KS_, R_)                                                          \
+    if (c.nw == NW_ && c.rg == RG_ && c.ks == KS_ && c.r == R_)                            \
+        return launch_wv_t<WT, NW_, RG_, KS_, R_>(c, x, gain, eps, W, y, N, K, epi, st);
+    QLM_WV(4, 1, 1, 4)
+    QLM_WV(8, 1, 1, 4)
+    QLM_WV(4, 2, 1, 3)
+    QLM_WV(8, 2, 1, 3)
+    QLM_WV(4, 4, 1, 2)
+    QLM_WV(8, 2, 4, 3)
+    QLM_WV(8, 1, 4, 4)
+    QLM_WV(16, 1, 8, 4)
+#undef QLM_WV
+    return QLM_ERR_ARG;
+}
+
+// Measured per projection of the 4B model (bf16 rows; the tied lm_head is
+// the fp32 embedding table), graph-replayed over rotating weight copies.
+struct WvTuned {
+    int N, K, epi, elt;
+    WvConfig c;
+};
+constexpr WvTuned kWvTuned[] = {
+    {9728, 2560, EPI_SWIGLU, 2, {4, 1, 1, 4, 768}},  // gate/up: 19.2 us, 5.2 TB/s
+    {2560, 9728, EPI_RESID, 2, {8, 2, 4, 3, 256}},   // down: 11.4 us, 4.4 TB/s
+    {8224, 2560, EPI_STORE, 2, {4, 2, 1, 3, 512}},   // DeltaNet in-projection: 10.0 us
+    {5120, 2560, EPI_STORE, 2, {4, 2, 1, 3, 512}},   // attention q/k/v: 7.6 us
+    {2560, 2048, EPI_RESID, 2, {4, 4, 1, 2, 160}},   // output projections: 5.2 us
+    {151936, 2560, EPI_STORE, 4, {4, 2, 1, 3, 256}}, // lm_head (fp32): 240 us, 6.5 TB/s
+};
+
+WvConfig wv_config(int N, int K, int epi, int elt) {
+    for (const WvTuned& t : kWvTuned)
+        if (t.N == N && t.K == K && t.epi == epi && t.elt == elt) return t.c;
+    return WvConfig{4, 2, 1, 3, 512};
+}
+
+template <typename WT>
+int wv_auto(const float* x, const float* gain, float eps, const WT* W, float* y, int N, int K,
+            int epi, hipStream_t st) {
+    return launch_wv<WT>(wv_config(N, K, epi, (int)sizeof(WT)), x, gain, eps, W, y, N, K, epi,
+                         st);
+}
+
 }  // namespace
+
+extern "C" int qlm_gemv_w_config(const float* x, const float* norm_w, float eps, const void* w,
+                                 int w_bf16, float* y, int N, int K, int epilogue, int waves,
+                                 int rows_per_wave, int k_phases, int ring, int grid,
+                                 void* stream) {
+    if (!x || !w || !y || N <= 0 || K <= 0) return QLM_ERR_ARG;
+    if (epilogue < EPI_STORE || epilogue > EPI_SWIGLU) return QLM_ERR_ARG;
+    if (epilogue == EPI_SWIGLU && !norm_w) return QLM_ERR_ARG;
+    if (epilogue == EPI_RESID && norm_w) return QLM_ERR_ARG;
+    if (K % 16 != 0) return QLM_ERR_SHAPE;
+    if (((uintptr_t)x | (uintptr_t)w | (uintptr_t)norm_w) & 15u) return QLM_ERR_SHAPE;
+    const WvConfig c{waves, rows_per_wave, k_phases, ring, grid};
+    hipStream_t st = as_stream(stream);
+    return w_bf16 ? launch_wv<uint16_t>(c, x, norm_w, eps, static_cast<const uint16_t*>(w), y, N,
+                                        K, epilogue, st)
+                  : launch_wv<float>(c, x, norm_w, eps, static_cast<const float*>(w), y, N, K,
+                                     epilogue, st);
+}
 
 extern "C" size_t qlm_matmul_w_workspace_bytes(int K) {
     if (K <= 0) return 0;
@@ -264,6 +604,13 @@ extern "C" int qlm_matmul_w(const float* x, int ldx, const float* norm_w, float 
                    ((uintptr_t)work & 15u)))
         return QLM_ERR_ARG;
     hipStream_t st = as_stream(stream);
+    if (M == 1) {  // one row: the vector-ALU GEMV (QLM_ERR_SHAPE: K too long for it)
+        const int rc = w_bf16 ? wv_auto<uint16_t>(x, norm_w, eps, static_cast<const uint16_t*>(w),
+                                                  y, N, K, epilogue, st)
+                              : wv_auto<float>(x, norm_w, eps, static_cast<const float*>(w), y,
+                                               N, K, epilogue, st);
+        if (rc != QLM_ERR_SHAPE) return rc;
+    }
     return w_bf16 ? w_dispatch<uint16_t>(x, ldx, norm_w, eps, static_cast<const uint16_t*>(w),
                                          y, ldy, M, N, K, epilogue, work, work_bytes, st)
                   : w_dispatch<float>(x, ldx, norm_w, eps, static_cast<const float*>(w), y, ldy,

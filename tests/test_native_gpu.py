@@ -3,8 +3,9 @@
 qlm_matmul_w against the oracle's fp32 dot products over fp32 or bf16 rows
 (orc_matmul_w, itself bit-exact with the reference's dot_avx2 /
 dot_avx2_bf16, tests/test_oracle.py). The summation order differs (matrix
-cores, 16-row tiles split over waves), so the bar is fp32 rounding: 1e-5
-normwise per call.
+cores over 16-row tiles for several rows, per-lane fp32 sums and lane
+reductions for one row), so the bar is fp32 rounding: 1e-5 normwise per
+call.
 """
 
 import numpy as np
@@ -98,3 +99,52 @@ def test_matmul_w_rejects_bad_args(hip):
         hip.call("qlm_matmul_w", d, 64, d, 1e-6, d, 0, d, 8, 1, 8, 64, 0, None, 0, None)
     with pytest.raises(hip.HipError):  # workspace too small
         hip.call("qlm_matmul_w", d, 64, d, 1e-6, d, 0, d, 8, 1, 8, 64, 0, d, wb - 4, None)
+
+
+WV_SHAPES = [(4, 1, 1, 4), (8, 1, 1, 4), (4, 2, 1, 3), (8, 2, 1, 3), (4, 4, 1, 2), (8, 2, 4, 3),
+             (8, 1, 4, 4), (16, 1, 8, 4)]
+WV_CASES = [  # (N, K, grid): ragged K (a part chunk), K under one chunk, N off the tile size
+    (100, 1040, 0), (37, 48, 3), (300, 2560, 7), (64, 9728, 0), (1001, 512, 5)]
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("epi", ["store", "norm", "resid", "swiglu"])
+def test_gemv_w_shapes(hip, orc, rng, dtype, epi):
+    """Every built one-row launch shape against the oracle."""
+    eps = 1e-6
+    for N, K, grid in WV_CASES:
+        rows_w = 2 * N if epi == "swiglu" else N
+        w32 = (rng.standard_normal((rows_w, K)) * 0.02).astype(np.float32)
+        w = bf16_bits(w32) if dtype == "bf16" else w32
+        x = rng.standard_normal((1, K)).astype(np.float32)
+        nw = (rng.standard_normal(K) * 0.02).astype(np.float32)
+        y0 = rng.standard_normal((1, N)).astype(np.float32)
+        ref = _ref(orc, epi, x, w, nw, y0, N, eps)
+        dx, dw = dev(hip, x), dev(hip, w)
+        dnw = dev(hip, nw) if epi in ("norm", "swiglu") else None
+        cw = 64 * (8 if dtype == "bf16" else 4)
+        kp4 = ((K + cw - 1) // cw + 1) * (cw // 4)  # staged float4, zero chunk included
+        for nwv, rg, ks, ring in WV_SHAPES:
+            say("gemv_w_config", dtype, epi, N, K, grid, nwv, rg, ks, ring)
+            yp = np.full((1, N + 8), 7.0, np.float32)
+            yp[:, :N] = y0
+            dy = dev(hip, yp)
+            if kp4 > 5 * 64 * nwv:  # more than 20 staged columns per thread: refused
+                with pytest.raises(hip.HipError):
+                    hip.call("qlm_gemv_w_config", dx, dnw, eps, dw, 1 if dtype == "bf16" else 0,
+                             dy, N, K, EPI[epi], nwv, rg, ks, ring, grid, None)
+                continue
+            hip.call("qlm_gemv_w_config", dx, dnw, eps, dw, 1 if dtype == "bf16" else 0, dy, N,
+                     K, EPI[epi], nwv, rg, ks, ring, grid, None)
+            got = dy.to_numpy((1, N + 8), np.float32)
+            assert np.all(got[:, N:] == 7.0), "wrote past N"
+            err = rel_err(got[:, :N], ref)
+            assert err < TOL, (dtype, epi, N, K, grid, nwv, rg, ks, ring, err)
+
+
+def test_gemv_w_config_rejects(hip):
+    d = hip.DeviceBuffer(1 << 16)
+    with pytest.raises(hip.HipError):  # a shape that is not built
+        hip.call("qlm_gemv_w_config", d, None, 1e-6, d, 1, d, 8, 64, 0, 8, 3, 1, 3, 0, None)
+    with pytest.raises(hip.HipError):  # K past the staged-x limit
+        hip.call("qlm_gemv_w_config", d, None, 1e-6, d, 0, d, 8, 65536, 0, 4, 1, 1, 4, 0, None)
