@@ -70,6 +70,44 @@ int qlm_engine_last_logits(void* handle, int b, float* logits);
 /* Kernel launches in one captured decode step of batch B (after a step ran). */
 int qlm_engine_kernels_per_step(void* handle);
 
+/* ---- speculative decoding and sessions (sequence 0) --------------------------
+ * DecoderModel::snapshot_states / restore_states (model.cpp:139-149,
+ * attention.cpp:766-790): one device slot holding every DeltaNet recurrence
+ * and conv ring; restore before any snapshot is an error. */
+int qlm_engine_snapshot(void* handle);
+int qlm_engine_restore(void* handle);
+
+/* DecoderModel::forward(token) at pos followed by the greedy pick
+ * (model.cpp:151-211, :263-274): one replayed decode step; *next = argmax. */
+int qlm_engine_forward_greedy(void* handle, int token, int pos, int* next);
+
+/* DecoderModel::forward_batch (model.cpp:213-258): tokens[0..n) at positions
+ * pos..pos+n-1 through every layer at once (n == 1: one decode step). argmax
+ * [n] (host, may be NULL): the greedy pick of each row; logits [n, vocab]
+ * (host, may be NULL): the rows' logits. With both NULL the lm_head is not
+ * run (a replay or a prompt prefill). */
+int qlm_engine_forward_batch(void* handle, const int* tokens, int n, int pos, int* argmax,
+                             float* logits);
+
+/* The CLI's turn loop (main.cpp:455-690) over token ids, with
+ * SpeculativeDecoder (speculative.cpp:1-222) when draft is non-NULL: target
+ * and draft are engine handles (kept alive by the caller; the draft is
+ * usually the same checkpoint at "int4", main.cpp:366-394). draft_tokens is
+ * K (>= 1); eos_id / im_end_id end a turn (never emitted); kv_reuse keeps the
+ * live state for a turn whose ids extend the ids already consumed. */
+int qlm_session_create(void* target, void* draft, int draft_tokens, int eos_id, int im_end_id,
+                       int kv_reuse, void** session);
+int qlm_session_free(void* session);
+int qlm_session_reset(void* session);
+/* One turn: ids [n] = the turn's whole prompt; up to max_tokens tokens to
+ * out [cap], count in *n_out; info [7] (may be NULL) = reused prompt
+ * positions, recomputed positions, speculative rounds, drafted, accepted,
+ * emitted, rejections; prefill and decode wall times in seconds. */
+int qlm_session_turn(void* session, const int* ids, int n, int max_tokens, int* out, int cap,
+                     int* n_out, int* info, double* prefill_s, double* decode_s);
+/* The ids whose state both models hold (*n of them; out [cap] may be NULL). */
+int qlm_session_cached(void* session, int* out, int cap, int* n);
+
 /* ---- synthetic checkpoints (no reference counterpart) ----
  * Deterministic counter-based generators used to write random-init weights
  * of a given architecture: element i of a tensor with seed s depends only on

@@ -1,11 +1,14 @@
 // extern "C" face of the host engine (include/qlm_engine.h). Exceptions never
 // cross the ABI: they become a nonzero return plus qlm_engine_last_error().
 
+#include <algorithm>
 #include <cstring>
 #include <exception>
 #include <string>
+#include <vector>
 
 #include "model.hpp"
+#include "speculative.hpp"
 #include "qlm_engine.h"
 
 namespace {
@@ -28,6 +31,11 @@ int guarded(F&& f) {
 qlm::DecoderModel* M(void* h) {
     if (!h) throw std::runtime_error("null engine handle");
     return static_cast<qlm::DecoderModel*>(h);
+}
+
+qlm::Session* S(void* h) {
+    if (!h) throw std::runtime_error("null session handle");
+    return static_cast<qlm::Session*>(h);
 }
 }  // namespace
 
@@ -112,6 +120,70 @@ int qlm_engine_tokens(void* handle, int b, int first, int count, int* out) {
     return guarded([&] {
         if (!out) throw std::runtime_error("null output");
         M(handle)->tokens(b, first, count, out);
+    });
+}
+
+int qlm_engine_snapshot(void* handle) { return guarded([&] { M(handle)->snapshot_states(); }); }
+
+int qlm_engine_restore(void* handle) { return guarded([&] { M(handle)->restore_states(); }); }
+
+int qlm_engine_forward_greedy(void* handle, int token, int pos, int* next) {
+    return guarded([&] {
+        const int t = M(handle)->forward_greedy(token, pos);
+        if (next) *next = t;
+    });
+}
+
+int qlm_engine_forward_batch(void* handle, const int* tokens, int n, int pos, int* argmax,
+                             float* logits) {
+    return guarded([&] { M(handle)->forward_batch(tokens, n, pos, argmax, logits); });
+}
+
+int qlm_session_create(void* target, void* draft, int draft_tokens, int eos_id, int im_end_id,
+                       int kv_reuse, void** session) {
+    return guarded([&] {
+        if (!session) throw std::runtime_error("null argument");
+        *session = nullptr;
+        *session = new qlm::Session(*M(target), draft ? M(draft) : nullptr, draft_tokens, eos_id,
+                                    im_end_id, kv_reuse != 0);
+    });
+}
+
+int qlm_session_free(void* session) {
+    return guarded([&] { delete static_cast<qlm::Session*>(session); });
+}
+
+int qlm_session_reset(void* session) {
+    return guarded([&] { S(session)->reset(); });
+}
+
+int qlm_session_turn(void* session, const int* ids, int n, int max_tokens, int* out, int cap,
+                     int* n_out, int* info, double* prefill_s, double* decode_s) {
+    return guarded([&] {
+        if (!ids || n < 0 || !out || !n_out) throw std::runtime_error("null argument");
+        const qlm::TurnResult r = S(session)->turn(std::vector<int>(ids, ids + n), max_tokens);
+        if ((int)r.tokens.size() > cap) throw std::runtime_error("session: output too small");
+        std::copy(r.tokens.begin(), r.tokens.end(), out);
+        *n_out = (int)r.tokens.size();
+        if (info) {
+            const int v[7] = {r.reused,          r.recomputed,     r.spec.rounds,
+                              r.spec.drafted,    r.spec.draft_accepted, r.spec.emitted,
+                              r.spec.rejections};
+            std::copy(v, v + 7, info);
+        }
+        if (prefill_s) *prefill_s = r.prefill_s;
+        if (decode_s) *decode_s = r.decode_s;
+    });
+}
+
+int qlm_session_cached(void* session, int* out, int cap, int* n) {
+    return guarded([&] {
+        const auto& c = S(session)->cached_ids();
+        if (n) *n = (int)c.size();
+        if (out) {
+            if ((int)c.size() > cap) throw std::runtime_error("session: output too small");
+            std::copy(c.begin(), c.end(), out);
+        }
     });
 }
 

@@ -33,6 +33,9 @@ std::vector<float> to_f32(const TensorView& t) {
 }
 
 constexpr int kPrefillChunk = 1024;  // prompt rows per pass through the layers
+constexpr int kLmRows = 64;          // rows per lm_head pass of a batched forward
+constexpr int kRowsMax = 64;         // batched forwards up to this many rows run the
+                                     // DeltaNet recurrence row by row
 
 double now_s() {
     return std::chrono::duration<double>(std::chrono::steady_clock::now().time_since_epoch()).count();
@@ -558,9 +561,13 @@ void DecoderModel::ensure_prefill_buffers(int rows) {
 // token is forwarded by the first decode step). Fills the conv rings,
 // DeltaNet states and KV caches of sequence b; no logits are needed.
 void DecoderModel::prefill(int b, int n, bool chunked_deltanet) {
-    const int total = n - 1;
-    if (total <= 0) return;
-    const int chunk = std::min(total, kPrefillChunk);
+    run_rows(b, 0, n - 1, chunked_deltanet);
+}
+
+void DecoderModel::run_rows(int b, int first, int count, bool chunked_deltanet, int* lm_idx,
+                            float* logits_host) {
+    if (count <= 0) return;
+    const int chunk = std::min(count, kPrefillChunk);
     ensure_prefill_buffers(chunk);
     math::set_stream(stream_);
     math::set_matmul_workspace(mm_work_.get(), mm_work_.bytes());
@@ -570,8 +577,8 @@ void DecoderModel::prefill(int b, int n, bool chunked_deltanet) {
     const float eps = cfg_.rms_norm_eps;
     const int Pmax = std::max(PD_, PQ_);
     const int C = 3 * HD_;
-    for (int p0 = 0; p0 < total; p0 += chunk) {
-        const int rows = std::min(chunk, total - p0);
+    for (int p0 = first; p0 < first + count; p0 += chunk) {
+        const int rows = std::min(chunk, first + count - p0);
         check(qlm_embed_tokens(embed_.get<float>(), V, H,
                                tokens_.get<int>() + (size_t)b * ld_tokens_ + p0, 1, nullptr,
                                hx_pf_.get<float>(), H, rows, stream_),
@@ -625,7 +632,106 @@ void DecoderModel::prefill(int b, int n, bool chunked_deltanet) {
             math::matmul_swiglu_rmsnorm(hx, post_ln, eps, w.gate_up.view(), act);
             math::matmul_residual(act, w.down.view(), hx);
         }
+        if (!lm_idx && !logits_host) continue;
+        // final norm + lm_head + greedy pick of these rows (model.cpp:246-255),
+        // kLmRows rows at a time
+        Tensor fn({H}, final_norm_.get<float>());
+        for (int r0 = 0; r0 < rows; r0 += kLmRows) {
+            const int m = std::min(kLmRows, rows - r0);
+            const size_t row = (size_t)(p0 - first + r0);
+            Tensor xs({m, H}, hx_pf_.get<float>() + (size_t)r0 * H);
+            Tensor lg({m, V}, lm_pf_.get<float>());
+            math::matmul_rmsnorm(xs, fn, eps, lm_head_.view(), lg);
+            if (lm_idx)
+                check(qlm_argmax(lm_pf_.get<float>(), V, V, m, lm_idx + row, lm_pf_work_.get(),
+                                 stream_),
+                      "argmax");
+            if (logits_host)
+                check(qlm_memcpy_d2h(logits_host + row * V, lm_pf_.get(),
+                                     (size_t)m * V * sizeof(float), stream_),
+                      "download");
+        }
     }
+}
+
+void DecoderModel::snapshot_states() {
+    if (conv_snap_.size() != conv_state_.size()) {
+        conv_snap_.clear();
+        dn_snap_.clear();
+        for (auto& b : conv_state_) conv_snap_.emplace_back(b.bytes());
+        for (auto& b : dn_state_) dn_snap_.emplace_back(b.bytes());
+    }
+    for (size_t i = 0; i < conv_state_.size(); ++i) {
+        check(qlm_memcpy_d2d(conv_snap_[i].get(), conv_state_[i].get(), conv_state_[i].bytes(),
+                             stream_),
+              "snapshot");
+        check(qlm_memcpy_d2d(dn_snap_[i].get(), dn_state_[i].get(), dn_state_[i].bytes(), stream_),
+              "snapshot");
+    }
+    have_snapshot_ = true;
+}
+
+void DecoderModel::restore_states() {
+    if (!have_snapshot_)
+        throw std::runtime_error("restore_states() called before any snapshot_states()");
+    for (size_t i = 0; i < conv_state_.size(); ++i) {
+        check(qlm_memcpy_d2d(conv_state_[i].get(), conv_snap_[i].get(), conv_state_[i].bytes(),
+                             stream_),
+              "restore");
+        check(qlm_memcpy_d2d(dn_state_[i].get(), dn_snap_[i].get(), dn_state_[i].bytes(), stream_),
+              "restore");
+    }
+}
+
+int DecoderModel::forward_greedy(int token, int pos) {
+    if (pos < 0 || pos >= max_seq_)
+        throw std::runtime_error("context length exceeded max_seq_len (" + std::to_string(max_seq_) +
+                                 ")");
+    if (token < 0 || token >= cfg_.vocab_size)
+        throw std::runtime_error("forward: token id out of range");
+    const int zero = 0;
+    // the step's tail stores its pick as token pos + 1 (past the "prompt")
+    check(qlm_memcpy_h2d(tokens_.get<int>() + pos, &token, sizeof(int), stream_), "upload");
+    check(qlm_memcpy_h2d(pos_.get<int>(), &pos, sizeof(int), stream_), "upload");
+    check(qlm_memcpy_h2d(prompt_len_.get<int>(), &zero, sizeof(int), stream_), "upload");
+    embed_current(1);
+    check(qlm_graph_launch(graph_for(1), stream_), "graph launch");
+    int next = 0;
+    check(qlm_memcpy_d2h(&next, tokens_.get<int>() + pos + 1, sizeof(int), stream_), "download");
+    check(qlm_stream_sync(stream_), "sync");
+    return next;
+}
+
+void DecoderModel::forward_batch(const int* toks, int n, int pos, int* argmax, float* logits) {
+    if (n <= 0) return;
+    if (!toks) throw std::runtime_error("forward_batch: null tokens");
+    if (pos < 0 || pos + n > max_seq_)
+        throw std::runtime_error("context length exceeded max_seq_len (" + std::to_string(max_seq_) +
+                                 ")");
+    for (int i = 0; i < n; ++i)
+        if (toks[i] < 0 || toks[i] >= cfg_.vocab_size)
+            throw std::runtime_error("forward_batch: token id out of range");
+    if (n == 1) {  // model.cpp:215-219: one row is a plain forward
+        const int t = forward_greedy(toks[0], pos);
+        if (argmax) argmax[0] = t;
+        if (logits) last_logits(0, logits);
+        return;
+    }
+    const bool lm = argmax || logits;
+    if (lm && !lm_pf_) {
+        lm_pf_.alloc((size_t)kLmRows * cfg_.vocab_size * sizeof(float));
+        lm_pf_work_.alloc(qlm_argmax_workspace_bytes(kLmRows, cfg_.vocab_size));
+    }
+    if (argmax && lm_pf_idx_.bytes() < (size_t)n * sizeof(int)) lm_pf_idx_.alloc((size_t)n * 4);
+    check(qlm_memcpy_h2d(tokens_.get<int>() + pos, toks, (size_t)n * sizeof(int), stream_),
+          "upload");
+    // short runs (a verify batch, a replay) take the row-by-row recurrence,
+    // the decode step's arithmetic; long prompt suffixes the chunked form
+    run_rows(0, pos, n, n > kRowsMax, argmax ? lm_pf_idx_.get<int>() : nullptr, logits);
+    if (argmax)
+        check(qlm_memcpy_d2h(argmax, lm_pf_idx_.get(), (size_t)n * sizeof(int), stream_),
+              "download");
+    check(qlm_stream_sync(stream_), "sync");
 }
 
 double DecoderModel::steps(int k, bool use_graph) {

@@ -24,6 +24,7 @@
 #include "config.hpp"
 #include "device.hpp"
 #include "safetensors.hpp"
+#include "speculative.hpp"
 #include "tensor.hpp"
 
 namespace qlm {
@@ -86,17 +87,37 @@ struct GenStats {
     int steps = 0;
 };
 
-class DecoderModel {
+class DecoderModel : public GreedyModel {
    public:
     DecoderModel() = default;
-    ~DecoderModel();
+    ~DecoderModel() override;
 
     // precision: "int8" (reference Q8_0, group 32) or "int8_row" (one scale
     // per output row). max_batch sequences of up to max_seq_len positions.
     void load(const std::string& dir, int max_seq_len, const std::string& precision,
               int max_batch);
 
-    void reset_states();
+    void reset_states() override;
+
+    // GreedyModel on sequence 0, for speculative decoding and sessions.
+    // snapshot_states / restore_states (model.cpp:139-149,
+    // attention.cpp:766-790): device copies of every DeltaNet recurrence and
+    // conv ring (one slot, allocated on first use).
+    void snapshot_states() override;
+    void restore_states() override;
+    int vocab_size() const override { return cfg_.vocab_size; }
+    int max_seq_len() const override { return max_seq_; }
+    // forward(token) at pos (one decode step, the replayed graph); returns
+    // the greedy pick, which the step also stores as token pos + 1.
+    int forward_greedy(int token, int pos) override;
+    // forward_batch (model.cpp:213-258): tokens[0..n) at positions
+    // pos..pos+n-1 through every layer at once; with argmax / logits (host
+    // arrays [n] / [n, vocab]) the final norm and lm_head run over every row.
+    // n == 1 is a decode step, as in the reference.
+    void forward_batch(const int* tokens, int n, int pos, int* argmax, float* logits);
+    void forward_batch_greedy(const int* tokens, int n, int pos, int* argmax) override {
+        forward_batch(tokens, n, pos, argmax, nullptr);
+    }
 
     // Reference-shaped single-sequence step (model.cpp:151-211) on sequence 0:
     // forwards `token` at position `pos` and copies the logits to the host.
@@ -139,6 +160,12 @@ class DecoderModel {
    private:
     void enqueue_step(int B);
     void prefill(int b, int n, bool chunked_deltanet);
+    // rows first..first+count-1 of sequence b's tokens through every layer;
+    // with lm_rows, each pass's rows also get the final norm, lm_head and a
+    // greedy pick (stored at lm_idx[row - first], device) and, with
+    // logits_host, their logits copied out
+    void run_rows(int b, int first, int count, bool chunked_deltanet, int* lm_idx = nullptr,
+                  float* logits_host = nullptr);
     void ensure_prefill_buffers(int rows);
     size_t matmul_workspace(int M) const;
     void embed_current(int B);
@@ -175,6 +202,12 @@ class DecoderModel {
     DeviceBuffer hx_pf_, proj_pf_, core_pf_, act_pf_, gqa_pf_work_, dn_pf_work_;
     int pf_rows_ = 0;
     DeviceBuffer staging_;
+
+    // speculative decoding: the state snapshot slot, per-row lm_head logits
+    // and greedy picks of a batched forward
+    std::vector<DeviceBuffer> conv_snap_, dn_snap_;
+    bool have_snapshot_ = false;
+    DeviceBuffer lm_pf_, lm_pf_idx_, lm_pf_work_;
 
     std::map<int, void*> graphs_;
     int run_B_ = 0, run_n_ = 0, run_steps_ = 0;

@@ -36,6 +36,16 @@ def lib() -> C.CDLL:
         L.qlm_engine_steps.argtypes = [_vp, _i, _i, C.POINTER(C.c_double)]
         L.qlm_engine_tokens.argtypes = [_vp, _i, _i, _i, _vp]
         L.qlm_engine_kernels_per_step.argtypes = [_vp]
+        L.qlm_engine_snapshot.argtypes = [_vp]
+        L.qlm_engine_restore.argtypes = [_vp]
+        L.qlm_engine_forward_greedy.argtypes = [_vp, _i, _i, C.POINTER(_i)]
+        L.qlm_engine_forward_batch.argtypes = [_vp, _vp, _i, _i, _vp, _vp]
+        L.qlm_session_create.argtypes = [_vp, _vp, _i, _i, _i, _i, C.POINTER(_vp)]
+        L.qlm_session_free.argtypes = [_vp]
+        L.qlm_session_reset.argtypes = [_vp]
+        L.qlm_session_turn.argtypes = [_vp, _vp, _i, _i, _vp, _i, C.POINTER(_i), _vp,
+                                       C.POINTER(C.c_double), C.POINTER(C.c_double)]
+        L.qlm_session_cached.argtypes = [_vp, _vp, _i, C.POINTER(_i)]
         _lib = L
     return _lib
 
@@ -126,12 +136,89 @@ class Engine:
         _check(lib().qlm_engine_last_logits(self.h, b, lg.ctypes.data))
         return lg
 
+    def snapshot(self) -> None:
+        """Snapshot every DeltaNet recurrence and conv ring (one slot)."""
+        _check(lib().qlm_engine_snapshot(self.h))
+
+    def restore(self) -> None:
+        _check(lib().qlm_engine_restore(self.h))
+
+    def forward_greedy(self, token: int, pos: int) -> int:
+        """One decode step of `token` at `pos`; returns the greedy pick."""
+        nx = _i()
+        _check(lib().qlm_engine_forward_greedy(self.h, token, pos, C.byref(nx)))
+        return nx.value
+
+    def forward_batch(self, tokens, pos: int, argmax: bool = True, logits: bool = False):
+        """tokens at positions pos.. through every layer at once; returns
+        (argmax [n] or None, logits [n, vocab] or None)."""
+        t = np.ascontiguousarray(tokens, np.int32).ravel()
+        am = np.empty(t.size, np.int32) if argmax else None
+        lg = np.empty((t.size, self.vocab), np.float32) if logits else None
+        _check(lib().qlm_engine_forward_batch(self.h, t.ctypes.data, t.size, pos,
+                                              None if am is None else am.ctypes.data,
+                                              None if lg is None else lg.ctypes.data))
+        return am, lg
+
     def kernels_per_step(self) -> int:
         return int(lib().qlm_engine_kernels_per_step(self.h))
 
     def close(self) -> None:
         if getattr(self, "h", None):
             lib().qlm_engine_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Session:
+    """The CLI's multi-turn loop over token ids (include/qlm_engine.h,
+    qlm_session_*): kv-reuse of the live state, batched prefill of the new
+    prompt suffix, then speculative decoding when a draft engine is given
+    (K = draft_tokens drafted per round), else plain greedy steps."""
+
+    INFO = ("reused", "recomputed", "rounds", "drafted", "accepted", "emitted", "rejections")
+
+    def __init__(self, target: Engine, draft: Engine | None = None, draft_tokens: int = 4,
+                 eos_id: int = -1, im_end_id: int = -1, kv_reuse: bool = True):
+        h = _vp()
+        _check(lib().qlm_session_create(target.h, None if draft is None else draft.h,
+                                        draft_tokens, eos_id, im_end_id, 1 if kv_reuse else 0,
+                                        C.byref(h)))
+        self.h = h.value
+        self._keep = (target, draft)
+
+    def turn(self, ids, max_tokens: int):
+        """-> (tokens, info dict with the INFO counters and prefill_s / decode_s)."""
+        p = np.ascontiguousarray(ids, np.int32).ravel()
+        out = np.empty(max(1, max_tokens), np.int32)
+        n_out = _i()
+        info = np.zeros(7, np.int32)
+        pre, dec = C.c_double(), C.c_double()
+        _check(lib().qlm_session_turn(self.h, p.ctypes.data, p.size, max_tokens, out.ctypes.data,
+                                      out.size, C.byref(n_out), info.ctypes.data, C.byref(pre),
+                                      C.byref(dec)))
+        d = dict(zip(self.INFO, (int(v) for v in info)))
+        d.update(prefill_s=pre.value, decode_s=dec.value)
+        return out[:n_out.value].copy(), d
+
+    def cached(self) -> np.ndarray:
+        n = _i()
+        _check(lib().qlm_session_cached(self.h, None, 0, C.byref(n)))
+        out = np.empty(n.value, np.int32)
+        _check(lib().qlm_session_cached(self.h, out.ctypes.data, out.size, C.byref(n)))
+        return out
+
+    def reset(self) -> None:
+        _check(lib().qlm_session_reset(self.h))
+
+    def close(self) -> None:
+        if getattr(self, "h", None):
+            lib().qlm_session_free(self.h)
             self.h = None
 
     def __del__(self):
