@@ -251,6 +251,26 @@ def run_decode(eng, prompts, warmup, steps, graph=True):
             "tokens": toks}
 
 
+def run_spec(target, draft, prompt, n_new, K, name):
+    """One session turn: prefill the prompt on both models, then n_new tokens
+    by speculative rounds; also the plain greedy stream for comparison."""
+    from quicklm_amd.engine import Session
+
+    s = Session(target, draft, draft_tokens=K)
+    out, info = s.turn(prompt, n_new)
+    s.close()
+    p = Session(target)
+    plain, pinfo = p.turn(prompt, n_new)
+    p.close()
+    return {"target": name, "draft": "int4", "draft_tokens": K, "tokens": int(len(out)),
+            "tok_s": round(len(out) / info["decode_s"], 2),
+            "decode_s": round(info["decode_s"], 4), "rounds": info["rounds"],
+            "drafted": info["drafted"], "accepted": info["accepted"],
+            "rejections": info["rejections"],
+            "plain_session_tok_s": round(len(plain) / pinfo["decode_s"], 2),
+            "matches_plain_greedy": bool(np.array_equal(out, plain))}
+
+
 def cpu_baseline(model_dir, prompt, n_prompt, n_decode, threads):
     """The reference QuickLM CPU path (its own sources, -O3 -ffast-math) on the
     same checkpoint: batched prefill of n_prompt-1 ids, then n_decode greedy
@@ -288,6 +308,9 @@ def main():
                     help="skip the batch-1 decode at --precision int4")
     ap.add_argument("--skip-native", action="store_true",
                     help="skip the batch-1 decode at --precision bf16 (weights as stored)")
+    ap.add_argument("--skip-spec", action="store_true",
+                    help="skip the speculative sessions (int4 draft, K = --draft-tokens)")
+    ap.add_argument("--draft-tokens", type=int, default=4)
     ap.add_argument("--skip-row", action="store_true",
                     help="skip the batch-1 decode with one scale per output row (int8_row)")
     ap.add_argument("--model-dir", default=None)
@@ -383,7 +406,8 @@ def main():
             e4 = Engine(mdir, max_seq_len=max_seq, max_batch=1, precision="int4")
             r4 = run_decode(e4, prompts[:1], args.warmup, args.steps, graph)
             r4["weight_bytes"] = e4.weight_bytes
-            e4.close()
+            if args.skip_spec:
+                e4.close()
             log(f"batch 1, int4 weights: {r4['tok_s']:.1f} tok/s "
                 f"({r4['ms_per_step']:.3f} ms/step), {r4['weight_bytes'] / 1e9:.3f} GB")
         rn = None
@@ -393,9 +417,28 @@ def main():
             en = Engine(mdir, max_seq_len=max_seq, max_batch=1, precision="bf16")
             rn = run_decode(en, prompts[:1], args.warmup, args.steps, graph)
             rn["weight_bytes"] = en.weight_bytes
-            en.close()
             log(f"batch 1, native weights: {rn['tok_s']:.1f} tok/s "
                 f"({rn['ms_per_step']:.3f} ms/step), {rn['weight_bytes'] / 1e9:.3f} GB")
+
+        spec = []
+        if not args.skip_spec and not args.skip_int4:
+            # the reference's default decode: the same checkpoint at int4 drafts
+            # K tokens per round for the target (main.cpp:166-172, :366-394)
+            targets = [("int8", Engine(mdir, max_seq_len=max_seq, max_batch=1,
+                                       precision="int8"))]
+            if rn is not None:
+                targets.append(("bf16", en))
+            for name, et in targets:
+                spec.append(run_spec(et, e4, prompts[0], args.steps, args.draft_tokens, name))
+                log(f"speculative, target {name} + int4 draft, K={args.draft_tokens}: "
+                    f"{spec[-1]['tok_s']:.1f} tok/s, accepted {spec[-1]['accepted']}/"
+                    f"{spec[-1]['drafted']} drafted, stream equals plain greedy: "
+                    f"{spec[-1]['matches_plain_greedy']}")
+            targets[0][1].close()
+        if rn is not None:
+            en.close()
+        if r4 is not None and not args.skip_spec:
+            e4.close()
     finally:
         if own_dir:
             import shutil
@@ -455,6 +498,7 @@ def main():
             "frac_of_weight_roofline": round(
                 rn["weight_bytes"] / (rn["ms_per_step"] / 1000.0) / 1e9 / HBM_PEAK_GBS, 4),
             "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / rn["weight_bytes"], 1)},
+        "speculative": spec or None,
         "gemv": gemv,
     })
     traffic, traffic_src = None, None
