@@ -169,6 +169,30 @@ int qlm_matmul_i8_mx(const float* x, int ldx, const float* norm_w, float eps,
                      int M, int N, int K, int epilogue, void* work, size_t work_bytes,
                      void* stream);
 
+/* Batched decode (2 <= M <= 16 rows) on the bf16 matrix cores over the same
+ * tile-major weights (qlm_mx_swizzle, group 32), weights streamed from
+ * registers: each 64-column fragment regrouped by lane swaps into its two
+ * scale groups, bf16-exact, against the activation split into bf16 hi + lo
+ * (loaded with the weights, times 1 + norm_w for the RMSNorm prologue); K split into slices whose partial sums are then added in order
+ * with the epilogue applied (a second launch). Same semantics and epilogues
+ * as qlm_matmul_i8 (~1e-6 normwise); K a multiple of 64; QLM_ERR_SHAPE for
+ * other groups, K or M > 16. work: qlm_matmul_i8_t_workspace_bytes(M, N,
+ * K, epilogue) bytes (slice partial sums of the launch shape it picks), no
+ * initial contents needed; calls sharing it must be ordered on one stream.
+ * _config takes the launch shape (waves, tiles per workgroup, ring slots, K
+ * slices; work then holds slices x M x N (x 2 for SwiGLU) floats); built shapes
+ * (4,4,2) (4,2,3) (8,2,2) (8,4,2) (4,8,1), others QLM_ERR_ARG; slices of
+ * more than 64 blocks QLM_ERR_SHAPE. */
+size_t qlm_matmul_i8_t_workspace_bytes(int M, int N, int K, int epilogue);
+int qlm_matmul_i8_t(const float* x, int ldx, const float* norm_w, float eps,
+                    const int8_t* q_tiles, const float* s_tiles, int group, float* y, int ldy,
+                    int M, int N, int K, int epilogue, void* work, size_t work_bytes,
+                    void* stream);
+int qlm_matmul_i8_t_config(const float* x, int ldx, const float* norm_w, float eps,
+                           const int8_t* q_tiles, const float* s_tiles, int group, float* y,
+                           int ldy, int M, int N, int K, int epilogue, int waves, int tiles,
+                           int ring, int k_slices, void* work, size_t work_bytes, void* stream);
+
 /* Fused forms used by the decode step (same arithmetic as the unfused
  * reference sequence, one launch instead of two or three):
  *   _rmsnorm: x is first replaced by rms_norm(x, norm_w, eps) (zero-centred

@@ -38,13 +38,14 @@ void matmul_native(const Tensor& A, const float* norm_w, float eps, const Tensor
 }  // namespace
 
 bool use_tiles_batched(int64_t M, int64_t N, int64_t K) {
-    return M >= 2 && M <= 8 && (N >= 4096 || K <= 2048);
+    (void)N;
+    return M >= 2 && M <= 16 && K % 64 == 0;
 }
 
 int matmul_launches(int64_t M, int64_t N, int64_t K, bool norm, bool native) {
     if (native) return (int)((M + 15) / 16) * (norm ? 2 : 1);  // row prep + matmul per 16 rows
     if (M == 1) return 1;
-    if (use_tiles_batched(M, N, K)) return 2;  // digits + matmul
+    if (use_tiles_batched(M, N, K)) return 2;  // matmul + ordered reduction
     if (M < kMfmaMinRows) return (int)((M + 3) / 4);
     (void)norm;  // row norms are folded into the reduction (or precede a direct store)
     return 2;    // split-K matmul + ordered reduction
@@ -84,6 +85,21 @@ bool gemm_tiles(const Tensor& A, const float* norm_w, float eps, const Tensor& B
                 int64_t ldc, int64_t N, int epilogue) {
     const int64_t M = A.rows(), K = A.cols();
     if (!use_tiles_batched(M, N, K) || !B.int8_tiles) return false;
+    if (B.int8_group == 32) {  // weights streamed from registers on the bf16 matrix cores
+        const size_t need_t = qlm_matmul_i8_t_workspace_bytes((int)M, (int)N, (int)K, epilogue);
+        need(g_mm_work && g_mm_work_bytes >= need_t,
+             "matmul: batched rows need set_matmul_workspace() of qlm_matmul_i8_t_workspace_bytes()");
+        const int rt = qlm_matmul_i8_t(A.data, (int)A.row_stride(), norm_w, eps, B.int8_tiles,
+                                       B.int8_tile_scales, B.int8_group, C, (int)ldc, (int)M,
+                                       (int)N, (int)K, epilogue, g_mm_work, g_mm_work_bytes,
+                                       g_stream);
+        if (rt != QLM_ERR_SHAPE) {
+            check(rt, "qlm_matmul_i8_t");
+            return true;
+        }
+    }
+    // per-row scales: the int8 digit form, up to 8 rows
+    if (M > 8 || (N < 4096 && K > 2048)) return false;
     const size_t need_b = qlm_matmul_i8_mx_workspace_bytes((int)M, (int)K);
     need(g_mm_work && g_mm_work_bytes >= need_b,
          "matmul: batched rows need set_matmul_workspace() of qlm_matmul_i8_mx_workspace_bytes()");

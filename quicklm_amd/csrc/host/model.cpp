@@ -520,6 +520,7 @@ size_t DecoderModel::matmul_workspace(int M) const {
     auto upd = [&](int N, int K, int epi) {
         b = std::max(b, qlm_matmul_i8_workspace_bytes(M, N, K, epi));
         if (M <= 16) b = std::max(b, qlm_matmul_i8_mx_workspace_bytes(M, K));
+        if (M >= 2) b = std::max(b, qlm_matmul_i8_t_workspace_bytes(std::min(M, 16), N, K, epi));
         b = std::max(b, qlm_matmul_w_workspace_bytes(K));
     };
     if (PD_ > 0) {

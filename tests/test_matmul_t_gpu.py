@@ -1,0 +1,122 @@
+"""Batched decode matmul on the bf16 matrix cores over tile-major weights
+(qlm_matmul_i8_t): the weights streamed from registers, regrouped by lane
+swaps into their scale groups; activations split into bf16 hi + lo.
+
+Bars: within 1e-5 normwise of the fp32 oracle (orc_matmul_i8, bit-exact with
+the reference's int8 matmul) for every epilogue, launch shape and K slicing;
+bit-exact on small-integer activations with power-of-two scales, where every
+product and sum is exact.
+"""
+
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from tests.test_kernels_gpu import _mx_layout, _weights, dev
+from tests.util import rel_err, say
+
+pytestmark = pytest.mark.gpu
+
+EPI = {"store": 0, "store_norm": 0, "resid": 1, "swiglu_norm": 2}
+CASES = [  # (M, N, K)
+    (2, 300, 1024), (3, 517, 2560), (16, 2560, 9728), (16, 1000, 2560), (16, 77, 3584),
+    (7, 300, 512), (12, 130, 2560), (16, 2560, 2048), (5, 40, 64),
+]
+SHAPES = [(4, 4, 2), (4, 2, 3), (8, 2, 2), (8, 4, 2), (4, 8, 1)]
+
+
+def _case(hip, orc, rng, M, N, K, epi, eps=1e-6):
+    rows_w = 2 * N if epi.startswith("swiglu") else N
+    q, s = _weights(orc, rng, rows_w, K, 32)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    nw = (rng.standard_normal(K) * 0.02).astype(np.float32)
+    ldy = N + 5
+    y0 = rng.standard_normal((M, ldy)).astype(np.float32)
+    lg = orc.matmul_i8(orc.rms_norm(x, nw, eps) if epi.endswith("norm") else x, q, s, 32)
+    if epi == "resid":
+        ref = y0[:, :N] + lg
+    elif epi.startswith("store"):
+        ref = lg
+    else:
+        ref = orc.silu_mul(lg[:, :N].copy(), lg[:, N:].copy())
+    dq, ds, keep = _mx_layout(hip, q, s, 32, N, K, 2 if epi.startswith("swiglu") else 1)
+    return dict(x=dev(hip, x), nw=dev(hip, nw) if epi.endswith("norm") else None, dq=dq, ds=ds,
+                keep=keep, y0=y0, ldy=ldy, ref=ref)
+
+
+def _check(hip, c, M, N):
+    y = c["dy"].to_numpy((M, c["ldy"]), np.float32)
+    assert np.array_equal(y[:, N:], c["y0"][:, N:])  # the stride gap is untouched
+    return rel_err(y[:, :N], c["ref"])
+
+
+@pytest.mark.parametrize("M,N,K", CASES)
+@pytest.mark.parametrize("epi", ["store", "store_norm", "resid", "swiglu_norm"])
+def test_matmul_t(hip, orc, rng, M, N, K, epi):
+    c = _case(hip, orc, rng, M, N, K, epi)
+    nwork = hip.lib().qlm_matmul_i8_t_workspace_bytes(M, N, K, EPI[epi])
+    work = hip.DeviceBuffer(nwork)
+    work.upload(np.full(nwork, 0x5A, np.uint8))  # no initial contents are required
+    c["dy"] = dev(hip, c["y0"])
+    say("matmul_t", epi, M, N, K)
+    hip.call("qlm_matmul_i8_t", c["x"], K, c["nw"], 1e-6, c["dq"], c["ds"], 32, c["dy"],
+             c["ldy"], M, N, K, EPI[epi], work, nwork, None)
+    err = _check(hip, c, M, N)
+    assert err < 1e-5, (epi, M, N, K, err)
+
+
+@pytest.mark.parametrize("epi", ["store_norm", "resid", "swiglu_norm"])
+def test_matmul_t_shapes(hip, orc, rng, epi):
+    """Every built launch shape and several K slicings, including slices
+    with fewer blocks than waves and a ragged last slice."""
+    M, N, K = 16, 200, 2560  # 40 blocks
+    c = _case(hip, orc, rng, M, N, K, epi)
+    rows_w = 2 * N if epi.startswith("swiglu") else N
+    nwork = (K // 64) * M * rows_w * 4  # one block per slice at most
+    work = hip.DeviceBuffer(nwork)
+    for nw_, nt, p in SHAPES:
+        for ks in (3, 4, 7, 13, 40):
+            c["dy"] = dev(hip, c["y0"])
+            say("matmul_t_config", epi, nw_, nt, p, ks)
+            hip.call("qlm_matmul_i8_t_config", c["x"], K, c["nw"], 1e-6, c["dq"], c["ds"], 32,
+                     c["dy"], c["ldy"], M, N, K, EPI[epi], nw_, nt, p, ks, work, nwork, None)
+            err = _check(hip, c, M, N)
+            assert err < 1e-5, (epi, nw_, nt, p, ks, err)
+
+
+def test_matmul_t_exact_integers(hip, orc, rng):
+    """Small-integer activations are exact in bf16 (lo = 0) and power-of-two
+    scales keep every product and sum exact: bit-identical to the oracle."""
+    M, N, K = 16, 300, 2048
+    q = rng.integers(-127, 128, (N, K), dtype=np.int8)
+    s = (2.0 ** rng.integers(-8, -2, (N, K // 32))).astype(np.float32)
+    x = rng.integers(-16, 17, (M, K)).astype(np.float32)
+    ref = orc.matmul_i8(x, q, s, 32)
+    dq, ds, keep = _mx_layout(hip, q, s, 32, N, K, 1)
+    nwork = hip.lib().qlm_matmul_i8_t_workspace_bytes(M, N, K, 0)
+    work = hip.DeviceBuffer(nwork)
+    dy = hip.DeviceBuffer(M * N * 4)
+    hip.call("qlm_matmul_i8_t", dev(hip, x), K, None, 0.0, dq, ds, 32, dy, N, M, N, K, 0, work,
+             nwork, None)
+    assert np.array_equal(dy.to_numpy((M, N), np.float32), ref)
+
+
+def test_matmul_t_refuses(hip, orc, rng):
+    """M > 16, K not a multiple of 64, group K, an unbuilt shape and a slice
+    longer than 64 blocks return an error before any launch."""
+    lib = hip.lib()
+    q, s = _weights(orc, rng, 64, 4096, 32)
+    dq, ds = dev(hip, q), dev(hip, s)
+    x = dev(hip, rng.standard_normal((17, 4096)).astype(np.float32))
+    y = hip.DeviceBuffer(17 * 64 * 4)
+    work = hip.DeviceBuffer(1 << 22)
+    for M, K, g in ((17, 2560, 32), (4, 2560 + 32, 32), (4, 2560, 2560)):
+        assert lib.qlm_matmul_i8_t(x.ptr, K, None, C.c_float(0.0), dq.ptr, ds.ptr, g, y.ptr, 64,
+                                   M, 64, K, 0, work.ptr, C.c_size_t(1 << 22), None) != 0
+    assert lib.qlm_matmul_i8_t_config(x.ptr, 4096, None, C.c_float(0.0), dq.ptr, ds.ptr, 32,
+                                      y.ptr, 64, 4, 64, 4096, 0, 4, 3, 2, 8, work.ptr,
+                                      C.c_size_t(1 << 22), None) != 0
+    assert lib.qlm_matmul_i8_t_config(x.ptr, 4160, None, C.c_float(0.0), dq.ptr, ds.ptr, 32,
+                                      y.ptr, 64, 4, 64, 4160, 0, 4, 4, 2, 1, work.ptr,
+                                      C.c_size_t(1 << 22), None) != 0  # 65-block slice
