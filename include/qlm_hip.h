@@ -181,7 +181,8 @@ int qlm_matmul_i8_mx(const float* x, int ldx, const float* norm_w, float eps,
  * initial contents needed; calls sharing it must be ordered on one stream.
  * _config takes the launch shape (waves, tiles per workgroup, ring slots, K
  * slices; work then holds slices x M x N (x 2 for SwiGLU) floats); built shapes
- * (4,4,2) (4,2,3) (8,2,2) (8,4,2) (4,8,1), others QLM_ERR_ARG; slices of
+ * (4,4,2) (4,2,3) (8,2,2) (8,4,2) (4,8,1) (4,8,2) (8,8,1), others QLM_ERR_ARG;
+ * slices of
  * more than 64 blocks QLM_ERR_SHAPE. */
 size_t qlm_matmul_i8_t_workspace_bytes(int M, int N, int K, int epilogue);
 int qlm_matmul_i8_t(const float* x, int ldx, const float* norm_w, float eps,

@@ -207,8 +207,8 @@ struct TTuned {
 };
 constexpr TTuned kTTuned[] = {
     {9728, 2560, EPI_SWIGLU, {4, 8, 1, 5}},  // gate/up: 21.5 us (split-K 28.2)
-    {2560, 9728, EPI_RESID, {4, 4, 2, 19}},  // down: 13.9 us (16.3)
-    {8224, 2560, EPI_STORE, {4, 8, 1, 13}},  // DeltaNet in-projection: 16.1 us (17.7)
+    {2560, 9728, EPI_RESID, {8, 8, 1, 10}},  // down: 13.2 us (16.2)
+    {8224, 2560, EPI_STORE, {8, 8, 1, 3}},   // DeltaNet in-projection: 15.4 us (17.5)
     {5120, 2560, EPI_STORE, {8, 4, 2, 3}},   // attention q/k/v: 11.3 us (14.0)
     {2560, 2048, EPI_RESID, {8, 2, 2, 2}},   // output projections: 7.2 us (7.9)
     {151936, 2560, EPI_STORE, {4, 8, 1, 1}}, // lm_head: 110 us (180)
@@ -261,6 +261,8 @@ int launch_t_shape(const TConfig& c, const float* x, int ldx, const float* gain,
     QLM_T(8, 2, 2)
     QLM_T(8, 4, 2)
     QLM_T(4, 8, 1)
+    QLM_T(4, 8, 2)
+    QLM_T(8, 8, 1)
 #undef QLM_T
     return QLM_ERR_ARG;
 }

@@ -23,7 +23,7 @@ CASES = [  # (M, N, K)
     (2, 300, 1024), (3, 517, 2560), (16, 2560, 9728), (16, 1000, 2560), (16, 77, 3584),
     (7, 300, 512), (12, 130, 2560), (16, 2560, 2048), (5, 40, 64),
 ]
-SHAPES = [(4, 4, 2), (4, 2, 3), (8, 2, 2), (8, 4, 2), (4, 8, 1)]
+SHAPES = [(4, 4, 2), (4, 2, 3), (8, 2, 2), (8, 4, 2), (4, 8, 1), (4, 8, 2), (8, 8, 1)]
 
 
 def _case(hip, orc, rng, M, N, K, epi, eps=1e-6):
