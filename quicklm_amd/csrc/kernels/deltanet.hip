@@ -27,6 +27,7 @@ constexpr int kRowsPer = kD / kRowGroups;      // 8
 
 struct DnShared {
     float q[kD], k[kD], v[kD];
+    float pad[kD];  // conv results of the threads past the 3d channels (unused)
     float red[kRowGroups][kD];
     float vec[kD];
     float scal[8];
@@ -151,35 +152,37 @@ __global__ __launch_bounds__(kThreads) void k_deltanet_decode(
     float* cs = conv_state + (size_t)b * 3 * C;
     float* Sh = state + ((size_t)b * H + h) * kD * kD;
 
-    float4 s[kRowsPer];
-    dn_load_state(Sh, s);
+    // The small operands are requested first, then the 64 KiB state slice:
+    // loads complete in order, so the conv, norms and gates below wait only
+    // for their own operands while the state is still arriving. Every load
+    // is unconditional (clamped index; unused values are dropped), since a
+    // load under a branch is waited for where the branch ends.
     const int pb = pos ? pos[b] : 0;
     // conv operands: channel ch = sec*HD + h*d + t for tid < 3d
     const bool conv_t = tid < 3 * kD;
     const int sec = tid / kD, t = tid % kD;
-    const int ch = sec * HD + h * kD + t;
-    float ring[3], w4[4], xin = 0.0f;
+    const int ch = conv_t ? sec * HD + h * kD + t : h * kD + t;
+    float ring[3], w4[4];
 #pragma unroll
-    for (int j = 0; j < 3; ++j) ring[j] = conv_t ? cs[(size_t)j * C + ch] : 0.0f;
+    for (int j = 0; j < 3; ++j) ring[j] = cs[(size_t)j * C + ch];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) w4[j] = conv_t ? wt[(size_t)j * C + ch] : 0.0f;
-    if (conv_t) xin = pr[ch];
-    // gate operands (wave 2, lane 0) and the output gate / gain (waves 0-1)
-    float ga = 0.0f, gb = 0.0f, gdt = 0.0f, galog = 0.0f;
-    if (wave == 2 && lane == 0) {
-        ga = pr[4 * HD + H + h];
-        gb = pr[4 * HD + h];
-        gdt = dt_bias[h];
-        galog = A_log[h];
-    }
-    float zj = 0.0f, nwj = 0.0f;
-    if (tid < kD) {
-        zj = pr[3 * HD + h * kD + tid];
-        nwj = norm_w[tid];
-    }
+    for (int j = 0; j < 4; ++j) w4[j] = wt[(size_t)j * C + ch];
+    const float xin = pr[ch];
+    // gate operands (used by wave 2, lane 0) and the output gate / gain
+    // (used by waves 0-1)
+    const float ga = pr[4 * HD + H + h], gb = pr[4 * HD + h];
+    const float gdt = dt_bias[h], galog = A_log[h];
+    const float zj = pr[3 * HD + h * kD + (tid & (kD - 1))];
+    const float nwj = norm_w[tid & (kD - 1)];
+    float4 s[kRowsPer];
+    dn_load_state(Sh, s);
 
-    // conv1d (kernel 4, taps chronological from the oldest ring row) + SiLU
-    if (conv_t) {
+    // conv1d (kernel 4, taps chronological from the oldest ring row) + SiLU,
+    // computed and stored to LDS by every thread (the others into a pad row),
+    // so that no branch holds the operand loads, which the compiler would
+    // otherwise sink behind the state's; the conv ring is updated by the 3d
+    // conv threads
+    {
         const int oldest = pb % 3;
         float acc = 0.0f;
 #pragma unroll
@@ -189,11 +192,10 @@ __global__ __launch_bounds__(kThreads) void k_deltanet_decode(
             acc = nc_add_mul(acc, rv, w4[j]);
         }
         acc = nc_add_mul(acc, xin, w4[3]);
-        cs[(size_t)oldest * C + ch] = xin;
         const float y = silu_f(acc);
-        if (sec == 0) sh.q[t] = y;
-        else if (sec == 1) sh.k[t] = y;
-        else sh.v[t] = y;
+        float* dst = !conv_t ? sh.pad : sec == 0 ? sh.q : sec == 1 ? sh.k : sh.v;
+        dst[t] = y;
+        if (conv_t) cs[(size_t)oldest * C + ch] = xin;
     }
     __syncthreads();
 
