@@ -418,7 +418,8 @@ def main():
             rn = run_decode(en, prompts[:1], args.warmup, args.steps, graph)
             rn["weight_bytes"] = en.weight_bytes
             log(f"batch 1, native weights: {rn['tok_s']:.1f} tok/s "
-                f"({rn['ms_per_step']:.3f} ms/step), {rn['weight_bytes'] / 1e9:.3f} GB")
+                f"({rn['ms_per_step']:.3f} ms/step), {rn['weight_bytes'] / 1e9:.3f} GB, "
+                f"prefill {rn['prefill_s']:.3f}s")
 
         spec = []
         if not args.skip_spec and not args.skip_int4:
@@ -493,6 +494,7 @@ def main():
             "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / r4["weight_bytes"], 1)},
         "native": None if rn is None else {
             "tok_s": round(rn["tok_s"], 2), "ms_per_step": round(rn["ms_per_step"], 4),
+            "prefill_s": round(rn["prefill_s"], 4),
             "batch": 1, "precision": "bf16 (weights as stored: bf16 linears, fp32 tied lm_head)",
             "weight_bytes": rn["weight_bytes"],
             "frac_of_weight_roofline": round(

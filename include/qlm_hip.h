@@ -413,11 +413,24 @@ int qlm_lm_head_greedy_mx4(const float* x, const float* norm_w, float eps,
  * :820-900). Replaces those branches: y = x . W^T on the fp32 matrix cores
  * (bf16 widened exactly), fp32 accumulation. W [N, K] row-major fp32
  * (w_bf16 = 0) or bf16 bits (w_bf16 = 1); x [M, ldx], y [M, ldy], any M (16
- * rows per launch). norm_w / epilogue as qlm_matmul_i8 (RMSNorm prologue:
+ * rows per launch; bf16 rows with M > 16 go to qlm_matmul_bf16, whose
+ * workspace must then fit as well). norm_w / epilogue as qlm_matmul_i8
+ * (RMSNorm prologue:
  * the row scale multiplies the finished sums; SwiGLU: W is [2N, K], gate
  * rows then up rows; it needs norm_w); work holds
  * qlm_matmul_w_workspace_bytes(K) bytes when norm_w is given. K a multiple
  * of 16; x, W, norm_w 16-byte aligned. */
+/* bf16 weight rows (no scales) with many activation rows, the prefill form:
+ * 128 x 64 output tiles on the bf16 matrix cores, the weights staged through
+ * LDS as they are, the activation split into bf16 hi + lo (2^-17 of x), the
+ * MFMAs chained over K in fp32. Same arguments and epilogues as
+ * qlm_matmul_w (which calls it for bf16 weights and M > 16); work holds
+ * qlm_matmul_bf16_workspace_bytes(M) bytes (the RMSNorm row scales) when
+ * norm_w is given. K a multiple of 32. */
+size_t qlm_matmul_bf16_workspace_bytes(int M);
+int qlm_matmul_bf16(const float* x, int ldx, const float* norm_w, float eps, const uint16_t* w,
+                    float* y, int ldy, int M, int N, int K, int epilogue, void* work,
+                    size_t work_bytes, void* stream);
 size_t qlm_matmul_w_workspace_bytes(int K);
 int qlm_matmul_w(const float* x, int ldx, const float* norm_w, float eps, const void* w,
                  int w_bf16, float* y, int ldy, int M, int N, int K, int epilogue, void* work,

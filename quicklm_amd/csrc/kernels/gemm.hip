@@ -95,7 +95,10 @@ __device__ __forceinline__ void store_w16(unsigned short* dst, int4 w) {
     reinterpret_cast<uint4*>(dst)[1] = o[1];
 }
 
-template <int WM, int WN, int WK, int TM, int TN, bool ROWSCALE, int EPI, bool NORM>
+// WB16: the weights are bf16 rows (the native --precision bf16 form, no
+// scales): copied to LDS as they are, the MFMAs chained over K.
+template <int WM, int WN, int WK, int TM, int TN, bool ROWSCALE, int EPI, bool NORM,
+          bool WB16 = false>
 __global__ __launch_bounds__(kThreads) void k_mm_i8(const float* __restrict__ x, int ldx,
                                                     const float* __restrict__ rs,
                                                     const float* __restrict__ nw,
@@ -161,6 +164,7 @@ __global__ __launch_bounds__(kThreads) void k_mm_i8(const float* __restrict__ x,
     float4 gr[NORM ? XPT : 1];  // RMSNorm gain of the same columns
     float rr[NORM ? XPT : 1];   // RMSNorm row scale
     int4 wr[WPT];
+    int4 wr2[WB16 ? WPT : 1];  // bf16 rows: the second 16 bytes of a unit
     float sr[TN];
     auto load_chunk = [&](int c) {
         const int k0 = c * KC;
@@ -182,10 +186,17 @@ __global__ __launch_bounds__(kThreads) void k_mm_i8(const float* __restrict__ x,
             const int i = tid + u * kThreads;
             if (i < WV) {
                 const int r = i / (KC / 16), c16 = i % (KC / 16);
-                wr[u] = *reinterpret_cast<const int4*>(q + (size_t)w_row(r) * K + k0 + c16 * 16);
+                if constexpr (WB16) {
+                    const int4* p = reinterpret_cast<const int4*>(
+                        reinterpret_cast<const uint16_t*>(q) + (size_t)w_row(r) * K + k0 + c16 * 16);
+                    wr[u] = p[0];
+                    wr2[u] = p[1];
+                } else {
+                    wr[u] = *reinterpret_cast<const int4*>(q + (size_t)w_row(r) * K + k0 + c16 * 16);
+                }
             }
         }
-        if constexpr (!ROWSCALE) {
+        if constexpr (!ROWSCALE && !WB16) {
             const int g = (k0 >> 5) + kw;
 #pragma unroll
             for (int tn = 0; tn < TN; ++tn)
@@ -217,7 +228,12 @@ __global__ __launch_bounds__(kThreads) void k_mm_i8(const float* __restrict__ x,
 #pragma unroll
         for (int u = 0; u < WPT; ++u) {
             const int i = tid + u * kThreads;
-            if (i < WV) {
+            if (i < WV && WB16) {
+                const int r = i / (KC / 16), c16 = i % (KC / 16);
+                uint4* dst = reinterpret_cast<uint4*>(&ws[r * WP + c16 * 16]);
+                dst[0] = __builtin_bit_cast(uint4, wr[u]);
+                dst[1] = __builtin_bit_cast(uint4, wr2[WB16 ? u : 0]);
+            } else if (i < WV) {
                 const int r = i / (KC / 16), c16 = i % (KC / 16);
                 const int wv[4] = {wr[u].x, wr[u].y, wr[u].z, wr[u].w};
                 uint4 o[2];
@@ -268,7 +284,7 @@ __global__ __launch_bounds__(kThreads) void k_mm_i8(const float* __restrict__ x,
         for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
             for (int tn = 0; tn < TN; ++tn) {
-                if constexpr (ROWSCALE) {
+                if constexpr (ROWSCALE || WB16) {
                     acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[tm], bw[tn], acc[tm][tn], 0, 0, 0);
                     acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[tm], bw[tn], acc[tm][tn], 0, 0, 0);
                 } else {
@@ -306,7 +322,7 @@ __global__ __launch_bounds__(kThreads) void k_mm_i8(const float* __restrict__ x,
                     for (int i = 0; i < 4; ++i) acc[tm][tn][i] += o[i];
                 }
     }
-    if constexpr (ROWSCALE) {
+    if constexpr (ROWSCALE && !WB16) {
 #pragma unroll
         for (int tn = 0; tn < TN; ++tn) {
             const float s = sc[w_row(tile_row(tn) + (lane & 15))];
@@ -594,6 +610,18 @@ int launch_mm(const float* x, int ldx, const float* rs, const float* nw, const i
     return qlm_launch_status();
 }
 
+template <int EPI, bool NORM>
+int launch_mm16(const float* x, int ldx, const float* rs, const float* nw, const uint16_t* w,
+                float* y, int ldy, int M, int N, int K, hipStream_t st) {
+    constexpr int BM = 2 * 4 * 16;
+    constexpr int BN_OUT = 2 * (EPI == EPI_SWIGLU ? 2 : 4) * 16;
+    const dim3 grid((N + BN_OUT - 1) / BN_OUT, (M + BM - 1) / BM);
+    hipLaunchKernelGGL((k_mm_i8<2, 2, 1, 4, 4, false, EPI, NORM, true>), grid, dim3(kThreads), 0,
+                       st, x, ldx, rs, nw, reinterpret_cast<const int8_t*>(w), nullptr, y, ldy,
+                       M, N, K, N);
+    return qlm_launch_status();
+}
+
 template <bool RS, bool NORM>
 int mm_run(const float* x, int ldx, float* rs, const float* nw, float eps, const int8_t* q,
            const float* sc, float* y, int ldy, int M, int N, int K, int epi, float* part,
@@ -642,6 +670,36 @@ int mm_run(const float* x, int ldx, float* rs, const float* nw, float eps, const
 extern "C" size_t qlm_matmul_i8_workspace_bytes(int M, int N, int K, int epilogue) {
     if (M <= 0 || N <= 0 || K <= 0 || epilogue < EPI_STORE || epilogue > EPI_SWIGLU) return 0;
     return mm_workspace(M, N, K, epilogue);
+}
+
+extern "C" size_t qlm_matmul_bf16_workspace_bytes(int M) {
+    return M <= 0 ? 0 : align256((size_t)M * sizeof(float));
+}
+
+extern "C" int qlm_matmul_bf16(const float* x, int ldx, const float* norm_w, float eps,
+                               const uint16_t* w, float* y, int ldy, int M, int N, int K,
+                               int epilogue, void* work, size_t work_bytes, void* stream) {
+    if (!x || !w || !y || M <= 0 || N <= 0 || K <= 0) return QLM_ERR_ARG;
+    if (epilogue < EPI_STORE || epilogue > EPI_SWIGLU) return QLM_ERR_ARG;
+    if (epilogue == EPI_SWIGLU && !norm_w) return QLM_ERR_ARG;
+    if (epilogue == EPI_RESID && norm_w) return QLM_ERR_ARG;
+    if (K % 32 != 0 || ldx < K || ldx % 4 != 0 || ldy < N) return QLM_ERR_SHAPE;
+    if (((uintptr_t)x | (uintptr_t)w | (uintptr_t)norm_w) & 15u) return QLM_ERR_SHAPE;
+    hipStream_t st = as_stream(stream);
+    float* rs = nullptr;
+    if (norm_w) {
+        if (!work || work_bytes < qlm_matmul_bf16_workspace_bytes(M)) return QLM_ERR_ARG;
+        rs = static_cast<float*>(work);
+        hipLaunchKernelGGL(k_row_rs, dim3(M), dim3(kThreads), 0, st, x, ldx, K, eps, rs);
+        const int rc = qlm_launch_status();
+        if (rc != QLM_OK) return rc;
+    }
+    if (epilogue == EPI_SWIGLU)
+        return launch_mm16<EPI_SWIGLU, true>(x, ldx, rs, norm_w, w, y, ldy, M, N, K, st);
+    if (epilogue == EPI_RESID)
+        return launch_mm16<EPI_RESID, false>(x, ldx, nullptr, nullptr, w, y, ldy, M, N, K, st);
+    if (norm_w) return launch_mm16<EPI_STORE, true>(x, ldx, rs, norm_w, w, y, ldy, M, N, K, st);
+    return launch_mm16<EPI_STORE, false>(x, ldx, nullptr, nullptr, w, y, ldy, M, N, K, st);
 }
 
 extern "C" int qlm_matmul_i8(const float* x, int ldx, const float* norm_w, float eps,

@@ -604,6 +604,9 @@ extern "C" int qlm_matmul_w(const float* x, int ldx, const float* norm_w, float 
                    ((uintptr_t)work & 15u)))
         return QLM_ERR_ARG;
     hipStream_t st = as_stream(stream);
+    if (w_bf16 && M > kWRows && K % 32 == 0)  // bf16 rows, many rows: the tiled GEMM
+        return qlm_matmul_bf16(x, ldx, norm_w, eps, static_cast<const uint16_t*>(w), y, ldy, M, N,
+                               K, epilogue, work, work_bytes, stream);
     if (M == 1) {  // one row: the vector-ALU GEMV (QLM_ERR_SHAPE: K too long for it)
         const int rc = w_bf16 ? wv_auto<uint16_t>(x, norm_w, eps, static_cast<const uint16_t*>(w),
                                                   y, N, K, epilogue, st)

@@ -40,7 +40,8 @@ def _run(hip, epi, x, ldx, w, nw, y0, ldy, M, N, K, eps):
     yp[:, :N] = y0
     dx, dy, dw = dev(hip, xp), dev(hip, yp), dev(hip, w)
     dnw = dev(hip, nw) if epi in ("norm", "swiglu") else None
-    wb = hip.lib().qlm_matmul_w_workspace_bytes(K)
+    wb = max(hip.lib().qlm_matmul_w_workspace_bytes(K),
+             hip.lib().qlm_matmul_bf16_workspace_bytes(M))
     work = hip.DeviceBuffer(wb) if dnw is not None else None
     hip.call("qlm_matmul_w", dx, ldx, dnw, eps, dw, 1 if w.dtype == np.uint16 else 0, dy, ldy,
              M, N, K, EPI[epi], work, wb if work is not None else 0, None)
@@ -49,9 +50,9 @@ def _run(hip, epi, x, ldx, w, nw, y0, ldy, M, N, K, eps):
     return got[:, :N]
 
 
-CASES = [  # (M, N, K)
+CASES = [  # (M, N, K); bf16 rows with M > 16 take the tiled prefill GEMM
     (1, 100, 256), (3, 37, 48), (16, 513, 1040), (20, 200, 2560), (1, 2560, 9728),
-    (5, 16, 16), (17, 1000, 512),
+    (5, 16, 16), (17, 1000, 512), (130, 300, 1024), (300, 70, 512),
 ]
 
 
