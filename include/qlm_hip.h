@@ -424,10 +424,12 @@ int qlm_lm_head_greedy_mx4(const float* x, const float* norm_w, float eps,
  * 128 x 64 output tiles on the bf16 matrix cores, the weights staged through
  * LDS as they are, the activation split into bf16 hi + lo (2^-17 of x), the
  * MFMAs chained over K in fp32. Same arguments and epilogues as
- * qlm_matmul_w (which calls it for bf16 weights and M > 16); work holds
- * qlm_matmul_bf16_workspace_bytes(M) bytes (the RMSNorm row scales) when
- * norm_w is given. K a multiple of 32. */
-size_t qlm_matmul_bf16_workspace_bytes(int M);
+ * qlm_matmul_w (which calls it for bf16 weights and M > 16). work: with
+ * qlm_matmul_bf16_workspace_bytes(M, K) bytes the activation is split once
+ * (RMSNorm applied) into bf16 planes there; with less, each workgroup
+ * splits its chunks itself, and then norm_w still needs the first M floats
+ * (row scales). K a multiple of 32. */
+size_t qlm_matmul_bf16_workspace_bytes(int M, int K);
 int qlm_matmul_bf16(const float* x, int ldx, const float* norm_w, float eps, const uint16_t* w,
                     float* y, int ldy, int M, int N, int K, int epilogue, void* work,
                     size_t work_bytes, void* stream);

@@ -522,7 +522,7 @@ size_t DecoderModel::matmul_workspace(int M) const {
         if (M <= 16) b = std::max(b, qlm_matmul_i8_mx_workspace_bytes(M, K));
         if (M >= 2) b = std::max(b, qlm_matmul_i8_t_workspace_bytes(std::min(M, 16), N, K, epi));
         b = std::max(b, qlm_matmul_w_workspace_bytes(K));
-        b = std::max(b, qlm_matmul_bf16_workspace_bytes(M));
+        b = std::max(b, qlm_matmul_bf16_workspace_bytes(M, K));
     };
     if (PD_ > 0) {
         upd(PD_, H, 0);

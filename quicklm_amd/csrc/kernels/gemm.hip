@@ -97,8 +97,11 @@ __device__ __forceinline__ void store_w16(unsigned short* dst, int4 w) {
 
 // WB16: the weights are bf16 rows (the native --precision bf16 form, no
 // scales): copied to LDS as they are, the MFMAs chained over K.
+// XS: x is already split (k_split_rows): x points at the bf16 hi plane
+// [M, ldx] and the lo plane follows it (M * ldx further); any RMSNorm has
+// been applied there, so NORM is false.
 template <int WM, int WN, int WK, int TM, int TN, bool ROWSCALE, int EPI, bool NORM,
-          bool WB16 = false>
+          bool WB16 = false, bool XS = false>
 __global__ __launch_bounds__(kThreads) void k_mm_i8(const float* __restrict__ x, int ldx,
                                                     const float* __restrict__ rs,
                                                     const float* __restrict__ nw,
@@ -165,6 +168,9 @@ __global__ __launch_bounds__(kThreads) void k_mm_i8(const float* __restrict__ x,
     float rr[NORM ? XPT : 1];   // RMSNorm row scale
     int4 wr[WPT];
     int4 wr2[WB16 ? WPT : 1];  // bf16 rows: the second 16 bytes of a unit
+    // XS: hi and lo bf16 quadruples, kept in integer registers (as floats a
+    // pair could read as a denormal and be flushed)
+    uint4 xq[XS ? XPT : 1];
     float sr[TN];
     auto load_chunk = [&](int c) {
         const int k0 = c * KC;
@@ -174,7 +180,15 @@ __global__ __launch_bounds__(kThreads) void k_mm_i8(const float* __restrict__ x,
             if (i < XV) {
                 const int r = i / (KC / 4), c4 = i % (KC / 4);
                 const int m = min(m0 + r, M - 1);
-                xr[u] = *reinterpret_cast<const float4*>(x + (size_t)m * ldx + k0 + c4 * 4);
+                if constexpr (XS) {
+                    const uint16_t* xh = reinterpret_cast<const uint16_t*>(x);
+                    const size_t o = (size_t)m * ldx + k0 + c4 * 4;
+                    const uint2 h = *reinterpret_cast<const uint2*>(xh + o);
+                    const uint2 l = *reinterpret_cast<const uint2*>(xh + (size_t)M * ldx + o);
+                    xq[u] = make_uint4(h.x, h.y, l.x, l.y);
+                } else {
+                    xr[u] = *reinterpret_cast<const float4*>(x + (size_t)m * ldx + k0 + c4 * 4);
+                }
                 if constexpr (NORM) {
                     gr[u] = *reinterpret_cast<const float4*>(nw + k0 + c4 * 4);
                     rr[u] = rs[m];
@@ -207,7 +221,12 @@ __global__ __launch_bounds__(kThreads) void k_mm_i8(const float* __restrict__ x,
 #pragma unroll
         for (int u = 0; u < XPT; ++u) {
             const int i = tid + u * kThreads;
-            if (i < XV) {
+            if (i < XV && XS) {
+                const int r = i / (KC / 4), c4 = i % (KC / 4);
+                const uint4 v = xq[XS ? u : 0];
+                *reinterpret_cast<uint2*>(&xs_hi[r * XP + c4 * 4]) = make_uint2(v.x, v.y);
+                *reinterpret_cast<uint2*>(&xs_lo[r * XP + c4 * 4]) = make_uint2(v.z, v.w);
+            } else if (i < XV) {
                 const int r = i / (KC / 4), c4 = i % (KC / 4);
                 float4 v = xr[u];
                 if constexpr (NORM) v = norm4(v, rr[u], gr[u]);
@@ -541,6 +560,47 @@ __global__ __launch_bounds__(kThreads) void k_row_rs(const float* __restrict__ x
     if (threadIdx.x == 0) rs[blockIdx.x] = 1.0f / sqrtf(ss / (float)K + eps);
 }
 
+// The activation of the prefill GEMM split once into bf16 hi and lo planes
+// ([M, K] each, the lo plane after the hi one), with the RMSNorm applied when
+// NORM (rs from k_row_rs): the GEMM's workgroups along N then copy them
+// instead of each converting the same chunk again.
+template <bool NORM>
+__global__ __launch_bounds__(kThreads) void k_split_rows(const float* __restrict__ x, int ldx,
+                                                        const float* __restrict__ rs,
+                                                        const float* __restrict__ nw, int M,
+                                                        int K, uint16_t* __restrict__ xh) {
+    const int k4 = K >> 2;
+    const size_t n4 = (size_t)M * k4;
+    for (size_t i = blockIdx.x * (size_t)kThreads + threadIdx.x; i < n4;
+         i += (size_t)gridDim.x * kThreads) {
+        const int m = (int)(i / k4), c4 = (int)(i % k4);
+        float4 v = *reinterpret_cast<const float4*>(x + (size_t)m * ldx + c4 * 4);
+        if constexpr (NORM)
+            v = norm4(v, rs[m], *reinterpret_cast<const float4*>(nw + c4 * 4));
+        unsigned short h[4], l[4];
+        split_bf16(v.x, h[0], l[0]);
+        split_bf16(v.y, h[1], l[1]);
+        split_bf16(v.z, h[2], l[2]);
+        split_bf16(v.w, h[3], l[3]);
+        const size_t o = (size_t)m * K + c4 * 4;
+        *reinterpret_cast<uint2*>(xh + o) = make_uint2((unsigned)h[0] | ((unsigned)h[1] << 16),
+                                                       (unsigned)h[2] | ((unsigned)h[3] << 16));
+        *reinterpret_cast<uint2*>(xh + (size_t)M * K + o) =
+            make_uint2((unsigned)l[0] | ((unsigned)l[1] << 16),
+                       (unsigned)l[2] | ((unsigned)l[3] << 16));
+    }
+}
+
+template <bool NORM>
+int launch_split(const float* x, int ldx, const float* rs, const float* nw, int M, int K,
+                 uint16_t* xh, hipStream_t st) {
+    const size_t n4 = (size_t)M * (K >> 2);
+    const size_t g = (n4 + kThreads - 1) / kThreads;
+    hipLaunchKernelGGL(k_split_rows<NORM>, dim3((unsigned)(g < 2048 ? g : 2048)),
+                       dim3(kThreads), 0, st, x, ldx, rs, nw, M, K, xh);
+    return qlm_launch_status();
+}
+
 // K slices for the M <= 64 path: the fewest that divide the 128-column
 // chunk count, leave each workgroup at most 4 chunks (one ring) and give at
 // least ~640 workgroups; a tall matrix (>= 1024 row tiles) is one slice.
@@ -566,6 +626,8 @@ size_t mm_workspace(int M, int N, int K, int epi) {
         const int NR = epi == EPI_SWIGLU ? 2 * N : N;
         const int ks = sk_splits(NR, K);
         if (!(ks == 1 && epi == EPI_STORE)) b += (size_t)ks * M * NR * sizeof(float);
+    } else {
+        b += align256((size_t)4 * M * K);  // the split activation (bf16 hi, lo)
     }
     return b;
 }
@@ -599,25 +661,25 @@ void launch_reduce(const float* part, int ks, int M, int NR, int N, float* y, in
                        y, ldy, x, ldx, K, eps);
 }
 
-template <int WM, int WN, int WK, int TM, int TN, bool RS, int EPI, bool NORM>
+template <int WM, int WN, int WK, int TM, int TN, bool RS, int EPI, bool NORM, bool XS = false>
 int launch_mm(const float* x, int ldx, const float* rs, const float* nw, const int8_t* q,
               const float* sc, float* y, int ldy, int M, int N, int K, hipStream_t st) {
     constexpr int BM = WM * TM * 16;
     constexpr int BN_OUT = WN * (EPI == EPI_SWIGLU ? TN / 2 : TN) * 16;
     const dim3 grid((N + BN_OUT - 1) / BN_OUT, (M + BM - 1) / BM);
-    hipLaunchKernelGGL((k_mm_i8<WM, WN, WK, TM, TN, RS, EPI, NORM>), grid, dim3(kThreads), 0, st,
-                       x, ldx, rs, nw, q, sc, y, ldy, M, N, K, N);
+    hipLaunchKernelGGL((k_mm_i8<WM, WN, WK, TM, TN, RS, EPI, NORM, false, XS>), grid,
+                       dim3(kThreads), 0, st, x, ldx, rs, nw, q, sc, y, ldy, M, N, K, N);
     return qlm_launch_status();
 }
 
-template <int EPI, bool NORM>
+template <int EPI, bool NORM, bool XS>
 int launch_mm16(const float* x, int ldx, const float* rs, const float* nw, const uint16_t* w,
                 float* y, int ldy, int M, int N, int K, hipStream_t st) {
     constexpr int BM = 2 * 4 * 16;
     constexpr int BN_OUT = 2 * (EPI == EPI_SWIGLU ? 2 : 4) * 16;
     const dim3 grid((N + BN_OUT - 1) / BN_OUT, (M + BM - 1) / BM);
-    hipLaunchKernelGGL((k_mm_i8<2, 2, 1, 4, 4, false, EPI, NORM, true>), grid, dim3(kThreads), 0,
-                       st, x, ldx, rs, nw, reinterpret_cast<const int8_t*>(w), nullptr, y, ldy,
+    hipLaunchKernelGGL((k_mm_i8<2, 2, 1, 4, 4, false, EPI, NORM, true, XS>), grid, dim3(kThreads),
+                       0, st, x, ldx, rs, nw, reinterpret_cast<const int8_t*>(w), nullptr, y, ldy,
                        M, N, K, N);
     return qlm_launch_status();
 }
@@ -658,11 +720,19 @@ int mm_run(const float* x, int ldx, float* rs, const float* nw, float eps, const
         const int rc = qlm_launch_status();
         if (rc != QLM_OK) return rc;
     }
+    // the activation split once (RMSNorm applied), then the GEMM copies it
+    uint16_t* xh = reinterpret_cast<uint16_t*>(part);
+    const int rc = launch_split<NORM>(x, ldx, rs, nw, M, K, xh, st);
+    if (rc != QLM_OK) return rc;
+    const float* xs = reinterpret_cast<const float*>(xh);
     if (epi == EPI_STORE)
-        return launch_mm<2, 2, 1, 4, 4, RS, EPI_STORE, NORM>(x, ldx, rs, nw, q, sc, y, ldy, M, N, K, st);
+        return launch_mm<2, 2, 1, 4, 4, RS, EPI_STORE, false, true>(xs, K, nullptr, nullptr, q, sc,
+                                                                    y, ldy, M, N, K, st);
     if (epi == EPI_RESID)
-        return launch_mm<2, 2, 1, 4, 4, RS, EPI_RESID, NORM>(x, ldx, rs, nw, q, sc, y, ldy, M, N, K, st);
-    return launch_mm<2, 2, 1, 4, 4, RS, EPI_SWIGLU, NORM>(x, ldx, rs, nw, q, sc, y, ldy, M, N, K, st);
+        return launch_mm<2, 2, 1, 4, 4, RS, EPI_RESID, false, true>(xs, K, nullptr, nullptr, q, sc,
+                                                                    y, ldy, M, N, K, st);
+    return launch_mm<2, 2, 1, 4, 4, RS, EPI_SWIGLU, false, true>(xs, K, nullptr, nullptr, q, sc, y,
+                                                                 ldy, M, N, K, st);
 }
 
 }  // namespace
@@ -672,8 +742,9 @@ extern "C" size_t qlm_matmul_i8_workspace_bytes(int M, int N, int K, int epilogu
     return mm_workspace(M, N, K, epilogue);
 }
 
-extern "C" size_t qlm_matmul_bf16_workspace_bytes(int M) {
-    return M <= 0 ? 0 : align256((size_t)M * sizeof(float));
+extern "C" size_t qlm_matmul_bf16_workspace_bytes(int M, int K) {
+    if (M <= 0 || K <= 0) return 0;
+    return align256((size_t)M * sizeof(float)) + align256((size_t)4 * M * K);
 }
 
 extern "C" int qlm_matmul_bf16(const float* x, int ldx, const float* norm_w, float eps,
@@ -684,22 +755,42 @@ extern "C" int qlm_matmul_bf16(const float* x, int ldx, const float* norm_w, flo
     if (epilogue == EPI_SWIGLU && !norm_w) return QLM_ERR_ARG;
     if (epilogue == EPI_RESID && norm_w) return QLM_ERR_ARG;
     if (K % 32 != 0 || ldx < K || ldx % 4 != 0 || ldy < N) return QLM_ERR_SHAPE;
-    if (((uintptr_t)x | (uintptr_t)w | (uintptr_t)norm_w) & 15u) return QLM_ERR_SHAPE;
+    if (((uintptr_t)x | (uintptr_t)w | (uintptr_t)norm_w | (uintptr_t)work) & 15u)
+        return QLM_ERR_SHAPE;
     hipStream_t st = as_stream(stream);
-    float* rs = nullptr;
+    const size_t rsb = align256((size_t)M * sizeof(float));
+    if (norm_w && (!work || work_bytes < rsb)) return QLM_ERR_ARG;
+    float* rs = static_cast<float*>(work);
     if (norm_w) {
-        if (!work || work_bytes < qlm_matmul_bf16_workspace_bytes(M)) return QLM_ERR_ARG;
-        rs = static_cast<float*>(work);
         hipLaunchKernelGGL(k_row_rs, dim3(M), dim3(kThreads), 0, st, x, ldx, K, eps, rs);
         const int rc = qlm_launch_status();
         if (rc != QLM_OK) return rc;
     }
+    if (work && work_bytes >= qlm_matmul_bf16_workspace_bytes(M, K)) {
+        // the activation split once (RMSNorm applied), then the GEMM copies it
+        uint16_t* xh = reinterpret_cast<uint16_t*>(static_cast<char*>(work) + rsb);
+        const int rc = norm_w ? launch_split<true>(x, ldx, rs, norm_w, M, K, xh, st)
+                              : launch_split<false>(x, ldx, nullptr, nullptr, M, K, xh, st);
+        if (rc != QLM_OK) return rc;
+        const float* xs = reinterpret_cast<const float*>(xh);
+        if (epilogue == EPI_SWIGLU)
+            return launch_mm16<EPI_SWIGLU, false, true>(xs, K, nullptr, nullptr, w, y, ldy, M, N,
+                                                        K, st);
+        if (epilogue == EPI_RESID)
+            return launch_mm16<EPI_RESID, false, true>(xs, K, nullptr, nullptr, w, y, ldy, M, N, K,
+                                                       st);
+        return launch_mm16<EPI_STORE, false, true>(xs, K, nullptr, nullptr, w, y, ldy, M, N, K,
+                                                   st);
+    }
+    // a smaller workspace: each workgroup converts its activation chunks itself
     if (epilogue == EPI_SWIGLU)
-        return launch_mm16<EPI_SWIGLU, true>(x, ldx, rs, norm_w, w, y, ldy, M, N, K, st);
+        return launch_mm16<EPI_SWIGLU, true, false>(x, ldx, rs, norm_w, w, y, ldy, M, N, K, st);
     if (epilogue == EPI_RESID)
-        return launch_mm16<EPI_RESID, false>(x, ldx, nullptr, nullptr, w, y, ldy, M, N, K, st);
-    if (norm_w) return launch_mm16<EPI_STORE, true>(x, ldx, rs, norm_w, w, y, ldy, M, N, K, st);
-    return launch_mm16<EPI_STORE, false>(x, ldx, nullptr, nullptr, w, y, ldy, M, N, K, st);
+        return launch_mm16<EPI_RESID, false, false>(x, ldx, nullptr, nullptr, w, y, ldy, M, N, K,
+                                                    st);
+    if (norm_w)
+        return launch_mm16<EPI_STORE, true, false>(x, ldx, rs, norm_w, w, y, ldy, M, N, K, st);
+    return launch_mm16<EPI_STORE, false, false>(x, ldx, nullptr, nullptr, w, y, ldy, M, N, K, st);
 }
 
 extern "C" int qlm_matmul_i8(const float* x, int ldx, const float* norm_w, float eps,

@@ -103,7 +103,7 @@ _SIGS = {
                                 _vp, _i, _vp, _vp]),
     "qlm_embed_tokens": (_i, [_vp, _i, _i, _vp, _i, _vp, _vp, _i, _i, _vp]),
     "qlm_matmul_w_workspace_bytes": (_sz, [_i]),
-    "qlm_matmul_bf16_workspace_bytes": (_sz, [_i]),
+    "qlm_matmul_bf16_workspace_bytes": (_sz, [_i, _i]),
     "qlm_matmul_bf16": (_i, [_vp, _i, _vp, _f, _vp, _vp, _i, _i, _i, _i, _i, _vp, _sz, _vp]),
     "qlm_matmul_w": (_i, [_vp, _i, _vp, _f, _vp, _i, _vp, _i, _i, _i, _i, _i, _vp, _sz, _vp]),
     "qlm_gemv_w_config": (_i, [_vp, _vp, _f, _vp, _i, _vp, _i, _i, _i, _i, _i, _i, _i, _i, _vp]),
