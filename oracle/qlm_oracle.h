@@ -4,7 +4,8 @@
  * A plain-C restatement of the reference QuickLM CPU arithmetic for the
  * hybrid decode path, written from the reference's source (each function
  * cites the file:line it follows). Only tests/, __graft_entry__.smoke() and
- * bench.py's cpu_baseline leg may load this library, and only as the checker.
+ * bench.py's cpu_baseline leg may load this library, and only as the oracle
+ * the results are compared with.
  * The product path never links it.
  *
  * Every reduction keeps the reference's operation order (its 8-lane AVX2

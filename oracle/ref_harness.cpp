@@ -1,7 +1,7 @@
 // Test infrastructure only: an extern "C" face over the reference QuickLM CPU
 // engine, compiled from the reference's own sources where they lie (see
 // oracle/Makefile). Nothing in the product links or loads this; tests, golden
-// generation and bench.py's cpu_baseline leg use it as the checker / baseline.
+// generation and bench.py's cpu_baseline leg use it as oracle and baseline.
 //
 // The reference keeps its int8 quantiser in file-static functions
 // (src/io/safetensors.cpp:296-391), so this TU includes that .cpp directly to

@@ -1,6 +1,6 @@
 """Operator parity: each HIP kernel (through the C ABI) against the CPU oracle.
 
-Bars (north_star): int8 quantisation and argmax bit-exact; fp32-accumulating
+Bars: int8 quantisation and argmax bit-exact; fp32-accumulating
 ops within a normwise relative error of 1e-3 (FP32_TOL). Where the GPU
 evaluates exactly the reference's per-element arithmetic (conv1d tap sums,
 RoPE from the reference's own cos/sin table), the bar is bit-exactness.

@@ -2,7 +2,7 @@
 
 import numpy as np
 
-# north_star tolerance: per-op normwise max relative error with fp32 accumulation.
+# The decode path's tolerance: per-op normwise max relative error, fp32 accumulation.
 FP32_TOL = 1e-3
 
 
