@@ -100,8 +100,10 @@ __device__ __forceinline__ void store_w16(unsigned short* dst, int4 w) {
 // XS: x is already split (k_split_rows): x points at the bf16 hi plane
 // [M, ldx] and the lo plane follows it (M * ldx further); any RMSNorm has
 // been applied there, so NORM is false.
+// KG: 32-column scale groups per staged chunk and wave (more matrix-core work
+// between the chunk's load and its use).
 template <int WM, int WN, int WK, int TM, int TN, bool ROWSCALE, int EPI, bool NORM,
-          bool WB16 = false, bool XS = false>
+          bool WB16 = false, bool XS = false, int KG = 1>
 __global__ __launch_bounds__(kThreads) void k_mm_i8(const float* __restrict__ x, int ldx,
                                                     const float* __restrict__ rs,
                                                     const float* __restrict__ nw,
@@ -113,7 +115,7 @@ __global__ __launch_bounds__(kThreads) void k_mm_i8(const float* __restrict__ x,
     static_assert(EPI != EPI_SWIGLU || TN % 2 == 0, "SwiGLU pairs gate and up tiles");
     constexpr int BM = WM * TM * 16;
     constexpr int BN = WN * TN * 16;  // weight rows staged per chunk
-    constexpr int KC = 32 * WK;
+    constexpr int KC = 32 * WK * KG;
     constexpr int XP = KC + 8;        // padded LDS rows (bf16 elements)
     constexpr int WP = KC + 8;
     constexpr int XV = BM * KC / 4;   // float4 per x chunk
@@ -171,7 +173,7 @@ __global__ __launch_bounds__(kThreads) void k_mm_i8(const float* __restrict__ x,
     // XS: hi and lo bf16 quadruples, kept in integer registers (as floats a
     // pair could read as a denormal and be flushed)
     uint4 xq[XS ? XPT : 1];
-    float sr[TN];
+    float sr[KG][TN];
     auto load_chunk = [&](int c) {
         const int k0 = c * KC;
 #pragma unroll
@@ -211,10 +213,13 @@ __global__ __launch_bounds__(kThreads) void k_mm_i8(const float* __restrict__ x,
             }
         }
         if constexpr (!ROWSCALE && !WB16) {
-            const int g = (k0 >> 5) + kw;
 #pragma unroll
-            for (int tn = 0; tn < TN; ++tn)
-                sr[tn] = sc[(size_t)w_row(tile_row(tn) + (lane & 15)) * nblk + g];
+            for (int gg = 0; gg < KG; ++gg) {
+                const int g = (k0 >> 5) + kw * KG + gg;
+#pragma unroll
+                for (int tn = 0; tn < TN; ++tn)
+                    sr[gg][tn] = sc[(size_t)w_row(tile_row(tn) + (lane & 15)) * nblk + g];
+            }
         }
     };
     auto store_chunk = [&]() {
@@ -281,14 +286,18 @@ __global__ __launch_bounds__(kThreads) void k_mm_i8(const float* __restrict__ x,
     const int nch = K / KC;
     load_chunk(0);
     for (int c = 0; c < nch; ++c) {
-        float s_cur[TN];
+        float s_cur[KG][TN];
 #pragma unroll
-        for (int tn = 0; tn < TN; ++tn) s_cur[tn] = sr[tn];
+        for (int gg = 0; gg < KG; ++gg)
+#pragma unroll
+            for (int tn = 0; tn < TN; ++tn) s_cur[gg][tn] = sr[gg][tn];
         __syncthreads();  // the previous chunk's LDS reads are done
         store_chunk();
         __syncthreads();
         if (c + 1 < nch) load_chunk(c + 1);
-        const int kofs = kw * 32 + (lane >> 4) * 8;
+#pragma unroll
+        for (int gg = 0; gg < KG; ++gg) {
+        const int kofs = (kw * KG + gg) * 32 + (lane >> 4) * 8;
         bf16x8 ah[TM], al[TM], bw[TN];
 #pragma unroll
         for (int tm = 0; tm < TM; ++tm) {
@@ -310,11 +319,12 @@ __global__ __launch_bounds__(kThreads) void k_mm_i8(const float* __restrict__ x,
                     f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
                     d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[tm], bw[tn], d, 0, 0, 0);
                     d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[tm], bw[tn], d, 0, 0, 0);
-                    const float s = s_cur[tn];
+                    const float s = s_cur[gg][tn];
 #pragma unroll
                     for (int i = 0; i < 4; ++i) acc[tm][tn][i] = fmaf(d[i], s, acc[tm][tn][i]);
                 }
             }
+        }
     }
 
     // ---- sum the WK partial tiles (fixed order) ----
@@ -667,8 +677,12 @@ int launch_mm(const float* x, int ldx, const float* rs, const float* nw, const i
     constexpr int BM = WM * TM * 16;
     constexpr int BN_OUT = WN * (EPI == EPI_SWIGLU ? TN / 2 : TN) * 16;
     const dim3 grid((N + BN_OUT - 1) / BN_OUT, (M + BM - 1) / BM);
-    hipLaunchKernelGGL((k_mm_i8<WM, WN, WK, TM, TN, RS, EPI, NORM, false, XS>), grid,
-                       dim3(kThreads), 0, st, x, ldx, rs, nw, q, sc, y, ldy, M, N, K, N);
+    if (K % (64 * WK) == 0)  // two scale groups a chunk
+        hipLaunchKernelGGL((k_mm_i8<WM, WN, WK, TM, TN, RS, EPI, NORM, false, XS, 2>), grid,
+                           dim3(kThreads), 0, st, x, ldx, rs, nw, q, sc, y, ldy, M, N, K, N);
+    else
+        hipLaunchKernelGGL((k_mm_i8<WM, WN, WK, TM, TN, RS, EPI, NORM, false, XS>), grid,
+                           dim3(kThreads), 0, st, x, ldx, rs, nw, q, sc, y, ldy, M, N, K, N);
     return qlm_launch_status();
 }
 
@@ -678,9 +692,13 @@ int launch_mm16(const float* x, int ldx, const float* rs, const float* nw, const
     constexpr int BM = 2 * 4 * 16;
     constexpr int BN_OUT = 2 * (EPI == EPI_SWIGLU ? 2 : 4) * 16;
     const dim3 grid((N + BN_OUT - 1) / BN_OUT, (M + BM - 1) / BM);
-    hipLaunchKernelGGL((k_mm_i8<2, 2, 1, 4, 4, false, EPI, NORM, true, XS>), grid, dim3(kThreads),
-                       0, st, x, ldx, rs, nw, reinterpret_cast<const int8_t*>(w), nullptr, y, ldy,
-                       M, N, K, N);
+    const int8_t* wq = reinterpret_cast<const int8_t*>(w);
+    if (K % 64 == 0)
+        hipLaunchKernelGGL((k_mm_i8<2, 2, 1, 4, 4, false, EPI, NORM, true, XS, 2>), grid,
+                           dim3(kThreads), 0, st, x, ldx, rs, nw, wq, nullptr, y, ldy, M, N, K, N);
+    else
+        hipLaunchKernelGGL((k_mm_i8<2, 2, 1, 4, 4, false, EPI, NORM, true, XS>), grid,
+                           dim3(kThreads), 0, st, x, ldx, rs, nw, wq, nullptr, y, ldy, M, N, K, N);
     return qlm_launch_status();
 }
 
