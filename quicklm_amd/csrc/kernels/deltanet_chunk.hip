@@ -233,6 +233,12 @@ __global__ __launch_bounds__(256) void k_dn_chunk_intra(
     }
 }
 
+// The chunk operands (Wk, q and Mq rows, U, k columns, the cumulative gates)
+// do not depend on the state: each is reloaded for the next chunk right after
+// its last use in this one, so only the state chain is serial. Contractions
+// whose A operand is a row (Wk S, Q S, Mq W) take the row as float4s, lane
+// (l16, l4) holding columns 16kb + 4 l4 + j, and the LDS operand is read in
+// the same K order.
 __global__ __launch_bounds__(256) void k_dn_chunk_inter(
     const float* __restrict__ qn, const float* __restrict__ kn, const float* __restrict__ U,
     const float* __restrict__ Wk, const float* __restrict__ Mq, const float* __restrict__ Gc,
@@ -245,6 +251,8 @@ __global__ __launch_bounds__(256) void k_dn_chunk_inter(
     const int l16 = lane & 15, l4 = lane >> 4;
     float* Sg = state + (size_t)h * kD * kD;
     const float rsd = 1.0f / sqrtf((float)kD);
+    const int nch = (T + kC - 1) / kC;
+    const int tr = wave * 16 + l16;  // A-operand row of this wave's tiles
 
     // state rows 32w .. 32w+31 (two 16-row tiles), columns jb .. jb+15
     f32x4 sacc[2];
@@ -256,42 +264,108 @@ __global__ __launch_bounds__(256) void k_dn_chunk_inter(
             sacc[tt][i] = Sg[(size_t)row * kD + jb + l16];
             Ss[row * SP + l16] = sacc[tt][i];
         }
+
+    // chunk operands in registers (rows clamped into [0, T); masked at use)
+    float4 pw[8], pq[8], pm[4];
+    float pu[4], pk[2][16], pg = 0.0f;
+    auto row_of = [&](int c, int t) { return min(c * kC + t, T - 1); };
+    auto load_w = [&](int c) {
+        const float4* r = reinterpret_cast<const float4*>(Wk + rix(row_of(c, tr), h, H));
+#pragma unroll
+        for (int kb = 0; kb < 8; ++kb) pw[kb] = r[4 * kb + l4];
+    };
+    auto load_q = [&](int c) {
+        const float4* r = reinterpret_cast<const float4*>(qn + rix(row_of(c, tr), h, H));
+#pragma unroll
+        for (int kb = 0; kb < 8; ++kb) pq[kb] = r[4 * kb + l4];
+    };
+    auto load_m = [&](int c) {
+        const float4* r =
+            reinterpret_cast<const float4*>(Mq + (((size_t)c * H + h) * kC + tr) * kC);
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) pm[kb] = r[4 * kb + l4];
+    };
+    auto load_u = [&](int c) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pu[i] = U[rix(row_of(c, wave * 16 + l4 * 4 + i), h, H) + jb + l16];
+    };
+    auto load_k = [&](int c) {
+#pragma unroll
+        for (int s4 = 0; s4 < 16; ++s4) {
+            const float* kr = kn + rix(row_of(c, 4 * s4 + l4), h, H);
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) pk[tt][s4] = kr[(2 * wave + tt) * 16 + l16];
+        }
+    };
+    auto load_g = [&](int c) {
+        if (tid < kC) pg = Gc[(size_t)row_of(c, tid) * H + h];
+    };
+    load_g(0);
+    load_w(0);
+    load_u(0);
+    load_q(0);
+    load_m(0);
+    load_k(0);
     __syncthreads();
 
-    const int nch = (T + kC - 1) / kC;
     for (int c = 0; c < nch; ++c) {
-        const int t0 = c * kC;
-        const int nt = min(kC, T - t0);
-        if (tid < kC) gs[tid] = tid < nt ? Gc[(size_t)(t0 + tid) * H + h] : 0.0f;
-        const int tr = wave * 16 + l16;  // A-operand row of this wave's tile
+        const int cn = min(c + 1, nch - 1);
+        const int nt = min(kC, T - c * kC);
         const bool tv = tr < nt;
+        if (tid < kC) gs[tid] = tid < nt ? pg : 0.0f;
+        load_g(cn);
         // W = U - Wk S: wave w rows 16w..16w+15
-        f32x4 w = f32x4{0.f, 0.f, 0.f, 0.f};
-        {
-            const float* wkr = Wk + rix(t0 + (tv ? tr : 0), h, H);
-            for (int k0 = 0; k0 < kD; k0 += 4)
-                w = mma(tv ? wkr[k0 + l4] : 0.0f, Ss[(k0 + l4) * SP + l16], w);
+        f32x4 wa = f32x4{0.f, 0.f, 0.f, 0.f}, wb = wa;
+#pragma unroll
+        for (int kb = 0; kb < 8; ++kb) {
+            const float a[4] = {pw[kb].x, pw[kb].y, pw[kb].z, pw[kb].w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float b = Ss[(16 * kb + 4 * l4 + j) * SP + l16];
+                if (kb & 1)
+                    wb = mma(tv ? a[j] : 0.0f, b, wb);
+                else
+                    wa = mma(tv ? a[j] : 0.0f, b, wa);
+            }
         }
+        load_w(cn);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int t = wave * 16 + l4 * 4 + i;
-            Ws[t * SP + l16] = t < nt ? U[rix(t0 + t, h, H) + jb + l16] - w[i] : 0.0f;
+            Ws[t * SP + l16] = t < nt ? pu[i] - (wa[i] + wb[i]) : 0.0f;
         }
+        load_u(cn);
         __syncthreads();
         // O = (gamma_t (Q S) + Mq W) / sqrt(d)
         {
-            f32x4 qs = f32x4{0.f, 0.f, 0.f, 0.f}, mw = f32x4{0.f, 0.f, 0.f, 0.f};
-            const float* qr = qn + rix(t0 + (tv ? tr : 0), h, H);
-            for (int k0 = 0; k0 < kD; k0 += 4)
-                qs = mma(tv ? qr[k0 + l4] : 0.0f, Ss[(k0 + l4) * SP + l16], qs);
-            const float* mr = Mq + (((size_t)c * H + h) * kC + tr) * kC;
-            for (int k0 = 0; k0 < kC; k0 += 4)
-                mw = mma(tv ? mr[k0 + l4] : 0.0f, Ws[(k0 + l4) * SP + l16], mw);
+            f32x4 qa = f32x4{0.f, 0.f, 0.f, 0.f}, qb = qa, mw = qa;
+#pragma unroll
+            for (int kb = 0; kb < 8; ++kb) {
+                const float a[4] = {pq[kb].x, pq[kb].y, pq[kb].z, pq[kb].w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float b = Ss[(16 * kb + 4 * l4 + j) * SP + l16];
+                    if (kb & 1)
+                        qb = mma(tv ? a[j] : 0.0f, b, qb);
+                    else
+                        qa = mma(tv ? a[j] : 0.0f, b, qa);
+                }
+            }
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) {
+                const float a[4] = {pm[kb].x, pm[kb].y, pm[kb].z, pm[kb].w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    mw = mma(tv ? a[j] : 0.0f, Ws[(16 * kb + 4 * l4 + j) * SP + l16], mw);
+            }
+            load_q(cn);
+            load_m(cn);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int t = wave * 16 + l4 * 4 + i;
                 if (t < nt)
-                    O[rix(t0 + t, h, H) + jb + l16] = (expf(gs[t]) * qs[i] + mw[i]) * rsd;
+                    O[rix(c * kC + t, h, H) + jb + l16] =
+                        (expf(gs[t]) * (qa[i] + qb[i]) + mw[i]) * rsd;
             }
         }
         // S = gamma_end S + K^T diag(gamma_end / gamma) W
@@ -302,17 +376,17 @@ __global__ __launch_bounds__(256) void k_dn_chunk_inter(
             for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) sacc[tt][i] *= ge;
-            for (int k0 = 0; k0 < kC; k0 += 4) {
-                const int t = k0 + l4;
+#pragma unroll
+            for (int s4 = 0; s4 < 16; ++s4) {
+                const int t = 4 * s4 + l4;
                 const bool ok = t < nt;
                 const float b = ok ? Ws[t * SP + l16] * expf(gend - gs[t]) : 0.0f;
-                const float* kr = kn + rix(t0 + (ok ? t : 0), h, H);
 #pragma unroll
-                for (int tt = 0; tt < 2; ++tt)
-                    sacc[tt] = mma(ok ? kr[(2 * wave + tt) * 16 + l16] : 0.0f, b, sacc[tt]);
+                for (int tt = 0; tt < 2; ++tt) sacc[tt] = mma(ok ? pk[tt][s4] : 0.0f, b, sacc[tt]);
             }
+            load_k(cn);
         }
-        __syncthreads();  // every read of Ss and Ws of this chunk is done
+        __syncthreads();  // every read of Ss, Ws and gs of this chunk is done
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
