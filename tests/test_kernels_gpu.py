@@ -709,7 +709,8 @@ def test_deltanet_prefill(hip, orc, rng, p0, T):
                           dconv2.to_numpy(conv.shape, np.float32))
 
 
-@pytest.mark.parametrize("p0,T", [(0, 64), (0, 200), (5, 130), (1, 2), (0, 1024)])
+@pytest.mark.parametrize("p0,T", [(0, 64), (0, 200), (5, 130), (1, 2), (0, 1024), (0, 4096),
+                                  (9, 3001)])
 def test_deltanet_prefill_chunked(hip, orc, rng, p0, T):
     """Chunked (WY, matrix-core) prefill == the row-by-row recurrence: outputs
     against the oracle, state and conv ring against the sequential kernel
