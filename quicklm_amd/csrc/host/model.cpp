@@ -32,7 +32,7 @@ std::vector<float> to_f32(const TensorView& t) {
     return out;
 }
 
-constexpr int kPrefillChunk = 1024;  // prompt rows per pass through the layers
+constexpr int kPrefillChunk = 2048;  // prompt rows per pass through the layers
 constexpr int kLmRows = 64;          // rows per lm_head pass of a batched forward
 constexpr int kRowsMax = 64;         // batched forwards up to this many rows run the
                                      // DeltaNet recurrence row by row

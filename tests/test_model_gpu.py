@@ -118,9 +118,8 @@ def test_batch_rows_equal_single(engine, golden):
 @pytest.mark.parametrize("mode", [True, 2])
 def test_batched_prefill_equals_stepwise(engine, golden, n, mode):
     """Batched prefill (matrix-core projections, chunked or row-by-row
-    DeltaNet, prefill attention; 1300 rows span two 1024-row chunks) leaves
-    the model where n-1 decode steps leave it: same tokens, logits within
-    1e-4."""
+    DeltaNet, prefill attention) leaves the model where n-1 decode steps
+    leave it: same tokens, logits within 1e-4."""
     rng = np.random.default_rng(11)
     p = golden["prompt"][:n] if n <= 128 else rng.integers(0, 151936, n).astype(np.int32)
     a, pre_a, _ = engine.generate(p[None, :], 8, batched_prefill=mode)
@@ -128,6 +127,28 @@ def test_batched_prefill_equals_stepwise(engine, golden, n, mode):
     b, pre_b, _ = engine.generate(p[None, :], 8, batched_prefill=False)
     lb = engine.last_logits(0)
     say(f"n={n} mode={mode}: batched prefill {pre_a:.3f}s, stepwise {pre_b:.3f}s")
+    assert np.array_equal(a, b)
+    assert float(np.abs(la - lb).max() / np.abs(lb).max()) < 1e-4
+
+
+@pytest.mark.parametrize("mode", [True, 2])
+def test_prefill_across_passes(hip, tiny_dir, mode):
+    """A 2300-row prompt goes through the layers in two passes (2048 rows,
+    then 251), the second continuing the first's states and caches: same
+    tokens as 2299 decode steps, logits within 1e-4."""
+    from quicklm_amd.engine import Engine
+
+    rng = np.random.default_rng(12)
+    p = rng.integers(0, 151936, 2300).astype(np.int32)
+    e = Engine(tiny_dir, max_seq_len=2600, max_batch=1, precision="int8")
+    try:
+        a, pre_a, _ = e.generate(p[None, :], 8, batched_prefill=mode)
+        la = e.last_logits(0)
+        b, pre_b, _ = e.generate(p[None, :], 8, batched_prefill=False)
+        lb = e.last_logits(0)
+    finally:
+        e.close()
+    say(f"2300 rows mode={mode}: batched prefill {pre_a:.3f}s, stepwise {pre_b:.3f}s")
     assert np.array_equal(a, b)
     assert float(np.abs(la - lb).max() / np.abs(lb).max()) < 1e-4
 
