@@ -459,6 +459,8 @@ void DecoderModel::forward(int token, int pos, float* logits_host) {
     if (pos < 0 || pos >= max_seq_)
         throw std::runtime_error("KV cache index out of bounds: pos = " + std::to_string(pos) +
                                  ", max_seq_len = " + std::to_string(max_seq_));
+    if (token < 0 || token >= cfg_.vocab_size)
+        throw std::runtime_error("forward: token id out of range");
     const int big = INT_MAX;
     check(qlm_memcpy_h2d(tokens_.get<int>() + pos, &token, sizeof(int), stream_), "upload");
     check(qlm_memcpy_h2d(pos_.get<int>(), &pos, sizeof(int), stream_), "upload");

@@ -14,6 +14,16 @@
 
 namespace qlm {
 
+size_t dtype_size(const std::string& dtype) {
+    if (dtype == "F64" || dtype == "I64" || dtype == "U64") return 8;
+    if (dtype == "F32" || dtype == "I32" || dtype == "U32") return 4;
+    if (dtype == "BF16" || dtype == "F16" || dtype == "I16" || dtype == "U16") return 2;
+    if (dtype == "I8" || dtype == "U8" || dtype == "BOOL" || dtype == "F8_E4M3" ||
+        dtype == "F8_E5M2")
+        return 1;
+    return 0;
+}
+
 SafetensorsFile::SafetensorsFile(const std::string& path) : path_(path) {
     fd_ = ::open(path.c_str(), O_RDONLY);
     if (fd_ < 0) throw std::runtime_error("safetensors: cannot open " + path);
@@ -35,13 +45,34 @@ SafetensorsFile::SafetensorsFile(const std::string& path) : path_(path) {
         const Json& t = kv.second;
         Info info;
         info.dtype = t.at("dtype").string();
-        for (const auto& d : t.at("shape").arr) info.shape.push_back((int64_t)d.number());
+        // element count, with every dimension checked: a negative or
+        // non-integral dimension, or a product past 2^62, is a bad header
+        uint64_t numel = 1;
+        for (const auto& d : t.at("shape").arr) {
+            const double v = d.number();
+            if (!(v >= 0.0) || v != (double)(int64_t)v || v > (double)(1ull << 62))
+                throw std::runtime_error("safetensors: bad shape for " + kv.first);
+            info.shape.push_back((int64_t)v);
+            if (v != 0.0 && numel > (1ull << 62) / (uint64_t)v)
+                throw std::runtime_error("safetensors: shape too large for " + kv.first);
+            numel *= (uint64_t)v;
+        }
         const auto& off = t.at("data_offsets").arr;
         if (off.size() != 2) throw std::runtime_error("safetensors: bad data_offsets for " + kv.first);
-        info.begin = (size_t)off[0].number();
-        info.end = (size_t)off[1].number();
+        const double b0 = off[0].number(), b1 = off[1].number();
+        if (!(b0 >= 0.0) || !(b1 >= 0.0) || b0 > (double)size_ || b1 > (double)size_)
+            throw std::runtime_error("safetensors: tensor '" + kv.first + "' is out of file bounds");
+        info.begin = (size_t)b0;
+        info.end = (size_t)b1;
         if (info.end < info.begin || data_start_ + info.end > size_)
             throw std::runtime_error("safetensors: tensor '" + kv.first + "' is out of file bounds");
+        // the byte range must hold exactly shape x element size, so every
+        // consumer may size its reads and device copies by either one
+        const size_t esize = dtype_size(info.dtype);
+        if (esize && (uint64_t)(info.end - info.begin) != numel * esize)
+            throw std::runtime_error("safetensors: tensor '" + kv.first + "' holds " +
+                                     std::to_string(info.end - info.begin) + " bytes, its " +
+                                     info.dtype + " shape needs " + std::to_string(numel * esize));
         infos_[kv.first] = std::move(info);
     }
 }

@@ -26,6 +26,13 @@ struct TensorView {
     }
 };
 
+// Bytes per element of a safetensors dtype string; 0 for a dtype this
+// loader does not know (such tensors are only reachable by name, and every
+// consumer rejects dtypes other than F32 and BF16).
+size_t dtype_size(const std::string& dtype);
+
+// Every tensor's byte range is checked at open: inside the file, end >=
+// begin, and (for a known dtype) exactly prod(shape) x dtype_size bytes.
 class SafetensorsFile {
    public:
     explicit SafetensorsFile(const std::string& path);

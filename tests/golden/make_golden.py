@@ -15,9 +15,11 @@ plus the same stream from the reference's own -O3 -ffast-math build
 (tokens_fast) for the record; and tiny_greedy_int4.npz, the IEEE build's
 run of the same prompt at --precision int4 (prompt, tokens, top_idx,
 top_val, margin, logits0_head). Usage: python tests/golden/make_golden.py
-[--int4 | --native (those fixtures only)]; tiny_greedy_native.npz and
+[--int4 | --native | --4b (those fixtures only)]; tiny_greedy_native.npz and
 micro_greedy_native.npz are the --precision bf16 runs (weights in their
-checkpoint dtype: fp32 for the tiny model, bf16 for the micro one).
+checkpoint dtype: fp32 for the tiny model, bf16 for the micro one);
+4b_greedy.npz is the 4B-class int8 model (2048-token prompt, 128 greedy
+steps), written only with --4b (it takes minutes of CPU).
 """
 import hashlib
 import os
@@ -91,7 +93,58 @@ def native_streams():
             del m
 
 
+SHA_TENSORS_4B = ["model.embed_tokens.weight", "model.layers.0.linear_attn.in_proj_qkv.weight",
+                  "model.layers.3.self_attn.q_proj.weight", "model.layers.35.mlp.down_proj.weight",
+                  "model.layers.0.linear_attn.A_log", "model.layers.0.linear_attn.dt_bias"]
+N_4B_PROMPT, N_4B_STEPS, SEED_4B = 2048, 128, 4
+
+
+def fourb_stream():
+    """The 4B-class int8 workload (36 layers, hidden 2560), batch 1: the
+    2048-token prompt of seed 4 (sequence 0 of the decode benchmark), batched
+    prefill of prompt[0..2046], then N_4B_STEPS greedy steps, IEEE build ->
+    4b_greedy.npz (prompt, tokens, top_idx/top_val [steps, 32], margin,
+    logits0_head, tensor SHAs) plus the fast-math build's stream
+    (tokens_fast) for the record."""
+    out = os.path.join(os.path.dirname(os.path.abspath(__file__)), "4b_greedy.npz")
+    base = "/dev/shm" if os.path.isdir("/dev/shm") else None
+    with tempfile.TemporaryDirectory(dir=base) as d:
+        t0 = time.time()
+        synth.write_model(d, "4b")
+        print(f"4B checkpoint written in {time.time() - t0:.1f}s", flush=True)
+        from oracle.oracle import read_safetensors
+        t = read_safetensors(os.path.join(d, "model.safetensors"))
+        shas = [hashlib.sha256(t[n].tobytes()).hexdigest() for n in SHA_TENSORS_4B]
+        del t
+        prompt = synth.prompt_tokens(N_4B_PROMPT, seed=SEED_4B)[0]
+        res = {}
+        for kind in ("ieee", "fast"):
+            ref = Reference(kind)
+            ref.init_threads(os.cpu_count() or 1)
+            m = ref.load_model(d, N_4B_PROMPT + N_4B_STEPS + 8, "int8")
+            toks, pre, dec, lg = m.generate(prompt, N_4B_STEPS, keep_logits=(kind == "ieee"))
+            print(f"4B {ref.kind}: prefill {pre:.1f}s decode {dec:.1f}s "
+                  f"({N_4B_STEPS / dec:.2f} tok/s) tokens {toks[:8]}...", flush=True)
+            res[kind] = (toks, lg)
+            del m
+        toks, lg = res["ieee"]
+        order = np.argsort(-lg, axis=1, kind="stable")[:, :32]
+        top_val = np.take_along_axis(lg, order, axis=1)
+        np.savez_compressed(
+            out, prompt=prompt.astype(np.int32), tokens=toks.astype(np.int32),
+            tokens_fast=res["fast"][0].astype(np.int32), top_idx=order.astype(np.int32),
+            top_val=top_val.astype(np.float32), margin=(top_val[:, 0] - top_val[:, 1]),
+            logits0_head=lg[0, :4096].copy(), tensor_names=np.array(SHA_TENSORS_4B),
+            tensor_sha=np.array(shas))
+        same = np.nonzero(res["fast"][0] != toks)[0]
+        print("wrote", out, "fast build splits from ieee at step",
+              int(same[0]) if same.size else None, flush=True)
+
+
 def main():
+    if "--4b" in sys.argv:  # only the 4B fixture
+        fourb_stream()
+        return
     if "--native" in sys.argv:  # only the native-precision fixtures
         native_streams()
         return
