@@ -32,6 +32,7 @@ extern "C" {
 #define QLM_ERR_ARG (-1)      /* null pointer or non-positive size */
 #define QLM_ERR_SHAPE (-2)    /* shape the kernels do not support */
 #define QLM_ERR_NO_DEVICE (-3)
+#define QLM_ERR_SCRATCH (-4)  /* work exceeds a no-allocation entry point's static scratch */
 
 /* ---- runtime plumbing (no reference counterpart: the reference is host-only) ---- */
 
@@ -321,6 +322,26 @@ int qlm_gqa_prefill(float* qkv, int ldqkv, const float* q_norm, const float* k_n
 int qlm_attention_decode(const float* q, const void* k_cache, const void* v_cache,
                          int kv_dtype, int max_seq, int ctx, float* out, int B, int n_q,
                          int n_kv, int hd, void* work, void* stream);
+
+/* No counterpart in the reference: qlm_attention_decode for callers that
+ * cannot allocate device memory (code under hipGraph capture, serving loops
+ * that forbid hipMalloc). Same arguments, kernels and results (bit for bit)
+ * as qlm_attention_decode, without `work`: the chunk records live in a
+ * static device array of QLM_ATTENTION_NOALLOC_MAX_BYTES (32 MiB) that every
+ * GPU running the library holds until the process ends. A call needs
+ * qlm_attention_decode_noalloc_bytes(B, n_q, hd, ctx) bytes of it
+ * (B * n_q * ceil(ctx / C) * (hd + 4) * 4, C = 256 positions at hd 128, 128
+ * at hd 256) and returns QLM_ERR_SCRATCH, launching nothing, when that
+ * exceeds the maximum. The call allocates nothing; its first call on a
+ * device looks the array's address up once. Every call on one GPU shares
+ * that GPU's array: calls that may overlap on one GPU (different streams,
+ * different host threads) race, so order them on one stream. Nothing in the
+ * array needs clearing between calls. */
+#define QLM_ATTENTION_NOALLOC_MAX_BYTES (32u << 20)
+size_t qlm_attention_decode_noalloc_bytes(int B, int n_q, int hd, int ctx);
+int qlm_attention_decode_noalloc(const float* q, const void* k_cache, const void* v_cache,
+                                 int kv_dtype, int max_seq, int ctx, float* out, int B, int n_q,
+                                 int n_kv, int hd, void* stream);
 
 /* ---- A14: greedy sampling ---------------------------------------------------
  * DecoderModel::sample with temperature <= 0 (model.cpp:263-274): index of

@@ -26,6 +26,8 @@
 // The graph-captured decode step launches the grid for max_seq; chunks past
 // pos[b] exit at once and are not counted.
 
+#include <mutex>
+
 #include "common.hpp"
 
 namespace {
@@ -552,13 +554,15 @@ size_t records_bytes(int B, int n_q, int hd, int max_seq, int nt) {
     return (size_t)B * n_q * nchunks_for(max_seq, chunk_len(hd, nt)) * (hd + 4) * sizeof(float);
 }
 
+// nch: chunks per (sequence, head) in the record layout and the grid; the
+// positions a launch may attend to (pos[b] + 1, or ctx + pstep * b) must fit
+// in nch chunks of tile_for<HD>() * NT.
 template <int HD, int NT, typename KV, bool PREP>
 int launch_g(int G, const float* q, int ldq, int qhs, const float* qn, const float* kn,
              const float* ct, const float* st, int rot, KV* kc, KV* vc, int max_seq, int n_kv,
-             const int* pos, int ctx, int pstep, size_t kvb, float* work, int n_q, int B,
-             hipStream_t s) {
+             const int* pos, int ctx, int pstep, size_t kvb, float* work, int nch, int n_q,
+             int B, hipStream_t s) {
     constexpr int T = tile_for<HD>();
-    const int nch = nchunks_for(max_seq, T * NT);
     const dim3 grid(nch, n_kv, B);
     const float scale = 1.0f / sqrtf((float)HD);
 #define QLM_ATTN_G(GG)                                                                          \
@@ -618,31 +622,41 @@ extern "C" int qlm_gqa_decode(float* qkv, int ldqkv, const float* q_norm, const 
     if (hd == 128) {
         rc = launch_g<128, kNtModel, float, true>(G, qkv, ldqkv, qstride, q_norm, k_norm, cos_tab,
                                                   sin_tab, rot_dim, k_cache, v_cache, max_seq,
-                                                  n_kv, pos, 0, 0, (size_t)max_seq, w, n_q, B, st);
+                                                  n_kv, pos, 0, 0, (size_t)max_seq, w, nch, n_q, B,
+                                                  st);
         if (rc != QLM_OK) return rc;
         return launch_combine<128>(w, nch, ch, max_seq, pos, 0, 0, gate, ldqkv, qstride, out,
                                    ldo, n_q, B, st);
     }
     rc = launch_g<256, kNtModel, float, true>(G, qkv, ldqkv, qstride, q_norm, k_norm, cos_tab,
                                               sin_tab, rot_dim, k_cache, v_cache, max_seq, n_kv,
-                                              pos, 0, 0, (size_t)max_seq, w, n_q, B, st);
+                                              pos, 0, 0, (size_t)max_seq, w, nch, n_q, B, st);
     if (rc != QLM_OK) return rc;
     return launch_combine<256>(w, nch, ch, max_seq, pos, 0, 0, gate, ldqkv, qstride, out, ldo,
                                n_q, B, st);
 }
 
-extern "C" int qlm_attention_decode(const float* q, const void* k_cache, const void* v_cache,
-                                    int kv_dtype, int max_seq, int ctx, float* out, int B, int n_q,
-                                    int n_kv, int hd, void* work, void* stream) {
-    if (!q || !k_cache || !v_cache || !out || !work) return QLM_ERR_ARG;
+namespace {
+
+int check_attention_args(const float* q, const void* k_cache, const void* v_cache, int kv_dtype,
+                         int max_seq, int ctx, const float* out, int B, int n_q, int n_kv,
+                         int hd) {
+    if (!q || !k_cache || !v_cache || !out) return QLM_ERR_ARG;
     if (B <= 0 || n_q <= 0 || n_kv <= 0 || ctx <= 0 || ctx > max_seq) return QLM_ERR_ARG;
     if (n_q % n_kv != 0 || (hd != 128 && hd != 256)) return QLM_ERR_SHAPE;
     if (kv_dtype != 0 && kv_dtype != 1) return QLM_ERR_ARG;
     const int G = n_q / n_kv;
-    hipStream_t st = as_stream(stream);
+    if (G != 1 && G != 2 && G != 4 && G != 8) return QLM_ERR_SHAPE;
+    return QLM_OK;
+}
+
+// The two launches of the isolated attention, with nch chunk records per
+// (sequence, query head) in w (nch chunks must cover ctx positions).
+int attention_launch(const float* q, const void* k_cache, const void* v_cache, int kv_dtype,
+                     int max_seq, int ctx, float* out, int B, int n_q, int n_kv, int hd,
+                     float* w, int nch, hipStream_t st) {
+    const int G = n_q / n_kv;
     const int ch = chunk_len(hd, kNtLong);
-    const int nch = nchunks_for(max_seq, ch);
-    float* w = reinterpret_cast<float*>(work);
     const int ldq = n_q * hd;
     int rc;
 #define QLM_ISO(HDV)                                                                             \
@@ -650,11 +664,11 @@ extern "C" int qlm_attention_decode(const float* q, const void* k_cache, const v
              ? launch_g<HDV, kNtLong, float, false>(                                             \
                    G, q, ldq, hd, nullptr, nullptr, nullptr, nullptr, 0,                         \
                    (float*)const_cast<void*>(k_cache), (float*)const_cast<void*>(v_cache),       \
-                   max_seq, n_kv, nullptr, ctx, 0, (size_t)max_seq, w, n_q, B, st)               \
+                   max_seq, n_kv, nullptr, ctx, 0, (size_t)max_seq, w, nch, n_q, B, st)          \
              : launch_g<HDV, kNtLong, uint16_t, false>(                                          \
                    G, q, ldq, hd, nullptr, nullptr, nullptr, nullptr, 0,                         \
                    (uint16_t*)const_cast<void*>(k_cache), (uint16_t*)const_cast<void*>(v_cache), \
-                   max_seq, n_kv, nullptr, ctx, 0, (size_t)max_seq, w, n_q, B, st);              \
+                   max_seq, n_kv, nullptr, ctx, 0, (size_t)max_seq, w, nch, n_q, B, st);         \
     if (rc != QLM_OK) return rc;                                                                 \
     return launch_combine<HDV>(w, nch, ch, max_seq, nullptr, ctx, 0, nullptr, 0, 0, out, ldq,    \
                                n_q, B, st);
@@ -663,6 +677,75 @@ extern "C" int qlm_attention_decode(const float* q, const void* k_cache, const v
     }
     QLM_ISO(256)
 #undef QLM_ISO
+}
+
+}  // namespace
+
+// Device scratch of qlm_attention_decode_noalloc: the chunk records live in
+// this array instead of a caller workspace. Each GPU that runs the library
+// holds its own copy until the process ends; its device address is looked
+// up once per device (hipGetSymbolAddress, with that device current) and
+// only that address is ever handed to a kernel or a copy.
+static constexpr size_t kScratchBytes = (size_t)QLM_ATTENTION_NOALLOC_MAX_BYTES;
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's address of `scratch` (resolved on its first call).
+int scratch_ptr(float** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return qlm_status(e);
+    if (dev < 0 || dev >= kMaxDevices) return QLM_ERR_ARG;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return qlm_status(e);
+        if (!p) return QLM_ERR_NO_DEVICE;
+        g_scratch_ptr[dev] = p;
+    }
+    *out = static_cast<float*>(g_scratch_ptr[dev]);
+    return QLM_OK;
+}
+
+}  // namespace
+
+extern "C" int qlm_attention_decode(const float* q, const void* k_cache, const void* v_cache,
+                                    int kv_dtype, int max_seq, int ctx, float* out, int B, int n_q,
+                                    int n_kv, int hd, void* work, void* stream) {
+    if (!work) return QLM_ERR_ARG;
+    const int rc = check_attention_args(q, k_cache, v_cache, kv_dtype, max_seq, ctx, out, B, n_q,
+                                        n_kv, hd);
+    if (rc != QLM_OK) return rc;
+    return attention_launch(q, k_cache, v_cache, kv_dtype, max_seq, ctx, out, B, n_q, n_kv, hd,
+                            reinterpret_cast<float*>(work),
+                            nchunks_for(max_seq, chunk_len(hd, kNtLong)), as_stream(stream));
+}
+
+extern "C" size_t qlm_attention_decode_noalloc_bytes(int B, int n_q, int hd, int ctx) {
+    if (B <= 0 || n_q <= 0 || (hd != 128 && hd != 256) || ctx <= 0) return 0;
+    return records_bytes(B, n_q, hd, ctx, kNtLong);
+}
+
+extern "C" int qlm_attention_decode_noalloc(const float* q, const void* k_cache,
+                                            const void* v_cache, int kv_dtype, int max_seq,
+                                            int ctx, float* out, int B, int n_q, int n_kv, int hd,
+                                            void* stream) {
+    int rc = check_attention_args(q, k_cache, v_cache, kv_dtype, max_seq, ctx, out, B, n_q, n_kv,
+                                  hd);
+    if (rc != QLM_OK) return rc;
+    // records for the chunks that cover ctx positions only (the grid stops there)
+    if (records_bytes(B, n_q, hd, ctx, kNtLong) > kScratchBytes) return QLM_ERR_SCRATCH;
+    float* w = nullptr;
+    rc = scratch_ptr(&w);
+    if (rc != QLM_OK) return rc;
+    return attention_launch(q, k_cache, v_cache, kv_dtype, max_seq, ctx, out, B, n_q, n_kv, hd,
+                            w, nchunks_for(ctx, chunk_len(hd, kNtLong)), as_stream(stream));
 }
 
 extern "C" size_t qlm_gqa_prefill_workspace_bytes(int n_q, int hd, int max_seq) {
@@ -707,16 +790,16 @@ extern "C" int qlm_gqa_prefill(float* qkv, int ldqkv, const float* q_norm, const
         if (hd == 128) {
             rc = launch_g<128, kNtLong, float, false>(G, q, ldqkv, qstride, nullptr, nullptr,
                                                       nullptr, nullptr, 0, k_cache, v_cache,
-                                                      max_seq, n_kv, nullptr, ctx, 1, 0, w, n_q,
-                                                      rows, st);
+                                                      max_seq, n_kv, nullptr, ctx, 1, 0, w, nch,
+                                                      n_q, rows, st);
             if (rc != QLM_OK) return rc;
             rc = launch_combine<128>(w, nch, ch, max_seq, nullptr, ctx, 1, gated ? q : nullptr,
                                      ldqkv, qstride, out + (size_t)s0 * ldo, ldo, n_q, rows, st);
         } else {
             rc = launch_g<256, kNtLong, float, false>(G, q, ldqkv, qstride, nullptr, nullptr,
                                                       nullptr, nullptr, 0, k_cache, v_cache,
-                                                      max_seq, n_kv, nullptr, ctx, 1, 0, w, n_q,
-                                                      rows, st);
+                                                      max_seq, n_kv, nullptr, ctx, 1, 0, w, nch,
+                                                      n_q, rows, st);
             if (rc != QLM_OK) return rc;
             rc = launch_combine<256>(w, nch, ch, max_seq, nullptr, ctx, 1, gated ? q : nullptr,
                                      ldqkv, qstride, out + (size_t)s0 * ldo, ldo, n_q, rows, st);

@@ -11,6 +11,8 @@ extern "C" const char* qlm_error_string(int status) {
         case QLM_ERR_ARG: return "invalid argument (null pointer or non-positive size)";
         case QLM_ERR_SHAPE: return "unsupported shape";
         case QLM_ERR_NO_DEVICE: return "no HIP device";
+        case QLM_ERR_SCRATCH:
+            return "work exceeds the static device scratch of a no-allocation entry point";
         default: break;
     }
     if (status > 0) return hipGetErrorString((hipError_t)status);

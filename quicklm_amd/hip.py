@@ -93,6 +93,8 @@ _SIGS = {
     "qlm_gqa_decode": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _i, _i,
                             _i, _i, _i, _i, _vp, _vp]),
     "qlm_attention_decode": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp, _i, _i, _i, _i, _vp, _vp]),
+    "qlm_attention_decode_noalloc_bytes": (_sz, [_i, _i, _i, _i]),
+    "qlm_attention_decode_noalloc": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp, _i, _i, _i, _i, _vp]),
     "qlm_argmax": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp]),
     "qlm_argmax_workspace_bytes": (_sz, [_i, _i]),
     "qlm_greedy_advance": (_i, [_vp, _i, _i, _i, _vp, _vp, _i, _vp, _vp, _vp]),

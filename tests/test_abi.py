@@ -56,3 +56,26 @@ def test_shape_checks_run_before_any_launch():
                                  64, None) == -2  # d must be 128
     assert L.qlm_gqa_decode(fake, 4096, fake, fake, fake, fake, 32, fake, fake, 64, fake, fake,
                             4096, 1, 3, 2, 128, 1, fake, None) == -2  # 3 q heads over 2 kv heads
+
+
+def test_noalloc_attention_rejects_oversize_on_host():
+    """qlm_attention_decode_noalloc refuses work beyond its static scratch
+    (QLM_ERR_SCRATCH) before touching any device memory."""
+    from quicklm_amd import hip
+
+    L = hip.lib()
+    cap = 32 << 20
+    # B * n_q * ceil(ctx / C) * (hd + 4) * 4 bytes, C = 128 positions at hd 256
+    assert L.qlm_attention_decode_noalloc_bytes(16, 16, 256, 32768) == 16 * 16 * 256 * 260 * 4
+    assert L.qlm_attention_decode_noalloc_bytes(1, 16, 128, 300) == 16 * 2 * 132 * 4
+    assert L.qlm_attention_decode_noalloc_bytes(0, 16, 128, 300) == 0
+    assert L.qlm_attention_decode_noalloc_bytes(1, 16, 64, 300) == 0
+    assert L.qlm_attention_decode_noalloc_bytes(16, 16, 256, 32768) > cap
+    fake = 4096  # never dereferenced: the checks fire first
+    assert L.qlm_attention_decode_noalloc(fake, fake, fake, 1, 32768, 32768, fake, 16, 16, 2, 256,
+                                          None) == -4
+    assert b"static device scratch" in L.qlm_error_string(-4)
+    assert L.qlm_attention_decode_noalloc(fake, fake, fake, 1, 100, 200, fake, 1, 16, 2, 256,
+                                          None) == -1  # ctx > max_seq
+    assert L.qlm_attention_decode_noalloc(fake, fake, fake, 1, 100, 50, fake, 1, 16, 2, 96,
+                                          None) == -2  # head dim
