@@ -1,20 +1,35 @@
 #!/usr/bin/env python3
-"""Benchmark: 4B-class int8 hybrid decode on one MI355X, plus the isolated
-int8 GEMV, with the reference CPU path timed beside it.
+"""Benchmark: 4B-class int8 hybrid decode on one MI355X, the isolated
+kernels of the path at their own workload sizes, and the reference CPU path
+timed beside them.
 
-Workload (one "step" = one greedy decode step of every sequence in the batch):
+Workload of `value` (one "step" = one greedy decode step of every sequence):
   4B-class hybrid LM, 36 layers (27 Gated DeltaNet + 9 GQA), hidden 2560,
   FFN 9728, vocab 151936, seeded random-init weights quantised to int8 at load
   (Q8_0 group-32 scales, the reference's format), 2048-token uniform random
   prompts (batched prefill of positions 0..2046, untimed), greedy decode; the
-  whole step is one replayed hipGraph.
-  `value` = batch-1 decode tokens/s over exactly --steps timed steps after
-  --warmup untimed steps; batch 16 is reported beside it. The GEMV section
-  times the config-1 matrices in isolation (M <= 4: GEMV, M > 4: matrix cores).
-  `roofline` is the dominant decode kernel (the fused RMSNorm + gate/up GEMV +
-  SwiGLU, 36 launches per step) timed with HIP events on its own stream.
-  `cpu_baseline` is the reference's own sources built with its release flags
-  on this host's cores, on a bounded sample of the same 4B workload.
+  whole step is one replayed hipGraph. `value` = batch-1 decode tokens/s over
+  exactly --steps timed steps after --warmup untimed steps; batch 16 beside it.
+  `parity` compares the batch-1 stream with the reference's IEEE build on the
+  same checkpoint and prompt (tests/golden/4b_greedy.npz, 128 steps).
+
+Isolated kernels (every launch timed with HIP events around graph replays of
+back-to-back launches on the launching stream, operands cycled over copies
+larger than the 256 MB last-level cache so each launch streams from HBM):
+  config1_gemv       int8 matmul, N x K in {4096^2, 12288x4096, 4096x12288,
+                     151936x2560}, M in {1, 4, 16, 64}: HBM GB/s, and MFMA
+                     utilisation at M = 64
+  config2_deltanet   Gated DeltaNet step at batch 1/8/32 x 32 heads (GB/s) and
+                     the chunked prefill of 4096 rows (fp32 matrix-core
+                     utilisation)
+  config3_attention  GQA decode attention, 16 q / 2 kv heads, hd 256, bf16 KV,
+                     batch 1/16 x ctx 2048/8192/32768 (GB/s)
+  prefill            the 4B 2047-row prefill and its gate/up matmul (bf16
+                     matrix-core utilisation)
+`roofline` is the dominant decode kernel (the fused RMSNorm + gate/up GEMV +
+SwiGLU, 36 launches per step). `cpu_baseline` is the reference's own sources
+built with its release flags, one thread per physical core, on a bounded
+sample of the same 4B workload.
 
 Usage: python bench.py [--gpus 1] [--steps 256] [--warmup 8] [--kernel-only]
 """
@@ -22,8 +37,10 @@ Usage: python bench.py [--gpus 1] [--steps 256] [--warmup 8] [--kernel-only]
 from __future__ import annotations
 
 import argparse
+import ctypes as C
 import json
 import os
+import subprocess
 import sys
 import tempfile
 import time
@@ -34,115 +51,333 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
-BF16_PEAK_FLOPS = 2.5e15  # dense bf16 matrix-core peak of MI355X
+BF16_PEAK_FLOPS = 2.5e15   # dense bf16 matrix-core peak of MI355X
+FP32_MFMA_PEAK_FLOPS = 157.3e12  # dense fp32 matrix-core peak of MI355X
 METRIC = "decode tokens/sec at batch 1 and 16 (4B int8); int8 GEMV achieved HBM GB/s"
+GOLDEN_4B = os.path.join(ROOT, "tests", "golden", "4b_greedy.npz")
+POOL_BYTES = 1 << 30  # operands cycled over at least this many bytes
 
 
 def log(*a):
     print("[bench]", *a, file=sys.stderr, flush=True)
 
 
+def n_copies(nbytes, lo=2, hi=256):
+    return int(max(lo, min(hi, -(-POOL_BYTES // max(1, nbytes)))))
+
+
+def graph_time(hip, st, launch, per, launches=400):
+    """Average duration (us) of one launch: `per` launches (launch(i), i <
+    per) captured into one graph, replayed until about `launches` have run,
+    HIP events recorded on the same stream around the replays."""
+    lib = hip.lib()
+    for i in range(per):  # warm-up: code objects loaded, copies touched
+        launch(i)
+    hip.check(lib.qlm_graph_begin(st.ptr))
+    for i in range(per):
+        launch(i)
+    g = C.c_void_p()
+    hip.check(lib.qlm_graph_end(st.ptr, C.byref(g)))
+    hip.check(lib.qlm_graph_launch(g, st.ptr))
+    reps = max(1, launches // per)
+    e0, e1 = hip.Event(), hip.Event()
+    e0.record(st.ptr)
+    for _ in range(reps):
+        hip.check(lib.qlm_graph_launch(g, st.ptr))
+    e1.record(st.ptr)
+    st.sync()
+    us = e0.elapsed_ms(e1) * 1000.0 / (reps * per)
+    hip.check(lib.qlm_graph_destroy(g))
+    return us
+
+
+def dev_copies(hip, a, n):
+    """n device copies of host array a (one upload, then device copies)."""
+    first = hip.DeviceBuffer.from_numpy(a)
+    out = [first]
+    for _ in range(n - 1):
+        b = hip.DeviceBuffer(first.nbytes)
+        hip.check(hip.lib().qlm_memcpy_d2d(b.ptr, first.ptr, first.nbytes, None))
+        out.append(b)
+    hip.sync()
+    return out
+
+
+def free_all(bufs):
+    for b in bufs:
+        b.free()
+
+
+# ------------------------------------------------------------ config 1
 def gemv_bytes(N, K, M, group):
     nb = 1 if group == K else K // group
     return N * K + 4 * N * nb + 4 * M * K + 4 * M * N
 
 
-def bench_gemv(hip, shapes, Ms, group_kind, iters=100, pool_bytes=2 << 30):
-    """Config-1 GEMV: y = x (q s)^T with W int8 U{-127..127}, s U(0.001,0.01),
-    x N(0,1). Weights are cycled over copies totalling > 2 GiB so every launch
-    streams from HBM (the 256 MB last-level cache cannot hold them)."""
-    rng = np.random.default_rng(0)
-    st = hip.Stream()
-    out = []
-    for (N, K) in shapes:
-        group = K if group_kind == "row" else 32
-        nb = 1 if group == K else K // group
-        wb = N * K + 4 * N * nb
-        ncopy = int(max(2, min(48, pool_bytes // wb)))
-        q = rng.integers(-127, 128, (N, K), dtype=np.int8)
-        s = rng.uniform(0.001, 0.01, (N, nb)).astype(np.float32)
-        dq = [hip.DeviceBuffer.from_numpy(q) for _ in range(ncopy)]
-        ds = [hip.DeviceBuffer.from_numpy(s) for _ in range(ncopy)]
-        dz = _tile_major(hip, dq, ds, group, N, K, 1)
-        for M in Ms:
-            x = hip.DeviceBuffer.from_numpy(rng.standard_normal((M, K)).astype(np.float32))
-            y = hip.DeviceBuffer(M * N * 4)
-            n_it = iters if M <= 4 else max(10, iters // 4)
-            # M <= 4: the GEMV; M > 4: the matrix-core matmul (one weight pass)
-            fn = "qlm_gemv_i8" if M <= 4 else "qlm_matmul_i8"
-            nwork = hip.lib().qlm_matmul_i8_workspace_bytes(M, N, K, 0)
-            work = hip.DeviceBuffer(nwork)
-
-            def launch(i):
-                if M <= 4:
-                    hip.call(fn, x, K, dq[i % ncopy], ds[i % ncopy], group, y, N, M, N, K, st.ptr)
-                else:
-                    hip.call(fn, x, K, None, 0.0, dq[i % ncopy], ds[i % ncopy], group, y, N, M,
-                             N, K, 0, work, nwork, st.ptr)
-
-            for i in range(ncopy):
-                launch(i)
-            e0, e1 = hip.Event(), hip.Event()
-            e0.record(st.ptr)
-            for i in range(n_it):
-                launch(i)
-            e1.record(st.ptr)
-            us = e0.elapsed_ms(e1) * 1000.0 / n_it
-            b = gemv_bytes(N, K, M, group)
-            r = {"N": N, "K": K, "M": M, "group": group, "kernel": fn, "us": round(us, 2),
-                 "GBps": round(b / us / 1e3, 1), "bytes": b,
-                 "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
-            if M > 4:
-                # algorithmic flops over the dense bf16 matrix-core peak
-                r["mfma_util"] = round(2.0 * M * N * K / (us * 1e-6) / BF16_PEAK_FLOPS, 5)
-            out.append(r)
-            log(f"gemv {N}x{K} M={M} G={group}: {us:.1f} us {b / us / 1e3:.0f} GB/s")
-            if M == 1 and dz:
-                # the same product on the matrix cores over tile-major weights
-                def launch_mx(i):
-                    qz, sz = dz[i % ncopy]
-                    hip.call("qlm_gemv_i8_mx", x, None, 0.0, qz, sz, group, y, N, K, 0, st.ptr)
-
-                for i in range(ncopy):
-                    launch_mx(i)
-                e0, e1 = hip.Event(), hip.Event()
-                e0.record(st.ptr)
-                for i in range(n_it):
-                    launch_mx(i)
-                e1.record(st.ptr)
-                us = e0.elapsed_ms(e1) * 1000.0 / n_it
-                out.append({"N": N, "K": K, "M": M, "group": group, "kernel": "qlm_gemv_i8_mx",
-                            "layout": "tile-major", "us": round(us, 2),
-                            "GBps": round(b / us / 1e3, 1), "bytes": b,
-                            "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4)})
-                log(f"gemv_mx {N}x{K} M=1 G={group}: {us:.1f} us {b / us / 1e3:.0f} GB/s")
-            x.free()
-            y.free()
-            work.free()
-        for b_ in dq + ds + [t for pair in dz for t in pair if t not in ds]:
-            b_.free()
-    return out
-
-
-def _tile_major(hip, dq, ds, group, rows, K, halves):
-    """Tile-major copies (qlm_mx_swizzle) of each weight copy; [] when K has
-    no matrix-core launch shape. Per-row scales keep their layout."""
-    import ctypes as C
-
+def tile_major(hip, dq, ds, group, rows, K):
+    """Tile-major copies (qlm_mx_swizzle) of each weight copy; per-row scales
+    keep their layout."""
     qb, sb = C.c_size_t(), C.c_size_t()
-    if hip.lib().qlm_mx_layout_bytes(rows, K, group, halves, C.byref(qb), C.byref(sb)) != 0:
-        return []
+    hip.check(hip.lib().qlm_mx_layout_bytes(rows, K, group, 1, C.byref(qb), C.byref(sb)))
     out = []
     for q_, s_ in zip(dq, ds):
         qz = hip.DeviceBuffer(qb.value)
         sz = hip.DeviceBuffer(sb.value) if sb.value else s_
-        hip.call("qlm_mx_swizzle", q_, s_, group, rows, K, halves, qz,
-                 sz if sb.value else None, None)
+        hip.call("qlm_mx_swizzle", q_, s_, group, rows, K, 1, qz, sz if sb.value else None, None)
         out.append((qz, sz))
     hip.sync()
     return out
 
 
+def bench_config1(hip, Ms=(1, 4, 16, 64)):
+    """int8 matmul y = x (Wq s)^T: Wq U{-127..127}, s U(0.001, 0.01), x N(0,1).
+    Per-row scales (the workload's scheme) with the kernel the engine runs at
+    each M: M = 1 the matrix-core GEMV over tile-major weights; M = 4, 16, 64
+    the matrix-core matmul over row-major weights. Group-32 scales beside
+    them, where M = 4 and 16 take the batched-decode form over tile-major
+    weights (qlm_matmul_i8_t)."""
+    rng = np.random.default_rng(0)
+    st = hip.Stream()
+    out = []
+    for (N, K) in [(4096, 4096), (12288, 4096), (4096, 12288), (151936, 2560)]:
+        q = rng.integers(-127, 128, (N, K), dtype=np.int8)
+        for group in (K, 32):
+            nb = 1 if group == K else K // group
+            s = rng.uniform(0.001, 0.01, (N, nb)).astype(np.float32)
+            ncopy = n_copies(N * K + 4 * N * nb, lo=3, hi=128)
+            dq, ds = dev_copies(hip, q, ncopy), dev_copies(hip, s, ncopy)
+            dz = tile_major(hip, dq, ds, group, N, K)
+            for M in Ms:
+                x = hip.DeviceBuffer.from_numpy(rng.standard_normal((M, K)).astype(np.float32))
+                y = hip.DeviceBuffer(M * N * 4)
+                if M == 1:
+                    kern = "qlm_gemv_i8_mx"
+
+                    def launch(i):
+                        qz, sz = dz[i % ncopy]
+                        hip.call(kern, x, None, 0.0, qz, sz, group, y, N, K, 0, st.ptr)
+                    work = None
+                elif M <= 16 and group == 32:
+                    kern = "qlm_matmul_i8_t"
+                    nwork = hip.lib().qlm_matmul_i8_t_workspace_bytes(M, N, K, 0)
+                    work = hip.DeviceBuffer(nwork)
+
+                    def launch(i):
+                        qz, sz = dz[i % ncopy]
+                        hip.call(kern, x, K, None, 0.0, qz, sz, group, y, N, M, N, K, 0, work,
+                                 nwork, st.ptr)
+                else:
+                    kern = "qlm_matmul_i8"
+                    nwork = hip.lib().qlm_matmul_i8_workspace_bytes(M, N, K, 0)
+                    work = hip.DeviceBuffer(nwork)
+
+                    def launch(i):
+                        hip.call(kern, x, K, None, 0.0, dq[i % ncopy], ds[i % ncopy], group, y,
+                                 N, M, N, K, 0, work, nwork, st.ptr)
+                us = graph_time(hip, st, launch, ncopy, launches=max(100, 2 * ncopy))
+                b = gemv_bytes(N, K, M, group)
+                r = {"N": N, "K": K, "M": M, "scales": "row" if group == K else "group32",
+                     "kernel": kern, "us": round(us, 2), "GBps": round(b / us / 1e3, 1),
+                     "bytes": b, "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
+                if M == 64:  # algorithmic flops over the dense bf16 matrix-core peak
+                    r["mfma_util"] = round(2.0 * M * N * K / (us * 1e-6) / BF16_PEAK_FLOPS, 4)
+                out.append(r)
+                log(f"config1 {N}x{K} M={M} {r['scales']} {kern}: {us:.2f} us, "
+                    f"{r['GBps']:.0f} GB/s" + (f", MFMA util {r['mfma_util']:.3f}"
+                                               if M == 64 else ""))
+                x.free()
+                y.free()
+                if work is not None:
+                    work.free()
+            free_all(dq + ds + [t for pair in dz for t in pair if t not in ds])
+    return out
+
+
+# ------------------------------------------------------------ config 2
+def l2n(x):
+    return (x / np.linalg.norm(x, axis=-1, keepdims=True)).astype(np.float32)
+
+
+def sigmoid(x):
+    return (1.0 / (1.0 + np.exp(-x))).astype(np.float32)
+
+
+def bench_config2(hip, H=32, d=128, T=4096):
+    """Gated DeltaNet: the recurrent step (attention.cpp:498-571) at batch
+    1/8/32 x 32 heads, S N(0, 0.01), q/k L2-normalised N(0,1), v N(0,1),
+    decay sigmoid(N(0,1)+2), beta sigmoid(N(0,1)); bytes = B H (2*4 d^2 +
+    4*4 d + 8). Then the chunked prefill of T rows (64-row chunks) at batch 1,
+    with the chunked form's matrix-core flops per chunk and head, 8 C^2 d +
+    6 C d^2 (K K^T, Q K^T, the triangular solve on [bK | bV], W S, Q S, the
+    masked intra-chunk product, K^T W), over the fp32 matrix-core peak."""
+    rng = np.random.default_rng(2)
+    st = hip.Stream()
+    res = {"heads": H, "head_dim": d, "decode": []}
+    for B in (1, 8, 32):
+        sbytes = B * H * d * d * 4
+        ncopy = n_copies(sbytes, lo=2, hi=256)
+        S = (rng.standard_normal((B, H, d, d)) * 0.01).astype(np.float32)
+        dS = dev_copies(hip, S, ncopy)
+        q = hip.DeviceBuffer.from_numpy(l2n(rng.standard_normal((B, H, d))))
+        k = hip.DeviceBuffer.from_numpy(l2n(rng.standard_normal((B, H, d))))
+        v = hip.DeviceBuffer.from_numpy(rng.standard_normal((B, H, d)).astype(np.float32))
+        a = hip.DeviceBuffer.from_numpy(sigmoid(rng.standard_normal((B, H)) + 2))
+        bt = hip.DeviceBuffer.from_numpy(sigmoid(rng.standard_normal((B, H))))
+        o = hip.DeviceBuffer(B * H * d * 4)
+
+        def launch(i):
+            hip.call("qlm_gated_delta_step", q, k, v, a, bt, dS[i % ncopy], o, B, H, d, st.ptr)
+
+        us = graph_time(hip, st, launch, ncopy, launches=max(200, ncopy))
+        nbytes = B * H * (2 * 4 * d * d + 4 * 4 * d + 8)
+        res["decode"].append({"batch": B, "us": round(us, 2), "bytes": nbytes,
+                              "GBps": round(nbytes / us / 1e3, 1),
+                              "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)})
+        log(f"config2 DeltaNet step B={B} H={H}: {us:.2f} us, {nbytes / us / 1e3:.0f} GB/s")
+        free_all(dS + [q, k, v, a, bt, o])
+    # chunked prefill, batch 1
+    HD = H * d
+    ldp = 4 * HD + 2 * H
+    proj = hip.DeviceBuffer.from_numpy((rng.standard_normal((T, ldp)) * 0.6).astype(np.float32))
+    wt = hip.DeviceBuffer.from_numpy((rng.standard_normal((4, 3 * HD)) * 0.3).astype(np.float32))
+    A_log = hip.DeviceBuffer.from_numpy(np.log(rng.uniform(1, 16, H)).astype(np.float32))
+    dtb = hip.DeviceBuffer.from_numpy((rng.standard_normal(H) * 0.5 - 4).astype(np.float32))
+    nw = hip.DeviceBuffer.from_numpy((1 + rng.standard_normal(d) * 0.02).astype(np.float32))
+    conv, S1 = hip.DeviceBuffer(3 * 3 * HD * 4), hip.DeviceBuffer(H * d * d * 4)
+    out = hip.DeviceBuffer(T * HD * 4)
+    nbytes = hip.lib().qlm_deltanet_chunk_workspace_bytes(T, H, d)
+    work = hip.DeviceBuffer(nbytes)
+
+    conv.zero()
+    S1.zero()
+    hip.sync()
+
+    def launch_pf():
+        # each run continues from the last one's state (the arithmetic per
+        # row is the same); launched directly: four kernels of ~ms each
+        hip.call("qlm_deltanet_prefill_chunked", proj, ldp, T, conv, wt, A_log, dtb, nw, S1, 0,
+                 out, HD, H, d, work, nbytes, st.ptr)
+
+    launch_pf()
+    reps = 5
+    e0, e1 = hip.Event(), hip.Event()
+    e0.record(st.ptr)
+    for _ in range(reps):
+        launch_pf()
+    e1.record(st.ptr)
+    st.sync()
+    ms = e0.elapsed_ms(e1) / reps
+    C_ = 64
+    flops = (T // C_) * H * (8 * C_ * C_ * d + 6 * C_ * d * d)
+    res["chunked_prefill"] = {"rows": T, "chunk": C_, "batch": 1, "ms": round(ms, 3),
+                              "flops": flops, "TFLOPs": round(flops / ms / 1e9, 2),
+                              "mfma_util_fp32": round(flops / (ms * 1e-3) /
+                                                      FP32_MFMA_PEAK_FLOPS, 4),
+                              "rows_per_s": round(T / (ms * 1e-3), 1)}
+    log(f"config2 chunked prefill T={T} H={H}: {ms:.3f} ms, {flops / ms / 1e9:.1f} TFLOP/s")
+    free_all([proj, wt, A_log, dtb, nw, conv, S1, out, work])
+    return res
+
+
+# ------------------------------------------------------------ config 3
+def bf16_bits(x: np.ndarray) -> np.ndarray:
+    """fp32 -> bf16 bit patterns, round to nearest even (chunked, in place)."""
+    out = np.empty(x.shape, np.uint16)
+    flat, of = x.reshape(-1), out.reshape(-1)
+    step = 1 << 24
+    for i in range(0, flat.size, step):
+        u = flat[i:i + step].view(np.uint32)
+        of[i:i + step] = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    return out
+
+
+def bench_config3(hip, n_q=16, n_kv=2, hd=256, ctx_max=32768, Bmax=16):
+    """GQA decode attention over a bf16 KV cache [B, max_seq, n_kv, hd]
+    (attention.cpp:54-82; the reference's fp32 cache upcast): K/V N(0,1), q
+    fp32 N(0,1) (already rotated), softmax over ctx positions; bytes =
+    B * 2 * ctx * n_kv * hd * 2 + 8 * B * n_q * hd. One 16 x 32768-position
+    cache is generated; smaller cases read windows of it at distinct
+    offsets, so that successive launches stream different bytes."""
+    rng = np.random.default_rng(3)
+    st = hip.Stream()
+    shape = (Bmax, ctx_max, n_kv, hd)
+    kv = [hip.DeviceBuffer.from_numpy(bf16_bits(rng.standard_normal(shape, dtype=np.float32)))
+          for _ in range(2)]
+    row = n_kv * hd * 2  # bytes per cached position
+    total_pos = Bmax * ctx_max
+    res = []
+    for B in (1, Bmax):
+        q = hip.DeviceBuffer.from_numpy(rng.standard_normal((B, n_q, hd)).astype(np.float32))
+        o = hip.DeviceBuffer(B * n_q * hd * 4)
+        for ctx in (2048, 8192, 32768):
+            # windows of B sequences (stride ctx_max) starting at distinct offsets
+            last = total_pos - ((B - 1) * ctx_max + ctx)
+            offs = list(range(0, last + 1, ctx))[:64] or [0]
+            work = hip.DeviceBuffer(hip.lib().qlm_gqa_workspace_bytes(B, n_q, hd, ctx_max))
+
+            def launch(i):
+                off = offs[i % len(offs)] * row
+                hip.check(hip.lib().qlm_attention_decode(q.ptr, kv[0].ptr + off, kv[1].ptr + off,
+                                                         1, ctx_max, ctx, o.ptr, B, n_q, n_kv,
+                                                         hd, work.ptr, st.ptr))
+
+            per = max(2, len(offs))
+            us = graph_time(hip, st, launch, per, launches=max(100, per))
+            nbytes = B * 2 * ctx * n_kv * hd * 2 + 8 * B * n_q * hd
+            res.append({"batch": B, "ctx": ctx, "us": round(us, 2), "bytes": nbytes,
+                        "GBps": round(nbytes / us / 1e3, 1),
+                        "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)})
+            log(f"config3 attention B={B} ctx={ctx}: {us:.2f} us, {nbytes / us / 1e3:.0f} GB/s")
+            work.free()
+        free_all([q, o])
+    free_all(kv)
+    return {"n_q": n_q, "n_kv": n_kv, "head_dim": hd, "kv_dtype": "bf16", "cases": res}
+
+
+# ------------------------------------------------------------ prefill matmul
+def bench_prefill_matmul(hip, M=2047, F=9728, K=2560):
+    """The 4B prefill's largest matmul: RMSNorm + gate/up (2F = 19456 int8
+    rows, group-32 scales) + SwiGLU over M prompt rows, bf16 matrix cores;
+    utilisation = 2 M (2F) K / t over the dense bf16 peak."""
+    rng = np.random.default_rng(5)
+    st = hip.Stream()
+    rows = 2 * F
+    q = rng.integers(-127, 128, (rows, K), dtype=np.int8)
+    s = rng.uniform(0.001, 0.01, (rows, K // 32)).astype(np.float32)
+    ncopy = n_copies(rows * K, lo=2, hi=16)
+    dq, ds = dev_copies(hip, q, ncopy), dev_copies(hip, s, ncopy)
+    x = hip.DeviceBuffer.from_numpy(rng.standard_normal((M, K)).astype(np.float32))
+    nw = hip.DeviceBuffer.from_numpy((rng.standard_normal(K) * 0.02).astype(np.float32))
+    y = hip.DeviceBuffer(M * F * 4)
+    nwork = hip.lib().qlm_matmul_i8_workspace_bytes(M, F, K, 2)
+    work = hip.DeviceBuffer(nwork)
+
+    def launch(i):
+        hip.call("qlm_matmul_i8", x, K, nw, 1e-6, dq[i % ncopy], ds[i % ncopy], 32, y, F, M, F,
+                 K, 2, work, nwork, st.ptr)
+
+    us = graph_time(hip, st, launch, ncopy, launches=40)
+    flops = 2.0 * M * rows * K
+    free_all(dq + ds + [x, nw, y, work])
+    r = {"rows": M, "N": rows, "K": K, "kernel": "qlm_matmul_i8 (RMSNorm + gate/up + SwiGLU)",
+         "us": round(us, 1), "TFLOPs": round(flops / us / 1e6, 1),
+         "mfma_util": round(flops / (us * 1e-6) / BF16_PEAK_FLOPS, 4)}
+    log(f"prefill gate/up matmul M={M}: {us:.1f} us, {r['TFLOPs']} TFLOP/s, util "
+        f"{r['mfma_util']:.3f}")
+    return r
+
+
+def linear_params_4b():
+    """Weights of the 4B hybrid's linear layers (every projection but the
+    lm_head): what a prefill row multiplies."""
+    H, F, nh, d, nq, nkv, hd = 2560, 9728, 16, 128, 16, 4, 128
+    mlp = 2 * F * H + H * F
+    dn = (4 * nh * d + 2 * nh) * H + H * nh * d + mlp
+    at = (2 * nq * hd + 2 * nkv * hd) * H + H * nq * hd + mlp
+    return 27 * dn + 9 * at
+
+
+# ------------------------------------------------------------ dominant kernel
 # The dominant kernel of the batch-1 decode step (about a third of the step):
 # the fused RMSNorm + gate/up projection + SwiGLU GEMV of every layer, 4B
 # shape (F = 9728 outputs from 2F = 19456 int8 rows of K = 2560, group-32
@@ -160,62 +395,40 @@ def dominant_bytes():
     return rows * DOM_K + 4 * rows * (DOM_K // 32) + 4 * DOM_K + 4 * DOM_K + 4 * DOM_F
 
 
-def measure_dominant(hip, launches=400, pool_bytes=2 << 30):
+def measure_dominant(hip):
     """Average launch duration of the dominant kernel, HIP events recorded on
     the stream it is launched on (around graph replays of back-to-back
-    launches), weights cycled over > 2 GiB of copies so every launch streams
-    them from HBM (not the 256 MB last-level cache)."""
+    launches), weights cycled over > 1 GiB of copies."""
     rng = np.random.default_rng(1)
     st = hip.Stream()
     rows, nb = 2 * DOM_F, DOM_K // 32
-    wb = rows * DOM_K + 4 * rows * nb
-    ncopy = int(max(2, min(64, pool_bytes // wb)))
     q = rng.integers(-127, 128, (rows, DOM_K), dtype=np.int8)
     s = rng.uniform(0.001, 0.01, (rows, nb)).astype(np.float32)
     dq1 = [hip.DeviceBuffer.from_numpy(q)]
     ds1 = [hip.DeviceBuffer.from_numpy(s)]
-    z = _tile_major(hip, dq1, ds1, 32, DOM_F, DOM_K, 2)[0]
-    dq1[0].free()
-    ds1[0].free()
-    # ncopy tile-major copies: the first swizzled, the rest device copies of it
-    dz = [z] + [(hip.DeviceBuffer(z[0].nbytes), hip.DeviceBuffer(z[1].nbytes))
-                for _ in range(ncopy - 1)]
-    for qz, sz in dz[1:]:
-        hip.check(hip.lib().qlm_memcpy_d2d(qz.ptr, z[0].ptr, z[0].nbytes, None))
-        hip.check(hip.lib().qlm_memcpy_d2d(sz.ptr, z[1].ptr, z[1].nbytes, None))
+    qb, sb = C.c_size_t(), C.c_size_t()
+    hip.check(hip.lib().qlm_mx_layout_bytes(DOM_F, DOM_K, 32, 2, C.byref(qb), C.byref(sb)))
+    qz, sz = hip.DeviceBuffer(qb.value), hip.DeviceBuffer(sb.value)
+    hip.call("qlm_mx_swizzle", dq1[0], ds1[0], 32, DOM_F, DOM_K, 2, qz, sz, None)
+    hip.sync()
+    free_all(dq1 + ds1)
+    ncopy = n_copies(qb.value + sb.value, lo=2, hi=64)
+    dz = [(qz, sz)] + [(hip.DeviceBuffer(qb.value), hip.DeviceBuffer(sb.value))
+                       for _ in range(ncopy - 1)]
+    for a, b in dz[1:]:
+        hip.check(hip.lib().qlm_memcpy_d2d(a.ptr, qz.ptr, qb.value, None))
+        hip.check(hip.lib().qlm_memcpy_d2d(b.ptr, sz.ptr, sb.value, None))
     hip.sync()
     x = hip.DeviceBuffer.from_numpy(rng.standard_normal(DOM_K).astype(np.float32))
     nw = hip.DeviceBuffer.from_numpy((rng.standard_normal(DOM_K) * 0.02).astype(np.float32))
     y = hip.DeviceBuffer(DOM_F * 4)
 
     def launch(i):
-        qz, sz = dz[i % ncopy]
-        hip.call("qlm_gemv_i8_mx", x, nw, 1e-6, qz, sz, 32, y, DOM_F, DOM_K, 2, st.ptr)
+        a, b = dz[i % ncopy]
+        hip.call("qlm_gemv_i8_mx", x, nw, 1e-6, a, b, 32, y, DOM_F, DOM_K, 2, st.ptr)
 
-    # launched as in the decode step: back-to-back kernels replayed from one
-    # captured graph (no host launch gaps between them)
-    import ctypes as C
-
-    lib = hip.lib()
-    for i in range(ncopy):
-        launch(i)
-    per = 4 * ncopy
-    hip.check(lib.qlm_graph_begin(st.ptr))
-    for i in range(per):
-        launch(i)
-    g = C.c_void_p()
-    hip.check(lib.qlm_graph_end(st.ptr, C.byref(g)))
-    hip.check(lib.qlm_graph_launch(g, st.ptr))
-    reps = max(1, launches // per)
-    e0, e1 = hip.Event(), hip.Event()
-    e0.record(st.ptr)
-    for _ in range(reps):
-        hip.check(lib.qlm_graph_launch(g, st.ptr))
-    e1.record(st.ptr)
-    us = e0.elapsed_ms(e1) * 1000.0 / (reps * per)
-    hip.check(lib.qlm_graph_destroy(g))
-    for b_ in [t for pair in dz for t in pair] + [x, nw, y]:
-        b_.free()
+    us = graph_time(hip, st, launch, 4 * ncopy, launches=400)
+    free_all([t for pair in dz for t in pair] + [x, nw, y])
     return us
 
 
@@ -227,28 +440,53 @@ def copy_calibration(hip, nbytes=256 << 20, reps=4):
     for _ in range(reps):
         hip.check(hip.lib().qlm_memcpy_d2d(b.ptr, a.ptr, nbytes, None))
     hip.sync()
-    a.free()
-    b.free()
+    free_all([a, b])
 
 
+# ------------------------------------------------------------ decode runs
 def run_decode(eng, prompts, warmup, steps, graph=True):
     """Batched prefill of positions 0..n-2, warmup, then exactly `steps` timed
-    decode steps."""
+    decode steps (HIP events on the engine stream, device synchronised on
+    both sides)."""
+    from quicklm_amd import hip
+
     B, n = prompts.shape
     prefill_s = eng.start(prompts, batched_prefill=True)
     if warmup:
         eng.steps(warmup, graph)
-    from quicklm_amd import hip
-
     hip.sync()
     t1 = time.perf_counter()
     gpu_ms = eng.steps(steps, graph)
     hip.sync()
     wall_s = time.perf_counter() - t1
     toks = np.stack([eng.tokens(b, n, warmup + steps) for b in range(B)])
-    return {"batch": B, "prefill_s": round(prefill_s, 3), "gpu_ms": gpu_ms, "wall_s": wall_s,
+    return {"batch": B, "prefill_s": round(prefill_s, 4), "gpu_ms": gpu_ms, "wall_s": wall_s,
             "ms_per_step": gpu_ms / steps, "tok_s": B * steps / (gpu_ms / 1000.0),
             "tokens": toks}
+
+
+def ieee_parity(prompt, tokens):
+    """The batch-1 stream against the reference's IEEE build on the same
+    checkpoint and prompt (committed fixture, 128 steps): first divergence and
+    the reference's top-2 logit margin there."""
+    if not os.path.exists(GOLDEN_4B):
+        return None
+    g = np.load(GOLDEN_4B)
+    if len(prompt) != len(g["prompt"]) or not np.array_equal(prompt, g["prompt"]):
+        return {"note": "prompt differs from the fixture's (non-default --prompt-len)"}
+    ref = g["tokens"]
+    got = tokens[: len(ref)]
+    diff = np.nonzero(got != ref[: len(got)])[0]
+    first = int(diff[0]) if diff.size else int(len(got))
+    fast = g["tokens_fast"]
+    fd = np.nonzero(fast != ref)[0]
+    margin = g["margin"]
+    return {"reference": "reference sources built with IEEE flags, same checkpoint and prompt "
+                         "(tests/golden/4b_greedy.npz)",
+            "steps_compared": int(len(got)), "gpu_tokens_match_prefix_ieee": first,
+            "margin_at_divergence": float(margin[first]) if first < len(got) else None,
+            "min_margin_in_prefix": float(margin[:first].min()) if first else None,
+            "reference_fast_math_matches_ieee_prefix": int(fd[0]) if fd.size else int(len(ref))}
 
 
 def run_spec(target, draft, prompt, n_new, K, name):
@@ -271,23 +509,61 @@ def run_spec(target, draft, prompt, n_new, K, name):
             "matches_plain_greedy": bool(np.array_equal(out, plain))}
 
 
-def cpu_baseline(model_dir, prompt, n_prompt, n_decode, threads):
+# ------------------------------------------------------------ CPU baseline
+def host_cpus():
+    """Physical cores of this process's CPU set (one logical CPU each, SMT
+    siblings left out) and what lscpu says about the host."""
+    cpus = sorted(os.sched_getaffinity(0))
+    seen, phys = set(), []
+    for c in cpus:
+        base = f"/sys/devices/system/cpu/cpu{c}/topology/"
+        try:
+            key = (open(base + "physical_package_id").read().strip(),
+                   open(base + "core_id").read().strip())
+        except OSError:
+            key = ("?", str(c))
+        if key not in seen:
+            seen.add(key)
+            phys.append(c)
+    info = {"logical_cpus_in_affinity": len(cpus), "physical_cores_in_affinity": len(phys)}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=20).stdout
+        kv = dict(l.split(":", 1) for l in out.splitlines() if ":" in l)
+        kv = {k.strip(): v.strip() for k, v in kv.items()}
+        info.update({"model": kv.get("Model name"), "sockets": kv.get("Socket(s)"),
+                     "threads_per_core": kv.get("Thread(s) per core"),
+                     "numa_nodes": kv.get("NUMA node(s)")})
+    except (OSError, subprocess.SubprocessError):
+        pass
+    tpc = info.get("threads_per_core")
+    info["smt"] = "off" if tpc == "1" else f"on ({tpc} threads per core; one per core used)"
+    return phys, info
+
+
+def cpu_baseline(model_dir, prompt, n_prompt, n_decode):
     """The reference QuickLM CPU path (its own sources, -O3 -ffast-math) on the
     same checkpoint: batched prefill of n_prompt-1 ids, then n_decode greedy
-    steps; decode tokens/s as the reference CLI reports it (main.cpp:686-690)."""
+    steps; decode tokens/s as the reference CLI reports it (main.cpp:686-690).
+    One thread per physical core of this process's CPU set, pinned there."""
     from oracle.oracle import Reference
 
+    phys, info = host_cpus()
+    os.sched_setaffinity(0, phys)
     ref = Reference("fast")
-    ref.init_threads(threads)
+    ref.init_threads(len(phys))
     t0 = time.perf_counter()
     m = ref.load_model(model_dir, n_prompt + n_decode + 8, "int8")
     load_s = time.perf_counter() - t0
     toks, pre, dec, _ = m.generate(prompt[:n_prompt], n_decode)
     del m
-    return {"value": round(n_decode / dec, 3), "unit": "tokens/s", "cores": threads,
+    numa = info.get("numa_nodes")
+    return {"value": round(n_decode / dec, 3), "unit": "tokens/s", "cores": len(phys),
             "kind": "reference", "build": f"reference sources, -O3 -ffast-math -march=x86-64-"
-                                           f"{ref.kind}", "load_s": round(load_s, 1),
-            "prefill_s": round(pre, 2), "decode_s": round(dec, 2), "tokens": toks}
+                                           f"{ref.kind}",
+            "host": dict(info, numa_binding="single NUMA node: none needed" if numa == "1"
+                         else "threads pinned to the affinity set's physical cores"),
+            "load_s": round(load_s, 1), "prefill_s": round(pre, 2), "decode_s": round(dec, 2),
+            "tokens": toks}
 
 
 def main():
@@ -297,19 +573,21 @@ def main():
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--prompt-len", type=int, default=2048)
     ap.add_argument("--batch", type=int, default=16, help="second batch size (0 to skip)")
-    ap.add_argument("--cpu-prompt", type=int, default=128)
-    ap.add_argument("--cpu-decode", type=int, default=256)
+    ap.add_argument("--cpu-prompt", type=int, default=512,
+                    help="prompt ids prefilled by the CPU baseline (a prefix of the 2048)")
+    ap.add_argument("--cpu-decode", type=int, default=128)
     ap.add_argument("--kernel-only", action="store_true",
                     help="only the dominant-kernel timing and the copy of known size (for "
                          "rocprofv3 --pmc passes)")
     ap.add_argument("--skip-cpu", action="store_true")
-    ap.add_argument("--skip-gemv", action="store_true")
+    ap.add_argument("--skip-kernels", action="store_true",
+                    help="skip the isolated-kernel sections (config 1-3, prefill matmul)")
     ap.add_argument("--skip-int4", action="store_true",
                     help="skip the batch-1 decode at --precision int4")
     ap.add_argument("--skip-native", action="store_true",
                     help="skip the batch-1 decode at --precision bf16 (weights as stored)")
-    ap.add_argument("--skip-spec", action="store_true",
-                    help="skip the speculative sessions (int4 draft, K = --draft-tokens)")
+    ap.add_argument("--spec", action="store_true",
+                    help="also run speculative sessions (int4 draft, K = --draft-tokens)")
     ap.add_argument("--draft-tokens", type=int, default=4)
     ap.add_argument("--skip-row", action="store_true",
                     help="skip the batch-1 decode with one scale per output row (int8_row)")
@@ -341,15 +619,10 @@ def main():
         return
 
     result = {"metric": METRIC}
-    gemv = []
-    if not args.skip_gemv:
-        shapes = [(4096, 4096), (12288, 4096), (4096, 12288), (151936, 2560)]
-        gemv = bench_gemv(hip, shapes, [1, 4, 16, 64], "row")
-        gemv += bench_gemv(hip, [(151936, 2560)], [1], "g32")
-
     base = "/dev/shm" if os.path.isdir("/dev/shm") else tempfile.gettempdir()
     own_dir = args.model_dir is None
     mdir = args.model_dir or tempfile.mkdtemp(prefix="qlm_4b_", dir=base)
+    spec = []
     try:
         t0 = time.perf_counter()
         if own_dir:
@@ -366,6 +639,9 @@ def main():
         r1 = run_decode(eng, prompts[:1], args.warmup, args.steps, graph)
         log(f"batch 1: {r1['tok_s']:.1f} tok/s ({r1['ms_per_step']:.3f} ms/step), prefill "
             f"{r1['prefill_s']:.3f}s, kernels/step {eng.kernels_per_step()}")
+        parity = ieee_parity(prompts[0], r1["tokens"][0])
+        if parity:
+            log(f"IEEE reference parity: {parity}")
         rB = None
         if args.batch > 1:
             rB = run_decode(eng, prompts[:args.batch], args.warmup, args.steps, graph)
@@ -373,26 +649,24 @@ def main():
             a0, b0 = rB["tokens"][0], r1["tokens"][0]
             same = len(a0) if np.array_equal(a0, b0) else int(np.argmax(a0 != b0))
             rB["row0_matches_batch1"] = same
-            log(f"batch row 0 matches the batch-1 stream for {same}/{len(a0)} tokens "
-                "(matrix-core vs GEMV rounding)")
+            log(f"batch row 0 matches the batch-1 stream for {same}/{len(a0)} tokens")
 
         cpu = None
         if not args.skip_cpu:
-            threads = min(16, os.cpu_count() or 1)
-            cpu = cpu_baseline(mdir, prompts[0], args.cpu_prompt, args.cpu_decode, threads)
-            # same short prompt on the GPU for a token-stream check at 4B scale
+            cpu = cpu_baseline(mdir, prompts[0], args.cpu_prompt, args.cpu_decode)
+            # the same short prompt on the GPU: the fast-math build's stream beside it
             g, _, _ = eng.generate(prompts[:1, :args.cpu_prompt], args.cpu_decode)
             match = int(np.argmax(g[0] != cpu["tokens"])) if not np.array_equal(
                 g[0], cpu["tokens"]) else args.cpu_decode
-            cpu["gpu_tokens_match_prefix"] = match
-            log(f"cpu baseline {cpu['value']} tok/s on {threads} threads; GPU stream matches "
-                f"the reference for {match}/{args.cpu_decode} tokens")
+            cpu["gpu_tokens_match_prefix_fast_math"] = match
+            log(f"cpu baseline {cpu['value']} tok/s on {cpu['cores']} cores "
+                f"({cpu['host'].get('model')}); GPU stream matches the fast-math build for "
+                f"{match}/{args.cpu_decode} tokens")
             cpu.pop("tokens")
         eng.close()
 
         rrow = None
         if not args.skip_row:
-            # the same checkpoint quantised with one fp32 scale per output row
             erow = Engine(mdir, max_seq_len=max_seq, max_batch=1, precision="int8_row")
             rrow = run_decode(erow, prompts[:1], args.warmup, args.steps, graph)
             rrow["weight_bytes"] = erow.weight_bytes
@@ -400,57 +674,55 @@ def main():
             log(f"batch 1, per-row scales: {rrow['tok_s']:.1f} tok/s "
                 f"({rrow['ms_per_step']:.3f} ms/step), {rrow['weight_bytes'] / 1e9:.3f} GB")
 
-        r4 = None
+        r4 = e4 = None
         if not args.skip_int4:
-            # the same checkpoint at --precision int4 (Q4_0 weights, lm_head included)
             e4 = Engine(mdir, max_seq_len=max_seq, max_batch=1, precision="int4")
             r4 = run_decode(e4, prompts[:1], args.warmup, args.steps, graph)
             r4["weight_bytes"] = e4.weight_bytes
-            if args.skip_spec:
-                e4.close()
             log(f"batch 1, int4 weights: {r4['tok_s']:.1f} tok/s "
                 f"({r4['ms_per_step']:.3f} ms/step), {r4['weight_bytes'] / 1e9:.3f} GB")
-        rn = None
+        rn = en = None
         if not args.skip_native:
-            # the same checkpoint at --precision bf16, the reference's default:
-            # linears as stored (bf16), tied lm_head = the fp32 embedding table
             en = Engine(mdir, max_seq_len=max_seq, max_batch=1, precision="bf16")
             rn = run_decode(en, prompts[:1], args.warmup, args.steps, graph)
             rn["weight_bytes"] = en.weight_bytes
             log(f"batch 1, native weights: {rn['tok_s']:.1f} tok/s "
                 f"({rn['ms_per_step']:.3f} ms/step), {rn['weight_bytes'] / 1e9:.3f} GB, "
                 f"prefill {rn['prefill_s']:.3f}s")
-
-        spec = []
-        if not args.skip_spec and not args.skip_int4:
-            # the reference's default decode: the same checkpoint at int4 drafts
-            # K tokens per round for the target (main.cpp:166-172, :366-394)
-            targets = [("int8", Engine(mdir, max_seq_len=max_seq, max_batch=1,
-                                       precision="int8"))]
-            if rn is not None:
-                targets.append(("bf16", en))
-            for name, et in targets:
-                spec.append(run_spec(et, e4, prompts[0], args.steps, args.draft_tokens, name))
-                log(f"speculative, target {name} + int4 draft, K={args.draft_tokens}: "
-                    f"{spec[-1]['tok_s']:.1f} tok/s, accepted {spec[-1]['accepted']}/"
-                    f"{spec[-1]['drafted']} drafted, stream equals plain greedy: "
-                    f"{spec[-1]['matches_plain_greedy']}")
-            targets[0][1].close()
-        if rn is not None:
-            en.close()
-        if r4 is not None and not args.skip_spec:
-            e4.close()
+        if args.spec and e4 is not None:
+            et = Engine(mdir, max_seq_len=max_seq, max_batch=1, precision="int8")
+            targets = [("int8", et)] + ([("bf16", en)] if en is not None else [])
+            for name, t_ in targets:
+                spec.append(run_spec(t_, e4, prompts[0], args.steps, args.draft_tokens, name))
+                log(f"speculative, target {name} + int4 draft: {spec[-1]['tok_s']:.1f} tok/s, "
+                    f"accepted {spec[-1]['accepted']}/{spec[-1]['drafted']}")
+            et.close()
+        for e_ in (e4, en):
+            if e_ is not None:
+                e_.close()
     finally:
         if own_dir:
             import shutil
 
             shutil.rmtree(mdir, ignore_errors=True)
 
+    kern = {}
+    if not args.skip_kernels:
+        kern["config1_gemv"] = bench_config1(hip)
+        kern["config2_deltanet"] = bench_config2(hip)
+        kern["config3_attention"] = bench_config3(hip)
+        kern["prefill_gate_up"] = bench_prefill_matmul(hip)
+
     dom_us = measure_dominant(hip)
     dom_b = dominant_bytes()
     log(f"dominant kernel: {dom_us:.2f} us/launch, {dom_b / dom_us / 1e3:.0f} GB/s")
     wbytes = eng.weight_bytes
     step_s = r1["ms_per_step"] / 1000.0
+    pf_flops = 2.0 * (args.prompt_len - 1) * linear_params_4b()
+
+    def frac_w(r):
+        return round(r["weight_bytes"] / (r["ms_per_step"] / 1000.0) / 1e9 / HBM_PEAK_GBS, 4)
+
     result.update({
         "value": round(r1["tok_s"], 2),
         "unit": "tokens/s",
@@ -471,6 +743,7 @@ def main():
                    "batch": 1, "prompt_len": args.prompt_len, "scale_group": 32,
                    "launch": "eager" if args.eager else "hipGraph",
                    "weight_bytes": wbytes, "parallelism": "single GPU"},
+        "parity": parity,
         "batch16": None if rB is None else {"tok_s": round(rB["tok_s"], 2),
                                             "ms_per_step": round(rB["ms_per_step"], 4),
                                             "batch": rB["batch"],
@@ -481,27 +754,30 @@ def main():
                             "peak": HBM_PEAK_GBS, "unit": "GB/s",
                             "frac": round(wbytes / step_s / 1e9 / HBM_PEAK_GBS, 4),
                             "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / wbytes, 1)},
+        "prefill": {"rows": args.prompt_len - 1, "batch": 1, "s": r1["prefill_s"],
+                    "rows_per_s": round((args.prompt_len - 1) / r1["prefill_s"], 1),
+                    "linear_flops": pf_flops,
+                    "mfma_util_linear": round(pf_flops / r1["prefill_s"] / BF16_PEAK_FLOPS, 4),
+                    "gate_up_matmul": kern.get("prefill_gate_up")},
         "per_row_scales": None if rrow is None else {
             "tok_s": round(rrow["tok_s"], 2), "ms_per_step": round(rrow["ms_per_step"], 4),
             "batch": 1, "scale_group": "row", "weight_bytes": rrow["weight_bytes"],
-            "frac_of_weight_roofline": round(
-                rrow["weight_bytes"] / (rrow["ms_per_step"] / 1000.0) / 1e9 / HBM_PEAK_GBS, 4)},
+            "frac_of_weight_roofline": frac_w(rrow)},
         "int4": None if r4 is None else {
             "tok_s": round(r4["tok_s"], 2), "ms_per_step": round(r4["ms_per_step"], 4),
             "batch": 1, "precision": "int4 (Q4_0, group 32)", "weight_bytes": r4["weight_bytes"],
-            "frac_of_weight_roofline": round(
-                r4["weight_bytes"] / (r4["ms_per_step"] / 1000.0) / 1e9 / HBM_PEAK_GBS, 4),
+            "frac_of_weight_roofline": frac_w(r4),
             "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / r4["weight_bytes"], 1)},
         "native": None if rn is None else {
             "tok_s": round(rn["tok_s"], 2), "ms_per_step": round(rn["ms_per_step"], 4),
             "prefill_s": round(rn["prefill_s"], 4),
             "batch": 1, "precision": "bf16 (weights as stored: bf16 linears, fp32 tied lm_head)",
-            "weight_bytes": rn["weight_bytes"],
-            "frac_of_weight_roofline": round(
-                rn["weight_bytes"] / (rn["ms_per_step"] / 1000.0) / 1e9 / HBM_PEAK_GBS, 4),
+            "weight_bytes": rn["weight_bytes"], "frac_of_weight_roofline": frac_w(rn),
             "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / rn["weight_bytes"], 1)},
         "speculative": spec or None,
-        "gemv": gemv,
+        "config1_gemv": kern.get("config1_gemv"),
+        "config2_deltanet": kern.get("config2_deltanet"),
+        "config3_attention": kern.get("config3_attention"),
     })
     traffic, traffic_src = None, None
     if os.path.exists(PMC_FILE):
@@ -517,8 +793,9 @@ def main():
                           "us_per_launch": round(dom_us, 3), "launches_per_step": 36}
     if cpu:
         result["cpu_baseline"] = dict(cpu, sample=(
-            f"4B checkpoint, batch 1: prefill of {args.cpu_prompt - 1} prompt ids "
-            f"(untimed), then {args.cpu_decode} greedy decode steps (timed)"))
+            f"4B checkpoint, batch 1: prefill (untimed) of the first {args.cpu_prompt - 1} ids "
+            f"of the same 2048-token prompt, then {args.cpu_decode} greedy decode steps (timed) "
+            f"at context {args.cpu_prompt}-{args.cpu_prompt + args.cpu_decode}"))
     print(json.dumps(result), flush=True)
 
 
