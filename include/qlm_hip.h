@@ -128,6 +128,18 @@ int qlm_gemv_i8_mx_config(const float* x, const float* norm_w, float eps, const 
 int qlm_gemv_i8_mx(const float* x, const float* norm_w, float eps, const int8_t* q_tiles,
                    const float* s_tiles, int group, float* y, int N, int K, int epilogue,
                    void* stream);
+/* qlm_gemv_i8_mx over the output of qlm_deltanet_decode_cols: x[j] =
+ * u[j] / sqrt(sum_s ss[j / 128][s] / 128 + eps) for each 128-column head
+ * (ss [K / 128][8]), the head RMSNorm of Qwen3_5GatedDeltaNet::forward
+ * (attention.cpp:574-578) applied before the out-projection; epilogue 0
+ * store or 1 residual add. K a multiple of 128; u and ss 16-byte aligned.
+ * The int4 form takes qlm_mx4_swizzle tiles (group 32). */
+int qlm_gemv_i8_mx_headnorm(const float* u, const float* ss, float eps, const int8_t* q_tiles,
+                            const float* s_tiles, int group, float* y, int N, int K, int epilogue,
+                            void* stream);
+int qlm_gemv_i4_mx_headnorm(const float* u, const float* ss, float eps, const uint8_t* q_tiles,
+                            const float* s_tiles, float* y, int N, int K, int epilogue,
+                            void* stream);
 /* The launch shape qlm_gemv_i8_mx picks (waves per workgroup, blocks per
  * wave, workgroups), or QLM_ERR_SHAPE. Host only. */
 int qlm_gemv_i8_mx_shape(int N, int K, int epilogue, int* waves, int* ring, int* grid);
@@ -260,6 +272,26 @@ int qlm_deltanet_decode(const float* proj, int ldp, float* conv_state, const flo
                         const float* A_log, const float* dt_bias, const float* norm_w,
                         float* state, const int* pos, float* out, int ldo, int B, int H, int d,
                         void* stream);
+
+/* The same mixer with each head's 128 value columns split over 8
+ * workgroups (16 columns each), for small batches: H * 8 workgroups per
+ * sequence instead of H. The recurrence, conv ring and state updates are
+ * qlm_deltanet_decode's; the head RMSNorm, which needs all 128 outputs of a
+ * head, is left to the consumer: u[b] [H*d] (row stride ldu) holds
+ * o[j] * norm_w[j] * silu(z[j]) and ss [B, H, 8] the sums of o[j]^2 over
+ * each 16-column slice, so the mixer output is
+ * u[j] / sqrt(sum_s ss[b, h, s] / d + 1e-6) (qlm_gemv_i8_mx_headnorm applies
+ * it in its prologue). ticket: B*H*QLM_DN_TICKET_STRIDE unsigned (the
+ * ticket of (b, h) at index (b*H + h) * QLM_DN_TICKET_STRIDE), zero before
+ * the first call, left at multiples of 8 by every call (the workgroups of a
+ * head take one ticket each; the last one overwrites the head's q/k
+ * conv-ring row, which all of them read). Calls sharing a ticket array must
+ * be ordered on one stream. d = 128. */
+#define QLM_DN_TICKET_STRIDE 32
+int qlm_deltanet_decode_cols(const float* proj, int ldp, float* conv_state,
+                             const float* conv_w_t, const float* A_log, const float* dt_bias,
+                             const float* norm_w, float* state, const int* pos, float* u, int ldu,
+                             float* ss, unsigned* ticket, int B, int H, int d, void* stream);
 
 /* ---- A13: DeltaNet prefill of one sequence -----------------------------------
  * Qwen3_5GatedDeltaNet::forward_chunk (attention.cpp:600-758): the mixer of

@@ -179,6 +179,28 @@ void matmul_residual(const Tensor& A, const Tensor& B, Tensor& residual) {
           "qlm_gemv_i8_residual");
 }
 
+bool headnorm_supported(const Tensor& B) {
+    if (B.is_native() || !B.is_int8() || !B.int8_tiles || B.shape.size() != 2) return false;
+    const int64_t N = B.shape[0], K = B.shape[1];
+    int waves = 0, ring = 0, grid = 0;
+    return K % 128 == 0 && qlm_gemv_i8_mx_shape((int)N, (int)K, 1, &waves, &ring, &grid) == QLM_OK;
+}
+
+void matmul_headnorm_residual(const Tensor& U, const float* ss, float eps, const Tensor& B,
+                              Tensor& residual) {
+    const int64_t K = U.cols(), N = B.shape[0];
+    need(U.rows() == 1 && B.shape[1] == K && residual.cols() == N,
+         "matmul_headnorm_residual: shape mismatch");
+    need(headnorm_supported(B), "matmul_headnorm_residual: weight has no tile-major copy");
+    const int rc = B.int4_tiles
+                       ? qlm_gemv_i4_mx_headnorm(U.data, ss, eps, B.int4_tiles, B.int8_tile_scales,
+                                                 residual.data, (int)N, (int)K, 1, g_stream)
+                       : qlm_gemv_i8_mx_headnorm(U.data, ss, eps, B.int8_tiles, B.int8_tile_scales,
+                                                 B.int8_group, residual.data, (int)N, (int)K, 1,
+                                                 g_stream);
+    check(rc, "qlm_gemv_i8_mx_headnorm");
+}
+
 void matmul_swiglu_rmsnorm(const Tensor& A, const Tensor& norm_w, float eps, const Tensor& B,
                            Tensor& C) {
     const int64_t K = A.cols(), M = A.rows(), F = B.shape[0] / 2;

@@ -53,6 +53,14 @@ void causal_conv1d_update_tapmajor(const float* input, float* state, int oldest_
 void matmul_rmsnorm(const Tensor& A, const Tensor& norm_w, float eps, const Tensor& B, Tensor& C);
 // residual[m, n] += (A * B^T)[m, n] (matmul + elementwise_add).
 void matmul_residual(const Tensor& A, const Tensor& B, Tensor& residual);
+// One row of the column-split DeltaNet mixer (qlm_deltanet_decode_cols)
+// through its out-projection: residual += (U scaled per 128-column head by
+// 1/sqrt(sum of ss[head][0..7] / 128 + eps)) * B^T, the head RMSNorm of
+// attention.cpp:574-578 applied in the GEMV prologue. headnorm_supported()
+// says whether B has the tile-major copy and launch shape this needs.
+bool headnorm_supported(const Tensor& B);
+void matmul_headnorm_residual(const Tensor& U, const float* ss, float eps, const Tensor& B,
+                              Tensor& residual);
 // SwiGLU: B holds [gate; up] rows; C = silu(norm(A) gate^T) * (norm(A) up^T).
 void matmul_swiglu_rmsnorm(const Tensor& A, const Tensor& norm_w, float eps, const Tensor& B,
                            Tensor& C);

@@ -315,6 +315,11 @@ void DecoderModel::load(const std::string& dir, int max_seq_len, const std::stri
     argmax_work_.alloc(qlm_argmax_workspace_bytes((int)B, cfg_.vocab_size));
     tail_work_.alloc(qlm_lm_head_greedy_workspace_bytes());
     check(qlm_fill_u8(tail_work_.get(), 0, tail_work_.bytes(), stream_), "fill");
+    if (nh > 0) {  // the column-split mixer's partial sums and tickets (batch 1)
+        dn_ss_.alloc((size_t)nh * 8 * sizeof(float));
+        dn_ticket_.alloc((size_t)nh * QLM_DN_TICKET_STRIDE * sizeof(unsigned));
+        check(qlm_fill_u8(dn_ticket_.get(), 0, dn_ticket_.bytes(), stream_), "fill");
+    }
     if (QR_ > 0) {
         attn_work_.alloc(qlm_gqa_workspace_bytes((int)B, nq, hd, max_seq_));
         check(qlm_fill_u8(attn_work_.get(), 0, attn_work_.bytes(), stream_), "fill");
@@ -349,7 +354,25 @@ void DecoderModel::enqueue_step(int B) {
     int dn_i = 0, at_i = 0;
     for (auto& w : layers_) {
         Tensor in_ln({H}, w.in_ln.get<float>()), post_ln({H}, w.post_ln.get<float>());
-        if (w.linear) {
+        if (w.linear && B == 1 && math::headnorm_supported(w.dn_out.view())) {
+            // one sequence: the mixer over H x 8 workgroups, its head RMSNorm
+            // applied by the out-projection's prologue
+            Tensor proj({B, PD_}, proj_.get<float>());
+            proj.strides = {Pmax, 1};
+            math::matmul_rmsnorm(hx, in_ln, eps, w.dn_in.view(), proj);
+            check(qlm_deltanet_decode_cols(proj_.get<float>(), Pmax, conv_state_[dn_i].get<float>(),
+                                           w.conv_wt.get<float>(), w.A_log.get<float>(),
+                                           w.dt_bias.get<float>(), w.dn_norm.get<float>(),
+                                           dn_state_[dn_i].get<float>(), pos_.get<int>(),
+                                           core_.get<float>(), CORE_, dn_ss_.get<float>(),
+                                           dn_ticket_.get<unsigned>(), 1, nh, d, stream_),
+                  "deltanet");
+            Tensor core({B, HD_}, core_.get<float>());
+            core.strides = {CORE_, 1};
+            math::matmul_headnorm_residual(core, dn_ss_.get<float>(), 1e-6f, w.dn_out.view(), hx);
+            ++dn_i;
+            n += math::matmul_launches(B, PD_, H, true, native_) + 2;
+        } else if (w.linear) {
             Tensor proj({B, PD_}, proj_.get<float>());
             proj.strides = {Pmax, 1};
             math::matmul_rmsnorm(hx, in_ln, eps, w.dn_in.view(), proj);

@@ -198,6 +198,9 @@ class DecoderModel : public GreedyModel {
     // activations
     DeviceBuffer h_, proj_, core_, act_, logits_, argmax_work_, attn_work_, tail_work_;
     DeviceBuffer mm_work_;  // workspace of the matrix-core matmuls (M > 1)
+    // batch-1 column-split DeltaNet mixer: per-head partial sums of squares
+    // [nh, 8] (consumed by the out-projection) and tickets [nh]
+    DeviceBuffer dn_ss_, dn_ticket_;
     // prefill activations for up to pf_rows_ prompt rows per chunk
     DeviceBuffer hx_pf_, proj_pf_, core_pf_, act_pf_, gqa_pf_work_, dn_pf_work_;
     int pf_rows_ = 0;

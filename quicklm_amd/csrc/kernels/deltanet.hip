@@ -235,6 +235,177 @@ __global__ __launch_bounds__(kThreads) void k_deltanet_decode(
     }
 }
 
+// Column-split form of the decode mixer, for small batches: the 128 value
+// columns of a head are spread over kSplit workgroups of kColW columns, so
+// a batch-1 step runs H * kSplit workgroups instead of H (the recurrence is
+// independent per value column j: kv[j], delta[j] and o[j] reduce over the
+// key index i only, attention.cpp:513-569). Each workgroup recomputes the
+// head's conv1d + SiLU + L2 norm of q and k (256 channels) and the gates,
+// and owns its 16 v channels and the state columns [16 s, 16 s + 16) of all
+// 128 rows. The head RMSNorm needs all 128 outputs, so it is left to the
+// consumer: the workgroup writes u[j] = o[j] * w[j] * silu(z[j]) and the sum
+// of o[j]^2 over its columns (ss[b, h, s]); the mixer output is
+// u[j] / sqrt(sum_s ss[b, h, s] / d + 1e-6) (the out-projection GEMV applies
+// it in its prologue).
+//
+// Every workgroup of a head reads the q/k channels' oldest ring row, which
+// this step overwrites with the new input. The workgroup that overwrites it
+// is the last one to have read it: each workgroup takes a ticket (one
+// atomic add on ticket[b, h], each in a 128-byte line of its own: atomics
+// on one line serialise) once its ring values have arrived and looks
+// at it at its end; the one holding ticket kSplit - 1 (mod kSplit) writes
+// the q/k ring row. No workgroup waits for another; the tickets stay a
+// multiple of kSplit between launches (and wrap consistently, kSplit
+// dividing 2^32). The L2 norms of q and k enter as the scalars 1/|q| and
+// 1/|k| on the reductions (the reference divides each element; the same
+// value to rounding).
+constexpr int kColW = 16;                       // value columns per workgroup
+constexpr int kSplit = kD / kColW;              // workgroups per head
+constexpr int kColThreads = 256;
+constexpr int kColRG = kColThreads / kColW;     // row groups
+constexpr int kColRows = kD / kColRG;           // state rows per thread
+
+__global__ __launch_bounds__(kColThreads) void k_deltanet_cols(
+    const float* __restrict__ proj, int ldp, float* __restrict__ conv_state,
+    const float* __restrict__ wt, const float* __restrict__ A_log,
+    const float* __restrict__ dt_bias, const float* __restrict__ norm_w,
+    float* __restrict__ state, const int* __restrict__ pos, float* __restrict__ u, int ldu,
+    float* __restrict__ ss, unsigned* __restrict__ ticket, int H) {
+    constexpr int NWV = kColThreads / QLM_WAVE;
+    __shared__ float qs[kD], ks[kD], vs[kColW], dl[kColW];
+    __shared__ float red[NWV][kColW];
+    __shared__ float ssq[NWV], gsc[2];
+    const int h = blockIdx.x / kSplit, sp = blockIdx.x % kSplit;
+    const int b = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int HD = H * kD;
+    const int C = 3 * HD;
+    const float* pr = proj + (size_t)b * ldp;
+    float* cs = conv_state + (size_t)b * 3 * C;
+    float* Sh = state + ((size_t)b * H + h) * kD * kD;
+    const int j = tid & (kColW - 1), rg = tid / kColW;
+    const int col = sp * kColW + j;  // value column of this thread
+
+    // Operands, all unconditional: the position, thread tid's q/k channel
+    // (q_h for tid < d, else k_h), the v channel of column col, z, gain and
+    // gates, then the state slice rows rg*8 .. rg*8+7 of column col.
+    const int pb = pos ? pos[b] : 0;
+    const int chqk = h * kD + tid + (tid < kD ? 0 : HD - kD);
+    const int chv = 2 * HD + h * kD + col;
+    float rq[3], wq[4], rv[3], wv[4];
+#pragma unroll
+    for (int t = 0; t < 3; ++t) {
+        rq[t] = cs[(size_t)t * C + chqk];
+        rv[t] = cs[(size_t)t * C + chv];
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        wq[t] = wt[(size_t)t * C + chqk];
+        wv[t] = wt[(size_t)t * C + chv];
+    }
+    const float xq = pr[chqk], xv = pr[chv];
+    const float zj = pr[3 * HD + h * kD + col];
+    const float nwj = norm_w[col];
+    const float ga = pr[4 * HD + H + h], gb = pr[4 * HD + h];
+    const float gdt = dt_bias[h], galog = A_log[h];
+    float sr[kColRows];
+#pragma unroll
+    for (int r = 0; r < kColRows; ++r) sr[r] = Sh[(size_t)(rg * kColRows + r) * kD + col];
+
+    // conv1d (taps chronological from the oldest ring row) + SiLU; the
+    // sums of squares of q (waves 0-1) and k (waves 2-3) and the gates are
+    // formed in the same phase: the L2 norms enter the recurrence as the
+    // scalars 1/|q| and 1/|k| (attention.cpp:463-470)
+    const int oldest = pb % 3;
+    auto conv = [&](const float (&ring)[3], const float (&w)[4], float x) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 3; ++t) {
+            const int row = (oldest + t) % 3;
+            const float r = row == 0 ? ring[0] : (row == 1 ? ring[1] : ring[2]);
+            acc = nc_add_mul(acc, r, w[t]);
+        }
+        acc = nc_add_mul(acc, x, w[3]);
+        return silu_f(acc);
+    };
+    const float yq = conv(rq, wq, xq);
+    const float yv = conv(rv, wv, xv);
+    if (tid < kD) qs[tid] = yq;
+    else ks[tid - kD] = yq;
+    const float wsq = wave_sum(yq * yq);
+    if (lane == 0) ssq[wave] = wsq;
+    if (tid < kColW) {
+        vs[tid] = yv;
+        cs[(size_t)oldest * C + chv] = xv;  // this workgroup's own v channels
+    }
+    if (tid == kColThreads - 1) {  // gates (attention.cpp:472-483)
+        const float dt = ga + gdt;
+        const float sp_ = dt > 20.0f ? dt : log1pf(expf(dt));
+        const float alpha = -expf(galog) * sp_;
+        gsc[0] = expf(alpha);
+        gsc[1] = 1.0f / (1.0f + expf(-gb));
+    }
+    __syncthreads();  // every thread's ring values have arrived
+    // Ticket, taken now; its value is needed only at the end. The workgroup
+    // drawing the last ticket of the head overwrites the q/k ring row.
+    unsigned t0 = 0;
+    if (tid == 0) t0 = atomicAdd(&ticket[((size_t)b * H + h) * QLM_DN_TICKET_STRIDE], 1u);
+
+    const float rqn = 1.0f / sqrtf((ssq[0] + ssq[1]) + 1e-6f);
+    const float rkn = 1.0f / sqrtf((ssq[2] + ssq[3]) + 1e-6f);
+    const float dec = gsc[0], beta = gsc[1];
+
+    // (1) decay and kv[col] = k . S_decayed[:, col]
+    float kv = 0.0f;
+#pragma unroll
+    for (int r = 0; r < kColRows; ++r) {
+        sr[r] *= dec;
+        kv = fmaf(ks[rg * kColRows + r], sr[r], kv);
+    }
+    // the 4 row groups of a wave share column j at lanes j, j+16, j+32, j+48
+    kv += __shfl_xor(kv, 16, QLM_WAVE);
+    kv += __shfl_xor(kv, 32, QLM_WAVE);
+    if (lane < kColW) red[wave][lane] = kv;
+    __syncthreads();
+    if (tid < kColW)
+        dl[tid] = vs[tid] - ((red[0][tid] + red[1][tid]) + (red[2][tid] + red[3][tid])) * rkn;
+    __syncthreads();
+
+    // (2) S += (beta k) delta^T ; (3) o[col] = q . S_new[:, col]
+    const float dj = dl[j];
+    const float bk = beta * rkn;
+    float o = 0.0f;
+#pragma unroll
+    for (int r = 0; r < kColRows; ++r) {
+        const int i = rg * kColRows + r;
+        sr[r] = fmaf(bk * ks[i], dj, sr[r]);
+        o = fmaf(qs[i], sr[r], o);
+        Sh[(size_t)i * kD + col] = sr[r];
+    }
+    o += __shfl_xor(o, 16, QLM_WAVE);
+    o += __shfl_xor(o, 32, QLM_WAVE);
+    if (lane < kColW) red[wave][lane] = o;  // red's kv sums were read before the last barrier
+    __syncthreads();
+    if (wave == 0) {
+        float oj = 0.0f;
+        if (lane < kColW) {
+            oj = ((red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane])) *
+                 (rqn * (1.0f / sqrtf((float)kD)));
+            u[(size_t)b * ldu + h * kD + col] = (oj * nwj) * silu_f(zj);
+        }
+        const float sq = group_sum<kColW>(oj * oj);
+        if (lane == 0) ss[((size_t)b * H + h) * kSplit + sp] = sq;
+        // the last workgroup of the head to have read the q/k ring row
+        // overwrites it with this step's inputs (lane l copies 4 of the 256)
+        t0 = __shfl(t0, 0, QLM_WAVE);
+        if (t0 % kSplit == kSplit - 1) {
+            const int c = h * kD + (lane & 31) * 4 + (lane < 32 ? 0 : HD);
+            *reinterpret_cast<float4*>(cs + (size_t)oldest * C + c) =
+                *reinterpret_cast<const float4*>(pr + c);
+        }
+    }
+}
+
 // Prefill of one sequence over T consecutive rows of proj (positions
 // p0 .. p0+T-1), one workgroup per head: the reference processes the rows of
 // a prompt one after another through the same recurrence
@@ -376,6 +547,24 @@ extern "C" int qlm_deltanet_decode(const float* proj, int ldp, float* conv_state
     if (ldp < 4 * H * d + 2 * H || ldo < H * d) return QLM_ERR_SHAPE;
     hipLaunchKernelGGL(k_deltanet_decode, dim3(H, B), dim3(kThreads), 0, as_stream(stream), proj,
                        ldp, conv_state, conv_w_t, A_log, dt_bias, norm_w, state, pos, out, ldo, H);
+    return qlm_launch_status();
+}
+
+extern "C" int qlm_deltanet_decode_cols(const float* proj, int ldp, float* conv_state,
+                                        const float* conv_w_t, const float* A_log,
+                                        const float* dt_bias, const float* norm_w, float* state,
+                                        const int* pos, float* u, int ldu, float* ss,
+                                        unsigned* ticket, int B, int H, int d, void* stream) {
+    if (!proj || !conv_state || !conv_w_t || !A_log || !dt_bias || !norm_w || !state || !u ||
+        !ss || !ticket || B <= 0 || H <= 0)
+        return QLM_ERR_ARG;
+    if (d != kD) return QLM_ERR_SHAPE;
+    if (ldp < 4 * H * d + 2 * H || ldu < H * d) return QLM_ERR_SHAPE;
+    // the last workgroup copies the q/k inputs into the ring as float4
+    if (ldp % 4 != 0 || (((uintptr_t)proj | (uintptr_t)conv_state) & 15u)) return QLM_ERR_SHAPE;
+    hipLaunchKernelGGL(k_deltanet_cols, dim3(H * kSplit, B), dim3(kColThreads), 0,
+                       as_stream(stream), proj, ldp, conv_state, conv_w_t, A_log, dt_bias, norm_w,
+                       state, pos, u, ldu, ss, ticket, H);
     return qlm_launch_status();
 }
 

@@ -31,7 +31,11 @@ constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / QLM_WAVE;
 constexpr int kLdsBudget = 64 * 1024;
 
-enum { PRO_NONE = 0, PRO_RMSNORM = 1 };
+// PRO_HEADNORM (k_gemv_mx only): x is the column-split DeltaNet mixer's
+// u, and each 128-column head of it is scaled by 1/sqrt(sum of the head's
+// eight partial sums of squares / 128 + eps), the head RMSNorm the mixer
+// left to its consumer (nw then points at the partial sums [K / 128][8]).
+enum { PRO_NONE = 0, PRO_RMSNORM = 1, PRO_HEADNORM = 2 };
 enum { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_ARGMAX = 3 };
 
 // Greedy tail of a decode step (EPI_ARGMAX, M = 1): the logits are stored and
@@ -733,12 +737,18 @@ __global__ __launch_bounds__(NW * QLM_WAVE) void k_gemv_mx(
     // unconditional (block clamped into K; lanes past the wave's blocks are
     // zeroed once the values are used): a load under a branch makes the
     // compiler wait for it at the branch's end, before the weight loads.
-    float4 xr[XL], gr[XL];
+    float4 xr[XL], gr[XL], hn[XL];
 #pragma unroll
     for (int i = 0; i < XL; ++i) {
         const int b = min(w + NW * (4 * i + qd), nblk - 1);
         xr[i] = reinterpret_cast<const float4*>(x)[b * 16 + n];
         if constexpr (PRO == PRO_RMSNORM) gr[i] = reinterpret_cast<const float4*>(nw)[b * 16 + n];
+        if constexpr (PRO == PRO_HEADNORM) {
+            // the head (two 64-column blocks) of block b: its eight partials
+            const float4* hp = reinterpret_cast<const float4*>(nw) + (size_t)(b >> 1) * 2;
+            gr[i] = hp[0];
+            hn[i] = hp[1];
+        }
     }
     __builtin_amdgcn_sched_barrier(0);
 
@@ -798,6 +808,15 @@ __global__ __launch_bounds__(NW * QLM_WAVE) void k_gemv_mx(
             v.y *= 1.0f + g.y;
             v.z *= 1.0f + g.z;
             v.w *= 1.0f + g.w;
+        }
+        if constexpr (PRO == PRO_HEADNORM) {
+            const float4 a = gr[i], c = hn[i];
+            const float tot = ((a.x + a.y) + (a.z + a.w)) + ((c.x + c.y) + (c.z + c.w));
+            const float sn = 1.0f / sqrtf(tot / 128.0f + eps);
+            v.x *= sn;
+            v.y *= sn;
+            v.z *= sn;
+            v.w *= sn;
         }
         m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
     }
@@ -1245,6 +1264,9 @@ int mx_dispatch(int pro, int epi, const MxConfig& c, const float* x, const float
         if (pro == PRO_NONE && epi == EPI_STORE) QLM_MX_CALL(false, PRO_NONE, EPI_STORE, true);
         if (pro == PRO_RMSNORM && epi == EPI_STORE) QLM_MX_CALL(false, PRO_RMSNORM, EPI_STORE, true);
         if (pro == PRO_NONE && epi == EPI_RESID) QLM_MX_CALL(false, PRO_NONE, EPI_RESID, true);
+        if (pro == PRO_HEADNORM && epi == EPI_RESID)
+            QLM_MX_CALL(false, PRO_HEADNORM, EPI_RESID, true);
+        if (pro == PRO_HEADNORM) QLM_MX_CALL(false, PRO_HEADNORM, EPI_STORE, true);
         QLM_MX_CALL(false, PRO_RMSNORM, EPI_SWIGLU, true);
     }
     if (epi == EPI_ARGMAX) {
@@ -1255,8 +1277,13 @@ int mx_dispatch(int pro, int epi, const MxConfig& c, const float* x, const float
         if (pro == PRO_NONE && epi == EPI_STORE) QLM_MX_CALL(true, PRO_NONE, EPI_STORE, false);
         if (pro == PRO_RMSNORM && epi == EPI_STORE) QLM_MX_CALL(true, PRO_RMSNORM, EPI_STORE, false);
         if (pro == PRO_NONE && epi == EPI_RESID) QLM_MX_CALL(true, PRO_NONE, EPI_RESID, false);
+        if (pro == PRO_HEADNORM && epi == EPI_RESID)
+            QLM_MX_CALL(true, PRO_HEADNORM, EPI_RESID, false);
+        if (pro == PRO_HEADNORM) QLM_MX_CALL(true, PRO_HEADNORM, EPI_STORE, false);
         QLM_MX_CALL(true, PRO_RMSNORM, EPI_SWIGLU, false);
     }
+    if (pro == PRO_HEADNORM && epi == EPI_RESID) QLM_MX_CALL(false, PRO_HEADNORM, EPI_RESID, false);
+    if (pro == PRO_HEADNORM) QLM_MX_CALL(false, PRO_HEADNORM, EPI_STORE, false);
     if (pro == PRO_NONE && epi == EPI_STORE) QLM_MX_CALL(false, PRO_NONE, EPI_STORE, false);
     if (pro == PRO_RMSNORM && epi == EPI_STORE) QLM_MX_CALL(false, PRO_RMSNORM, EPI_STORE, false);
     if (pro == PRO_NONE && epi == EPI_RESID) QLM_MX_CALL(false, PRO_NONE, EPI_RESID, false);
@@ -1505,6 +1532,37 @@ extern "C" int qlm_gemv_i8_mx(const float* x, const float* norm_w, float eps,
     if (c.nw == 0) return QLM_ERR_SHAPE;
     return mx_dispatch(pro, epilogue, c, x, norm_w, eps, q_tiles, s_tiles, rowscale, y, N, K,
                        as_stream(stream));
+}
+
+// The column-split DeltaNet mixer's output through a projection: x[j] =
+// u[j] / sqrt(sum of ss[j / 128][0..7] / 128 + eps), per 128-column head.
+namespace {
+int headnorm_mx(const float* u, const float* ss, float eps, const int8_t* q, const float* s,
+                int group, float* y, int N, int K, int epilogue, bool w4, void* stream) {
+    if (!u || !ss || !q || !s || !y || N <= 0 || K <= 0) return QLM_ERR_ARG;
+    if (epilogue != EPI_STORE && epilogue != EPI_RESID) return QLM_ERR_ARG;
+    if (K % 128 != 0) return QLM_ERR_SHAPE;  // whole heads of 128 columns
+    const bool rowscale = (group == K);
+    if (!rowscale && group != 32) return QLM_ERR_SHAPE;
+    if (((uintptr_t)u | (uintptr_t)q | (uintptr_t)ss) & 15u) return QLM_ERR_SHAPE;
+    const MxConfig c = mx_config(N, K, epilogue, w4);
+    if (c.nw == 0) return QLM_ERR_SHAPE;
+    return mx_dispatch(PRO_HEADNORM, epilogue, c, u, ss, eps, q, s, rowscale, y, N, K,
+                       as_stream(stream), GreedyTail{}, w4);
+}
+}  // namespace
+
+extern "C" int qlm_gemv_i8_mx_headnorm(const float* u, const float* ss, float eps,
+                                       const int8_t* q_tiles, const float* s_tiles, int group,
+                                       float* y, int N, int K, int epilogue, void* stream) {
+    return headnorm_mx(u, ss, eps, q_tiles, s_tiles, group, y, N, K, epilogue, false, stream);
+}
+
+extern "C" int qlm_gemv_i4_mx_headnorm(const float* u, const float* ss, float eps,
+                                       const uint8_t* q_tiles, const float* s_tiles, float* y,
+                                       int N, int K, int epilogue, void* stream) {
+    return headnorm_mx(u, ss, eps, reinterpret_cast<const int8_t*>(q_tiles), s_tiles, 32, y, N,
+                       K, epilogue, true, stream);
 }
 
 extern "C" int qlm_gemv_i8_rmsnorm(const float* x, int ldx, const float* norm_w, float eps,

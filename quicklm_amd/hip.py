@@ -89,6 +89,10 @@ _SIGS = {
     "qlm_gated_delta_step": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "qlm_deltanet_decode": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i,
                                  _i, _vp]),
+    "qlm_deltanet_decode_cols": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp,
+                                      _vp, _i, _i, _i, _vp]),
+    "qlm_gemv_i8_mx_headnorm": (_i, [_vp, _vp, _f, _vp, _vp, _i, _vp, _i, _i, _i, _vp]),
+    "qlm_gemv_i4_mx_headnorm": (_i, [_vp, _vp, _f, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "qlm_gqa_workspace_bytes": (_sz, [_i, _i, _i, _i]),
     "qlm_gqa_decode": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _i, _i,
                             _i, _i, _i, _i, _vp, _vp]),

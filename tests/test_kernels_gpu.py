@@ -852,3 +852,76 @@ def test_attention_decode(hip, orc, rng, kv, ctx):
     if ctx == 1:  # one position: the output is V[0] exactly up to rounding
         assert rel_err(do.to_numpy(q.shape, np.float32)[:, :n_q // n_kv],
                        np.broadcast_to(v[:, 0, :1], (B, n_q // n_kv, hd))) < 1e-6
+
+
+@pytest.mark.parametrize("B,H", [(1, 16), (2, 8)])
+def test_deltanet_decode_cols(hip, orc, rng, B, H):
+    """Column-split mixer over 5 steps (ring index pos % 3): u scaled by the
+    head norm from the 8 partial sums equals the oracle's mixer output; the
+    state and conv ring equal the oracle's; the tickets stay a multiple of 8."""
+    d = 128
+    HD = H * d
+    ldp = 4 * HD + 2 * H
+    wt = (rng.standard_normal((4, 3 * HD)) * 0.3).astype(np.float32)
+    A_log = np.log(rng.uniform(1, 16, H)).astype(np.float32)
+    dtb = (rng.standard_normal(H) * 0.5 - 4).astype(np.float32)
+    nw = (1 + rng.standard_normal(d) * 0.02).astype(np.float32)
+    conv = (rng.standard_normal((B, 3, 3 * HD)) * 0.5).astype(np.float32)
+    S = (rng.standard_normal((B, H, d, d)) * 0.01).astype(np.float32)
+    dconv, dS = dev(hip, conv), dev(hip, S)
+    conv_ref = [conv[b].copy() for b in range(B)]
+    S_ref = [S[b].copy() for b in range(B)]
+    dwt, dA, ddt, dnw = dev(hip, wt), dev(hip, A_log), dev(hip, dtb), dev(hip, nw)
+    stride = 32  # QLM_DN_TICKET_STRIDE
+    ticket = hip.DeviceBuffer(B * H * stride * 4)
+    ticket.zero()
+    du, dss = hip.DeviceBuffer(B * HD * 4), hip.DeviceBuffer(B * H * 8 * 4)
+    for step in range(5):
+        proj = (rng.standard_normal((B, ldp)) * 0.6).astype(np.float32)
+        pos = np.array([step + 11 * b for b in range(B)], np.int32)
+        ref = np.stack([orc.deltanet_core(proj[b], conv_ref[b], int(pos[b] % 3), wt, A_log, dtb,
+                                          nw, S_ref[b], H, d) for b in range(B)])
+        say("deltanet_decode_cols", B, H, step)
+        hip.call("qlm_deltanet_decode_cols", dev(hip, proj), ldp, dconv, dwt, dA, ddt, dnw, dS,
+                 dev(hip, pos), du, HD, dss, ticket, B, H, d, None)
+        u = du.to_numpy((B, H, d), np.float32).astype(np.float64)
+        ss = dss.to_numpy((B, H, 8), np.float32).astype(np.float64).sum(axis=2)
+        out = (u / np.sqrt(ss / d + 1e-6)[:, :, None]).reshape(B, HD)
+        assert rel_err(out, ref) < 1e-4
+        assert np.array_equal(dconv.to_numpy(conv.shape, np.float32), np.stack(conv_ref))
+        assert rel_err(dS.to_numpy(S.shape, np.float32), np.stack(S_ref)) < 1e-5
+        tk = ticket.to_numpy(B * H * stride, np.uint32).reshape(B * H, stride)
+        assert np.all(tk[:, 0] == 8 * (step + 1)) and not tk[:, 1:].any()
+
+
+@pytest.mark.parametrize("group", [32, "K", "int4"])
+def test_gemv_mx_headnorm(hip, orc, rng, group):
+    """The out-projection over the column-split mixer's output: x = u scaled
+    per 128-column head by 1/sqrt(sum of its 8 partials / 128 + eps), then
+    y += W x (residual epilogue), against the oracle's matmul of x."""
+    N, K, eps = 2560, 2048, 1e-6
+    u = rng.standard_normal(K).astype(np.float32)
+    ss = rng.uniform(0.5, 40.0, (K // 128, 8)).astype(np.float32)
+    sn = (1.0 / np.sqrt(ss.astype(np.float64).sum(axis=1) / 128.0 + eps))
+    x = (u.reshape(-1, 128) * sn[:, None]).reshape(1, K).astype(np.float32)
+    res = rng.standard_normal(N).astype(np.float32)
+    w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    dy = dev(hip, res)
+    say("gemv_mx_headnorm", group)
+    if group == "int4":
+        p4, s4 = orc.quantize_q4(w)
+        ref = res + orc.matmul_i4(x, p4, s4)[0]
+        qb, sb = C.c_size_t(), C.c_size_t()
+        hip.check(hip.lib().qlm_mx4_layout_bytes(N, K, 1, C.byref(qb), C.byref(sb)))
+        qz, sz = hip.DeviceBuffer(qb.value), hip.DeviceBuffer(sb.value)
+        hip.call("qlm_mx4_swizzle", dev(hip, p4), dev(hip, s4), N, K, 1, qz, sz, None)
+        hip.call("qlm_gemv_i4_mx_headnorm", dev(hip, u), dev(hip, ss), eps, qz, sz, dy, N, K, 1,
+                 None)
+    else:
+        g = K if group == "K" else 32
+        q, s = orc.quantize(w, g)
+        ref = res + orc.matmul_i8(x, q, s, g)[0]
+        qz, sz, keep = _mx_layout(hip, q, s, g, N, K, 1)
+        hip.call("qlm_gemv_i8_mx_headnorm", dev(hip, u), dev(hip, ss), eps, qz, sz, g, dy, N, K,
+                 1, None)
+    assert rel_err(dy.to_numpy(N, np.float32), ref) < 1e-5
