@@ -362,8 +362,9 @@ int qlm_attention_decode(const float* q, const void* k_cache, const void* v_cach
  * static device array of QLM_ATTENTION_NOALLOC_MAX_BYTES (32 MiB) that every
  * GPU running the library holds until the process ends. A call needs
  * qlm_attention_decode_noalloc_bytes(B, n_q, hd, ctx) bytes of it
- * (B * n_q * ceil(ctx / C) * (hd + 4) * 4, C = 256 positions at hd 128, 128
- * at hd 256) and returns QLM_ERR_SCRATCH, launching nothing, when that
+ * (B * n_q * ceil(ctx / C) * (hd + 4) * 4 for the chunk length C that
+ * qlm_attention_decode picks: 64 to 512 positions at hd 128, 32 to 256 at
+ * hd 256) and returns QLM_ERR_SCRATCH, launching nothing, when that
  * exceeds the maximum. The call allocates nothing; its first call on a
  * device looks the array's address up once. Every call on one GPU shares
  * that GPU's array: calls that may overlap on one GPU (different streams,

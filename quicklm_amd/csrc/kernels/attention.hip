@@ -116,12 +116,14 @@ __global__ __launch_bounds__(kThreads) void k_attn(
     const size_t row0 = ((size_t)b * kvb + start) * n_kv + g;
     float kr[NS][8];
     float4 vv[NV];
-    auto load_kv = [&](int t0) {
+    auto load_k = [&](int t0) {
 #pragma unroll
         for (int u = 0; u < NS; ++u) {
             const int pl = min(t0 + u * SPS + wave * PPW + pw, n - 1);
             load8<KV>(kc + (row0 + (size_t)pl * n_kv) * HD + sub * 8, kr[u]);
         }
+    };
+    auto load_v = [&](int t0) {
 #pragma unroll
         for (int u = 0; u < NV; ++u) {
             const int pl = min(t0 + u * NPG + pg, n - 1);
@@ -166,7 +168,8 @@ __global__ __launch_bounds__(kThreads) void k_attn(
         }
     }
     __builtin_amdgcn_sched_barrier(0);
-    load_kv(0);
+    load_k(0);
+    load_v(0);
 
     // ---- query rows (+ QK-norm, RoPE, k_p/v_p when PREP) ----
     if constexpr (PREP) {
@@ -247,11 +250,14 @@ __global__ __launch_bounds__(kThreads) void k_attn(
         l_run[i] = 0.0f;
     }
 
+    // Sub-tile t+1's K rows are requested once sub-tile t's scores have
+    // consumed kr, its V rows once t's P.V has consumed vv, so each sub-tile's
+    // loads overlap the previous one's softmax and P.V.
     for (int t = 0; t < NT; ++t) {
         const int t0 = t * T;
         if (t0 >= n) break;  // uniform
         const int nt = min(T, n - t0);
-        if (t > 0) load_kv(t0);
+        const bool more = t + 1 < NT && t0 + T < n;
 
         // ---- scores s = q.k * scale ----
 #pragma unroll
@@ -270,6 +276,7 @@ __global__ __launch_bounds__(kThreads) void k_attn(
                 if (sub == 0 && pli < nt) sc[gh][pli] = d * scale;
             }
         }
+        if (more) load_k(t0 + T);
         __syncthreads();
 
         // ---- per-head max, exponentials, sums (online across sub-tiles) ----
@@ -321,6 +328,7 @@ __global__ __launch_bounds__(kThreads) void k_attn(
                 }
             }
         }
+        if (more) load_v(t0 + T);
         if (NT > 1) __syncthreads();  // sc is rewritten by the next sub-tile
     }
 
@@ -550,6 +558,18 @@ constexpr int kPrefillSlice = 256;  // query rows per prefill attention launch
 int chunk_len(int hd, int nt) { return (hd == 128 ? 64 : 32) * nt; }
 int nchunks_for(int max_seq, int ch) { return (max_seq + ch - 1) / ch; }
 
+// Sub-tiles per chunk of the isolated attention over ctx positions: the
+// fewest that keep the records of one head at most 256 (the merge reads
+// them all), then doubled while B * chunks stays >= 1024 (with one
+// workgroup per (chunk, kv head, sequence), >= 4 per compute unit).
+int isolated_nt(int B, int hd, int ctx) {
+    int nt = 1;
+    while (nt < 8 && nchunks_for(ctx, chunk_len(hd, nt)) > 256) nt *= 2;
+    while (nt < 8 && (long long)B * nchunks_for(ctx, chunk_len(hd, 2 * nt)) >= 1024) nt *= 2;
+    return nt;
+}
+
+
 size_t records_bytes(int B, int n_q, int hd, int max_seq, int nt) {
     return (size_t)B * n_q * nchunks_for(max_seq, chunk_len(hd, nt)) * (hd + 4) * sizeof(float);
 }
@@ -650,33 +670,41 @@ int check_attention_args(const float* q, const void* k_cache, const void* v_cach
     return QLM_OK;
 }
 
-// The two launches of the isolated attention, with nch chunk records per
-// (sequence, query head) in w (nch chunks must cover ctx positions).
+template <int HDV, int NT>
+int attention_launch_nt(const float* q, const void* k_cache, const void* v_cache, int kv_dtype,
+                        int max_seq, int ctx, float* out, int B, int n_q, int n_kv, float* w,
+                        int nch, hipStream_t st) {
+    const int G = n_q / n_kv;
+    const int ldq = n_q * HDV;
+    const int rc =
+        kv_dtype == 0
+            ? launch_g<HDV, NT, float, false>(
+                  G, q, ldq, HDV, nullptr, nullptr, nullptr, nullptr, 0,
+                  (float*)const_cast<void*>(k_cache), (float*)const_cast<void*>(v_cache), max_seq,
+                  n_kv, nullptr, ctx, 0, (size_t)max_seq, w, nch, n_q, B, st)
+            : launch_g<HDV, NT, uint16_t, false>(
+                  G, q, ldq, HDV, nullptr, nullptr, nullptr, nullptr, 0,
+                  (uint16_t*)const_cast<void*>(k_cache), (uint16_t*)const_cast<void*>(v_cache),
+                  max_seq, n_kv, nullptr, ctx, 0, (size_t)max_seq, w, nch, n_q, B, st);
+    if (rc != QLM_OK) return rc;
+    return launch_combine<HDV>(w, nch, chunk_len(HDV, NT), max_seq, nullptr, ctx, 0, nullptr, 0,
+                               0, out, ldq, n_q, B, st);
+}
+
+// The two launches of the isolated attention with nt sub-tiles per chunk
+// and nch chunk records per (sequence, query head) in w (nch chunks of
+// chunk_len(hd, nt) positions must cover ctx).
 int attention_launch(const float* q, const void* k_cache, const void* v_cache, int kv_dtype,
                      int max_seq, int ctx, float* out, int B, int n_q, int n_kv, int hd,
-                     float* w, int nch, hipStream_t st) {
-    const int G = n_q / n_kv;
-    const int ch = chunk_len(hd, kNtLong);
-    const int ldq = n_q * hd;
-    int rc;
-#define QLM_ISO(HDV)                                                                             \
-    rc = kv_dtype == 0                                                                           \
-             ? launch_g<HDV, kNtLong, float, false>(                                             \
-                   G, q, ldq, hd, nullptr, nullptr, nullptr, nullptr, 0,                         \
-                   (float*)const_cast<void*>(k_cache), (float*)const_cast<void*>(v_cache),       \
-                   max_seq, n_kv, nullptr, ctx, 0, (size_t)max_seq, w, nch, n_q, B, st)          \
-             : launch_g<HDV, kNtLong, uint16_t, false>(                                          \
-                   G, q, ldq, hd, nullptr, nullptr, nullptr, nullptr, 0,                         \
-                   (uint16_t*)const_cast<void*>(k_cache), (uint16_t*)const_cast<void*>(v_cache), \
-                   max_seq, n_kv, nullptr, ctx, 0, (size_t)max_seq, w, nch, n_q, B, st);         \
-    if (rc != QLM_OK) return rc;                                                                 \
-    return launch_combine<HDV>(w, nch, ch, max_seq, nullptr, ctx, 0, nullptr, 0, 0, out, ldq,    \
-                               n_q, B, st);
-    if (hd == 128) {
-        QLM_ISO(128)
-    }
-    QLM_ISO(256)
+                     float* w, int nt, int nch, hipStream_t st) {
+#define QLM_ISO(HDV, NTV)                                                                       \
+    if (hd == HDV && nt == NTV)                                                                 \
+        return attention_launch_nt<HDV, NTV>(q, k_cache, v_cache, kv_dtype, max_seq, ctx, out, B, \
+                                             n_q, n_kv, w, nch, st);
+    QLM_ISO(128, 1) QLM_ISO(128, 2) QLM_ISO(128, 4) QLM_ISO(128, 8)
+    QLM_ISO(256, 1) QLM_ISO(256, 2) QLM_ISO(256, 4) QLM_ISO(256, 8)
 #undef QLM_ISO
+    return QLM_ERR_SHAPE;
 }
 
 }  // namespace
@@ -722,14 +750,18 @@ extern "C" int qlm_attention_decode(const float* q, const void* k_cache, const v
     const int rc = check_attention_args(q, k_cache, v_cache, kv_dtype, max_seq, ctx, out, B, n_q,
                                         n_kv, hd);
     if (rc != QLM_OK) return rc;
+    // records laid out for the positions the launch attends to (ctx): at
+    // most qlm_gqa_workspace_bytes(B, n_q, hd, max_seq), the one-sub-tile
+    // layout over max_seq
+    const int nt = isolated_nt(B, hd, ctx);
     return attention_launch(q, k_cache, v_cache, kv_dtype, max_seq, ctx, out, B, n_q, n_kv, hd,
-                            reinterpret_cast<float*>(work),
-                            nchunks_for(max_seq, chunk_len(hd, kNtLong)), as_stream(stream));
+                            reinterpret_cast<float*>(work), nt,
+                            nchunks_for(ctx, chunk_len(hd, nt)), as_stream(stream));
 }
 
 extern "C" size_t qlm_attention_decode_noalloc_bytes(int B, int n_q, int hd, int ctx) {
     if (B <= 0 || n_q <= 0 || (hd != 128 && hd != 256) || ctx <= 0) return 0;
-    return records_bytes(B, n_q, hd, ctx, kNtLong);
+    return records_bytes(B, n_q, hd, ctx, isolated_nt(B, hd, ctx));
 }
 
 extern "C" int qlm_attention_decode_noalloc(const float* q, const void* k_cache,
@@ -740,12 +772,13 @@ extern "C" int qlm_attention_decode_noalloc(const float* q, const void* k_cache,
                                   hd);
     if (rc != QLM_OK) return rc;
     // records for the chunks that cover ctx positions only (the grid stops there)
-    if (records_bytes(B, n_q, hd, ctx, kNtLong) > kScratchBytes) return QLM_ERR_SCRATCH;
+    const int nt = isolated_nt(B, hd, ctx);
+    if (records_bytes(B, n_q, hd, ctx, nt) > kScratchBytes) return QLM_ERR_SCRATCH;
     float* w = nullptr;
     rc = scratch_ptr(&w);
     if (rc != QLM_OK) return rc;
     return attention_launch(q, k_cache, v_cache, kv_dtype, max_seq, ctx, out, B, n_q, n_kv, hd,
-                            w, nchunks_for(ctx, chunk_len(hd, kNtLong)), as_stream(stream));
+                            w, nt, nchunks_for(ctx, chunk_len(hd, nt)), as_stream(stream));
 }
 
 extern "C" size_t qlm_gqa_prefill_workspace_bytes(int n_q, int hd, int max_seq) {

@@ -65,9 +65,10 @@ def test_noalloc_attention_rejects_oversize_on_host():
 
     L = hip.lib()
     cap = 32 << 20
-    # B * n_q * ceil(ctx / C) * (hd + 4) * 4 bytes, C = 128 positions at hd 256
-    assert L.qlm_attention_decode_noalloc_bytes(16, 16, 256, 32768) == 16 * 16 * 256 * 260 * 4
-    assert L.qlm_attention_decode_noalloc_bytes(1, 16, 128, 300) == 16 * 2 * 132 * 4
+    # B * n_q * ceil(ctx / C) * (hd + 4) * 4 bytes: C = 256 positions for 16
+    # sequences of 32768 at hd 256 (128 chunks), 64 for one of 300 at hd 128
+    assert L.qlm_attention_decode_noalloc_bytes(16, 16, 256, 32768) == 16 * 16 * 128 * 260 * 4
+    assert L.qlm_attention_decode_noalloc_bytes(1, 16, 128, 300) == 16 * 5 * 132 * 4
     assert L.qlm_attention_decode_noalloc_bytes(0, 16, 128, 300) == 0
     assert L.qlm_attention_decode_noalloc_bytes(1, 16, 64, 300) == 0
     assert L.qlm_attention_decode_noalloc_bytes(16, 16, 256, 32768) > cap

@@ -925,3 +925,30 @@ def test_gemv_mx_headnorm(hip, orc, rng, group):
         hip.call("qlm_gemv_i8_mx_headnorm", dev(hip, u), dev(hip, ss), eps, qz, sz, g, dy, N, K,
                  1, None)
     assert rel_err(dy.to_numpy(N, np.float32), ref) < 1e-5
+
+
+def test_gqa_decode_batches_share_workspace(hip, orc, rng):
+    """Calls with 2, 1, 2 and 1 sequences on one workspace sized for 2: the
+    records of each call are laid out for its own batch and merged by its own
+    combine launch, whatever earlier calls left in the workspace."""
+    n_q, n_kv, hd, rot, max_seq, theta = 16, 4, 128, 32, 700, 1e6
+    ld = n_q * 2 * hd + 2 * n_kv * hd
+    qn = (rng.standard_normal(hd) * 0.02).astype(np.float32)
+    kn = (rng.standard_normal(hd) * 0.02).astype(np.float32)
+    cos_t, sin_t = orc.rope_table(theta, rot, max_seq)
+    kref = [rng.standard_normal((max_seq, n_kv, hd)).astype(np.float32) for _ in range(2)]
+    vref = [rng.standard_normal((max_seq, n_kv, hd)).astype(np.float32) for _ in range(2)]
+    dkc, dvc = dev(hip, np.stack(kref)), dev(hip, np.stack(vref))
+    work = hip.DeviceBuffer(hip.lib().qlm_gqa_workspace_bytes(2, n_q, hd, max_seq))
+    work.zero()
+    dcos, dsin = dev(hip, cos_t), dev(hip, sin_t)
+    for step, B in enumerate((2, 1, 2, 1)):
+        pos = np.array([300 + 70 * step, 600 - 50 * step][:B], np.int32)
+        qkv = rng.standard_normal((B, ld)).astype(np.float32)
+        ref = np.stack([orc.gqa_core(qkv[b].copy(), qn, kn, theta, rot, kref[b], vref[b],
+                                     int(pos[b]), n_q, n_kv, hd, True) for b in range(B)])
+        do = hip.DeviceBuffer(B * n_q * hd * 4)
+        say("gqa shared workspace", step, B)
+        hip.call("qlm_gqa_decode", dev(hip, qkv), ld, dev(hip, qn), dev(hip, kn), dcos, dsin, rot,
+                 dkc, dvc, max_seq, dev(hip, pos), do, n_q * hd, B, n_q, n_kv, hd, 1, work, None)
+        assert rel_err(do.to_numpy((B, n_q * hd), np.float32), ref) < 1e-5
