@@ -28,6 +28,8 @@
 // slice's partial sums go to part[ks, m, n]; k_mm_reduce sums the slices in
 // order and applies the epilogue (and the RMSNorm's 1/rms).
 
+#include <type_traits>
+
 #include "common.hpp"
 #include "mm_reduce.hpp"
 
@@ -38,6 +40,9 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 enum { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2 };
 constexpr int kMaxRowsT = 16;
+constexpr int kMaxGainK = 4096;  // K of the whole-K form's staged RMSNorm gains
+// Word 3 of a gfx9 buffer resource for untyped (raw) loads.
+constexpr int kBufferWord3 = 0x00020000;
 constexpr int kMaxSliceBlocks = 64;  // blocks of one K slice
 
 // eight fp32 as bf16 (RNE) hi and lo planes, x = hi + lo + O(2^-17 |x|)
@@ -193,6 +198,253 @@ __global__ __launch_bounds__(NW * QLM_WAVE) void k_mm_t(
     }
 }
 
+// Whole-K form for K <= 64 * NW * PX (no partial sums, no second launch):
+// the NW waves of a workgroup split K (wave w takes the blocks w, w + NW,
+// ..., PX of them) and the workgroup walks tile groups grid-stride, NTH
+// 16-row tiles per half at a time (both halves of a [gate; up] matrix). A
+// wave's blocks are the same for every tile group, so its activation
+// columns are loaded, multiplied by 1 + gain (deferred RMSNorm) and split
+// into bf16 hi + lo once, at kernel start, and stay in registers; the ring
+// holds weight fragments and their group scales only, one slot per block,
+// each slot refilled with the next group's fragment as soon as it is
+// consumed (the loads of the first group are issued before the activation
+// arithmetic). At a group's end the waves' partial tiles meet in LDS
+// (double-buffered by group parity) and every thread of the workgroup takes
+// a share of the outputs: partials summed in wave order, then 1/rms (from
+// the waves' sums of squares of x), the epilogue and the store.
+template <int NW, int NTH, int PX, int D, bool NORM, int EPI>
+__global__ __launch_bounds__(NW * QLM_WAVE) void k_mm_b(
+    const float* __restrict__ x, int ldx, const float* __restrict__ gain, float eps,
+    const int8_t* __restrict__ qz, const float* __restrict__ sz, float* __restrict__ y, int ldy,
+    int M, int N, int tiles_half, int nblk) {
+    constexpr int H2 = EPI == EPI_SWIGLU ? 2 : 1;
+    constexpr int NT = NTH * H2;  // fragments per ring slot
+    constexpr int NTHR = NW * QLM_WAVE;
+    __shared__ f32x4 red[2][NW][NT][QLM_WAVE];
+    __shared__ float rsum[NW][kMaxRowsT];
+    __shared__ float4 gsh[NORM ? kMaxGainK / 4 : 1];  // 1 + gain, staged once
+
+    const int tid = threadIdx.x, lane = tid & (QLM_WAVE - 1);
+    const int w = __builtin_amdgcn_readfirstlane(tid / QLM_WAVE);
+    const int q = lane >> 4, mr = lane & 15;
+    const int ngroups = (tiles_half + NTH - 1) / NTH;
+    // this wave's last block (a wave past the last block repeats block
+    // nblk - 1, which then meets zero activations)
+    const int blast = w < nblk ? nblk - 1 - ((nblk - 1 - w) % NW) : nblk - 1;
+
+    // ---- activation of this wave's blocks: lane (q, m) holds row m's columns
+    // c0(q) .. +7 and 32 + c0(q) .. +7 of each block (c0 = 0, 16, 8, 24), the
+    // order the weights take after the lane swaps. Unconditional loads (row
+    // and block clamped), issued before the weight ring.
+    // The RMSNorm gains are the same for every row: the workgroup stages
+    // 1 + gain in LDS once (kGainPer float4 per thread) instead of every
+    // lane holding its columns' gains in registers.
+    const int coff = (q & 1) * 16 + (q >> 1) * 8;
+    const int K4 = nblk * 16;
+    constexpr int kGainPer = NORM ? (kMaxGainK / 4 + NTHR - 1) / NTHR : 1;
+    float4 gl[kGainPer];
+    if constexpr (NORM) {
+#pragma unroll
+        for (int j = 0; j < kGainPer; ++j)
+            gl[j] = reinterpret_cast<const float4*>(gain)[min(tid + j * NTHR, K4 - 1)];
+    }
+    // Operands are read through buffer resources: the per-lane part of each
+    // address is a constant register offset and the rest a wave-uniform
+    // scalar offset, so no vector arithmetic is spent on addresses (and a
+    // read past a resource's extent returns zero instead of faulting).
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(x), 0, ((M - 1) * ldx + nblk * 64) * 4, kBufferWord3);
+    const int xoff = (min(mr, M - 1) * ldx + coff) * 4;
+    float4 xa[PX][4];
+#pragma unroll
+    for (int u = 0; u < PX; ++u) {
+        const int b = min(w + NW * u, nblk - 1);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            xa[u][j] = __builtin_bit_cast(
+                float4, __builtin_amdgcn_raw_buffer_load_b128(rx, xoff, 256 * b + 16 * (j & 1) +
+                                                                            128 * (j >> 1), 0));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- weight ring: slot u holds block w + NW u of the current group's
+    // NT tiles (tile index clamped for a ragged last group; its rows are not
+    // stored)
+    // D rings: the groups g, g + grid, ... go to ring (their ordinal) mod D,
+    // so D groups' fragments are in flight; a ring past the last group
+    // re-requests the current group (a cache hit) instead of branching.
+    const int nfrag = H2 * tiles_half * nblk;
+    const __amdgpu_buffer_rsrc_t rq =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(qz), 0, nfrag * 1024, kBufferWord3);
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(sz), 0, nfrag * 128, kBufferWord3);
+    uint4 wq[D][PX][NT];
+    float s0[D][PX][NT], s1[D][PX][NT];
+    auto issue = [&](int g, int d, int u) {
+        const int b = min(w + NW * u, blast);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const int th = min(g * NTH + (t % NTH), tiles_half - 1);
+            const int fb = (th + (t / NTH) * tiles_half) * nblk + b;
+            wq[d][u][t] = __builtin_bit_cast(
+                uint4, __builtin_amdgcn_raw_buffer_load_b128(rq, lane * 16, fb * 1024, 0));
+            s0[d][u][t] = __builtin_bit_cast(
+                float, __builtin_amdgcn_raw_buffer_load_b32(rs, mr * 4, fb * 128, 0));
+            s1[d][u][t] = __builtin_bit_cast(
+                float, __builtin_amdgcn_raw_buffer_load_b32(rs, 64 + mr * 4, fb * 128, 0));
+        }
+    };
+    int g = blockIdx.x;
+    const int G = (int)gridDim.x;
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        const int gd = g + d * G < ngroups ? g + d * G : g;
+#pragma unroll
+        for (int u = 0; u < PX; ++u) issue(gd, d, u);
+    }
+
+    if constexpr (NORM) {
+#pragma unroll
+        for (int j = 0; j < kGainPer; ++j) {
+            const int i = tid + j * NTHR;
+            if (i < K4)
+                gsh[i] = make_float4(1.0f + gl[j].x, 1.0f + gl[j].y, 1.0f + gl[j].z,
+                                     1.0f + gl[j].w);
+        }
+        __syncthreads();
+    }
+
+    // ---- split the activation once (zero past K and past row M - 1)
+    uint4 xh[PX][2], xl[PX][2];
+    float ss = 0.0f;
+#pragma unroll
+    for (int u = 0; u < PX; ++u) {
+        const bool real = w + NW * u < nblk && mr < M;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            float4 a = xa[u][2 * h], c = xa[u][2 * h + 1];
+            if (!real) {
+                a = make_float4(0.f, 0.f, 0.f, 0.f);
+                c = a;
+            }
+            if constexpr (NORM) {
+                ss = fmaf(a.x, a.x, ss);
+                ss = fmaf(a.y, a.y, ss);
+                ss = fmaf(a.z, a.z, ss);
+                ss = fmaf(a.w, a.w, ss);
+                ss = fmaf(c.x, c.x, ss);
+                ss = fmaf(c.y, c.y, ss);
+                ss = fmaf(c.z, c.z, ss);
+                ss = fmaf(c.w, c.w, ss);
+                const int gi = (coff + 64 * min(w + NW * u, nblk - 1)) / 4 + 8 * h;
+                const float4 ha = gsh[gi], hc = gsh[gi + 1];
+                a = make_float4(a.x * ha.x, a.y * ha.y, a.z * ha.z, a.w * ha.w);
+                c = make_float4(c.x * hc.x, c.y * hc.y, c.z * hc.z, c.w * hc.w);
+            }
+            const float e[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
+            split8(e, xh[u][h], xl[u][h]);
+        }
+    }
+    if constexpr (NORM) {
+        // row m's sum over the wave's columns: the four quarters of the wave
+        ss += __shfl_xor(ss, 16, QLM_WAVE);
+        ss += __shfl_xor(ss, 32, QLM_WAVE);
+        if (lane < kMaxRowsT) rsum[w][lane] = ss;
+    }
+
+    f32x4 acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    auto consume = [&](int d, int u) {
+        const bf16x8 a0h = __builtin_bit_cast(bf16x8, xh[u][0]);
+        const bf16x8 a0l = __builtin_bit_cast(bf16x8, xl[u][0]);
+        const bf16x8 a1h = __builtin_bit_cast(bf16x8, xh[u][1]);
+        const bf16x8 a1l = __builtin_bit_cast(bf16x8, xl[u][1]);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const uint4 v = wq[d][u][t];
+            // upper half of (x, y) <-> lower half of (z, w): group 0 in x, y
+            const auto p0 = __builtin_amdgcn_permlane32_swap(v.x, v.z, false, false);
+            const auto p1 = __builtin_amdgcn_permlane32_swap(v.y, v.w, false, false);
+            const bf16x8 b0v = i8x8_bf16(p0[0], p1[0]);
+            const bf16x8 b1v = i8x8_bf16(p0[1], p1[1]);
+            f32x4 t0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0h, b0v, f32x4{0.f, 0.f, 0.f, 0.f},
+                                                               0, 0, 0);
+            t0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0l, b0v, t0, 0, 0, 0);
+            f32x4 t1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1h, b1v, f32x4{0.f, 0.f, 0.f, 0.f},
+                                                               0, 0, 0);
+            t1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1l, b1v, t1, 0, 0, 0);
+            const float f0 = s0[d][u][t], f1 = s1[d][u][t];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[t][i] = fmaf(t1[i], f1, fmaf(t0[i], f0, acc[t][i]));
+        }
+    };
+
+    const int K = nblk * 64;
+    int par = 0;
+    // one tile group from ring d (a compile-time ring index); true when it
+    // was the workgroup's last
+    auto step = [&](auto dc) {
+        constexpr int d = decltype(dc)::value;
+        const int refill = g + D * G;  // the group ring d takes next
+        if (refill < ngroups) {
+#pragma unroll
+            for (int u = 0; u < PX; ++u) {
+                consume(d, u);
+                issue(refill, d, u);
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < PX; ++u) consume(d, u);
+        }
+        // the waves' partial tiles meet in LDS; lane l holds D[4 (l / 16) + i][l % 16]
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            red[par][w][t][lane] = acc[t];
+            acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+        __syncthreads();
+        for (int o = tid; o < NTH * QLM_WAVE * 4; o += NTHR) {
+            const int t = o / (QLM_WAVE * 4), rem = o % (QLM_WAVE * 4);
+            const int l2 = rem >> 2, i = rem & 3;
+            const int m = 4 * (l2 >> 4) + i, n = l2 & 15;
+            const int th = g * NTH + t;
+            const int row = th * 16 + n;
+            if (m >= M || th >= tiles_half || row >= N) continue;
+            float v = 0.0f, up = 0.0f;
+#pragma unroll
+            for (int ww = 0; ww < NW; ++ww) {
+                v += red[par][ww][t][l2][i];
+                if constexpr (EPI == EPI_SWIGLU) up += red[par][ww][t + NTH][l2][i];
+            }
+            if constexpr (NORM) {
+                float tot = 0.0f;
+#pragma unroll
+                for (int ww = 0; ww < NW; ++ww) tot += rsum[ww][m];
+                const float rs = 1.0f / sqrtf(tot / (float)K + eps);
+                v *= rs;
+                up *= rs;
+            }
+            float* dst = y + (size_t)m * ldy + row;
+            if constexpr (EPI == EPI_SWIGLU)
+                *dst = silu_f(v) * up;
+            else if constexpr (EPI == EPI_RESID)
+                *dst += v;
+            else
+                *dst = v;
+        }
+        par ^= 1;
+        if (g + G >= ngroups) return true;
+        g += G;
+        return false;
+    };
+    for (;;) {
+        if (step(std::integral_constant<int, 0>{})) break;
+        if constexpr (D == 2)
+            if (step(std::integral_constant<int, 1>{})) break;
+    }
+}
+
 struct TConfig {
     int nw, nt, p, ks;
 };
@@ -312,13 +564,143 @@ int t_check(const float* x, int ldx, const float* norm_w, const int8_t* qz, cons
     return QLM_OK;
 }
 
+// Whole-K launch shapes (waves, tiles per half per group, rings, grid)
+// measured per 4B projection at 16 rows (graph replays over rotating weight
+// copies, the K-sliced form's reduction included in its time); the other
+// shapes (the attention q/k/v, 12.1 us whole-K against 11.6, and the down
+// projection, whose activation does not fit) take the K-sliced form.
+struct BConfig {
+    int nw, nth, depth, grid;
+};
+struct BTuned {
+    int N, K, epi;
+    BConfig c;
+};
+constexpr BTuned kBTuned[] = {
+    {9728, 2560, EPI_SWIGLU, {8, 1, 1, 224}},   // gate/up: 19.1 us (K-sliced 23.5)
+    {8224, 2560, EPI_STORE, {8, 1, 1, 256}},    // DeltaNet in-projection: 13.8 us (15.5)
+    {2560, 2048, EPI_RESID, {16, 1, 1, 160}},   // output projections: 6.5 us (7.9)
+    {151936, 2560, EPI_STORE, {8, 2, 1, 256}},  // lm_head: 87.9 us (113.5)
+};
+
+bool b_lookup(int N, int K, int epi, BConfig* c) {
+    for (const BTuned& t : kBTuned)
+        if (t.N == N && t.K == K && t.epi == epi) {
+            *c = t.c;
+            return true;
+        }
+    return false;
+}
+
+template <int NW, int NTH, int PX, int D, bool NORM, int EPI>
+void launch_b(int grid, const float* x, int ldx, const float* gain, float eps, const int8_t* qz,
+              const float* sz, float* y, int ldy, int M, int N, int tiles_half, int nblk,
+              hipStream_t st) {
+    hipLaunchKernelGGL((k_mm_b<NW, NTH, PX, D, NORM, EPI>), dim3(grid), dim3(NW * QLM_WAVE), 0,
+                       st, x, ldx, gain, eps, qz, sz, y, ldy, M, N, tiles_half, nblk);
+}
+
+template <int NW, int NTH, int PX, int D>
+int launch_b_epi(int grid, const float* x, int ldx, const float* norm_w, float eps,
+                 const int8_t* qz, const float* sz, float* y, int ldy, int M, int N, int epi,
+                 int tiles_half, int nblk, hipStream_t st) {
+    if (epi == EPI_SWIGLU)
+        launch_b<NW, NTH, PX, D, true, EPI_SWIGLU>(grid, x, ldx, norm_w, eps, qz, sz, y, ldy, M,
+                                                  N, tiles_half, nblk, st);
+    else if (epi == EPI_RESID)
+        launch_b<NW, NTH, PX, D, false, EPI_RESID>(grid, x, ldx, nullptr, eps, qz, sz, y, ldy, M,
+                                                  N, tiles_half, nblk, st);
+    else if (norm_w)
+        launch_b<NW, NTH, PX, D, true, EPI_STORE>(grid, x, ldx, norm_w, eps, qz, sz, y, ldy, M, N,
+                                                 tiles_half, nblk, st);
+    else
+        launch_b<NW, NTH, PX, D, false, EPI_STORE>(grid, x, ldx, nullptr, eps, qz, sz, y, ldy, M,
+                                                  N, tiles_half, nblk, st);
+    return qlm_launch_status();
+}
+
+// Shapes whose registers do not fit (the compiler spills; counts from the
+// gfx950 build): 7 blocks a wave with the RMSNorm gains; SwiGLU with two
+// tiles per half at 5 blocks a wave (8 waves) or 2 (16 waves); 16 waves at
+// 3 blocks a wave with SwiGLU, or RMSNorm and two tiles per half; with two
+// rings, SwiGLU except one tile per half at 4 blocks a wave, and RMSNorm
+// with two tiles per half at 5 blocks a wave or 16 waves.
+bool b_spills(int nw, int nth, int px, int depth, bool norm, bool swiglu) {
+    if (px >= 7 && norm) return true;
+    if (swiglu && nth == 2 && (nw == 16 || px >= 5)) return true;
+    if (nw == 16 && px >= 3 && (swiglu || (norm && nth == 2))) return true;
+    if (depth == 2) {
+        if (swiglu && (nth == 2 || nw == 16 || px >= 5)) return true;
+        if (norm && nth == 2 && (nw == 16 || px >= 5)) return true;
+    }
+    return false;
+}
+
+// Built: (waves, blocks per wave) = (8, 2) (8, 4) (8, 5) (8, 7) (16, 2)
+// (16, 3), i.e. K <= 1024, 2048, 2560, 3584 (8 waves) or 2048, 3072 (16
+// waves), with 1 or
+// 2 tiles per half and one ring; two rings at (8, 4) (8, 5) (16, 2). The
+// blocks per wave are ceil(K / 64 / waves).
+int b_run(const BConfig& c, const float* x, int ldx, const float* norm_w, float eps,
+          const int8_t* qz, const float* sz, float* y, int ldy, int M, int N, int K, int epi,
+          hipStream_t st) {
+    const int nblk = K / 64;
+    const int tiles_half = (N + 15) / 16;
+    if ((c.nw != 8 && c.nw != 16) || (c.nth != 1 && c.nth != 2) ||
+        (c.depth != 1 && c.depth != 2))
+        return QLM_ERR_ARG;
+    const int px = (nblk + c.nw - 1) / c.nw;
+    if (b_spills(c.nw, c.nth, px, c.depth, norm_w != nullptr, epi == EPI_SWIGLU))
+        return QLM_ERR_SHAPE;
+    const int groups = (tiles_half + c.nth - 1) / c.nth;
+    const int grid = c.grid < groups ? c.grid : groups;
+    if (grid < 1) return QLM_ERR_ARG;
+#define QLM_B(NW_, NTH_, PX_, D_)                                                             \
+    if (c.nw == NW_ && c.nth == NTH_ && px == PX_ && c.depth == D_)                           \
+        return launch_b_epi<NW_, NTH_, PX_, D_>(grid, x, ldx, norm_w, eps, qz, sz, y, ldy, M, N, \
+                                                epi, tiles_half, nblk, st);
+    QLM_B(8, 1, 2, 1)
+    QLM_B(8, 1, 4, 1)
+    QLM_B(8, 1, 5, 1)
+    QLM_B(8, 1, 7, 1)
+    QLM_B(8, 2, 2, 1)
+    QLM_B(8, 2, 4, 1)
+    QLM_B(8, 2, 5, 1)
+    QLM_B(8, 2, 7, 1)
+    QLM_B(16, 1, 2, 1)
+    QLM_B(16, 2, 2, 1)
+    QLM_B(16, 1, 3, 1)
+    QLM_B(16, 2, 3, 1)
+    QLM_B(8, 1, 4, 2)
+    QLM_B(8, 1, 5, 2)
+    QLM_B(8, 2, 4, 2)
+    QLM_B(8, 2, 5, 2)
+    QLM_B(16, 1, 2, 2)
+    QLM_B(16, 2, 2, 2)
+#undef QLM_B
+    return QLM_ERR_SHAPE;
+}
+
 }  // namespace
 
 extern "C" size_t qlm_matmul_i8_t_workspace_bytes(int M, int N, int K, int epilogue) {
     if (M < 1 || N < 1 || K < 64) return 0;
+    BConfig bc;
+    if (b_lookup(N, K, epilogue, &bc)) return 0;  // whole-K form: no partial sums
     const int halves = epilogue == EPI_SWIGLU ? 2 : 1;
     const TConfig c = t_config(N, K, epilogue);
     return (size_t)t_slices(c, K) * M * halves * N * sizeof(float);
+}
+
+extern "C" int qlm_matmul_i8_t_whole_config(const float* x, int ldx, const float* norm_w,
+                                            float eps, const int8_t* q_tiles,
+                                            const float* s_tiles, int group, float* y, int ldy,
+                                            int M, int N, int K, int epilogue, int waves,
+                                            int tiles, int rings, int grid, void* stream) {
+    const int rc = t_check(x, ldx, norm_w, q_tiles, s_tiles, group, y, ldy, M, N, K, epilogue);
+    if (rc != QLM_OK) return rc;
+    return b_run(BConfig{waves, tiles, rings, grid}, x, ldx, norm_w, eps, q_tiles, s_tiles, y, ldy, M, N,
+                 K, epilogue, as_stream(stream));
 }
 
 extern "C" int qlm_matmul_i8_t_config(const float* x, int ldx, const float* norm_w, float eps,
@@ -339,6 +721,10 @@ extern "C" int qlm_matmul_i8_t(const float* x, int ldx, const float* norm_w, flo
                                size_t work_bytes, void* stream) {
     const int rc = t_check(x, ldx, norm_w, q_tiles, s_tiles, group, y, ldy, M, N, K, epilogue);
     if (rc != QLM_OK) return rc;
+    BConfig bc;
+    if (b_lookup(N, K, epilogue, &bc))
+        return b_run(bc, x, ldx, norm_w, eps, q_tiles, s_tiles, y, ldy, M, N, K, epilogue,
+                     as_stream(stream));
     if (!work) return QLM_ERR_ARG;
     const TConfig c = t_config(N, K, epilogue);
     return t_run(c, x, ldx, norm_w, eps, q_tiles, s_tiles, y, ldy, M, N, K, epilogue, work,
