@@ -206,30 +206,32 @@ int qlm_matmul_i8_t_config(const float* x, int ldx, const float* norm_w, float e
                            const int8_t* q_tiles, const float* s_tiles, int group, float* y,
                            int ldy, int M, int N, int K, int epilogue, int waves, int tiles,
                            int ring, int k_slices, void* work, size_t work_bytes, void* stream);
-/* Whole-K form of qlm_matmul_i8_t (one launch, no partial sums, no
- * workspace): the waves of a workgroup split K and keep their activation
- * columns split in registers for every tile group; the partial tiles meet
- * in LDS and the epilogue is applied in the same launch. qlm_matmul_i8_t
- * takes it where it measured faster (the 4B gate/up, DeltaNet
- * in-projection, output projections and lm_head; not the attention q/k/v,
- * nor the 9728-column down projection, whose activation does not fit a
- * wave's registers) and reports 0 workspace bytes there. _whole_config
- * takes (waves, tiles per half per tile group, rings, grid): with 2 rings
- * two tile groups' fragments are in flight per wave. Built: waves 8 with
- * K <= 1024, 2048, 2560 or 3584 (blocks per wave = ceil(K / 64 / 8) of 2, 4,
- * 5, 7) and waves 16 with K in (1024, 3072], 1 or 2 tiles per half, one
- * ring; two rings at 4 or 5 blocks a wave (8 waves) or 2 (16 waves);
- * QLM_ERR_SHAPE for other K and for the shapes whose registers spill (7
- * blocks a wave with RMSNorm; SwiGLU with 2 tiles per half at 5 blocks or
- * 16 waves; 16 waves at 3 blocks a wave with SwiGLU, or RMSNorm and 2
- * tiles per half; with 2 rings, SwiGLU except 8 waves x 1 tile x 4 blocks,
- * and RMSNorm with 2 tiles per half at 5 blocks or 16 waves); QLM_ERR_ARG
- * for other waves, tiles or rings. Same semantics,
- * epilogues and tolerance as qlm_matmul_i8_t. */
+/* Whole-K form of qlm_matmul_i8_t: the waves of a workgroup split K and
+ * keep their activation columns split in registers for every tile group;
+ * the partial tiles meet in LDS and the epilogue is applied in the same
+ * launch (no partial sums, no workspace). Where the activation does not fit
+ * a wave's registers, K is cut into k_slices slices, each launched the same
+ * way, whose raw sums go to work and are added in slice order by a second
+ * launch (RMSNorm, residual and SwiGLU applied there). qlm_matmul_i8_t takes
+ * it where it measured faster (the 4B gate/up, DeltaNet in-projection,
+ * output projections and lm_head, whole; not the attention q/k/v nor the
+ * 9728-column down projection) and reports the workspace of the form it
+ * takes. _whole_config takes (waves, tiles per half per tile group, grid,
+ * K slices); work: qlm_matmul_i8_t_whole_workspace_bytes(M, N, K,
+ * epilogue, k_slices) bytes (0 for one slice; work may then be NULL).
+ * Built: waves 8 with 2, 4, 5 or 7 blocks of 64 columns a wave in a slice
+ * (blocks per wave = ceil(blocks per slice / waves)) and waves 16 with 2,
+ * 1 or 2 tiles per half; QLM_ERR_SHAPE for other K, for the shapes whose
+ * registers spill (7 blocks a wave with RMSNorm; SwiGLU with 2 tiles per
+ * half at 5 blocks or 16 waves) and for RMSNorm with K > 4096; QLM_ERR_ARG
+ * for other waves or tiles, k_slices < 1, or a missing or short workspace.
+ * Same semantics, epilogues and tolerance as qlm_matmul_i8_t. */
+size_t qlm_matmul_i8_t_whole_workspace_bytes(int M, int N, int K, int epilogue, int k_slices);
 int qlm_matmul_i8_t_whole_config(const float* x, int ldx, const float* norm_w, float eps,
                                  const int8_t* q_tiles, const float* s_tiles, int group, float* y,
                                  int ldy, int M, int N, int K, int epilogue, int waves,
-                                 int tiles, int rings, int grid, void* stream);
+                                 int tiles, int grid, int k_slices, void* work,
+                                 size_t work_bytes, void* stream);
 
 /* Fused forms used by the decode step (same arithmetic as the unfused
  * reference sequence, one launch instead of two or three):

@@ -28,8 +28,6 @@
 // slice's partial sums go to part[ks, m, n]; k_mm_reduce sums the slices in
 // order and applies the epilogue (and the RMSNorm's 1/rms).
 
-#include <type_traits>
-
 #include "common.hpp"
 #include "mm_reduce.hpp"
 
@@ -212,11 +210,16 @@ __global__ __launch_bounds__(NW * QLM_WAVE) void k_mm_t(
 // (double-buffered by group parity) and every thread of the workgroup takes
 // a share of the outputs: partials summed in wave order, then 1/rms (from
 // the waves' sums of squares of x), the epilogue and the store.
-template <int NW, int NTH, int PX, int D, bool NORM, int EPI>
+// K-sliced use (part non-null, gridDim.y slices of bps blocks): the same
+// arithmetic over slice blockIdx.y's blocks only, the waves' sums written
+// raw to part[slice, m, n] (both halves of a SwiGLU matrix, the up rows at
+// n + N) for k_mm_reduce to add in slice order and finish (RMSNorm
+// included), for K whose activation does not fit the registers at once.
+template <int NW, int NTH, int PX, bool NORM, int EPI>
 __global__ __launch_bounds__(NW * QLM_WAVE) void k_mm_b(
     const float* __restrict__ x, int ldx, const float* __restrict__ gain, float eps,
     const int8_t* __restrict__ qz, const float* __restrict__ sz, float* __restrict__ y, int ldy,
-    int M, int N, int tiles_half, int nblk) {
+    int M, int N, int tiles_half, int nblk, int bps, float* __restrict__ part) {
     constexpr int H2 = EPI == EPI_SWIGLU ? 2 : 1;
     constexpr int NT = NTH * H2;  // fragments per ring slot
     constexpr int NTHR = NW * QLM_WAVE;
@@ -228,9 +231,12 @@ __global__ __launch_bounds__(NW * QLM_WAVE) void k_mm_b(
     const int w = __builtin_amdgcn_readfirstlane(tid / QLM_WAVE);
     const int q = lane >> 4, mr = lane & 15;
     const int ngroups = (tiles_half + NTH - 1) / NTH;
-    // this wave's last block (a wave past the last block repeats block
-    // nblk - 1, which then meets zero activations)
-    const int blast = w < nblk ? nblk - 1 - ((nblk - 1 - w) % NW) : nblk - 1;
+    // this workgroup's blocks: b0 .. b0 + nb - 1 (all of K when not sliced)
+    const int b0 = blockIdx.y * bps;
+    const int nb = min(bps, nblk - b0);
+    // this wave's last block (a wave past the slice's last block repeats
+    // block nb - 1, which then meets zero activations)
+    const int blast = w < nb ? nb - 1 - ((nb - 1 - w) % NW) : nb - 1;
 
     // ---- activation of this wave's blocks: lane (q, m) holds row m's columns
     // c0(q) .. +7 and 32 + c0(q) .. +7 of each block (c0 = 0, 16, 8, 24), the
@@ -258,7 +264,7 @@ __global__ __launch_bounds__(NW * QLM_WAVE) void k_mm_b(
     float4 xa[PX][4];
 #pragma unroll
     for (int u = 0; u < PX; ++u) {
-        const int b = min(w + NW * u, nblk - 1);
+        const int b = b0 + min(w + NW * u, nb - 1);
 #pragma unroll
         for (int j = 0; j < 4; ++j)
             xa[u][j] = __builtin_bit_cast(
@@ -270,38 +276,31 @@ __global__ __launch_bounds__(NW * QLM_WAVE) void k_mm_b(
     // ---- weight ring: slot u holds block w + NW u of the current group's
     // NT tiles (tile index clamped for a ragged last group; its rows are not
     // stored)
-    // D rings: the groups g, g + grid, ... go to ring (their ordinal) mod D,
-    // so D groups' fragments are in flight; a ring past the last group
-    // re-requests the current group (a cache hit) instead of branching.
     const int nfrag = H2 * tiles_half * nblk;
     const __amdgpu_buffer_rsrc_t rq =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(qz), 0, nfrag * 1024, kBufferWord3);
     const __amdgpu_buffer_rsrc_t rs =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(sz), 0, nfrag * 128, kBufferWord3);
-    uint4 wq[D][PX][NT];
-    float s0[D][PX][NT], s1[D][PX][NT];
-    auto issue = [&](int g, int d, int u) {
+    uint4 wq[PX][NT];
+    float s0[PX][NT], s1[PX][NT];
+    auto issue = [&](int g, int u) {
         const int b = min(w + NW * u, blast);
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
             const int th = min(g * NTH + (t % NTH), tiles_half - 1);
-            const int fb = (th + (t / NTH) * tiles_half) * nblk + b;
-            wq[d][u][t] = __builtin_bit_cast(
+            const int fb = (th + (t / NTH) * tiles_half) * nblk + b0 + b;
+            wq[u][t] = __builtin_bit_cast(
                 uint4, __builtin_amdgcn_raw_buffer_load_b128(rq, lane * 16, fb * 1024, 0));
-            s0[d][u][t] = __builtin_bit_cast(
+            s0[u][t] = __builtin_bit_cast(
                 float, __builtin_amdgcn_raw_buffer_load_b32(rs, mr * 4, fb * 128, 0));
-            s1[d][u][t] = __builtin_bit_cast(
+            s1[u][t] = __builtin_bit_cast(
                 float, __builtin_amdgcn_raw_buffer_load_b32(rs, 64 + mr * 4, fb * 128, 0));
         }
     };
     int g = blockIdx.x;
     const int G = (int)gridDim.x;
 #pragma unroll
-    for (int d = 0; d < D; ++d) {
-        const int gd = g + d * G < ngroups ? g + d * G : g;
-#pragma unroll
-        for (int u = 0; u < PX; ++u) issue(gd, d, u);
-    }
+    for (int u = 0; u < PX; ++u) issue(g, u);
 
     if constexpr (NORM) {
 #pragma unroll
@@ -319,7 +318,7 @@ __global__ __launch_bounds__(NW * QLM_WAVE) void k_mm_b(
     float ss = 0.0f;
 #pragma unroll
     for (int u = 0; u < PX; ++u) {
-        const bool real = w + NW * u < nblk && mr < M;
+        const bool real = w + NW * u < nb && mr < M;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             float4 a = xa[u][2 * h], c = xa[u][2 * h + 1];
@@ -336,7 +335,7 @@ __global__ __launch_bounds__(NW * QLM_WAVE) void k_mm_b(
                 ss = fmaf(c.y, c.y, ss);
                 ss = fmaf(c.z, c.z, ss);
                 ss = fmaf(c.w, c.w, ss);
-                const int gi = (coff + 64 * min(w + NW * u, nblk - 1)) / 4 + 8 * h;
+                const int gi = (coff + 64 * (b0 + min(w + NW * u, nb - 1))) / 4 + 8 * h;
                 const float4 ha = gsh[gi], hc = gsh[gi + 1];
                 a = make_float4(a.x * ha.x, a.y * ha.y, a.z * ha.z, a.w * ha.w);
                 c = make_float4(c.x * hc.x, c.y * hc.y, c.z * hc.z, c.w * hc.w);
@@ -355,14 +354,14 @@ __global__ __launch_bounds__(NW * QLM_WAVE) void k_mm_b(
     f32x4 acc[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    auto consume = [&](int d, int u) {
+    auto consume = [&](int u) {
         const bf16x8 a0h = __builtin_bit_cast(bf16x8, xh[u][0]);
         const bf16x8 a0l = __builtin_bit_cast(bf16x8, xl[u][0]);
         const bf16x8 a1h = __builtin_bit_cast(bf16x8, xh[u][1]);
         const bf16x8 a1l = __builtin_bit_cast(bf16x8, xl[u][1]);
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-            const uint4 v = wq[d][u][t];
+            const uint4 v = wq[u][t];
             // upper half of (x, y) <-> lower half of (z, w): group 0 in x, y
             const auto p0 = __builtin_amdgcn_permlane32_swap(v.x, v.z, false, false);
             const auto p1 = __builtin_amdgcn_permlane32_swap(v.y, v.w, false, false);
@@ -374,7 +373,7 @@ __global__ __launch_bounds__(NW * QLM_WAVE) void k_mm_b(
             f32x4 t1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1h, b1v, f32x4{0.f, 0.f, 0.f, 0.f},
                                                                0, 0, 0);
             t1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1l, b1v, t1, 0, 0, 0);
-            const float f0 = s0[d][u][t], f1 = s1[d][u][t];
+            const float f0 = s0[u][t], f1 = s1[u][t];
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc[t][i] = fmaf(t1[i], f1, fmaf(t0[i], f0, acc[t][i]));
         }
@@ -382,20 +381,17 @@ __global__ __launch_bounds__(NW * QLM_WAVE) void k_mm_b(
 
     const int K = nblk * 64;
     int par = 0;
-    // one tile group from ring d (a compile-time ring index); true when it
-    // was the workgroup's last
-    auto step = [&](auto dc) {
-        constexpr int d = decltype(dc)::value;
-        const int refill = g + D * G;  // the group ring d takes next
-        if (refill < ngroups) {
+    for (;;) {
+        const int next = g + G;
+        if (next < ngroups) {
 #pragma unroll
             for (int u = 0; u < PX; ++u) {
-                consume(d, u);
-                issue(refill, d, u);
+                consume(u);
+                issue(next, u);
             }
         } else {
 #pragma unroll
-            for (int u = 0; u < PX; ++u) consume(d, u);
+            for (int u = 0; u < PX; ++u) consume(u);
         }
         // the waves' partial tiles meet in LDS; lane l holds D[4 (l / 16) + i][l % 16]
 #pragma unroll
@@ -417,6 +413,12 @@ __global__ __launch_bounds__(NW * QLM_WAVE) void k_mm_b(
                 v += red[par][ww][t][l2][i];
                 if constexpr (EPI == EPI_SWIGLU) up += red[par][ww][t + NTH][l2][i];
             }
+            if (part) {  // a K slice: raw sums, finished by k_mm_reduce
+                float* pp = part + ((size_t)blockIdx.y * M + m) * (H2 * N) + row;
+                pp[0] = v;
+                if constexpr (EPI == EPI_SWIGLU) pp[N] = up;
+                continue;
+            }
             if constexpr (NORM) {
                 float tot = 0.0f;
 #pragma unroll
@@ -434,14 +436,8 @@ __global__ __launch_bounds__(NW * QLM_WAVE) void k_mm_b(
                 *dst = v;
         }
         par ^= 1;
-        if (g + G >= ngroups) return true;
-        g += G;
-        return false;
-    };
-    for (;;) {
-        if (step(std::integral_constant<int, 0>{})) break;
-        if constexpr (D == 2)
-            if (step(std::integral_constant<int, 1>{})) break;
+        if (next >= ngroups) break;
+        g = next;
     }
 }
 
@@ -564,23 +560,27 @@ int t_check(const float* x, int ldx, const float* norm_w, const int8_t* qz, cons
     return QLM_OK;
 }
 
-// Whole-K launch shapes (waves, tiles per half per group, rings, grid)
+// Whole-K launch shapes (waves, tiles per half per group, grid, K slices)
 // measured per 4B projection at 16 rows (graph replays over rotating weight
 // copies, the K-sliced form's reduction included in its time); the other
-// shapes (the attention q/k/v, 12.1 us whole-K against 11.6, and the down
-// projection, whose activation does not fit) take the K-sliced form.
+// shapes take the K-sliced form above: the attention q/k/v (12.1 us here
+// against 11.6) and the 9728-column down projection, whose activation does
+// not fit the registers at once (16.4 us in 3 slices against 13.3: every
+// slice's workgroup loads and splits its 16 x 2432 activation block for one
+// or two tiles, where the K-sliced form shares it across 8).
 struct BConfig {
-    int nw, nth, depth, grid;
+    int nw, nth, grid;
+    int ks;  // K slices (1: whole K in one launch)
 };
 struct BTuned {
     int N, K, epi;
     BConfig c;
 };
 constexpr BTuned kBTuned[] = {
-    {9728, 2560, EPI_SWIGLU, {8, 1, 1, 224}},   // gate/up: 19.1 us (K-sliced 23.5)
-    {8224, 2560, EPI_STORE, {8, 1, 1, 256}},    // DeltaNet in-projection: 13.8 us (15.5)
-    {2560, 2048, EPI_RESID, {16, 1, 1, 160}},   // output projections: 6.5 us (7.9)
-    {151936, 2560, EPI_STORE, {8, 2, 1, 256}},  // lm_head: 87.9 us (113.5)
+    {9728, 2560, EPI_SWIGLU, {8, 1, 224, 1}},   // gate/up: 19.1 us (K-sliced 23.5)
+    {8224, 2560, EPI_STORE, {8, 1, 256, 1}},    // DeltaNet in-projection: 13.8 us (15.5)
+    {2560, 2048, EPI_RESID, {16, 1, 160, 1}},   // output projections: 6.5 us (7.9)
+    {151936, 2560, EPI_STORE, {8, 2, 256, 1}},  // lm_head: 87.9 us (113.5)
 };
 
 bool b_lookup(int N, int K, int epi, BConfig* c) {
@@ -592,93 +592,117 @@ bool b_lookup(int N, int K, int epi, BConfig* c) {
     return false;
 }
 
-template <int NW, int NTH, int PX, int D, bool NORM, int EPI>
-void launch_b(int grid, const float* x, int ldx, const float* gain, float eps, const int8_t* qz,
-              const float* sz, float* y, int ldy, int M, int N, int tiles_half, int nblk,
-              hipStream_t st) {
-    hipLaunchKernelGGL((k_mm_b<NW, NTH, PX, D, NORM, EPI>), dim3(grid), dim3(NW * QLM_WAVE), 0,
-                       st, x, ldx, gain, eps, qz, sz, y, ldy, M, N, tiles_half, nblk);
+// blocks per K slice, and the slices that then exist
+int b_bps(const BConfig& c, int K) {
+    const int nblk = K / 64, ks = c.ks < 1 ? 1 : c.ks;
+    return (nblk + ks - 1) / ks;
+}
+int b_slices(const BConfig& c, int K) {
+    const int bps = b_bps(c, K);
+    return (K / 64 + bps - 1) / bps;
+}
+size_t b_work_bytes(const BConfig& c, int M, int N, int K, int epi) {
+    const int s = b_slices(c, K);
+    return s > 1 ? (size_t)s * M * (epi == EPI_SWIGLU ? 2 : 1) * N * sizeof(float) : 0;
 }
 
-template <int NW, int NTH, int PX, int D>
-int launch_b_epi(int grid, const float* x, int ldx, const float* norm_w, float eps,
+struct BLaunch {
+    int grid, slices, bps;
+    float* part;  // partial sums of the slices (null: whole K)
+};
+
+template <int NW, int NTH, int PX, bool NORM, int EPI>
+void launch_b(const BLaunch& l, const float* x, int ldx, const float* gain, float eps,
+              const int8_t* qz, const float* sz, float* y, int ldy, int M, int N, int tiles_half,
+              int nblk, hipStream_t st) {
+    hipLaunchKernelGGL((k_mm_b<NW, NTH, PX, NORM, EPI>), dim3(l.grid, l.slices),
+                       dim3(NW * QLM_WAVE), 0, st, x, ldx, gain, eps, qz, sz, y, ldy, M, N,
+                       tiles_half, nblk, l.bps, l.part);
+}
+
+template <int NW, int NTH, int PX>
+int launch_b_epi(const BLaunch& l, const float* x, int ldx, const float* norm_w, float eps,
                  const int8_t* qz, const float* sz, float* y, int ldy, int M, int N, int epi,
                  int tiles_half, int nblk, hipStream_t st) {
     if (epi == EPI_SWIGLU)
-        launch_b<NW, NTH, PX, D, true, EPI_SWIGLU>(grid, x, ldx, norm_w, eps, qz, sz, y, ldy, M,
-                                                  N, tiles_half, nblk, st);
+        launch_b<NW, NTH, PX, true, EPI_SWIGLU>(l, x, ldx, norm_w, eps, qz, sz, y, ldy, M, N,
+                                                  tiles_half, nblk, st);
     else if (epi == EPI_RESID)
-        launch_b<NW, NTH, PX, D, false, EPI_RESID>(grid, x, ldx, nullptr, eps, qz, sz, y, ldy, M,
-                                                  N, tiles_half, nblk, st);
+        launch_b<NW, NTH, PX, false, EPI_RESID>(l, x, ldx, nullptr, eps, qz, sz, y, ldy, M, N,
+                                                  tiles_half, nblk, st);
     else if (norm_w)
-        launch_b<NW, NTH, PX, D, true, EPI_STORE>(grid, x, ldx, norm_w, eps, qz, sz, y, ldy, M, N,
+        launch_b<NW, NTH, PX, true, EPI_STORE>(l, x, ldx, norm_w, eps, qz, sz, y, ldy, M, N,
                                                  tiles_half, nblk, st);
     else
-        launch_b<NW, NTH, PX, D, false, EPI_STORE>(grid, x, ldx, nullptr, eps, qz, sz, y, ldy, M,
-                                                  N, tiles_half, nblk, st);
+        launch_b<NW, NTH, PX, false, EPI_STORE>(l, x, ldx, nullptr, eps, qz, sz, y, ldy, M, N,
+                                                  tiles_half, nblk, st);
     return qlm_launch_status();
 }
 
 // Shapes whose registers do not fit (the compiler spills; counts from the
 // gfx950 build): 7 blocks a wave with the RMSNorm gains; SwiGLU with two
-// tiles per half at 5 blocks a wave (8 waves) or 2 (16 waves); 16 waves at
-// 3 blocks a wave with SwiGLU, or RMSNorm and two tiles per half; with two
-// rings, SwiGLU except one tile per half at 4 blocks a wave, and RMSNorm
-// with two tiles per half at 5 blocks a wave or 16 waves.
-bool b_spills(int nw, int nth, int px, int depth, bool norm, bool swiglu) {
+// tiles per half at 5 blocks a wave (8 waves) or 2 (16 waves).
+bool b_spills(int nw, int nth, int px, bool norm, bool swiglu) {
     if (px >= 7 && norm) return true;
     if (swiglu && nth == 2 && (nw == 16 || px >= 5)) return true;
-    if (nw == 16 && px >= 3 && (swiglu || (norm && nth == 2))) return true;
-    if (depth == 2) {
-        if (swiglu && (nth == 2 || nw == 16 || px >= 5)) return true;
-        if (norm && nth == 2 && (nw == 16 || px >= 5)) return true;
-    }
     return false;
 }
 
-// Built: (waves, blocks per wave) = (8, 2) (8, 4) (8, 5) (8, 7) (16, 2)
-// (16, 3), i.e. K <= 1024, 2048, 2560, 3584 (8 waves) or 2048, 3072 (16
-// waves), with 1 or
-// 2 tiles per half and one ring; two rings at (8, 4) (8, 5) (16, 2). The
-// blocks per wave are ceil(K / 64 / waves).
+// Built: (waves, blocks per wave) = (8, 2) (8, 4) (8, 5) (8, 7) (16, 2),
+// with 1 or 2 tiles per half; blocks per wave = ceil(blocks per slice /
+// waves). A slice count above 1 writes partial sums to work and adds the
+// ordered reduction (k_mm_reduce, with the RMSNorm when norm_w is given).
 int b_run(const BConfig& c, const float* x, int ldx, const float* norm_w, float eps,
           const int8_t* qz, const float* sz, float* y, int ldy, int M, int N, int K, int epi,
-          hipStream_t st) {
+          void* work, size_t work_bytes, hipStream_t st) {
     const int nblk = K / 64;
     const int tiles_half = (N + 15) / 16;
-    if ((c.nw != 8 && c.nw != 16) || (c.nth != 1 && c.nth != 2) ||
-        (c.depth != 1 && c.depth != 2))
-        return QLM_ERR_ARG;
-    const int px = (nblk + c.nw - 1) / c.nw;
-    if (b_spills(c.nw, c.nth, px, c.depth, norm_w != nullptr, epi == EPI_SWIGLU))
-        return QLM_ERR_SHAPE;
+    if ((c.nw != 8 && c.nw != 16) || (c.nth != 1 && c.nth != 2) || c.ks < 1) return QLM_ERR_ARG;
+    const int bps = b_bps(c, K), slices = b_slices(c, K);
+    const int px = (bps + c.nw - 1) / c.nw;
+    if (b_spills(c.nw, c.nth, px, norm_w != nullptr, epi == EPI_SWIGLU)) return QLM_ERR_SHAPE;
+    if (norm_w && K > kMaxGainK) return QLM_ERR_SHAPE;
     const int groups = (tiles_half + c.nth - 1) / c.nth;
     const int grid = c.grid < groups ? c.grid : groups;
     if (grid < 1) return QLM_ERR_ARG;
-#define QLM_B(NW_, NTH_, PX_, D_)                                                             \
-    if (c.nw == NW_ && c.nth == NTH_ && px == PX_ && c.depth == D_)                           \
-        return launch_b_epi<NW_, NTH_, PX_, D_>(grid, x, ldx, norm_w, eps, qz, sz, y, ldy, M, N, \
-                                                epi, tiles_half, nblk, st);
-    QLM_B(8, 1, 2, 1)
-    QLM_B(8, 1, 4, 1)
-    QLM_B(8, 1, 5, 1)
-    QLM_B(8, 1, 7, 1)
-    QLM_B(8, 2, 2, 1)
-    QLM_B(8, 2, 4, 1)
-    QLM_B(8, 2, 5, 1)
-    QLM_B(8, 2, 7, 1)
-    QLM_B(16, 1, 2, 1)
-    QLM_B(16, 2, 2, 1)
-    QLM_B(16, 1, 3, 1)
-    QLM_B(16, 2, 3, 1)
-    QLM_B(8, 1, 4, 2)
-    QLM_B(8, 1, 5, 2)
-    QLM_B(8, 2, 4, 2)
-    QLM_B(8, 2, 5, 2)
-    QLM_B(16, 1, 2, 2)
-    QLM_B(16, 2, 2, 2)
+    float* part = nullptr;
+    if (slices > 1) {
+        if (!work || work_bytes < b_work_bytes(c, M, N, K, epi)) return QLM_ERR_ARG;
+        part = static_cast<float*>(work);
+    }
+    const BLaunch l{grid, slices, bps, part};
+    int rc = QLM_ERR_SHAPE;
+#define QLM_B(NW_, NTH_, PX_)                                                                 \
+    if (c.nw == NW_ && c.nth == NTH_ && px == PX_)                                            \
+        rc = launch_b_epi<NW_, NTH_, PX_>(l, x, ldx, norm_w, eps, qz, sz, y, ldy, M, N, epi,     \
+                                          tiles_half, nblk, st);
+    QLM_B(8, 1, 2)
+    else QLM_B(8, 1, 4)
+    else QLM_B(8, 1, 5)
+    else QLM_B(8, 1, 7)
+    else QLM_B(8, 2, 2)
+    else QLM_B(8, 2, 4)
+    else QLM_B(8, 2, 5)
+    else QLM_B(8, 2, 7)
+    else QLM_B(16, 1, 2)
+    else QLM_B(16, 2, 2)
 #undef QLM_B
-    return QLM_ERR_SHAPE;
+    if (rc != QLM_OK || slices == 1) return rc;
+    const int NR = (epi == EPI_SWIGLU ? 2 : 1) * N;
+    const dim3 rgrid((N + kReduceThreads - 1) / kReduceThreads, M);
+    if (epi == EPI_SWIGLU)
+        hipLaunchKernelGGL((k_mm_reduce<MMR_SWIGLU, true>), rgrid, dim3(kReduceThreads), 0, st,
+                           part, slices, M, NR, N, y, ldy, x, ldx, K, eps);
+    else if (epi == EPI_RESID)
+        hipLaunchKernelGGL((k_mm_reduce<MMR_RESID, false>), rgrid, dim3(kReduceThreads), 0, st,
+                           part, slices, M, NR, N, y, ldy, x, ldx, K, eps);
+    else if (norm_w)
+        hipLaunchKernelGGL((k_mm_reduce<MMR_STORE, true>), rgrid, dim3(kReduceThreads), 0, st,
+                           part, slices, M, NR, N, y, ldy, x, ldx, K, eps);
+    else
+        hipLaunchKernelGGL((k_mm_reduce<MMR_STORE, false>), rgrid, dim3(kReduceThreads), 0, st,
+                           part, slices, M, NR, N, y, ldy, x, ldx, K, eps);
+    return qlm_launch_status();
 }
 
 }  // namespace
@@ -686,21 +710,28 @@ int b_run(const BConfig& c, const float* x, int ldx, const float* norm_w, float 
 extern "C" size_t qlm_matmul_i8_t_workspace_bytes(int M, int N, int K, int epilogue) {
     if (M < 1 || N < 1 || K < 64) return 0;
     BConfig bc;
-    if (b_lookup(N, K, epilogue, &bc)) return 0;  // whole-K form: no partial sums
+    if (b_lookup(N, K, epilogue, &bc)) return b_work_bytes(bc, M, N, K, epilogue);
     const int halves = epilogue == EPI_SWIGLU ? 2 : 1;
     const TConfig c = t_config(N, K, epilogue);
     return (size_t)t_slices(c, K) * M * halves * N * sizeof(float);
+}
+
+extern "C" size_t qlm_matmul_i8_t_whole_workspace_bytes(int M, int N, int K, int epilogue,
+                                                       int k_slices) {
+    if (M < 1 || N < 1 || K < 64 || k_slices < 1) return 0;
+    return b_work_bytes(BConfig{8, 1, 1, k_slices}, M, N, K, epilogue);
 }
 
 extern "C" int qlm_matmul_i8_t_whole_config(const float* x, int ldx, const float* norm_w,
                                             float eps, const int8_t* q_tiles,
                                             const float* s_tiles, int group, float* y, int ldy,
                                             int M, int N, int K, int epilogue, int waves,
-                                            int tiles, int rings, int grid, void* stream) {
+                                            int tiles, int grid, int k_slices, void* work,
+                                            size_t work_bytes, void* stream) {
     const int rc = t_check(x, ldx, norm_w, q_tiles, s_tiles, group, y, ldy, M, N, K, epilogue);
     if (rc != QLM_OK) return rc;
-    return b_run(BConfig{waves, tiles, rings, grid}, x, ldx, norm_w, eps, q_tiles, s_tiles, y, ldy, M, N,
-                 K, epilogue, as_stream(stream));
+    return b_run(BConfig{waves, tiles, grid, k_slices}, x, ldx, norm_w, eps, q_tiles, s_tiles, y,
+                 ldy, M, N, K, epilogue, work, work_bytes, as_stream(stream));
 }
 
 extern "C" int qlm_matmul_i8_t_config(const float* x, int ldx, const float* norm_w, float eps,
@@ -723,8 +754,8 @@ extern "C" int qlm_matmul_i8_t(const float* x, int ldx, const float* norm_w, flo
     if (rc != QLM_OK) return rc;
     BConfig bc;
     if (b_lookup(N, K, epilogue, &bc))
-        return b_run(bc, x, ldx, norm_w, eps, q_tiles, s_tiles, y, ldy, M, N, K, epilogue,
-                     as_stream(stream));
+        return b_run(bc, x, ldx, norm_w, eps, q_tiles, s_tiles, y, ldy, M, N, K, epilogue, work,
+                     work_bytes, as_stream(stream));
     if (!work) return QLM_ERR_ARG;
     const TConfig c = t_config(N, K, epilogue);
     return t_run(c, x, ldx, norm_w, eps, q_tiles, s_tiles, y, ldy, M, N, K, epilogue, work,

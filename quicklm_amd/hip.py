@@ -71,8 +71,9 @@ _SIGS = {
                              _vp]),
     "qlm_matmul_i8_t_config": (_i, [_vp, _i, _vp, _f, _vp, _vp, _i, _vp, _i, _i, _i, _i, _i, _i,
                                     _i, _i, _i, _vp, _sz, _vp]),
+    "qlm_matmul_i8_t_whole_workspace_bytes": (_sz, [_i, _i, _i, _i, _i]),
     "qlm_matmul_i8_t_whole_config": (_i, [_vp, _i, _vp, _f, _vp, _vp, _i, _vp, _i, _i, _i, _i,
-                                          _i, _i, _i, _i, _i, _vp]),
+                                          _i, _i, _i, _i, _i, _vp, _sz, _vp]),
     "qlm_matmul_i8_mx": (_i, [_vp, _i, _vp, _f, _vp, _vp, _i, _vp, _i, _i, _i, _i, _i, _vp, _sz,
                               _vp]),
     "qlm_gemv_i8_mx_shape": (_i, [_i, _i, _i, C.POINTER(_i), C.POINTER(_i), C.POINTER(_i)]),

@@ -87,25 +87,33 @@ def test_matmul_t_shapes(hip, orc, rng, epi):
 
 # whole-K form: (waves, tiles per half); grids 1 (one workgroup walks every
 # tile group), 3 (a ragged share) and one group per workgroup
-WHOLE = [(8, 1, 1), (8, 2, 1), (16, 1, 1), (16, 2, 1), (8, 1, 2), (8, 2, 2), (16, 1, 2)]
+WHOLE = [(8, 1), (8, 2), (16, 1), (16, 2)]
 WHOLE_CASES = [  # (M, N, K): K of 2, 4, 5 and 7 blocks per wave at 8 waves
     (16, 1000, 2560), (3, 517, 2560), (16, 2560, 2048), (7, 300, 1024), (16, 77, 3584),
     (12, 130, 2560), (2, 40, 1984), (16, 33, 960),
 ]
 
 
-def _whole_built(nw, nth, rings, K, norm, swiglu):
-    px = -(-(K // 64) // nw)
-    if rings == 1:
-        built = (nw == 8 and px in (2, 4, 5, 7)) or (nw == 16 and px in (2, 3))
-    else:
-        built = (nw == 8 and px in (4, 5)) or (nw == 16 and px == 2)
+def _whole_built(nw, nth, K, norm, swiglu, slices=1):
+    nblk = K // 64
+    bps = -(-nblk // slices)
+    px = -(-bps // nw)
+    built = (nw == 8 and px in (2, 4, 5, 7)) or (nw == 16 and px == 2)
     spills = (px >= 7 and norm) or (swiglu and nth == 2 and (nw == 16 or px >= 5))
-    spills = spills or (nw == 16 and px >= 3 and (swiglu or (norm and nth == 2)))
-    if rings == 2:
-        spills = spills or (swiglu and (nth == 2 or nw == 16 or px >= 5))
-        spills = spills or (norm and nth == 2 and (nw == 16 or px >= 5))
-    return built and not spills
+    return built and not spills and not (norm and K > 4096)
+
+
+def _run_whole(hip, c, M, N, K, epi, nw_, nth, grid, slices):
+    lib = hip.lib()
+    nwork = lib.qlm_matmul_i8_t_whole_workspace_bytes(M, N, K, EPI[epi], slices)
+    work = hip.DeviceBuffer(max(nwork, 16))
+    work.upload(np.full(max(nwork, 16), 0x5A, np.uint8))  # no initial contents are required
+    c["dy"] = dev(hip, c["y0"])
+    say("matmul_t_whole", epi, M, N, K, nw_, nth, grid, slices)
+    return lib.qlm_matmul_i8_t_whole_config(
+        c["x"].ptr, K, c["nw"].ptr if c["nw"] else None, C.c_float(1e-6), c["dq"].ptr,
+        c["ds"].ptr, 32, c["dy"].ptr, c["ldy"], M, N, K, EPI[epi], nw_, nth, grid, slices,
+        work.ptr if nwork else None, C.c_size_t(nwork), None)
 
 
 @pytest.mark.parametrize("M,N,K", WHOLE_CASES)
@@ -115,30 +123,46 @@ def test_matmul_t_whole(hip, orc, rng, M, N, K, epi):
     within the tolerance of the K-sliced form; unbuilt or spilling shapes are
     refused with QLM_ERR_SHAPE before any launch."""
     c = _case(hip, orc, rng, M, N, K, epi)
-    lib = hip.lib()
     tiles_half = -(-N // 16)
+    norm, swiglu = epi.endswith("norm"), epi.startswith("swiglu")
     ran = 0
-    for nw_, nth, rings in WHOLE:
-        ok = _whole_built(nw_, nth, rings, K, epi.endswith("norm"), epi.startswith("swiglu"))
+    for nw_, nth in WHOLE:
+        ok = _whole_built(nw_, nth, K, norm, swiglu)
         groups = -(-tiles_half // nth)
         for grid in sorted({1, min(3, groups), groups}):
-            c["dy"] = dev(hip, c["y0"])
-            say("matmul_t_whole", epi, M, N, K, nw_, nth, rings, grid)
-            rc = lib.qlm_matmul_i8_t_whole_config(
-                c["x"].ptr, K, c["nw"].ptr if c["nw"] else None, C.c_float(1e-6), c["dq"].ptr,
-                c["ds"].ptr, 32, c["dy"].ptr, c["ldy"], M, N, K, EPI[epi], nw_, nth, rings, grid,
-                None)
+            rc = _run_whole(hip, c, M, N, K, epi, nw_, nth, grid, 1)
             if not ok:
-                assert rc == -2, (nw_, nth, rings, K, rc)  # QLM_ERR_SHAPE
+                assert rc == -2, (nw_, nth, K, rc)  # QLM_ERR_SHAPE
                 continue
             hip.check(rc)
             err = _check(hip, c, M, N)
-            assert err < 1e-5, (epi, M, N, K, nw_, nth, rings, grid, err)
+            assert err < 1e-5, (epi, M, N, K, nw_, nth, grid, err)
             ran += 1
     # K = 3584 with the RMSNorm gains spills at every built shape
-    assert ran > 0 or (K == 3584 and epi.endswith("norm"))
-    assert ran > 0 or not any(_whole_built(a, b, r, K, epi.endswith("norm"),
-                                           epi.startswith("swiglu")) for a, b, r in WHOLE)
+    assert ran > 0 or (K == 3584 and norm)
+
+
+@pytest.mark.parametrize("M,N,K,slices", [(16, 2560, 9728, 4), (5, 300, 9728, 3), (16, 200, 2560, 2),
+                                          (16, 1000, 4096, 2), (7, 130, 3584, 2)])
+@pytest.mark.parametrize("epi", ["store", "store_norm", "resid", "swiglu_norm"])
+def test_matmul_t_whole_sliced(hip, orc, rng, M, N, K, slices, epi):
+    """K cut into slices (raw partial sums, then the ordered reduction with
+    the epilogue and the RMSNorm) at every built (waves, tiles), including a
+    ragged last slice; RMSNorm past K = 4096 is refused."""
+    c = _case(hip, orc, rng, M, N, K, epi)
+    norm, swiglu = epi.endswith("norm"), epi.startswith("swiglu")
+    ran = 0
+    for nw_, nth in WHOLE:
+        ok = _whole_built(nw_, nth, K, norm, swiglu, slices)
+        rc = _run_whole(hip, c, M, N, K, epi, nw_, nth, 160, slices)
+        if not ok:
+            assert rc == -2, (nw_, nth, K, slices, rc)
+            continue
+        hip.check(rc)
+        err = _check(hip, c, M, N)
+        assert err < 1e-5, (epi, M, N, K, slices, nw_, nth, err)
+        ran += 1
+    assert ran > 0 or (norm and K > 4096)
 
 
 @pytest.mark.parametrize("N,K,epi", [(9728, 2560, "swiglu_norm"), (8224, 2560, "store_norm"),
@@ -148,11 +172,13 @@ def test_matmul_t_4b_projections(hip, orc, rng, N, K, epi):
     whole-K form for them (no workspace)."""
     M = 16
     c = _case(hip, orc, rng, M, N, K, epi)
-    assert hip.lib().qlm_matmul_i8_t_workspace_bytes(M, N, K, EPI[epi]) == 0
+    nwork = hip.lib().qlm_matmul_i8_t_workspace_bytes(M, N, K, EPI[epi])
+    assert nwork == 0
+    work = hip.DeviceBuffer(nwork) if nwork else None
     c["dy"] = dev(hip, c["y0"])
     say("matmul_t_4b", epi, M, N, K)
     hip.call("qlm_matmul_i8_t", c["x"], K, c["nw"], 1e-6, c["dq"], c["ds"], 32, c["dy"],
-             c["ldy"], M, N, K, EPI[epi], None, 0, None)
+             c["ldy"], M, N, K, EPI[epi], work, nwork, None)
     err = _check(hip, c, M, N)
     assert err < 1e-5, (epi, N, K, err)
 
