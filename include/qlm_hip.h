@@ -40,6 +40,8 @@ const char* qlm_error_string(int status);
 int qlm_device_count(int* count);
 int qlm_set_device(int device);
 int qlm_device_name(char* buf, int len);
+/* Free and total device memory of the current device (hipMemGetInfo). */
+int qlm_mem_info(size_t* free_bytes, size_t* total_bytes);
 int qlm_malloc(void** ptr, size_t bytes);
 int qlm_free(void* ptr);
 int qlm_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream);
@@ -160,6 +162,15 @@ size_t qlm_matmul_i8_workspace_bytes(int M, int N, int K, int epilogue);
 int qlm_matmul_i8(const float* x, int ldx, const float* norm_w, float eps, const int8_t* q,
                   const float* scales, int group, float* y, int ldy, int M, int N, int K,
                   int epilogue, void* work, size_t work_bytes, void* stream);
+/* qlm_matmul_i8 over the tile-major copy of the weights (qlm_mx_swizzle:
+ * halves 2 for SwiGLU; group-32 scales as swizzled, per-row scales in their
+ * [rows] layout), so a model needs no row-major copy for its M > 1 rows.
+ * Same arithmetic, bit-identical to qlm_matmul_i8 on the same weights; K a
+ * multiple of 64; the same workspace. */
+int qlm_matmul_i8_tm(const float* x, int ldx, const float* norm_w, float eps,
+                     const int8_t* q_tiles, const float* s_tiles, int group, float* y, int ldy,
+                     int M, int N, int K, int epilogue, void* work, size_t work_bytes,
+                     void* stream);
 
 /* Batched decode (2 <= M <= 16 activation rows) on the int8 matrix cores
  * over the tile-major weights of qlm_mx_swizzle (per-row scales as

@@ -112,13 +112,21 @@ bool gemm_tiles(const Tensor& A, const float* norm_w, float eps, const Tensor& B
 }
 
 // The split-K bf16 matrix-core matmul for M > 1 rows (norm_w null: no
-// RMSNorm prologue).
+// RMSNorm prologue), over the tile-major copy when the model has one (then
+// the only copy), else the row-major weights; any M.
 void matmul_mfma(const Tensor& A, const float* norm_w, float eps, const Tensor& B, float* C,
                  int64_t ldc, int64_t N, int epilogue) {
     const int64_t M = A.rows(), K = A.cols();
     const size_t need_b = qlm_matmul_i8_workspace_bytes((int)M, (int)N, (int)K, epilogue);
     need(g_mm_work && g_mm_work_bytes >= need_b,
          "matmul: M > 1 needs set_matmul_workspace() of qlm_matmul_i8_workspace_bytes()");
+    if (B.int8_tiles) {
+        check(qlm_matmul_i8_tm(A.data, (int)A.row_stride(), norm_w, eps, B.int8_tiles,
+                               B.int8_tile_scales, B.int8_group, C, (int)ldc, (int)M, (int)N,
+                               (int)K, epilogue, g_mm_work, g_mm_work_bytes, g_stream),
+              "qlm_matmul_i8_tm");
+        return;
+    }
     check(qlm_matmul_i8(A.data, (int)A.row_stride(), norm_w, eps, B.int8_data, B.int8_scales,
                         B.int8_group, C, (int)ldc, (int)M, (int)N, (int)K, epilogue, g_mm_work,
                         g_mm_work_bytes, g_stream),
@@ -139,6 +147,7 @@ void matmul(const Tensor& A, const Tensor& B, Tensor& C, bool transpose_B) {
         return;
     }
     if (gemv_tiles(A, nullptr, 0.0f, B, C.data, N, 0)) return;
+    if (!B.int8_data) return matmul_mfma(A, nullptr, 0.0f, B, C.data, C.row_stride(), N, 0);
     check(qlm_gemv_i8(A.data, (int)A.row_stride(), B.int8_data, B.int8_scales, B.int8_group, C.data,
                       (int)C.row_stride(), (int)M, (int)N, (int)K, g_stream),
           "qlm_gemv_i8");
@@ -155,6 +164,7 @@ void matmul_rmsnorm(const Tensor& A, const Tensor& norm_w, float eps, const Tens
         return;
     }
     if (gemv_tiles(A, norm_w.data, eps, B, C.data, N, 0)) return;
+    if (!B.int8_data) return matmul_mfma(A, norm_w.data, eps, B, C.data, C.row_stride(), N, 0);
     check(qlm_gemv_i8_rmsnorm(A.data, (int)A.row_stride(), norm_w.data, eps, B.int8_data,
                               B.int8_scales, B.int8_group, C.data, (int)C.row_stride(), (int)M,
                               (int)N, (int)K, g_stream),
@@ -173,6 +183,8 @@ void matmul_residual(const Tensor& A, const Tensor& B, Tensor& residual) {
         return;
     }
     if (gemv_tiles(A, nullptr, 0.0f, B, residual.data, N, 1)) return;
+    if (!B.int8_data)
+        return matmul_mfma(A, nullptr, 0.0f, B, residual.data, residual.row_stride(), N, 1);
     check(qlm_gemv_i8_residual(A.data, (int)A.row_stride(), B.int8_data, B.int8_scales,
                                B.int8_group, residual.data, (int)residual.row_stride(), (int)M,
                                (int)N, (int)K, g_stream),
@@ -213,6 +225,7 @@ void matmul_swiglu_rmsnorm(const Tensor& A, const Tensor& norm_w, float eps, con
         return;
     }
     if (gemv_tiles(A, norm_w.data, eps, B, C.data, F, 2)) return;
+    if (!B.int8_data) return matmul_mfma(A, norm_w.data, eps, B, C.data, C.row_stride(), F, 2);
     check(qlm_gemv_i8_swiglu_rmsnorm(A.data, (int)A.row_stride(), norm_w.data, eps, B.int8_data,
                                      B.int8_scales, B.int8_group, C.data, (int)C.row_stride(),
                                      (int)M, (int)F, (int)K, g_stream),

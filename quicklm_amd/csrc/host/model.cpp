@@ -139,6 +139,12 @@ void DecoderModel::tile_linear(LinearI8& lin, int halves) {
                               lin.qz4.get<uint8_t>(), lin.sz.get<float>(), stream_),
               "int4 tile swizzle");
     }
+    // Every device matmul reads the tile-major copy, so the row-major one
+    // (and the packed int4 rows) go; per-row scales are the tile scales.
+    check(qlm_stream_sync(stream_), "sync");
+    lin.q.release();
+    lin.q4.release();
+    if (lin.sz.bytes()) lin.s.release();
 }
 
 void DecoderModel::upload_f32(DeviceBuffer& dst, const std::string& name, int64_t expect) {

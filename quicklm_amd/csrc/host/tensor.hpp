@@ -21,7 +21,10 @@ struct Tensor {
     const float* int8_scales = nullptr;
     int int8_group = 32;
     // The same weight in the matrix-core tile-major layout (qlm_mx_swizzle),
-    // streamed by the one-row GEMV; null where the model keeps no such copy.
+    // which every device matmul reads; null where the model keeps no such
+    // copy (K not a multiple of 64). A model holding the tile-major copy keeps
+    // no row-major one (int8_data and int8_scales null; with per-row scales
+    // the scales stay, as int8_tile_scales).
     const int8_t* int8_tiles = nullptr;
     const float* int8_tile_scales = nullptr;
     // int4 (Q4_0) weights: the int8 fields then hold the unpacked values
@@ -47,7 +50,8 @@ struct Tensor {
         return t;
     }
 
-    bool is_int8() const { return int8_data != nullptr; }
+    // int8 (or int4-unpacked) weights, row-major and/or tile-major
+    bool is_int8() const { return int8_data != nullptr || int8_tiles != nullptr; }
     bool is_native() const { return native_data != nullptr; }
 
     void compute_strides() {

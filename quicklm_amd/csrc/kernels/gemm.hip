@@ -95,6 +95,36 @@ __device__ __forceinline__ void store_w16(unsigned short* dst, int4 w) {
     reinterpret_cast<uint4*>(dst)[1] = o[1];
 }
 
+// Tile-major weights (qlm_mx_swizzle: 16-row x 64-column fragments of 1 KB
+// in lane order, each half of a [gate; up] matrix tiled on its own; group-32
+// scales as [fragment][h][n]). Row r of the stacked matrix is row r - half F
+// of half `half`; its 16 columns k .. k + 15 (k a multiple of 16) are one
+// lane's 16 bytes of fragment (tile, k / 64). Per-row scales keep their
+// [rows] layout.
+struct TileMap {
+    int F;           // rows per half (all rows when the matrix has one half)
+    int tiles_half;  // 16-row tiles per half
+    int nblk64;      // 64-column blocks per row
+};
+__device__ __forceinline__ int tm_frag(const TileMap& t, int r, int k, int& n) {
+    const int half = r >= t.F ? 1 : 0;
+    const int rh = r - half * t.F;
+    n = rh & 15;
+    return (half * t.tiles_half + (rh >> 4)) * t.nblk64 + (k >> 6);
+}
+// byte offset of row r's 16 columns k .. k + 15
+__device__ __forceinline__ size_t tm_off(const TileMap& t, int r, int k) {
+    int n;
+    const int fb = tm_frag(t, r, k, n);
+    return ((size_t)fb * 64 + ((k >> 4) & 3) * 16 + n) * 16;
+}
+// index of row r's scale for the 32-column group g
+__device__ __forceinline__ size_t tm_scale(const TileMap& t, int r, int g) {
+    int n;
+    const int fb = tm_frag(t, r, g * 32, n);
+    return (size_t)fb * 32 + (g & 1) * 16 + n;
+}
+
 // WB16: the weights are bf16 rows (the native --precision bf16 form, no
 // scales): copied to LDS as they are, the MFMAs chained over K.
 // XS: x is already split (k_split_rows): x points at the bf16 hi plane
@@ -102,15 +132,16 @@ __device__ __forceinline__ void store_w16(unsigned short* dst, int4 w) {
 // been applied there, so NORM is false.
 // KG: 32-column scale groups per staged chunk and wave (more matrix-core work
 // between the chunk's load and its use).
+// TL: q and sc are tile-major (TileMap tmap); otherwise row-major.
 template <int WM, int WN, int WK, int TM, int TN, bool ROWSCALE, int EPI, bool NORM,
-          bool WB16 = false, bool XS = false, int KG = 1>
+          bool WB16 = false, bool XS = false, int KG = 1, bool TL = false>
 __global__ __launch_bounds__(kThreads) void k_mm_i8(const float* __restrict__ x, int ldx,
                                                     const float* __restrict__ rs,
                                                     const float* __restrict__ nw,
                                                     const int8_t* __restrict__ q,
                                                     const float* __restrict__ sc,
                                                     float* __restrict__ y, int ldy, int M, int N,
-                                                    int K, int F) {
+                                                    int K, int F, TileMap tmap) {
     static_assert(WM * WN * WK == 4, "4 waves");
     static_assert(EPI != EPI_SWIGLU || TN % 2 == 0, "SwiGLU pairs gate and up tiles");
     constexpr int BM = WM * TM * 16;
@@ -207,6 +238,8 @@ __global__ __launch_bounds__(kThreads) void k_mm_i8(const float* __restrict__ x,
                         reinterpret_cast<const uint16_t*>(q) + (size_t)w_row(r) * K + k0 + c16 * 16);
                     wr[u] = p[0];
                     wr2[u] = p[1];
+                } else if constexpr (TL) {
+                    wr[u] = *reinterpret_cast<const int4*>(q + tm_off(tmap, w_row(r), k0 + c16 * 16));
                 } else {
                     wr[u] = *reinterpret_cast<const int4*>(q + (size_t)w_row(r) * K + k0 + c16 * 16);
                 }
@@ -217,8 +250,10 @@ __global__ __launch_bounds__(kThreads) void k_mm_i8(const float* __restrict__ x,
             for (int gg = 0; gg < KG; ++gg) {
                 const int g = (k0 >> 5) + kw * KG + gg;
 #pragma unroll
-                for (int tn = 0; tn < TN; ++tn)
-                    sr[gg][tn] = sc[(size_t)w_row(tile_row(tn) + (lane & 15)) * nblk + g];
+                for (int tn = 0; tn < TN; ++tn) {
+                    const int wr_ = w_row(tile_row(tn) + (lane & 15));
+                    sr[gg][tn] = TL ? sc[tm_scale(tmap, wr_, g)] : sc[(size_t)wr_ * nblk + g];
+                }
             }
         }
     };
@@ -403,11 +438,12 @@ constexpr int sk_ring(int tm) { return tm <= 2 ? 2 : 1; }
 // DEFER (with NORM): the activation is staged as x * (1 + w) and the row's
 // 1/rms multiplies the reduced sums instead (k_mm_reduce<..., true>), so no
 // separate row-scale launch precedes the matmul.
-template <int TM, bool ROWSCALE, bool NORM, bool DEFER>
+// TL: q and sc are tile-major (TileMap tmap); otherwise row-major.
+template <int TM, bool ROWSCALE, bool NORM, bool DEFER, bool TL = false>
 __global__ __launch_bounds__(kThreads) void k_mm_i8_sk(
     const float* __restrict__ x, int ldx, const float* __restrict__ rs,
     const float* __restrict__ nw, const int8_t* __restrict__ q, const float* __restrict__ sc,
-    float* __restrict__ part, int ldp, int M, int NR, int K, int kper) {
+    float* __restrict__ part, int ldp, int M, int NR, int K, int kper, TileMap tmap) {
     constexpr int BM = 16 * TM;
     constexpr int KC = kSkKc;
     constexpr int XP = KC + 8, WP = KC + 8;
@@ -457,11 +493,22 @@ __global__ __launch_bounds__(kThreads) void k_mm_i8_sk(
             if (i < WV) {
                 const int r = i / (KC / 16), c16 = i % (KC / 16);
                 const int n = min(n0 + r, NR - 1);
-                wr[j][u] = *reinterpret_cast<const int4*>(q + (size_t)n * K + k0 + c16 * 16);
+                if constexpr (TL)
+                    wr[j][u] = *reinterpret_cast<const int4*>(q + tm_off(tmap, n, k0 + c16 * 16));
+                else
+                    wr[j][u] = *reinterpret_cast<const int4*>(q + (size_t)n * K + k0 + c16 * 16);
             }
         }
-        if constexpr (!ROWSCALE)
-            sr[j] = *reinterpret_cast<const float4*>(sc + (size_t)nrow * nblk + (k0 >> 5));
+        if constexpr (!ROWSCALE) {
+            if constexpr (TL) {
+                const int g0 = k0 >> 5;
+                sr[j] = make_float4(sc[tm_scale(tmap, nrow, g0)], sc[tm_scale(tmap, nrow, g0 + 1)],
+                                    sc[tm_scale(tmap, nrow, g0 + 2)],
+                                    sc[tm_scale(tmap, nrow, g0 + 3)]);
+            } else {
+                sr[j] = *reinterpret_cast<const float4*>(sc + (size_t)nrow * nblk + (k0 >> 5));
+            }
+        }
     };
     auto store_chunk = [&](int j) {
 #pragma unroll
@@ -642,25 +689,25 @@ size_t mm_workspace(int M, int N, int K, int epi) {
     return b;
 }
 
-template <int TM, bool RS, bool NORM, bool DEFER>
+template <int TM, bool RS, bool NORM, bool DEFER, bool TL>
 void launch_sk(const float* x, int ldx, const float* rs, const float* nw, const int8_t* q,
                const float* sc, float* part, int ldp, int M, int NR, int K, int ks,
-               hipStream_t st) {
+               const TileMap& tm, hipStream_t st) {
     const dim3 grid((NR + kSkRows - 1) / kSkRows, ks, (M + 16 * TM - 1) / (16 * TM));
-    hipLaunchKernelGGL((k_mm_i8_sk<TM, RS, NORM, DEFER>), grid, dim3(kThreads), 0, st, x, ldx, rs,
-                       nw, q, sc, part, ldp, M, NR, K, K / ks);
+    hipLaunchKernelGGL((k_mm_i8_sk<TM, RS, NORM, DEFER, TL>), grid, dim3(kThreads), 0, st, x, ldx,
+                       rs, nw, q, sc, part, ldp, M, NR, K, K / ks, tm);
 }
 
-template <bool RS, bool NORM, bool DEFER>
+template <bool RS, bool NORM, bool DEFER, bool TL>
 void launch_sk_tm(const float* x, int ldx, const float* rs, const float* nw, const int8_t* q,
                   const float* sc, float* part, int ldp, int M, int NR, int K, int ks,
-                  hipStream_t st) {
+                  const TileMap& tm, hipStream_t st) {
     if (M <= 16)
-        launch_sk<1, RS, NORM, DEFER>(x, ldx, rs, nw, q, sc, part, ldp, M, NR, K, ks, st);
+        launch_sk<1, RS, NORM, DEFER, TL>(x, ldx, rs, nw, q, sc, part, ldp, M, NR, K, ks, tm, st);
     else if (M <= 32)
-        launch_sk<2, RS, NORM, DEFER>(x, ldx, rs, nw, q, sc, part, ldp, M, NR, K, ks, st);
+        launch_sk<2, RS, NORM, DEFER, TL>(x, ldx, rs, nw, q, sc, part, ldp, M, NR, K, ks, tm, st);
     else
-        launch_sk<4, RS, NORM, DEFER>(x, ldx, rs, nw, q, sc, part, ldp, M, NR, K, ks, st);
+        launch_sk<4, RS, NORM, DEFER, TL>(x, ldx, rs, nw, q, sc, part, ldp, M, NR, K, ks, tm, st);
 }
 
 template <int EPI, bool NORM>
@@ -671,18 +718,21 @@ void launch_reduce(const float* part, int ks, int M, int NR, int N, float* y, in
                        y, ldy, x, ldx, K, eps);
 }
 
-template <int WM, int WN, int WK, int TM, int TN, bool RS, int EPI, bool NORM, bool XS = false>
+template <int WM, int WN, int WK, int TM, int TN, bool RS, int EPI, bool NORM, bool XS, bool TL>
 int launch_mm(const float* x, int ldx, const float* rs, const float* nw, const int8_t* q,
-              const float* sc, float* y, int ldy, int M, int N, int K, hipStream_t st) {
+              const float* sc, float* y, int ldy, int M, int N, int K, const TileMap& tm,
+              hipStream_t st) {
     constexpr int BM = WM * TM * 16;
     constexpr int BN_OUT = WN * (EPI == EPI_SWIGLU ? TN / 2 : TN) * 16;
     const dim3 grid((N + BN_OUT - 1) / BN_OUT, (M + BM - 1) / BM);
     if (K % (64 * WK) == 0)  // two scale groups a chunk
-        hipLaunchKernelGGL((k_mm_i8<WM, WN, WK, TM, TN, RS, EPI, NORM, false, XS, 2>), grid,
-                           dim3(kThreads), 0, st, x, ldx, rs, nw, q, sc, y, ldy, M, N, K, N);
-    else
+        hipLaunchKernelGGL((k_mm_i8<WM, WN, WK, TM, TN, RS, EPI, NORM, false, XS, 2, TL>), grid,
+                           dim3(kThreads), 0, st, x, ldx, rs, nw, q, sc, y, ldy, M, N, K, N, tm);
+    else if constexpr (!TL)  // tile-major weights have whole 64-column blocks
         hipLaunchKernelGGL((k_mm_i8<WM, WN, WK, TM, TN, RS, EPI, NORM, false, XS>), grid,
-                           dim3(kThreads), 0, st, x, ldx, rs, nw, q, sc, y, ldy, M, N, K, N);
+                           dim3(kThreads), 0, st, x, ldx, rs, nw, q, sc, y, ldy, M, N, K, N, tm);
+    else
+        return QLM_ERR_SHAPE;
     return qlm_launch_status();
 }
 
@@ -693,19 +743,23 @@ int launch_mm16(const float* x, int ldx, const float* rs, const float* nw, const
     constexpr int BN_OUT = 2 * (EPI == EPI_SWIGLU ? 2 : 4) * 16;
     const dim3 grid((N + BN_OUT - 1) / BN_OUT, (M + BM - 1) / BM);
     const int8_t* wq = reinterpret_cast<const int8_t*>(w);
+    const TileMap none{N, 0, 0};
     if (K % 64 == 0)
         hipLaunchKernelGGL((k_mm_i8<2, 2, 1, 4, 4, false, EPI, NORM, true, XS, 2>), grid,
-                           dim3(kThreads), 0, st, x, ldx, rs, nw, wq, nullptr, y, ldy, M, N, K, N);
+                           dim3(kThreads), 0, st, x, ldx, rs, nw, wq, nullptr, y, ldy, M, N, K, N,
+                           none);
     else
         hipLaunchKernelGGL((k_mm_i8<2, 2, 1, 4, 4, false, EPI, NORM, true, XS>), grid,
-                           dim3(kThreads), 0, st, x, ldx, rs, nw, wq, nullptr, y, ldy, M, N, K, N);
+                           dim3(kThreads), 0, st, x, ldx, rs, nw, wq, nullptr, y, ldy, M, N, K, N,
+                           none);
     return qlm_launch_status();
 }
 
-template <bool RS, bool NORM>
+template <bool RS, bool NORM, bool TL>
 int mm_run(const float* x, int ldx, float* rs, const float* nw, float eps, const int8_t* q,
            const float* sc, float* y, int ldy, int M, int N, int K, int epi, float* part,
            hipStream_t st) {
+    const TileMap tm{N, (N + 15) / 16, K / 64};  // a SwiGLU matrix: gate rows, then up rows
     if (use_sk(M, K)) {
         const int NR = epi == EPI_SWIGLU ? 2 * N : N;
         const int ks = sk_splits(NR, K);
@@ -718,11 +772,12 @@ int mm_run(const float* x, int ldx, float* rs, const float* nw, float eps, const
                 const int rc = qlm_launch_status();
                 if (rc != QLM_OK) return rc;
             }
-            launch_sk_tm<RS, NORM, false>(x, ldx, rs, nw, q, sc, dst, ldp, M, NR, K, ks, st);
+            launch_sk_tm<RS, NORM, false, TL>(x, ldx, rs, nw, q, sc, dst, ldp, M, NR, K, ks, tm,
+                                              st);
             return qlm_launch_status();
         }
         // row scales folded into the reduction (no separate launch)
-        launch_sk_tm<RS, NORM, NORM>(x, ldx, rs, nw, q, sc, dst, ldp, M, NR, K, ks, st);
+        launch_sk_tm<RS, NORM, NORM, TL>(x, ldx, rs, nw, q, sc, dst, ldp, M, NR, K, ks, tm, st);
         int rc = qlm_launch_status();
         if (rc != QLM_OK) return rc;
         if (epi == EPI_STORE)
@@ -744,13 +799,13 @@ int mm_run(const float* x, int ldx, float* rs, const float* nw, float eps, const
     if (rc != QLM_OK) return rc;
     const float* xs = reinterpret_cast<const float*>(xh);
     if (epi == EPI_STORE)
-        return launch_mm<2, 2, 1, 4, 4, RS, EPI_STORE, false, true>(xs, K, nullptr, nullptr, q, sc,
-                                                                    y, ldy, M, N, K, st);
+        return launch_mm<2, 2, 1, 4, 4, RS, EPI_STORE, false, true, TL>(
+            xs, K, nullptr, nullptr, q, sc, y, ldy, M, N, K, tm, st);
     if (epi == EPI_RESID)
-        return launch_mm<2, 2, 1, 4, 4, RS, EPI_RESID, false, true>(xs, K, nullptr, nullptr, q, sc,
-                                                                    y, ldy, M, N, K, st);
-    return launch_mm<2, 2, 1, 4, 4, RS, EPI_SWIGLU, false, true>(xs, K, nullptr, nullptr, q, sc, y,
-                                                                 ldy, M, N, K, st);
+        return launch_mm<2, 2, 1, 4, 4, RS, EPI_RESID, false, true, TL>(
+            xs, K, nullptr, nullptr, q, sc, y, ldy, M, N, K, tm, st);
+    return launch_mm<2, 2, 1, 4, 4, RS, EPI_SWIGLU, false, true, TL>(
+        xs, K, nullptr, nullptr, q, sc, y, ldy, M, N, K, tm, st);
 }
 
 }  // namespace
@@ -811,14 +866,15 @@ extern "C" int qlm_matmul_bf16(const float* x, int ldx, const float* norm_w, flo
     return launch_mm16<EPI_STORE, false, false>(x, ldx, nullptr, nullptr, w, y, ldy, M, N, K, st);
 }
 
-extern "C" int qlm_matmul_i8(const float* x, int ldx, const float* norm_w, float eps,
-                             const int8_t* q, const float* scales, int group, float* y, int ldy,
-                             int M, int N, int K, int epilogue, void* work, size_t work_bytes,
-                             void* stream) {
+namespace {
+template <bool TL>
+int matmul_i8_entry(const float* x, int ldx, const float* norm_w, float eps, const int8_t* q,
+                    const float* scales, int group, float* y, int ldy, int M, int N, int K,
+                    int epilogue, void* work, size_t work_bytes, void* stream) {
     if (!x || !q || !scales || !y) return QLM_ERR_ARG;
     if (M <= 0 || N <= 0 || K <= 0) return QLM_ERR_ARG;
     if (epilogue < EPI_STORE || epilogue > EPI_SWIGLU) return QLM_ERR_ARG;
-    if (K % 32 != 0) return QLM_ERR_SHAPE;
+    if (K % (TL ? 64 : 32) != 0) return QLM_ERR_SHAPE;
     const bool rowscale = (group == K);
     if (!rowscale && group != 32) return QLM_ERR_SHAPE;
     if (ldx < K || ldy < N || ldx % 4 != 0) return QLM_ERR_SHAPE;
@@ -830,12 +886,29 @@ extern "C" int qlm_matmul_i8(const float* x, int ldx, const float* norm_w, float
     float* rs = reinterpret_cast<float*>(work);
     float* part = reinterpret_cast<float*>(reinterpret_cast<char*>(work) + align256((size_t)M * 4));
     if (norm_w)
-        return rowscale ? mm_run<true, true>(x, ldx, rs, norm_w, eps, q, scales, y, ldy, M, N, K,
-                                             epilogue, part, st)
-                        : mm_run<false, true>(x, ldx, rs, norm_w, eps, q, scales, y, ldy, M, N,
-                                              K, epilogue, part, st);
-    return rowscale ? mm_run<true, false>(x, ldx, nullptr, nullptr, eps, q, scales, y, ldy, M, N,
-                                          K, epilogue, part, st)
-                    : mm_run<false, false>(x, ldx, nullptr, nullptr, eps, q, scales, y, ldy, M, N,
-                                           K, epilogue, part, st);
+        return rowscale ? mm_run<true, true, TL>(x, ldx, rs, norm_w, eps, q, scales, y, ldy, M, N,
+                                                 K, epilogue, part, st)
+                        : mm_run<false, true, TL>(x, ldx, rs, norm_w, eps, q, scales, y, ldy, M,
+                                                  N, K, epilogue, part, st);
+    return rowscale ? mm_run<true, false, TL>(x, ldx, nullptr, nullptr, eps, q, scales, y, ldy, M,
+                                              N, K, epilogue, part, st)
+                    : mm_run<false, false, TL>(x, ldx, nullptr, nullptr, eps, q, scales, y, ldy,
+                                               M, N, K, epilogue, part, st);
+}
+}  // namespace
+
+extern "C" int qlm_matmul_i8(const float* x, int ldx, const float* norm_w, float eps,
+                             const int8_t* q, const float* scales, int group, float* y, int ldy,
+                             int M, int N, int K, int epilogue, void* work, size_t work_bytes,
+                             void* stream) {
+    return matmul_i8_entry<false>(x, ldx, norm_w, eps, q, scales, group, y, ldy, M, N, K,
+                                  epilogue, work, work_bytes, stream);
+}
+
+extern "C" int qlm_matmul_i8_tm(const float* x, int ldx, const float* norm_w, float eps,
+                                const int8_t* q_tiles, const float* s_tiles, int group, float* y,
+                                int ldy, int M, int N, int K, int epilogue, void* work,
+                                size_t work_bytes, void* stream) {
+    return matmul_i8_entry<true>(x, ldx, norm_w, eps, q_tiles, s_tiles, group, y, ldy, M, N, K,
+                                 epilogue, work, work_bytes, stream);
 }

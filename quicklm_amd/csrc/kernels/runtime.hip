@@ -45,6 +45,11 @@ extern "C" int qlm_device_name(char* buf, int len) {
     return QLM_OK;
 }
 
+extern "C" int qlm_mem_info(size_t* free_bytes, size_t* total_bytes) {
+    if (!free_bytes || !total_bytes) return QLM_ERR_ARG;
+    return qlm_status(hipMemGetInfo(free_bytes, total_bytes));
+}
+
 extern "C" int qlm_malloc(void** ptr, size_t bytes) {
     if (!ptr) return QLM_ERR_ARG;
     *ptr = nullptr;

@@ -28,6 +28,7 @@ _SIGS = {
     "qlm_device_count": (_i, [C.POINTER(_i)]),
     "qlm_set_device": (_i, [_i]),
     "qlm_device_name": (_i, [C.c_char_p, _i]),
+    "qlm_mem_info": (_i, [C.POINTER(_sz), C.POINTER(_sz)]),
     "qlm_malloc": (_i, [C.POINTER(_vp), _sz]),
     "qlm_free": (_i, [_vp]),
     "qlm_memcpy_h2d": (_i, [_vp, _vp, _sz, _vp]),
@@ -60,6 +61,8 @@ _SIGS = {
     "qlm_matmul_i8_workspace_bytes": (_sz, [_i, _i, _i, _i]),
     "qlm_matmul_i8": (_i, [_vp, _i, _vp, _f, _vp, _vp, _i, _vp, _i, _i, _i, _i, _i, _vp, _sz,
                            _vp]),
+    "qlm_matmul_i8_tm": (_i, [_vp, _i, _vp, _f, _vp, _vp, _i, _vp, _i, _i, _i, _i, _i, _vp, _sz,
+                              _vp]),
     "qlm_gemv_i8_config": (_i, [_vp, _vp, _f, _vp, _vp, _i, _vp, _i, _i, _i, _i, _i, _i, _vp]),
     "qlm_gemv_i8_mx_config": (_i, [_vp, _vp, _f, _vp, _vp, _i, _vp, _i, _i, _i, _i, _i, _i,
                                    _vp]),
@@ -162,6 +165,13 @@ def device_name() -> str:
     buf = C.create_string_buffer(256)
     check(lib().qlm_device_name(buf, 256))
     return buf.value.decode()
+
+
+def mem_free() -> int:
+    """Free bytes of the current device."""
+    f, t = _sz(), _sz()
+    check(lib().qlm_mem_info(C.byref(f), C.byref(t)))
+    return f.value
 
 
 def sync() -> None:

@@ -218,3 +218,38 @@ def test_matmul_t_refuses(hip, orc, rng):
     assert lib.qlm_matmul_i8_t_config(x.ptr, 4160, None, C.c_float(0.0), dq.ptr, ds.ptr, 32,
                                       y.ptr, 64, 4, 64, 4160, 0, 4, 4, 2, 1, work.ptr,
                                       C.c_size_t(1 << 22), None) != 0  # 65-block slice
+
+
+@pytest.mark.parametrize("M,N,K", [(17, 300, 2560), (64, 2560, 9728), (5, 1000, 2048),
+                                   (130, 517, 1024), (300, 160, 2560), (1, 77, 3584)])
+@pytest.mark.parametrize("epi", ["store", "store_norm", "resid", "swiglu_norm"])
+@pytest.mark.parametrize("group", [32, "K"])
+def test_matmul_i8_tile_major(hip, orc, rng, M, N, K, epi, group):
+    """qlm_matmul_i8_tm (prefill tiles and the K-split path over the
+    tile-major weights, with its ragged last tiles) is bit-identical to
+    qlm_matmul_i8 over the row-major weights, and within 1e-5 of the oracle."""
+    g = K if group == "K" else 32
+    rows_w = 2 * N if epi.startswith("swiglu") else N
+    q, s = _weights(orc, rng, rows_w, K, g)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    nw = (rng.standard_normal(K) * 0.02).astype(np.float32)
+    ldy = N + 3
+    y0 = rng.standard_normal((M, ldy)).astype(np.float32)
+    lg = orc.matmul_i8(orc.rms_norm(x, nw, 1e-6) if epi.endswith("norm") else x, q, s, g)
+    ref = (y0[:, :N] + lg if epi == "resid" else lg if epi.startswith("store")
+           else orc.silu_mul(lg[:, :N].copy(), lg[:, N:].copy()))
+    dq, ds, keep = _mx_layout(hip, q, s, g, N, K, 2 if epi.startswith("swiglu") else 1)
+    dx = dev(hip, x)
+    dnw = dev(hip, nw) if epi.endswith("norm") else None
+    nbytes = hip.lib().qlm_matmul_i8_workspace_bytes(M, N, K, EPI[epi])
+    work = hip.DeviceBuffer(nbytes)
+    outs = []
+    for fn, wq, ws in (("qlm_matmul_i8", keep[0], keep[1]), ("qlm_matmul_i8_tm", dq, ds)):
+        dy = dev(hip, y0)
+        work.upload(np.full(nbytes, 0xA5, np.uint8))
+        say(fn, epi, g, M, N, K)
+        hip.call(fn, dx, K, dnw, 1e-6, wq, ws, g, dy, ldy, M, N, K, EPI[epi], work, nbytes, None)
+        outs.append(dy.to_numpy((M, ldy), np.float32))
+    assert np.array_equal(outs[0], outs[1])
+    assert np.array_equal(outs[1][:, N:], y0[:, N:])
+    assert rel_err(outs[1][:, :N], ref) < 1e-5

@@ -198,3 +198,30 @@ def test_micro_per_row_scales_match_oracle(hip, tmp_path):
     say("int8_row micro: last-step logit rel err", err)
     assert np.array_equal(got[0], want)
     assert err < 1e-3
+
+
+@pytest.mark.parametrize("precision", ["int8", "int4"])
+def test_one_weight_copy(hip, tiny_dir, precision):
+    """Every device matmul reads the tile-major copy of a linear, so the
+    engine keeps no row-major one: the device memory a loaded tiny model
+    takes stays within the tile-major weights (int8 values + group scales,
+    and at int4 the int4 copy beside them) plus the fp32 embedding and the
+    state, where the row-major copies would add 0.6 GB (int8) or 0.87 GB
+    (int4)."""
+    from quicklm_amd.engine import Engine
+
+    hip.sync()
+    free0 = hip.mem_free()
+    e = Engine(tiny_dir, max_seq_len=256, max_batch=1, precision=precision)
+    try:
+        hip.sync()
+        used = free0 - hip.mem_free()
+        wb = e.weight_bytes
+    finally:
+        e.close()
+    nk = wb / (1.125 if precision == "int8" else 0.625)  # int8 weights of the linears
+    tiles = nk * (1.125 if precision == "int8" else 1.625)
+    embed = 151936 * 1024 * 4
+    say(f"{precision}: device bytes {used / 1e9:.3f} GB, tile-major weights {tiles / 1e9:.3f} GB, "
+        f"embedding {embed / 1e9:.3f} GB")
+    assert used < tiles + embed + 450e6
