@@ -305,10 +305,12 @@ __global__ __launch_bounds__(NW * QLM_WAVE) void k_mm_b(
     if constexpr (NORM) {
 #pragma unroll
         for (int j = 0; j < kGainPer; ++j) {
-            const int i = tid + j * NTHR;
-            if (i < K4)
-                gsh[i] = make_float4(1.0f + gl[j].x, 1.0f + gl[j].y, 1.0f + gl[j].z,
-                                     1.0f + gl[j].w);
+            // unconditional store (entries past K hold a clamped copy, never
+            // read; the mask is the identity for tid < NTHR): under a branch
+            // the compiler sinks the gain load into it, behind the weight
+            // ring, and then waits for the whole ring
+            const int i = (tid + j * NTHR) & (kMaxGainK / 4 - 1);
+            gsh[i] = make_float4(1.0f + gl[j].x, 1.0f + gl[j].y, 1.0f + gl[j].z, 1.0f + gl[j].w);
         }
         __syncthreads();
     }
