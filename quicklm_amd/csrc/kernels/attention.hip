@@ -546,6 +546,232 @@ __global__ __launch_bounds__(kThreads) void k_gqa_prep_rows(
     }
 }
 
+// ---- bf16 K/V on the matrix cores (the isolated attention, kv_dtype 1) ----
+//
+// One wave per workgroup owns a chunk of 32 * spw positions of one (kv head
+// g, sequence b) and walks it in steps of 32 positions, with its own online
+// softmax; the chunk leaves k_attn's record [m, l, -, -, o[HD]] per query
+// head, merged by k_attn_combine. Both products run on
+// v_mfma_f32_16x16x32_bf16 (lane l = 16 qd + n; A lane: row n, k-slice qd;
+// B lane: k-slice qd, column n; D lane: rows 4 qd .. +3, column n):
+//   scores  A = the group's query heads, rows 0..7 their bf16 hi parts and
+//           rows 8..15 their lo parts (q = hi + lo to 2^-18 |q|; rows of
+//           heads >= G zero), B = 16 K rows as stored (bf16 is exact), so
+//           one product gives both halves and s = D[h] + D[h + 8] (one lane
+//           swap between the wave halves);
+//   P.V     A = the probabilities, hi rows 0..7 and lo rows 8..15 again
+//           (through a 1 KB LDS transpose), B = 32 V rows x 16 columns, read
+//           column-wise from an LDS copy of the step's V rows (the
+//           reduction runs over positions, which lie 512 bytes apart in the
+//           cache). The accumulator rows are the heads' hi and lo halves,
+//           added once at the end.
+// The next step's K rows are requested as soon as the scores have consumed
+// the current ones, its V rows once the current ones are in LDS; positions
+// past the chunk are clamped onto its last row (their scores are -inf).
+// Arithmetic intensity is n_q / n_kv flops per cache byte (8 at the 16 / 2
+// heads of the long-context workload): on the vector ALUs the dot products
+// and their reductions bound the old kernel at ~2.3 TB/s; here the matrix
+// cores take them and the loop is HBM-bound.
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ unsigned bf16_bits(float x) {
+    return (unsigned)__builtin_bit_cast(unsigned short, (__bf16)x);
+}
+
+// eight floats as the bf16 hi (lo = false) or lo (lo = true) parts
+__device__ __forceinline__ bf16x8_t split_part8(const float (&v)[8], bool lo) {
+    unsigned w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const __bf16 a = (__bf16)v[2 * i], c = (__bf16)v[2 * i + 1];
+        float ea = (float)a, ec = (float)c;
+        const unsigned ha = (unsigned)__builtin_bit_cast(unsigned short, a);
+        const unsigned hc = (unsigned)__builtin_bit_cast(unsigned short, c);
+        const unsigned la = bf16_bits(v[2 * i] - ea), lc = bf16_bits(v[2 * i + 1] - ec);
+        w[i] = lo ? (la | (lc << 16)) : (ha | (hc << 16));
+    }
+    return __builtin_bit_cast(bf16x8_t, make_uint4(w[0], w[1], w[2], w[3]));
+}
+
+// maximum over each row of 16 lanes; every lane of the row gets it
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, dpp_mov<kDppXor1>(v));
+    v = fmaxf(v, dpp_mov<kDppXor2>(v));
+    v = fmaxf(v, dpp_mov<kDppHalfMirror>(v));
+    return fmaxf(v, dpp_mov<kDppMirror>(v));
+}
+
+// D[r] + D[r + 8] of a 16 x 16 tile whose rows 8..15 (lanes 32..63) hold the
+// lo halves of rows 0..7: every lane gets the sum for its (qd & 1, n)
+__device__ __forceinline__ float add_halves(float d) {
+    const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(d), __float_as_uint(d), false,
+                                                    false);
+    return __uint_as_float(s[0]) + __uint_as_float(s[1]);
+}
+
+template <int HD, int G>
+__global__ __launch_bounds__(QLM_WAVE) void k_attn_mx(
+    const float* __restrict__ q, int ldq, const uint16_t* __restrict__ kc,
+    const uint16_t* __restrict__ vc, int max_seq, int n_kv, int ctx, float* __restrict__ work,
+    int nchunks, int n_q, float scale, int spw) {
+    static_assert(G >= 1 && G <= 8, "query heads per kv head");
+    constexpr int KS = HD / 32;          // k-steps of a score product
+    constexpr int DB = HD / 16;          // 16-column blocks of the output
+    constexpr int VST = HD + 8;          // LDS row stride of the V copy (bf16): +16 bytes
+    constexpr int LPR = HD / 8;          // lanes per V row (16 bytes each)
+    constexpr int RPI = QLM_WAVE / LPR;  // V rows per load instruction
+    constexpr int NVI = 32 / RPI;        // V loads per lane per step
+    __shared__ __align__(16) uint16_t vs[32 * VST];
+    __shared__ __align__(16) float ps[8][32];
+
+    const int lane = threadIdx.x, qd = lane >> 4, n = lane & 15;
+    const int chunk = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
+    const int start = chunk * 32 * spw;
+    const int cnt = min(32 * spw, ctx - start);
+    if (cnt <= 0) return;
+    const int steps = (cnt + 31) / 32;
+    // cache row (b, position start, head g); position p of the chunk adds p * n_kv rows
+    const uint16_t* kbase = kc + (((size_t)b * max_seq + start) * n_kv + g) * HD;
+    const uint16_t* vbase = vc + (((size_t)b * max_seq + start) * n_kv + g) * HD;
+    const size_t pstride = (size_t)n_kv * HD;
+
+    uint4 kr[2][KS], va[NVI / 2], vb[NVI / 2];  // V rows: two arrays (one 256-byte
+                                                 // array is left in scratch memory)
+    auto load_k = [&](int p0) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int p = min(p0 + 16 * j + n, cnt - 1);
+#pragma unroll
+            for (int kk = 0; kk < KS; ++kk)
+                kr[j][kk] = *reinterpret_cast<const uint4*>(kbase + p * pstride + 32 * kk + 8 * qd);
+        }
+    };
+    auto load_v = [&](int p0) {
+#pragma unroll
+        for (int i = 0; i < NVI; ++i) {
+            const int p = min(p0 + i * RPI + lane / LPR, cnt - 1);
+            const uint4 v = *reinterpret_cast<const uint4*>(vbase + p * pstride + (lane % LPR) * 8);
+            if (i < NVI / 2)
+                va[i] = v;
+            else
+                vb[i - NVI / 2] = v;
+        }
+    };
+    // ---- the first step's rows, then the query operand ----
+    load_k(0);
+    load_v(0);
+    const int hq = n & 7;
+    const bool lo_row = n >= 8, real_row = hq < G;
+    const float* qrow = q + (size_t)b * ldq + (size_t)(g * G + min(hq, G - 1)) * HD;
+    bf16x8_t qa[KS];
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) {
+        const float4 a = reinterpret_cast<const float4*>(qrow + 32 * kk + 8 * qd)[0];
+        const float4 c = reinterpret_cast<const float4*>(qrow + 32 * kk + 8 * qd)[1];
+        float e[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) e[i] = real_row ? e[i] : 0.0f;
+        qa[kk] = split_part8(e, lo_row);
+    }
+
+    // online softmax state of heads 4 (qd & 1) + i (the same in all 16 lanes of a row)
+    float m_run[4], l_run[4];
+    f32x4_t acc[DB];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        m_run[i] = -INFINITY;
+        l_run[i] = 0.0f;
+    }
+#pragma unroll
+    for (int db = 0; db < DB; ++db) acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    for (int s = 0; s < steps; ++s) {
+        const int p0 = 32 * s;
+        // ---- scores of positions p0 + 16 j + n ----
+        f32x4_t d[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            d[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kk = 0; kk < KS; ++kk)
+                d[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    qa[kk], __builtin_bit_cast(bf16x8_t, kr[j][kk]), d[j], 0, 0, 0);
+        }
+        load_k(min(p0 + 32, 32 * (steps - 1)));  // the next step's rows (the last step reloads its own)
+        float pv[2][4], f[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float sc0 = add_halves(d[0][i]) * scale, sc1 = add_halves(d[1][i]) * scale;
+            if (p0 + n >= cnt) sc0 = -INFINITY;
+            if (p0 + 16 + n >= cnt) sc1 = -INFINITY;
+            const float mn = fmaxf(m_run[i], row16_max(fmaxf(sc0, sc1)));
+            f[i] = expf(m_run[i] - mn);  // 0 on the first step
+            pv[0][i] = expf(sc0 - mn);
+            pv[1][i] = expf(sc1 - mn);
+            l_run[i] = fmaf(l_run[i], f[i], group_sum<16>(pv[0][i] + pv[1][i]));
+            m_run[i] = mn;
+        }
+        // ---- P and V into LDS (the same wave reads them back) ----
+        if (qd < 2) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) ps[4 * qd + i][16 * j + n] = pv[j][i];
+        }
+#pragma unroll
+        for (int i = 0; i < NVI; ++i)
+            *reinterpret_cast<uint4*>(vs + (i * RPI + lane / LPR) * VST + (lane % LPR) * 8) =
+                i < NVI / 2 ? va[i] : vb[i - NVI / 2];
+        load_v(min(p0 + 32, 32 * (steps - 1)));
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the LDS stores are done
+        __builtin_amdgcn_wave_barrier();
+        // ---- P.V ----
+        float pr[8];
+        {
+            const float4 a = reinterpret_cast<const float4*>(&ps[hq][8 * qd])[0];
+            const float4 c = reinterpret_cast<const float4*>(&ps[hq][8 * qd])[1];
+            pr[0] = a.x; pr[1] = a.y; pr[2] = a.z; pr[3] = a.w;
+            pr[4] = c.x; pr[5] = c.y; pr[6] = c.z; pr[7] = c.w;
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) pr[i] = real_row ? pr[i] : 0.0f;
+        const bf16x8_t pa = split_part8(pr, lo_row);
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+            unsigned w[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                w[j] = (unsigned)vs[(8 * qd + 2 * j) * VST + 16 * db + n] |
+                       ((unsigned)vs[(8 * qd + 2 * j + 1) * VST + 16 * db + n] << 16);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[db][i] *= f[i];
+            acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                pa, __builtin_bit_cast(bf16x8_t, make_uint4(w[0], w[1], w[2], w[3])), acc[db], 0,
+                0, 0);
+        }
+        // the next step rewrites ps and vs only after these reads have returned
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+        __builtin_amdgcn_wave_barrier();
+    }
+
+    // ---- chunk record [m, l, -, -, o[HD]] of heads 4 qd + i (lanes qd < 2) ----
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int h = 4 * qd + i;
+        float* rec = work + (((size_t)b * n_q + g * G + min(h, G - 1)) * nchunks + chunk) * (HD + 4);
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+            const float o = add_halves(acc[db][i]);
+            if (qd < 2 && h < G) rec[4 + 16 * db + n] = o;
+        }
+        if (qd < 2 && h < G && n == 0) {
+            rec[0] = m_run[i];
+            rec[1] = l_run[i];
+        }
+    }
+}
+
 // Sub-tile of positions held in registers per workgroup: 64 rows at hd 128,
 // 32 at hd 256 (the K and V rows of a sub-tile are requested together).
 template <int HD>
@@ -597,6 +823,27 @@ int launch_g(int G, const float* q, int ldq, int qhs, const float* qn, const flo
     QLM_ATTN_G(4)
     QLM_ATTN_G(8)
 #undef QLM_ATTN_G
+    return QLM_ERR_SHAPE;
+}
+
+// k_attn_mx over bf16 caches: nch chunks of 32 * spw positions per
+// (sequence, kv head), one wave each.
+template <int HD>
+int launch_mx(int G, const float* q, int ldq, const uint16_t* kc, const uint16_t* vc, int max_seq,
+              int n_kv, int ctx, float* work, int nch, int n_q, int B, int spw, hipStream_t s) {
+    const dim3 grid(nch, n_kv, B);
+    const float scale = 1.0f / sqrtf((float)HD);
+#define QLM_ATTN_MX(GG)                                                                         \
+    if (G == GG) {                                                                              \
+        hipLaunchKernelGGL((k_attn_mx<HD, GG>), grid, dim3(QLM_WAVE), 0, s, q, ldq, kc, vc,     \
+                           max_seq, n_kv, ctx, work, nch, n_q, scale, spw);                     \
+        return qlm_launch_status();                                                             \
+    }
+    QLM_ATTN_MX(1)
+    QLM_ATTN_MX(2)
+    QLM_ATTN_MX(4)
+    QLM_ATTN_MX(8)
+#undef QLM_ATTN_MX
     return QLM_ERR_SHAPE;
 }
 
@@ -682,10 +929,8 @@ int attention_launch_nt(const float* q, const void* k_cache, const void* v_cache
                   G, q, ldq, HDV, nullptr, nullptr, nullptr, nullptr, 0,
                   (float*)const_cast<void*>(k_cache), (float*)const_cast<void*>(v_cache), max_seq,
                   n_kv, nullptr, ctx, 0, (size_t)max_seq, w, nch, n_q, B, st)
-            : launch_g<HDV, NT, uint16_t, false>(
-                  G, q, ldq, HDV, nullptr, nullptr, nullptr, nullptr, 0,
-                  (uint16_t*)const_cast<void*>(k_cache), (uint16_t*)const_cast<void*>(v_cache),
-                  max_seq, n_kv, nullptr, ctx, 0, (size_t)max_seq, w, nch, n_q, B, st);
+            : launch_mx<HDV>(G, q, ldq, (const uint16_t*)k_cache, (const uint16_t*)v_cache,
+                             max_seq, n_kv, ctx, w, nch, n_q, B, chunk_len(HDV, NT) / 32, st);
     if (rc != QLM_OK) return rc;
     return launch_combine<HDV>(w, nch, chunk_len(HDV, NT), max_seq, nullptr, ctx, 0, nullptr, 0,
                                0, out, ldq, n_q, B, st);
