@@ -387,7 +387,10 @@ int qlm_gqa_prefill(float* qkv, int ldqkv, const float* q_norm, const float* k_n
 
 /* Isolated attention core (no norm/RoPE/write): out[b, h] = softmax(q.K^T *
  * scale) . V over the first ctx positions of a [B, max_seq, n_kv, hd] cache,
- * kv_dtype 0 = fp32, 1 = bf16. q, out are [B, n_q, hd] fp32. */
+ * kv_dtype 0 = fp32, 1 = bf16. q, out are [B, n_q, hd] fp32. A bf16 cache
+ * runs on the bf16 matrix cores (q and the probabilities split into bf16
+ * hi + lo, to 2^-18 of each; products and sums in fp32), an fp32 cache on
+ * the vector ALUs. */
 int qlm_attention_decode(const float* q, const void* k_cache, const void* v_cache,
                          int kv_dtype, int max_seq, int ctx, float* out, int B, int n_q,
                          int n_kv, int hd, void* work, void* stream);
@@ -398,11 +401,13 @@ int qlm_attention_decode(const float* q, const void* k_cache, const void* v_cach
  * as qlm_attention_decode, without `work`: the chunk records live in a
  * static device array of QLM_ATTENTION_NOALLOC_MAX_BYTES (32 MiB) that every
  * GPU running the library holds until the process ends. A call needs
- * qlm_attention_decode_noalloc_bytes(B, n_q, hd, ctx) bytes of it
- * (B * n_q * ceil(ctx / C) * (hd + 4) * 4 for the chunk length C that
- * qlm_attention_decode picks: 64 to 512 positions at hd 128, 32 to 256 at
- * hd 256) and returns QLM_ERR_SCRATCH, launching nothing, when that
- * exceeds the maximum. The call allocates nothing; its first call on a
+ * qlm_attention_decode_noalloc_bytes(B, n_q, hd, ctx) bytes of it (B * n_q
+ * * R * (hd + 4) * 4 with R chunk records a head: ceil(ctx / C) for the
+ * chunk length C qlm_attention_decode picks for an fp32 cache, 64 to 512
+ * positions at hd 128 and 32 to 256 at hd 256, or at most min(256,
+ * ceil(ctx / 64)) at hd 128 and min(256, ceil(ctx / 32)) at hd 256 for a
+ * bf16 cache; the larger of the two) and returns QLM_ERR_SCRATCH, launching
+ * nothing, when the call's records exceed the maximum. The call allocates nothing; its first call on a
  * device looks the array's address up once. Every call on one GPU shares
  * that GPU's array: calls that may overlap on one GPU (different streams,
  * different host threads) race, so order them on one stream. Nothing in the

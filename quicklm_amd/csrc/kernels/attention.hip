@@ -376,12 +376,14 @@ __global__ __launch_bounds__(kThreads) void k_attn(
 constexpr int kCombineThreads = 256;
 constexpr int kCombineTile = 256;
 
-template <int HD>
+template <int HD, int CS>
 __global__ __launch_bounds__(kCombineThreads) void k_attn_combine(
     const float* __restrict__ work, int nchunks, int CH, int max_seq, const int* __restrict__ pos,
     int ctx, int pstep, const float* __restrict__ gate, int ldg, int ghs, float* __restrict__ out,
     int ldo, int n_q) {
-    constexpr int C4 = HD / 4;                    // float4 columns
+    // CS workgroups (blockIdx.z) split a head's columns: few (head,
+    // sequence) pairs would otherwise leave most of the GPU idle
+    constexpr int C4 = HD / 4 / CS;               // float4 columns of this workgroup
     constexpr int NG = kCombineThreads / C4;      // chunk groups
     constexpr int KB = 8;                         // records per thread per request batch
     constexpr int RS = HD + 4;                    // record stride (floats)
@@ -390,6 +392,7 @@ __global__ __launch_bounds__(kCombineThreads) void k_attn_combine(
     __shared__ float red[kCombineThreads / QLM_WAVE];
     const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
     const int c4 = tid % C4, cg = tid / C4;
+    const int cb = blockIdx.z * C4;  // first float4 column of this workgroup
     const int L = min(pos ? pos[b] + 1 : ctx + pstep * b, max_seq);
     const int nc = min(nchunks, (L + CH - 1) / CH);
     const int last = max(nc, 1) - 1;  // clamp target of the unconditional loads
@@ -397,14 +400,15 @@ __global__ __launch_bounds__(kCombineThreads) void k_attn_combine(
 
     // ---- first-pass operands, all requested before any is used ----
     auto rec4 = [&](int c) {  // float4 column c4 of record c (clamped into the context)
-        return reinterpret_cast<const float4*>(base + (size_t)min(c, last) * RS + 4)[c4];
+        return reinterpret_cast<const float4*>(base + (size_t)min(c, last) * RS + 4)[cb + c4];
     };
     float mc = base[(size_t)min(tid, last) * RS];
     float lc = base[(size_t)min(tid, last) * RS + 1];
     float4 ov[KB];
 #pragma unroll
     for (int k = 0; k < KB; ++k) ov[k] = rec4(cg + NG * k);
-    const float* gp = (gate ? gate + (size_t)b * ldg + (size_t)h * ghs + HD : base + 4) + c4 * 4;
+    const float* gp = (gate ? gate + (size_t)b * ldg + (size_t)h * ghs + HD : base + 4) +
+                      (cb + c4) * 4;
     const float gg[4] = {gp[0], gp[1], gp[2], gp[3]};
 
     float M = -INFINITY, lsum = 0.0f;
@@ -475,7 +479,7 @@ __global__ __launch_bounds__(kCombineThreads) void k_attn_combine(
 #pragma unroll
             for (int i = 0; i < 4; ++i) r[i] *= 1.0f / (1.0f + expf(-gg[i]));
         }
-        float* dst = out + (size_t)b * ldo + (size_t)h * HD + c4 * 4;
+        float* dst = out + (size_t)b * ldo + (size_t)h * HD + (cb + c4) * 4;
 #pragma unroll
         for (int i = 0; i < 4; ++i) dst[i] = r[i];
     }
@@ -549,7 +553,7 @@ __global__ __launch_bounds__(kThreads) void k_gqa_prep_rows(
 // ---- bf16 K/V on the matrix cores (the isolated attention, kv_dtype 1) ----
 //
 // One wave per workgroup owns a chunk of 32 * spw positions of one (kv head
-// g, sequence b) and walks it in steps of 32 positions, with its own online
+// g, sequence b) and walks it in steps of 16 positions, with its own online
 // softmax; the chunk leaves k_attn's record [m, l, -, -, o[HD]] per query
 // head, merged by k_attn_combine. Both products run on
 // v_mfma_f32_16x16x32_bf16 (lane l = 16 qd + n; A lane: row n, k-slice qd;
@@ -559,15 +563,18 @@ __global__ __launch_bounds__(kThreads) void k_gqa_prep_rows(
 //           heads >= G zero), B = 16 K rows as stored (bf16 is exact), so
 //           one product gives both halves and s = D[h] + D[h + 8] (one lane
 //           swap between the wave halves);
-//   P.V     A = the probabilities, hi rows 0..7 and lo rows 8..15 again
-//           (through a 1 KB LDS transpose), B = 32 V rows x 16 columns, read
+//   P.V     on v_mfma_f32_16x16x16_bf16: A = the probabilities, hi rows
+//           0..7 and lo rows 8..15 again (through a 512-byte LDS
+//           transpose), B = 16 V rows x 16 columns, read
 //           column-wise from an LDS copy of the step's V rows (the
 //           reduction runs over positions, which lie 512 bytes apart in the
 //           cache). The accumulator rows are the heads' hi and lo halves,
 //           added once at the end.
 // The next step's K rows are requested as soon as the scores have consumed
-// the current ones, its V rows once the current ones are in LDS; positions
-// past the chunk are clamped onto its last row (their scores are -inf).
+// the current ones, its V rows once the current ones are in LDS (the last
+// step requests nothing: a wave cannot end before its loads return);
+// positions past the chunk are clamped onto its last row (their scores are
+// -inf).
 // Arithmetic intensity is n_q / n_kv flops per cache byte (8 at the 16 / 2
 // heads of the long-context workload): on the vector ALUs the dot products
 // and their reductions bound the old kernel at ~2.3 TB/s; here the matrix
@@ -611,7 +618,7 @@ __device__ __forceinline__ float add_halves(float d) {
 }
 
 template <int HD, int G>
-__global__ __launch_bounds__(QLM_WAVE) void k_attn_mx(
+__global__ __launch_bounds__(QLM_WAVE, 2) void k_attn_mx(
     const float* __restrict__ q, int ldq, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, int max_seq, int n_kv, int ctx, float* __restrict__ work,
     int nchunks, int n_q, float scale, int spw) {
@@ -621,54 +628,58 @@ __global__ __launch_bounds__(QLM_WAVE) void k_attn_mx(
     constexpr int VST = HD + 8;          // LDS row stride of the V copy (bf16): +16 bytes
     constexpr int LPR = HD / 8;          // lanes per V row (16 bytes each)
     constexpr int RPI = QLM_WAVE / LPR;  // V rows per load instruction
-    constexpr int NVI = 32 / RPI;        // V loads per lane per step
-    __shared__ __align__(16) uint16_t vs[32 * VST];
-    __shared__ __align__(16) float ps[8][32];
+    constexpr int NVI = 16 / RPI;        // V loads per lane per step
+    typedef short s16x4 __attribute__((ext_vector_type(4)));
+    __shared__ __align__(16) uint16_t vs[16 * VST];
+    __shared__ __align__(16) float ps[8][16];
 
     const int lane = threadIdx.x, qd = lane >> 4, n = lane & 15;
     const int chunk = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
     const int start = chunk * 32 * spw;
     const int cnt = min(32 * spw, ctx - start);
     if (cnt <= 0) return;
-    const int steps = (cnt + 31) / 32;
+    const int steps = (cnt + 15) / 16;
     // cache row (b, position start, head g); position p of the chunk adds p * n_kv rows
     const uint16_t* kbase = kc + (((size_t)b * max_seq + start) * n_kv + g) * HD;
     const uint16_t* vbase = vc + (((size_t)b * max_seq + start) * n_kv + g) * HD;
     const size_t pstride = (size_t)n_kv * HD;
 
-    uint4 kr[2][KS], va[NVI / 2], vb[NVI / 2];  // V rows: two arrays (one 256-byte
-                                                 // array is left in scratch memory)
+    // (vector types, not the uint4 struct: an aggregate copy into LDS keeps
+    // the array in scratch memory)
+    typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+    u32x4 kr[KS], vr[NVI];
     auto load_k = [&](int p0) {
+        const int p = min(p0 + n, cnt - 1);
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int p = min(p0 + 16 * j + n, cnt - 1);
-#pragma unroll
-            for (int kk = 0; kk < KS; ++kk)
-                kr[j][kk] = *reinterpret_cast<const uint4*>(kbase + p * pstride + 32 * kk + 8 * qd);
-        }
+        for (int kk = 0; kk < KS; ++kk)
+            kr[kk] = *reinterpret_cast<const u32x4*>(kbase + p * pstride + 32 * kk + 8 * qd);
     };
     auto load_v = [&](int p0) {
 #pragma unroll
         for (int i = 0; i < NVI; ++i) {
             const int p = min(p0 + i * RPI + lane / LPR, cnt - 1);
-            const uint4 v = *reinterpret_cast<const uint4*>(vbase + p * pstride + (lane % LPR) * 8);
-            if (i < NVI / 2)
-                va[i] = v;
-            else
-                vb[i - NVI / 2] = v;
+            vr[i] = *reinterpret_cast<const u32x4*>(vbase + p * pstride + (lane % LPR) * 8);
         }
     };
-    // ---- the first step's rows, then the query operand ----
-    load_k(0);
-    load_v(0);
+    // ---- the query operand's rows, then the first step's K and V rows, all
+    // requested before any is used (left to itself the compiler waits for
+    // each query load in turn, ahead of the K/V requests) ----
     const int hq = n & 7;
     const bool lo_row = n >= 8, real_row = hq < G;
     const float* qrow = q + (size_t)b * ldq + (size_t)(g * G + min(hq, G - 1)) * HD;
+    float4 qraw[KS][2];
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) {
+        qraw[kk][0] = reinterpret_cast<const float4*>(qrow + 32 * kk + 8 * qd)[0];
+        qraw[kk][1] = reinterpret_cast<const float4*>(qrow + 32 * kk + 8 * qd)[1];
+    }
+    load_k(0);
+    load_v(0);
+    __builtin_amdgcn_sched_barrier(0);
     bf16x8_t qa[KS];
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk) {
-        const float4 a = reinterpret_cast<const float4*>(qrow + 32 * kk + 8 * qd)[0];
-        const float4 c = reinterpret_cast<const float4*>(qrow + 32 * kk + 8 * qd)[1];
+        const float4 a = qraw[kk][0], c = qraw[kk][1];
         float e[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
 #pragma unroll
         for (int i = 0; i < 8; ++i) e[i] = real_row ? e[i] : 0.0f;
@@ -687,68 +698,60 @@ __global__ __launch_bounds__(QLM_WAVE) void k_attn_mx(
     for (int db = 0; db < DB; ++db) acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
     for (int s = 0; s < steps; ++s) {
-        const int p0 = 32 * s;
-        // ---- scores of positions p0 + 16 j + n ----
-        f32x4_t d[2];
+        const int p0 = 16 * s;
+        const bool more = s + 1 < steps;  // wave-uniform
+        // ---- scores of positions p0 + n ----
+        f32x4_t d = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            d[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int kk = 0; kk < KS; ++kk)
-                d[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                    qa[kk], __builtin_bit_cast(bf16x8_t, kr[j][kk]), d[j], 0, 0, 0);
-        }
-        load_k(min(p0 + 32, 32 * (steps - 1)));  // the next step's rows (the last step reloads its own)
-        float pv[2][4], f[4];
+        for (int kk = 0; kk < KS; ++kk)
+            d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[kk], __builtin_bit_cast(bf16x8_t, kr[kk]),
+                                                        d, 0, 0, 0);
+        if (more) load_k(p0 + 16);  // the next step's rows
+        float pv[4], f[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            float sc0 = add_halves(d[0][i]) * scale, sc1 = add_halves(d[1][i]) * scale;
-            if (p0 + n >= cnt) sc0 = -INFINITY;
-            if (p0 + 16 + n >= cnt) sc1 = -INFINITY;
-            const float mn = fmaxf(m_run[i], row16_max(fmaxf(sc0, sc1)));
+            float sc = add_halves(d[i]) * scale;
+            if (p0 + n >= cnt) sc = -INFINITY;
+            const float mn = fmaxf(m_run[i], row16_max(sc));
             f[i] = expf(m_run[i] - mn);  // 0 on the first step
-            pv[0][i] = expf(sc0 - mn);
-            pv[1][i] = expf(sc1 - mn);
-            l_run[i] = fmaf(l_run[i], f[i], group_sum<16>(pv[0][i] + pv[1][i]));
+            pv[i] = expf(sc - mn);
+            l_run[i] = fmaf(l_run[i], f[i], group_sum<16>(pv[i]));
             m_run[i] = mn;
         }
         // ---- P and V into LDS (the same wave reads them back) ----
         if (qd < 2) {
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) ps[4 * qd + i][16 * j + n] = pv[j][i];
+            for (int i = 0; i < 4; ++i) ps[4 * qd + i][n] = pv[i];
         }
 #pragma unroll
         for (int i = 0; i < NVI; ++i)
-            *reinterpret_cast<uint4*>(vs + (i * RPI + lane / LPR) * VST + (lane % LPR) * 8) =
-                i < NVI / 2 ? va[i] : vb[i - NVI / 2];
-        load_v(min(p0 + 32, 32 * (steps - 1)));
+            *reinterpret_cast<u32x4*>(vs + (i * RPI + lane / LPR) * VST + (lane % LPR) * 8) = vr[i];
+        if (more) load_v(p0 + 16);
         __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the LDS stores are done
         __builtin_amdgcn_wave_barrier();
-        // ---- P.V ----
-        float pr[8];
-        {
-            const float4 a = reinterpret_cast<const float4*>(&ps[hq][8 * qd])[0];
-            const float4 c = reinterpret_cast<const float4*>(&ps[hq][8 * qd])[1];
-            pr[0] = a.x; pr[1] = a.y; pr[2] = a.z; pr[3] = a.w;
-            pr[4] = c.x; pr[5] = c.y; pr[6] = c.z; pr[7] = c.w;
-        }
+        // ---- P.V on v_mfma_f32_16x16x16_bf16 (lane: row / column n, k = 4 qd .. +3) ----
+        const float4 pq = reinterpret_cast<const float4*>(&ps[hq][4 * qd])[0];
+        float pr[4] = {pq.x, pq.y, pq.z, pq.w};
+        unsigned pw[2];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) pr[i] = real_row ? pr[i] : 0.0f;
-        const bf16x8_t pa = split_part8(pr, lo_row);
+        for (int i = 0; i < 2; ++i) {
+            const float a = real_row ? pr[2 * i] : 0.0f, c = real_row ? pr[2 * i + 1] : 0.0f;
+            const __bf16 ha = (__bf16)a, hc = (__bf16)c;
+            pw[i] = lo_row ? (bf16_bits(a - (float)ha) | (bf16_bits(c - (float)hc) << 16))
+                           : ((unsigned)__builtin_bit_cast(unsigned short, ha) |
+                              ((unsigned)__builtin_bit_cast(unsigned short, hc) << 16));
+        }
+        const s16x4 pa = __builtin_bit_cast(s16x4, make_uint2(pw[0], pw[1]));
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
-            unsigned w[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                w[j] = (unsigned)vs[(8 * qd + 2 * j) * VST + 16 * db + n] |
-                       ((unsigned)vs[(8 * qd + 2 * j + 1) * VST + 16 * db + n] << 16);
+            const unsigned w0 = (unsigned)vs[(4 * qd) * VST + 16 * db + n] |
+                                ((unsigned)vs[(4 * qd + 1) * VST + 16 * db + n] << 16);
+            const unsigned w1 = (unsigned)vs[(4 * qd + 2) * VST + 16 * db + n] |
+                                ((unsigned)vs[(4 * qd + 3) * VST + 16 * db + n] << 16);
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc[db][i] *= f[i];
-            acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                pa, __builtin_bit_cast(bf16x8_t, make_uint4(w[0], w[1], w[2], w[3])), acc[db], 0,
-                0, 0);
+            acc[db] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
+                pa, __builtin_bit_cast(s16x4, make_uint2(w0, w1)), acc[db], 0, 0, 0);
         }
         // the next step rewrites ps and vs only after these reads have returned
         __builtin_amdgcn_s_waitcnt(0xc07f);
@@ -847,14 +850,29 @@ int launch_mx(int G, const float* q, int ldq, const uint16_t* kc, const uint16_t
     return QLM_ERR_SHAPE;
 }
 
+// cs: workgroups per (head, sequence), each merging HD / cs columns (1, 2 or 4)
 template <int HD>
 int launch_combine(const float* work, int nch, int ch, int max_seq, const int* pos, int ctx,
                    int pstep, const float* gate, int ldg, int ghs, float* out, int ldo, int n_q,
-                   int B, hipStream_t s) {
-    hipLaunchKernelGGL(k_attn_combine<HD>, dim3(n_q, B), dim3(kCombineThreads), 0, s, work, nch,
-                       ch, max_seq,
-                       pos, ctx, pstep, gate, ldg, ghs, out, ldo, n_q);
-    return qlm_launch_status();
+                   int B, hipStream_t s, int cs = 1) {
+#define QLM_COMBINE(CSV)                                                                        \
+    if (cs == CSV) {                                                                            \
+        hipLaunchKernelGGL((k_attn_combine<HD, CSV>), dim3(n_q, B, CSV), dim3(kCombineThreads), \
+                           0, s, work, nch, ch, max_seq, pos, ctx, pstep, gate, ldg, ghs, out,  \
+                           ldo, n_q);                                                           \
+        return qlm_launch_status();                                                             \
+    }
+    QLM_COMBINE(1)
+    QLM_COMBINE(2)
+    QLM_COMBINE(4)
+#undef QLM_COMBINE
+    return QLM_ERR_ARG;
+}
+
+// column split of the isolated attention's merge: ~256 workgroups or more
+int combine_splits(int n_q, int B) {
+    const int pairs = n_q * B;
+    return pairs >= 256 ? 1 : (pairs >= 128 ? 2 : 4);
 }
 
 }  // namespace
@@ -918,34 +936,82 @@ int check_attention_args(const float* q, const void* k_cache, const void* v_cach
 }
 
 template <int HDV, int NT>
-int attention_launch_nt(const float* q, const void* k_cache, const void* v_cache, int kv_dtype,
-                        int max_seq, int ctx, float* out, int B, int n_q, int n_kv, float* w,
-                        int nch, hipStream_t st) {
+int attention_launch_nt(const float* q, const float* k_cache, const float* v_cache, int max_seq,
+                        int ctx, float* out, int B, int n_q, int n_kv, float* w, int nch,
+                        hipStream_t st) {
     const int G = n_q / n_kv;
     const int ldq = n_q * HDV;
-    const int rc =
-        kv_dtype == 0
-            ? launch_g<HDV, NT, float, false>(
-                  G, q, ldq, HDV, nullptr, nullptr, nullptr, nullptr, 0,
-                  (float*)const_cast<void*>(k_cache), (float*)const_cast<void*>(v_cache), max_seq,
-                  n_kv, nullptr, ctx, 0, (size_t)max_seq, w, nch, n_q, B, st)
-            : launch_mx<HDV>(G, q, ldq, (const uint16_t*)k_cache, (const uint16_t*)v_cache,
-                             max_seq, n_kv, ctx, w, nch, n_q, B, chunk_len(HDV, NT) / 32, st);
+    const int rc = launch_g<HDV, NT, float, false>(
+        G, q, ldq, HDV, nullptr, nullptr, nullptr, nullptr, 0, const_cast<float*>(k_cache),
+        const_cast<float*>(v_cache), max_seq, n_kv, nullptr, ctx, 0, (size_t)max_seq, w, nch, n_q,
+        B, st);
     if (rc != QLM_OK) return rc;
     return launch_combine<HDV>(w, nch, chunk_len(HDV, NT), max_seq, nullptr, ctx, 0, nullptr, 0,
-                               0, out, ldq, n_q, B, st);
+                               0, out, ldq, n_q, B, st, combine_splits(n_q, B));
 }
 
-// The two launches of the isolated attention with nt sub-tiles per chunk
-// and nch chunk records per (sequence, query head) in w (nch chunks of
-// chunk_len(hd, nt) positions must cover ctx).
+// 32-position units per wave of the bf16 matrix-core attention: the largest
+// power of two up to 32 that keeps >= 1024 waves, then raised until a head
+// has <= 256 chunk records (the merge's cost grows with them); >= 2 at hd
+// 128. Measured on MI355X at 16 q / 2 kv heads, hd 256 (graph replays):
+// 16 x 32768 positions 215 us at 8 units, 193 us at 32; 16 x 8192 54 us at
+// 4, 49 us at 8; 1 x 32768 27 us at 2 (512 records), 23 us at 4.
+int mx_spw(int B, int n_kv, int hd, int ctx) {
+    int spw = hd == 128 ? 2 : 1;
+    while (spw < 32 && (long long)B * n_kv * nchunks_for(ctx, 64 * spw) >= 1024) spw *= 2;
+    while (spw < (1 << 20) && nchunks_for(ctx, 32 * spw) > 256) spw *= 2;
+    return spw;
+}
+
+// Chunking of one isolated attention call: chunk length and records per
+// (sequence, query head). fp32 caches take k_attn (nt sub-tiles a chunk),
+// bf16 caches k_attn_mx (32 * spw positions a wave). Either fits the
+// workspace of qlm_gqa_workspace_bytes(B, n_q, hd, max_seq) for ctx <=
+// max_seq: at most ceil(ctx / 32) records at hd 256 and ceil(ctx / 64) at
+// hd 128.
+struct IsoPlan {
+    int unit;  // nt (fp32) or spw (bf16)
+    int ch, nch;
+};
+IsoPlan iso_plan(int kv_dtype, int B, int n_kv, int hd, int ctx) {
+    IsoPlan p;
+    if (kv_dtype == 0) {
+        p.unit = isolated_nt(B, hd, ctx);
+        p.ch = chunk_len(hd, p.unit);
+    } else {
+        p.unit = mx_spw(B, n_kv, hd, ctx);
+        p.ch = 32 * p.unit;
+    }
+    p.nch = nchunks_for(ctx, p.ch);
+    return p;
+}
+
+// The two launches of the isolated attention under plan p, records in w.
 int attention_launch(const float* q, const void* k_cache, const void* v_cache, int kv_dtype,
                      int max_seq, int ctx, float* out, int B, int n_q, int n_kv, int hd,
-                     float* w, int nt, int nch, hipStream_t st) {
+                     float* w, const IsoPlan& p, hipStream_t st) {
+    const int G = n_q / n_kv;
+    if (kv_dtype == 1) {
+        const uint16_t* kc = static_cast<const uint16_t*>(k_cache);
+        const uint16_t* vc = static_cast<const uint16_t*>(v_cache);
+        int rc = hd == 128 ? launch_mx<128>(G, q, n_q * hd, kc, vc, max_seq, n_kv, ctx, w, p.nch,
+                                            n_q, B, p.unit, st)
+                           : launch_mx<256>(G, q, n_q * hd, kc, vc, max_seq, n_kv, ctx, w, p.nch,
+                                            n_q, B, p.unit, st);
+        if (rc != QLM_OK) return rc;
+        return hd == 128 ? launch_combine<128>(w, p.nch, p.ch, max_seq, nullptr, ctx, 0, nullptr,
+                                               0, 0, out, n_q * hd, n_q, B, st,
+                                               combine_splits(n_q, B))
+                         : launch_combine<256>(w, p.nch, p.ch, max_seq, nullptr, ctx, 0, nullptr,
+                                               0, 0, out, n_q * hd, n_q, B, st,
+                                               combine_splits(n_q, B));
+    }
+    const float* kc = static_cast<const float*>(k_cache);
+    const float* vc = static_cast<const float*>(v_cache);
 #define QLM_ISO(HDV, NTV)                                                                       \
-    if (hd == HDV && nt == NTV)                                                                 \
-        return attention_launch_nt<HDV, NTV>(q, k_cache, v_cache, kv_dtype, max_seq, ctx, out, B, \
-                                             n_q, n_kv, w, nch, st);
+    if (hd == HDV && p.unit == NTV)                                                             \
+        return attention_launch_nt<HDV, NTV>(q, kc, vc, max_seq, ctx, out, B, n_q, n_kv, w, p.nch, \
+                                             st);
     QLM_ISO(128, 1) QLM_ISO(128, 2) QLM_ISO(128, 4) QLM_ISO(128, 8)
     QLM_ISO(256, 1) QLM_ISO(256, 2) QLM_ISO(256, 4) QLM_ISO(256, 8)
 #undef QLM_ISO
@@ -998,15 +1064,21 @@ extern "C" int qlm_attention_decode(const float* q, const void* k_cache, const v
     // records laid out for the positions the launch attends to (ctx): at
     // most qlm_gqa_workspace_bytes(B, n_q, hd, max_seq), the one-sub-tile
     // layout over max_seq
-    const int nt = isolated_nt(B, hd, ctx);
     return attention_launch(q, k_cache, v_cache, kv_dtype, max_seq, ctx, out, B, n_q, n_kv, hd,
-                            reinterpret_cast<float*>(work), nt,
-                            nchunks_for(ctx, chunk_len(hd, nt)), as_stream(stream));
+                            reinterpret_cast<float*>(work), iso_plan(kv_dtype, B, n_kv, hd, ctx),
+                            as_stream(stream));
 }
 
 extern "C" size_t qlm_attention_decode_noalloc_bytes(int B, int n_q, int hd, int ctx) {
     if (B <= 0 || n_q <= 0 || (hd != 128 && hd != 256) || ctx <= 0) return 0;
-    return records_bytes(B, n_q, hd, ctx, isolated_nt(B, hd, ctx));
+    // the larger of the two caches' layouts; the bf16 one depends on n_kv
+    // only through a count of waves, and has at most min(256, ceil(ctx /
+    // 32 * spw)) records with spw >= 1 (2 at hd 128)
+    const int nf = nchunks_for(ctx, chunk_len(hd, isolated_nt(B, hd, ctx)));
+    const int nb0 = nchunks_for(ctx, hd == 128 ? 64 : 32);
+    const int nb = nb0 < 256 ? nb0 : 256;
+    const int n = nf > nb ? nf : nb;
+    return (size_t)B * n_q * n * (hd + 4) * sizeof(float);
 }
 
 extern "C" int qlm_attention_decode_noalloc(const float* q, const void* k_cache,
@@ -1017,13 +1089,13 @@ extern "C" int qlm_attention_decode_noalloc(const float* q, const void* k_cache,
                                   hd);
     if (rc != QLM_OK) return rc;
     // records for the chunks that cover ctx positions only (the grid stops there)
-    const int nt = isolated_nt(B, hd, ctx);
-    if (records_bytes(B, n_q, hd, ctx, nt) > kScratchBytes) return QLM_ERR_SCRATCH;
+    const IsoPlan p = iso_plan(kv_dtype, B, n_kv, hd, ctx);
+    if ((size_t)B * n_q * p.nch * (hd + 4) * sizeof(float) > kScratchBytes) return QLM_ERR_SCRATCH;
     float* w = nullptr;
     rc = scratch_ptr(&w);
     if (rc != QLM_OK) return rc;
     return attention_launch(q, k_cache, v_cache, kv_dtype, max_seq, ctx, out, B, n_q, n_kv, hd,
-                            w, nt, nchunks_for(ctx, chunk_len(hd, nt)), as_stream(stream));
+                            w, p, as_stream(stream));
 }
 
 extern "C" size_t qlm_gqa_prefill_workspace_bytes(int n_q, int hd, int max_seq) {

@@ -67,14 +67,19 @@ def test_noalloc_attention_rejects_oversize_on_host():
     cap = 32 << 20
     # B * n_q * ceil(ctx / C) * (hd + 4) * 4 bytes: C = 256 positions for 16
     # sequences of 32768 at hd 256 (128 chunks), 64 for one of 300 at hd 128
-    assert L.qlm_attention_decode_noalloc_bytes(16, 16, 256, 32768) == 16 * 16 * 128 * 260 * 4
+    # the bf16 layout bounds it here: min(256, 32768 / 32) records a head
+    assert L.qlm_attention_decode_noalloc_bytes(16, 16, 256, 32768) == 16 * 16 * 256 * 260 * 4
     assert L.qlm_attention_decode_noalloc_bytes(1, 16, 128, 300) == 16 * 5 * 132 * 4
     assert L.qlm_attention_decode_noalloc_bytes(0, 16, 128, 300) == 0
     assert L.qlm_attention_decode_noalloc_bytes(1, 16, 64, 300) == 0
     assert L.qlm_attention_decode_noalloc_bytes(16, 16, 256, 32768) > cap
     fake = 4096  # never dereferenced: the checks fire first
-    assert L.qlm_attention_decode_noalloc(fake, fake, fake, 1, 32768, 32768, fake, 16, 16, 2, 256,
+    # fp32 cache: 16 x 16 heads x 128 records of 260 floats = 34 MB
+    assert L.qlm_attention_decode_noalloc(fake, fake, fake, 0, 32768, 32768, fake, 16, 16, 2, 256,
                                           None) == -4
+    # bf16 cache: 128 x 16 heads x 32 records (1024 positions each) = 68 MB
+    assert L.qlm_attention_decode_noalloc(fake, fake, fake, 1, 32768, 32768, fake, 128, 16, 2,
+                                          256, None) == -4
     assert b"static device scratch" in L.qlm_error_string(-4)
     assert L.qlm_attention_decode_noalloc(fake, fake, fake, 1, 100, 200, fake, 1, 16, 2, 256,
                                           None) == -1  # ctx > max_seq

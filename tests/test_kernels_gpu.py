@@ -854,6 +854,28 @@ def test_attention_decode(hip, orc, rng, kv, ctx):
                        np.broadcast_to(v[:, 0, :1], (B, n_q // n_kv, hd))) < 1e-6
 
 
+@pytest.mark.parametrize("hd,n_q,n_kv", [(128, 8, 8), (128, 8, 4), (128, 16, 4), (256, 4, 2)])
+@pytest.mark.parametrize("ctx", [1, 17, 1000, 3000])
+def test_attention_decode_bf16_shapes(hip, orc, rng, hd, n_q, n_kv, ctx):
+    """The bf16 matrix-core attention at every group size (1, 2, 4 query
+    heads a kv head; 8 is the config-3 shape above), both head dims, and
+    contexts that end inside a 16-position step and a chunk, over 3
+    sequences of a cache longer than the context (max_seq 3072)."""
+    B, max_seq = 3, 3072
+    q = rng.standard_normal((B, n_q, hd)).astype(np.float32)
+    kb = bf16_bits(rng.standard_normal((B, max_seq, n_kv, hd)).astype(np.float32))
+    vb = bf16_bits(rng.standard_normal((B, max_seq, n_kv, hd)).astype(np.float32))
+    k, v = bf16_to_f32(kb), bf16_to_f32(vb)
+    ref = np.stack([orc.attention(q[b], k[b], v[b], ctx) for b in range(B)])
+    work = hip.DeviceBuffer(hip.lib().qlm_gqa_workspace_bytes(B, n_q, hd, max_seq))
+    do = hip.DeviceBuffer(q.nbytes)
+    hip.call("qlm_attention_decode", dev(hip, q), dev(hip, kb), dev(hip, vb), 1, max_seq, ctx, do,
+             B, n_q, n_kv, hd, work, None)
+    # q and the probabilities enter the matrix cores as bf16 hi + lo (2^-18
+    # of each value); the fp32 sums then differ from the oracle's order only
+    assert rel_err(do.to_numpy(q.shape, np.float32), ref) < 1e-5
+
+
 @pytest.mark.parametrize("B,H", [(1, 16), (2, 8)])
 def test_deltanet_decode_cols(hip, orc, rng, B, H):
     """Column-split mixer over 5 steps (ring index pos % 3): u scaled by the

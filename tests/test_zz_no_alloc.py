@@ -55,5 +55,7 @@ def test_noalloc_attention_equals_workspace_form(hip, orc, rng):
 
 def test_noalloc_attention_oversize_rejected(hip):
     fake = 4096  # rejected on the host before any launch
-    assert hip.lib().qlm_attention_decode_noalloc(fake, fake, fake, 1, 32768, 32768, fake, 16,
+    assert hip.lib().qlm_attention_decode_noalloc(fake, fake, fake, 0, 32768, 32768, fake, 16,
+                                                  16, 2, 256, None) == -4
+    assert hip.lib().qlm_attention_decode_noalloc(fake, fake, fake, 1, 32768, 32768, fake, 128,
                                                   16, 2, 256, None) == -4
