@@ -132,10 +132,11 @@ def tile_major(hip, dq, ds, group, rows, K):
 def bench_config1(hip, Ms=(1, 4, 16, 64)):
     """int8 matmul y = x (Wq s)^T: Wq U{-127..127}, s U(0.001, 0.01), x N(0,1).
     Per-row scales (the workload's scheme) with the kernel the engine runs at
-    each M: M = 1 the matrix-core GEMV over tile-major weights; M = 4, 16, 64
-    the matrix-core matmul over row-major weights. Group-32 scales beside
-    them, where M = 4 and 16 take the batched-decode form over tile-major
-    weights (qlm_matmul_i8_t)."""
+    each M over its tile-major weights: M = 1 the matrix-core GEMV; M = 4, 16
+    qlm_matmul_i8_tm (bf16 matrix cores), M = 64 its int8-digit form
+    (qlm_matmul_i8_rows64). Group-32 scales beside them, where M = 4 and 16
+    take the batched-decode form (qlm_matmul_i8_t) and M = 64
+    qlm_matmul_i8_tm."""
     rng = np.random.default_rng(0)
     st = hip.Stream()
     out = []
@@ -167,13 +168,16 @@ def bench_config1(hip, Ms=(1, 4, 16, 64)):
                         hip.call(kern, x, K, None, 0.0, qz, sz, group, y, N, M, N, K, 0, work,
                                  nwork, st.ptr)
                 else:
-                    kern = "qlm_matmul_i8"
+                    # the tile-major copy the engine holds: per-row scales at
+                    # 17..64 rows take the int8-digit form inside it
+                    kern = "qlm_matmul_i8_tm"
                     nwork = hip.lib().qlm_matmul_i8_workspace_bytes(M, N, K, 0)
                     work = hip.DeviceBuffer(nwork)
 
                     def launch(i):
-                        hip.call(kern, x, K, None, 0.0, dq[i % ncopy], ds[i % ncopy], group, y,
-                                 N, M, N, K, 0, work, nwork, st.ptr)
+                        qz, sz = dz[i % ncopy]
+                        hip.call(kern, x, K, None, 0.0, qz, sz, group, y, N, M, N, K, 0, work,
+                                 nwork, st.ptr)
                 us = graph_time(hip, st, launch, ncopy, launches=max(100, 2 * ncopy))
                 b = gemv_bytes(N, K, M, group)
                 r = {"N": N, "K": K, "M": M, "scales": "row" if group == K else "group32",

@@ -165,12 +165,33 @@ int qlm_matmul_i8(const float* x, int ldx, const float* norm_w, float eps, const
 /* qlm_matmul_i8 over the tile-major copy of the weights (qlm_mx_swizzle:
  * halves 2 for SwiGLU; group-32 scales as swizzled, per-row scales in their
  * [rows] layout), so a model needs no row-major copy for its M > 1 rows.
- * Same arithmetic, bit-identical to qlm_matmul_i8 on the same weights; K a
- * multiple of 64; the same workspace. */
+ * Same arithmetic, bit-identical to qlm_matmul_i8 on the same weights,
+ * except 17..64 rows with per-row scales, which take qlm_matmul_i8_rows64
+ * (within 1e-5 normwise, exact int32 sums); K a multiple of 64; the same
+ * workspace. */
 int qlm_matmul_i8_tm(const float* x, int ldx, const float* norm_w, float eps,
                      const int8_t* q_tiles, const float* s_tiles, int group, float* y, int ldy,
                      int M, int N, int K, int epilogue, void* work, size_t work_bytes,
                      void* stream);
+
+/* math::matmul's int8 branch (math_ops.cpp:845-871) for 17 <= M <= 64
+ * activation rows and one scale per weight row (group = K): tile-major
+ * weights (qlm_mx_swizzle) and their scales s_rows [N] as quantised. The
+ * rows are written as int8 digit planes, x = 2^E (d0 + d1/2^7 + d2/2^14 +
+ * d3/2^21) to within 2^-27 max|x| per row (the RMSNorm folded in when
+ * norm_w is given), and multiplied on v_mfma_i32_16x16x64_i8 with exact
+ * int32 sums over K, combined and scaled once in fp32 (~1e-7 normwise from
+ * the fp32 product). epilogue 0 (store) or 1 (y += result); K a multiple of
+ * 64, at most 2^18; QLM_ERR_SHAPE otherwise, for SwiGLU and for M outside
+ * 17..64. qlm_matmul_i8_tm takes this form for such calls (when its work is
+ * 256-byte aligned). work: device scratch of
+ * qlm_matmul_i8_rows64_workspace_bytes(M, N, K, epilogue) bytes (at most
+ * qlm_matmul_i8_workspace_bytes of the same arguments), 256-byte aligned, no
+ * initial contents needed. */
+size_t qlm_matmul_i8_rows64_workspace_bytes(int M, int N, int K, int epilogue);
+int qlm_matmul_i8_rows64(const float* x, int ldx, const float* norm_w, float eps,
+                         const int8_t* q_tiles, const float* s_rows, float* y, int ldy, int M,
+                         int N, int K, int epilogue, void* work, size_t work_bytes, void* stream);
 
 /* Batched decode (2 <= M <= 16 activation rows) on the int8 matrix cores
  * over the tile-major weights of qlm_mx_swizzle (per-row scales as

@@ -677,6 +677,19 @@ bool use_sk(int M, int K) { return M <= 64 && K % kSkKc == 0; }
 
 size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
+}  // namespace
+extern "C" size_t qlm_matmul_i8_rows64_workspace_bytes(int M, int N, int K, int epilogue);
+extern "C" int qlm_matmul_i8_rows64(const float* x, int ldx, const float* norm_w, float eps,
+                                    const int8_t* q_tiles, const float* s_rows, float* y,
+                                    int ldy, int M, int N, int K, int epilogue, void* work,
+                                    size_t work_bytes, void* stream);
+namespace {
+
+// the tile-major 17..64-row form with one scale per weight row (gemm_mx.hip)
+bool rows64_applies(int M, int K, int group, int epi) {
+    return group == K && M > 16 && M <= 64 && K % 64 == 0 && epi != EPI_SWIGLU;
+}
+
 size_t mm_workspace(int M, int N, int K, int epi) {
     size_t b = align256((size_t)M * sizeof(float));  // row scales
     if (use_sk(M, K)) {
@@ -685,6 +698,12 @@ size_t mm_workspace(int M, int N, int K, int epi) {
         if (!(ks == 1 && epi == EPI_STORE)) b += (size_t)ks * M * NR * sizeof(float);
     } else {
         b += align256((size_t)4 * M * K);  // the split activation (bf16 hi, lo)
+    }
+    // room for the 17..64-row digit form of qlm_matmul_i8_tm (one scale per
+    // weight row); the query cannot tell which scales a caller holds
+    if (M > 16 && M <= 64 && K % 64 == 0 && epi != EPI_SWIGLU) {
+        const size_t r = qlm_matmul_i8_rows64_workspace_bytes(M, N, K, epi);
+        if (r > b) b = r;
     }
     return b;
 }
@@ -882,6 +901,16 @@ int matmul_i8_entry(const float* x, int ldx, const float* norm_w, float eps, con
         return QLM_ERR_SHAPE;
     const size_t need = mm_workspace(M, N, K, epilogue);
     if (!work || work_bytes < need || ((uintptr_t)work & 15u)) return QLM_ERR_ARG;
+    if constexpr (TL) {
+        // 17..64 rows with one scale per weight row: int8 digits on the int8
+        // matrix cores (its workspace needs 256-byte alignment)
+        if (rows64_applies(M, K, group, epilogue) && !(epilogue == EPI_RESID && norm_w) &&
+            ((uintptr_t)work & 255u) == 0) {
+            const int rc = qlm_matmul_i8_rows64(x, ldx, norm_w, eps, q, scales, y, ldy, M, N, K,
+                                                epilogue, work, work_bytes, stream);
+            if (rc != QLM_ERR_SHAPE) return rc;
+        }
+    }
     hipStream_t st = as_stream(stream);
     float* rs = reinterpret_cast<float*>(work);
     float* part = reinterpret_cast<float*>(reinterpret_cast<char*>(work) + align256((size_t)M * 4));

@@ -29,6 +29,7 @@
 // tile), and the waves' partial sums meet in LDS at the end of each tile.
 
 #include "common.hpp"
+#include "mm_reduce.hpp"
 
 namespace {
 
@@ -431,6 +432,261 @@ int launch_gm_mp(const GmConfig& c, const int8_t* dg, const int* de, const int8_
     }
 }
 
+
+// ---- 17 <= M <= 64 activation rows, one scale per weight row ----
+//
+// y[m, n] = s[n] * sum_k x[m, k] q[n, k]. The rows are written as int8 digit
+// planes by k_act_digits (x_m = 2^E_m (d0 + d1 2^-7 + d2 2^-14 + d3 2^-21),
+// RMSNorm folded in) and multiplied on v_mfma_i32_16x16x64_i8 with
+//   A = 16 digit rows: activation rows 4a .. 4a+3, digits 0..3 (row 4 m' +
+//       d of product a holds digit d of row 4a + m' over the block's 64
+//       columns); MA products cover 4 MA rows;
+//   B = a tile-major weight fragment as stored (lane 16q + n: weight row n,
+//       columns 16q .. 16q+15).
+// D lane (q', n) holds the four digit sums of activation row 4a + q' and
+// weight row n; with one scale per weight row nothing is scaled inside the
+// K loop, so the products accumulate exact int32 sums over all of the
+// workgroup's blocks (|sum| <= 64 * 127 * K < 2^31 for K <= 2^18) and are
+// combined once at the end, in fp32: (D0 + 2^-7 (D1 + 2^-7 (D2 + 2^-7 D3)))
+// 2^E_m s[n].
+//
+// Work split: a workgroup of 8 waves owns 8 x 2 tiles (16 weight rows each)
+// and one K slice; wave w owns 2 of the tiles, so the waves share
+// every digit block, which the workgroup stages once through double-
+// buffered LDS in operand order (product a's 1 KB holds lane l's 16 bytes at
+// 16 l, so both the stores and the ds_read_b128 of an operand are lane-
+// contiguous and free of bank conflicts; rows padded to 80 bytes measured
+// half of the LDS cycles in conflicts) while each wave streams its 2
+// fragments a block; both are requested three
+// blocks ahead (a block's products take well under one load latency). The
+// digit traffic from L2 is then one block per workgroup and block, shared by
+// 16 tiles.
+//
+// Scheduling: a workgroup fills a CU (two waves a SIMD), so the tile groups
+// run in rounds of 256. Whole rounds take whole K ("full" units, results
+// stored directly); the groups of the last, partial round are split into K
+// slices so that it fills the chip too (on 151936 x 2560 the third round
+// would otherwise hold 82 workgroups and take as long as a whole one). The
+// slices write fp32 partial sums of their columns, added in slice order by
+// k_mm_reduce.
+constexpr int kR64Waves = 8;   // waves per workgroup (two a SIMD)
+constexpr int kR64Tiles = 2;   // tiles per wave
+
+template <int MA, int EPI>
+__global__ __launch_bounds__(kR64Waves * QLM_WAVE) void k_mm_rows64(
+    const int8_t* __restrict__ digits, const int* __restrict__ dexp,
+    const int8_t* __restrict__ qz, const float* __restrict__ srow, float* __restrict__ y, int ldy,
+    float* __restrict__ part, int M, int N, int K, int tiles, int full, int ks, int bps) {
+    constexpr int NT = kR64Waves * QLM_WAVE;
+    constexpr int AR = 16 * MA;       // digit rows of a block
+    constexpr int CH = AR * 4;        // 16-byte chunks of a block
+    constexpr int CPT = CH / NT;      // chunks per thread
+    static_assert(CH % NT == 0, "digit block must split evenly over the threads");
+    typedef int v4i __attribute__((ext_vector_type(4)));
+    __shared__ __align__(16) unsigned char abuf[2][AR * 64];
+
+    const int tid = threadIdx.x, lane = tid & (QLM_WAVE - 1);
+    const int w = tid / QLM_WAVE, qd = lane >> 4, n = lane & 15;
+    const int nblk = K >> 6;
+    // unit -> tile group, K range: whole K below `full`, then ks slices a group
+    const int u = blockIdx.x;
+    int g = u, b0 = 0, nb = nblk, slice = -1;
+    if (u >= full) {
+        const int v = u - full;
+        g = full + v / ks;
+        slice = v - (v / ks) * ks;
+        b0 = slice * bps;
+        nb = min(bps, nblk - b0);
+    }
+    const bool to_part = slice >= 0 && ks > 1;
+    const int tile0 = (g * kR64Waves + w) * kR64Tiles;
+
+    // Blocks are requested three ahead: digit block j goes through staging
+    // registers st[j & 3] into LDS buffer j & 1 at the end of iteration j - 1,
+    // weight block j into wr[j & 3] (rings of four, so that the slot of every
+    // access is a compile-time constant in the loop unrolled by four). Digit
+    // chunk c = tid + NT i is operand lane p = c & 63 (digit row 16 (c >> 6)
+    // + (p & 15), bytes 16 (p >> 4)) of product c >> 6, at LDS byte 16 c.
+    // Vector types: an aggregate copy into LDS would keep the staging array
+    // in scratch memory.
+    constexpr int RING = 4;
+    v4i st[RING][CPT];
+    v4i wr[RING][kR64Tiles];
+    auto issue = [&](int slot, int b) {
+#pragma unroll
+        for (int i = 0; i < CPT; ++i) {
+            const int c = tid + NT * i;
+            const int r = 16 * (c >> 6) + (c & 15);
+            st[slot][i] = *reinterpret_cast<const v4i*>(digits + (size_t)r * K + 64 * b +
+                                                        16 * ((c >> 4) & 3));
+        }
+        // weight fragments of this wave's tiles (tile index clamped: a ragged
+        // last group recomputes the last tile and stores nothing for it)
+#pragma unroll
+        for (int t = 0; t < kR64Tiles; ++t) {
+            const int tl = min(tile0 + t, tiles - 1);
+            wr[slot][t] = *reinterpret_cast<const v4i*>(
+                qz + ((size_t)tl * nblk + b) * 1024 + (size_t)lane * 16);
+        }
+    };
+    auto store_digits = [&](int slot, int buf) {
+#pragma unroll
+        for (int i = 0; i < CPT; ++i) {
+            const int c = tid + NT * i;
+            *reinterpret_cast<v4i*>(&abuf[buf][16 * c]) = st[slot][i];
+        }
+    };
+
+    v4i acc[kR64Tiles][MA];
+#pragma unroll
+    for (int t = 0; t < kR64Tiles; ++t)
+#pragma unroll
+        for (int a = 0; a < MA; ++a) acc[t][a] = v4i{0, 0, 0, 0};
+
+    // iteration i: request block i + 3, multiply block i, stage block i + 1.
+    // The requests are unconditional (past the slice they repeat its last
+    // block, an L2 hit): a load under a branch leaves the compiler unsure of
+    // how many loads are in flight, and it then waits for all of them.
+    auto mul = [&](int i, int slot) {
+        const int buf = i & 1;
+#pragma unroll
+        for (int a = 0; a < MA; ++a) {
+            const v4i av = *reinterpret_cast<const v4i*>(&abuf[buf][1024 * a + 16 * lane]);
+#pragma unroll
+            for (int t = 0; t < kR64Tiles; ++t)
+                acc[t][a] =
+                    __builtin_amdgcn_mfma_i32_16x16x64_i8(av, wr[slot][t], acc[t][a], 0, 0, 0);
+        }
+    };
+    // Block i + 1's digits go to LDS first (its buffer was last read by the
+    // products of block i - 1, which every wave finished before the barrier
+    // ending step i - 1), then block i + 3 is requested, then block i is
+    // multiplied; the barrier ending step i publishes block i + 1. The store
+    // is unconditional: at the last block it writes a clamped copy nobody
+    // reads, and a conditional store lets the compiler move the slot's load
+    // into the branch, where it is waited on at once.
+    auto step = [&](int i, int slot) {
+        store_digits((slot + 1) & (RING - 1), (i & 1) ^ 1);
+        issue((slot + RING - 1) & (RING - 1), b0 + min(i + RING - 1, nb - 1));
+        // the requests go out before the products (left to itself the
+        // scheduler sinks them below, shortening the prefetch to ~1 block)
+        __builtin_amdgcn_sched_barrier(0);
+        mul(i, slot);
+        __syncthreads();
+    };
+    auto tail = [&](int i, int slot) {  // the last blocks: nothing left to request
+        store_digits((slot + 1) & (RING - 1), (i & 1) ^ 1);
+        mul(i, slot);
+        __syncthreads();
+    };
+
+#pragma unroll
+    for (int j = 0; j < RING - 1; ++j) issue(j, b0 + min(j, nb - 1));
+    store_digits(0, 0);
+    __syncthreads();
+    int i0 = 0;
+    for (; i0 + RING <= nb; i0 += RING) {  // workgroup-uniform bounds
+        step(i0, 0);
+        step(i0 + 1, 1);
+        step(i0 + 2, 2);
+        step(i0 + 3, 3);
+    }
+    if (i0 < nb) tail(i0, 0);
+    if (i0 + 1 < nb) tail(i0 + 1, 1);
+    if (i0 + 2 < nb) tail(i0 + 2, 2);
+
+    // ---- lane (qd, n): activation rows 4a + qd, weight row 16 tile + n ----
+    const int row0 = full * kR64Waves * kR64Tiles * 16, nt = N - row0;
+    float ex[MA];
+#pragma unroll
+    for (int a = 0; a < MA; ++a) ex[a] = ldexpf(1.0f, dexp[min(4 * a + qd, M - 1)]);
+#pragma unroll
+    for (int t = 0; t < kR64Tiles; ++t) {
+        const int tile = tile0 + t;
+        const int row = tile * 16 + n;
+        if (tile >= tiles || row >= N) continue;
+        const float sn = srow[row];
+#pragma unroll
+        for (int a = 0; a < MA; ++a) {
+            const int m = 4 * a + qd;
+            if (m >= M) continue;
+            const v4i dd = acc[t][a];
+            const float v =
+                fmaf(fmaf(fmaf((float)dd[3], 0x1p-7f, (float)dd[2]), 0x1p-7f, (float)dd[1]),
+                     0x1p-7f, (float)dd[0]);
+            const float r = (v * ex[a]) * sn;
+            if (to_part)  // tail columns only: [slice][m][N - row0]
+                part[((size_t)slice * M + m) * nt + (row - row0)] = r;
+            else if constexpr (EPI == EPI_RESID)
+                y[(size_t)m * ldy + row] += r;
+            else
+                y[(size_t)m * ldy + row] = r;
+        }
+    }
+}
+
+constexpr int kR64MaxRows = 64;
+
+struct R64Plan {
+    int ma, groups, full, ks, bps, units;
+};
+
+// Whole rounds of 256 groups (one workgroup a CU) take whole K; the last
+// partial round's groups are cut into ks slices of bps blocks (about one
+// workgroup a CU again).
+R64Plan r64_plan(int M, int N, int K) {
+    R64Plan p;
+    p.ma = M <= 32 ? 8 : 16;
+    const int tiles = (N + 15) / 16, nblk = K / 64;
+    p.groups = (tiles + kR64Waves * kR64Tiles - 1) / (kR64Waves * kR64Tiles);
+    p.full = (p.groups / 256) * 256;
+    const int tail = p.groups - p.full;
+    int ks = tail > 0 ? 256 / tail : 1;
+    ks = ks < 1 ? 1 : (ks > nblk ? nblk : ks);
+    p.bps = (nblk + ks - 1) / ks;
+    p.ks = (nblk + p.bps - 1) / p.bps;
+    p.units = p.full + tail * p.ks;
+    return p;
+}
+
+size_t r64_digits_bytes(int K) { return (size_t)kR64MaxRows * 4 * K; }
+
+// columns of the partial round (the ones that go through partial sums)
+int r64_tail_rows(const R64Plan& p, int N) { return N - p.full * kR64Waves * kR64Tiles * 16; }
+
+size_t r64_work_bytes(int M, int N, int K, int epi) {
+    const R64Plan p = r64_plan(M, N, K);
+    size_t b = align256(r64_digits_bytes(K)) + align256((size_t)kR64MaxRows * sizeof(int));
+    if (p.ks > 1) b += (size_t)p.ks * M * r64_tail_rows(p, N) * sizeof(float);
+    (void)epi;
+    return b;
+}
+
+template <int MA>
+int launch_r64(const R64Plan& p, const int8_t* dg, const int* de, const int8_t* qz,
+               const float* sr, float* y, int ldy, float* part, int M, int N, int K, int epi,
+               hipStream_t st) {
+    const int tiles = (N + 15) / 16;
+    if (epi == EPI_RESID)
+        hipLaunchKernelGGL((k_mm_rows64<MA, EPI_RESID>), dim3(p.units), dim3(kR64Waves * QLM_WAVE),
+                           0, st, dg, de, qz, sr, y, ldy, part, M, N, K, tiles, p.full, p.ks,
+                           p.bps);
+    else
+        hipLaunchKernelGGL((k_mm_rows64<MA, EPI_STORE>), dim3(p.units), dim3(kR64Waves * QLM_WAVE),
+                           0, st, dg, de, qz, sr, y, ldy, part, M, N, K, tiles, p.full, p.ks,
+                           p.bps);
+    int rc = qlm_launch_status();
+    if (rc != QLM_OK || p.ks == 1) return rc;
+    const int row0 = N - r64_tail_rows(p, N), nt = N - row0;
+    const dim3 rgrid((nt + kReduceThreads - 1) / kReduceThreads, M);
+    if (epi == EPI_RESID)
+        hipLaunchKernelGGL((k_mm_reduce<MMR_RESID, false>), rgrid, dim3(kReduceThreads), 0, st,
+                           part, p.ks, M, nt, nt, y + row0, ldy, nullptr, 0, K, 0.0f);
+    else
+        hipLaunchKernelGGL((k_mm_reduce<MMR_STORE, false>), rgrid, dim3(kReduceThreads), 0, st,
+                           part, p.ks, M, nt, nt, y + row0, ldy, nullptr, 0, K, 0.0f);
+    return qlm_launch_status();
+}
 }  // namespace
 
 extern "C" size_t qlm_matmul_i8_mx_workspace_bytes(int M, int K) {
@@ -489,4 +745,44 @@ extern "C" int qlm_matmul_i8_mx(const float* x, int ldx, const float* norm_w, fl
     if (epilogue == EPI_RESID) QLM_GM_CALL(false, EPI_RESID);
     QLM_GM_CALL(false, EPI_SWIGLU);
 #undef QLM_GM_CALL
+}
+
+extern "C" size_t qlm_matmul_i8_rows64_workspace_bytes(int M, int N, int K, int epilogue) {
+    if (M <= 16 || M > kR64MaxRows || N <= 0 || K <= 0 || K % 64 != 0) return 0;
+    if (epilogue != EPI_STORE && epilogue != EPI_RESID) return 0;
+    return r64_work_bytes(M, N, K, epilogue);
+}
+
+extern "C" int qlm_matmul_i8_rows64(const float* x, int ldx, const float* norm_w, float eps,
+                                    const int8_t* q_tiles, const float* s_rows, float* y,
+                                    int ldy, int M, int N, int K, int epilogue, void* work,
+                                    size_t work_bytes, void* stream) {
+    if (!x || !q_tiles || !s_rows || !y || M <= 0 || N <= 0 || K <= 0) return QLM_ERR_ARG;
+    if (epilogue < EPI_STORE || epilogue > EPI_SWIGLU) return QLM_ERR_ARG;
+    if (epilogue == EPI_RESID && norm_w) return QLM_ERR_ARG;
+    if (epilogue == EPI_SWIGLU || M <= 16 || M > kR64MaxRows || K % 64 != 0 || K > (1 << 18))
+        return QLM_ERR_SHAPE;
+    if (ldx < K || ldy < N || ldx % 4 != 0) return QLM_ERR_SHAPE;
+    if (((uintptr_t)x | (uintptr_t)q_tiles | (uintptr_t)norm_w) & 15u) return QLM_ERR_SHAPE;
+    const size_t need = r64_work_bytes(M, N, K, epilogue);
+    if (!work || work_bytes < need || ((uintptr_t)work & 255u)) return QLM_ERR_ARG;
+    hipStream_t st = as_stream(stream);
+    int8_t* dg = reinterpret_cast<int8_t*>(work);
+    int* de = reinterpret_cast<int*>(reinterpret_cast<char*>(work) +
+                                     align256(r64_digits_bytes(K)));
+    float* part = reinterpret_cast<float*>(reinterpret_cast<char*>(de) +
+                                           align256((size_t)kR64MaxRows * sizeof(int)));
+    const R64Plan p = r64_plan(M, N, K);
+    const int rows = 4 * p.ma;  // digit rows written (zeros past M)
+    if (norm_w)
+        hipLaunchKernelGGL(k_act_digits<true>, dim3(rows), dim3(kPrepThreads), 0, st, x, ldx,
+                           norm_w, eps, M, K, dg, de);
+    else
+        hipLaunchKernelGGL(k_act_digits<false>, dim3(rows), dim3(kPrepThreads), 0, st, x, ldx,
+                           nullptr, eps, M, K, dg, de);
+    int rc = qlm_launch_status();
+    if (rc != QLM_OK) return rc;
+    return p.ma == 8 ? launch_r64<8>(p, dg, de, q_tiles, s_rows, y, ldy, part, M, N, K, epilogue, st)
+                     : launch_r64<16>(p, dg, de, q_tiles, s_rows, y, ldy, part, M, N, K, epilogue,
+                                      st);
 }

@@ -69,6 +69,9 @@ _SIGS = {
     "qlm_mx_layout_bytes": (_i, [_i, _i, _i, _i, C.POINTER(_sz), C.POINTER(_sz)]),
     "qlm_gemv_i8_mx": (_i, [_vp, _vp, _f, _vp, _vp, _i, _vp, _i, _i, _i, _vp]),
     "qlm_matmul_i8_mx_workspace_bytes": (_sz, [_i, _i]),
+    "qlm_matmul_i8_rows64_workspace_bytes": (_sz, [_i, _i, _i, _i]),
+    "qlm_matmul_i8_rows64": (_i, [_vp, _i, _vp, _f, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _sz,
+                                  _vp]),
     "qlm_matmul_i8_t_workspace_bytes": (_sz, [_i, _i, _i, _i]),
     "qlm_matmul_i8_t": (_i, [_vp, _i, _vp, _f, _vp, _vp, _i, _vp, _i, _i, _i, _i, _i, _vp, _sz,
                              _vp]),
