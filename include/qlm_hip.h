@@ -166,7 +166,8 @@ int qlm_matmul_i8(const float* x, int ldx, const float* norm_w, float eps, const
  * halves 2 for SwiGLU; group-32 scales as swizzled, per-row scales in their
  * [rows] layout), so a model needs no row-major copy for its M > 1 rows.
  * Same arithmetic, bit-identical to qlm_matmul_i8 on the same weights,
- * except 17..64 rows with per-row scales, which take qlm_matmul_i8_rows64
+ * except 2..64 rows with per-row scales (no SwiGLU; N >= 8192, or more than
+ * 16 rows and K > 4096), which take qlm_matmul_i8_rows64
  * (within 1e-5 normwise, exact int32 sums); K a multiple of 64; the same
  * workspace. */
 int qlm_matmul_i8_tm(const float* x, int ldx, const float* norm_w, float eps,
@@ -174,7 +175,7 @@ int qlm_matmul_i8_tm(const float* x, int ldx, const float* norm_w, float eps,
                      int M, int N, int K, int epilogue, void* work, size_t work_bytes,
                      void* stream);
 
-/* math::matmul's int8 branch (math_ops.cpp:845-871) for 17 <= M <= 64
+/* math::matmul's int8 branch (math_ops.cpp:845-871) for 2 <= M <= 64
  * activation rows and one scale per weight row (group = K): tile-major
  * weights (qlm_mx_swizzle) and their scales s_rows [N] as quantised. The
  * rows are written as int8 digit planes, x = 2^E (d0 + d1/2^7 + d2/2^14 +
@@ -183,8 +184,9 @@ int qlm_matmul_i8_tm(const float* x, int ldx, const float* norm_w, float eps,
  * int32 sums over K, combined and scaled once in fp32 (~1e-7 normwise from
  * the fp32 product). epilogue 0 (store) or 1 (y += result); K a multiple of
  * 64, at most 2^18; QLM_ERR_SHAPE otherwise, for SwiGLU and for M outside
- * 17..64. qlm_matmul_i8_tm takes this form for such calls (when its work is
- * 256-byte aligned). work: device scratch of
+ * 2..64. qlm_matmul_i8_tm takes this form for such calls where measured
+ * faster (N >= 8192, or more than 16 rows and K > 4096; its work 256-byte
+ * aligned). work: device scratch of
  * qlm_matmul_i8_rows64_workspace_bytes(M, N, K, epilogue) bytes (at most
  * qlm_matmul_i8_workspace_bytes of the same arguments), 256-byte aligned, no
  * initial contents needed. */

@@ -685,9 +685,14 @@ extern "C" int qlm_matmul_i8_rows64(const float* x, int ldx, const float* norm_w
                                     size_t work_bytes, void* stream);
 namespace {
 
-// the tile-major 17..64-row form with one scale per weight row (gemm_mx.hip)
-bool rows64_applies(int M, int K, int group, int epi) {
-    return group == K && M > 16 && M <= 64 && K % 64 == 0 && epi != EPI_SWIGLU;
+// the tile-major 2..64-row form with one scale per weight row (gemm_mx.hip),
+// where measured faster than the K-sliced bf16 form: N >= 8192 (32 or more
+// 256-row tile groups), or more than 16 rows and K > 4096. With fewer groups
+// its K slices and their reduction launch cost more (4096 x 4096: 15.4
+// against 12.6 us at 16 rows, 27.5 against 23.3 us at 64)
+bool rows64_applies(int M, int N, int K, int group, int epi) {
+    if (N < 8192 && (M <= 16 || K <= 4096)) return false;
+    return group == K && M >= 2 && M <= 64 && K % 64 == 0 && epi != EPI_SWIGLU;
 }
 
 size_t mm_workspace(int M, int N, int K, int epi) {
@@ -699,9 +704,9 @@ size_t mm_workspace(int M, int N, int K, int epi) {
     } else {
         b += align256((size_t)4 * M * K);  // the split activation (bf16 hi, lo)
     }
-    // room for the 17..64-row digit form of qlm_matmul_i8_tm (one scale per
+    // room for the 2..64-row digit form of qlm_matmul_i8_tm (one scale per
     // weight row); the query cannot tell which scales a caller holds
-    if (M > 16 && M <= 64 && K % 64 == 0 && epi != EPI_SWIGLU) {
+    if (M >= 2 && M <= 64 && K % 64 == 0 && epi != EPI_SWIGLU) {
         const size_t r = qlm_matmul_i8_rows64_workspace_bytes(M, N, K, epi);
         if (r > b) b = r;
     }
@@ -902,9 +907,9 @@ int matmul_i8_entry(const float* x, int ldx, const float* norm_w, float eps, con
     const size_t need = mm_workspace(M, N, K, epilogue);
     if (!work || work_bytes < need || ((uintptr_t)work & 15u)) return QLM_ERR_ARG;
     if constexpr (TL) {
-        // 17..64 rows with one scale per weight row: int8 digits on the int8
+        // 2..64 rows with one scale per weight row: int8 digits on the int8
         // matrix cores (its workspace needs 256-byte alignment)
-        if (rows64_applies(M, K, group, epilogue) && !(epilogue == EPI_RESID && norm_w) &&
+        if (rows64_applies(M, N, K, group, epilogue) && !(epilogue == EPI_RESID && norm_w) &&
             ((uintptr_t)work & 255u) == 0) {
             const int rc = qlm_matmul_i8_rows64(x, ldx, norm_w, eps, q, scales, y, ldy, M, N, K,
                                                 epilogue, work, work_bytes, stream);

@@ -433,7 +433,7 @@ int launch_gm_mp(const GmConfig& c, const int8_t* dg, const int* de, const int8_
 }
 
 
-// ---- 17 <= M <= 64 activation rows, one scale per weight row ----
+// ---- 2 <= M <= 64 activation rows, one scale per weight row ----
 //
 // y[m, n] = s[n] * sum_k x[m, k] q[n, k]. The rows are written as int8 digit
 // planes by k_act_digits (x_m = 2^E_m (d0 + d1 2^-7 + d2 2^-14 + d3 2^-21),
@@ -480,8 +480,13 @@ __global__ __launch_bounds__(kR64Waves * QLM_WAVE) void k_mm_rows64(
     constexpr int NT = kR64Waves * QLM_WAVE;
     constexpr int AR = 16 * MA;       // digit rows of a block
     constexpr int CH = AR * 4;        // 16-byte chunks of a block
-    constexpr int CPT = CH / NT;      // chunks per thread
-    static_assert(CH % NT == 0, "digit block must split evenly over the threads");
+    // chunks per thread; below 32 rows a block has fewer chunks than threads
+    // (whole waves of them: CH is a multiple of 64): every thread still
+    // loads (chunk index clamped, so the loads stay unconditional) and the
+    // first CH threads store
+    constexpr bool FEW = CH < NT;
+    constexpr int CPT = FEW ? 1 : CH / NT;
+    static_assert(FEW || CH % NT == 0, "digit block must split evenly over the threads");
     typedef int v4i __attribute__((ext_vector_type(4)));
     __shared__ __align__(16) unsigned char abuf[2][AR * 64];
 
@@ -515,7 +520,7 @@ __global__ __launch_bounds__(kR64Waves * QLM_WAVE) void k_mm_rows64(
     auto issue = [&](int slot, int b) {
 #pragma unroll
         for (int i = 0; i < CPT; ++i) {
-            const int c = tid + NT * i;
+            const int c = FEW ? min(tid, CH - 1) : tid + NT * i;
             const int r = 16 * (c >> 6) + (c & 15);
             st[slot][i] = *reinterpret_cast<const v4i*>(digits + (size_t)r * K + 64 * b +
                                                         16 * ((c >> 4) & 3));
@@ -533,7 +538,7 @@ __global__ __launch_bounds__(kR64Waves * QLM_WAVE) void k_mm_rows64(
 #pragma unroll
         for (int i = 0; i < CPT; ++i) {
             const int c = tid + NT * i;
-            *reinterpret_cast<v4i*>(&abuf[buf][16 * c]) = st[slot][i];
+            if (!FEW || tid < CH) *reinterpret_cast<v4i*>(&abuf[buf][16 * c]) = st[slot][i];
         }
     };
 
@@ -636,7 +641,7 @@ struct R64Plan {
 // workgroup a CU again).
 R64Plan r64_plan(int M, int N, int K) {
     R64Plan p;
-    p.ma = M <= 32 ? 8 : 16;
+    p.ma = M <= 4 ? 1 : (M <= 8 ? 2 : (M <= 16 ? 4 : (M <= 32 ? 8 : 16)));  // ceil(M / 4), 2^n
     const int tiles = (N + 15) / 16, nblk = K / 64;
     p.groups = (tiles + kR64Waves * kR64Tiles - 1) / (kR64Waves * kR64Tiles);
     p.full = (p.groups / 256) * 256;
@@ -748,7 +753,7 @@ extern "C" int qlm_matmul_i8_mx(const float* x, int ldx, const float* norm_w, fl
 }
 
 extern "C" size_t qlm_matmul_i8_rows64_workspace_bytes(int M, int N, int K, int epilogue) {
-    if (M <= 16 || M > kR64MaxRows || N <= 0 || K <= 0 || K % 64 != 0) return 0;
+    if (M < 2 || M > kR64MaxRows || N <= 0 || K <= 0 || K % 64 != 0) return 0;
     if (epilogue != EPI_STORE && epilogue != EPI_RESID) return 0;
     return r64_work_bytes(M, N, K, epilogue);
 }
@@ -760,7 +765,7 @@ extern "C" int qlm_matmul_i8_rows64(const float* x, int ldx, const float* norm_w
     if (!x || !q_tiles || !s_rows || !y || M <= 0 || N <= 0 || K <= 0) return QLM_ERR_ARG;
     if (epilogue < EPI_STORE || epilogue > EPI_SWIGLU) return QLM_ERR_ARG;
     if (epilogue == EPI_RESID && norm_w) return QLM_ERR_ARG;
-    if (epilogue == EPI_SWIGLU || M <= 16 || M > kR64MaxRows || K % 64 != 0 || K > (1 << 18))
+    if (epilogue == EPI_SWIGLU || M < 2 || M > kR64MaxRows || K % 64 != 0 || K > (1 << 18))
         return QLM_ERR_SHAPE;
     if (ldx < K || ldy < N || ldx % 4 != 0) return QLM_ERR_SHAPE;
     if (((uintptr_t)x | (uintptr_t)q_tiles | (uintptr_t)norm_w) & 15u) return QLM_ERR_SHAPE;
@@ -782,7 +787,12 @@ extern "C" int qlm_matmul_i8_rows64(const float* x, int ldx, const float* norm_w
                            nullptr, eps, M, K, dg, de);
     int rc = qlm_launch_status();
     if (rc != QLM_OK) return rc;
-    return p.ma == 8 ? launch_r64<8>(p, dg, de, q_tiles, s_rows, y, ldy, part, M, N, K, epilogue, st)
-                     : launch_r64<16>(p, dg, de, q_tiles, s_rows, y, ldy, part, M, N, K, epilogue,
-                                      st);
+    switch (p.ma) {
+        case 1: return launch_r64<1>(p, dg, de, q_tiles, s_rows, y, ldy, part, M, N, K, epilogue, st);
+        case 2: return launch_r64<2>(p, dg, de, q_tiles, s_rows, y, ldy, part, M, N, K, epilogue, st);
+        case 4: return launch_r64<4>(p, dg, de, q_tiles, s_rows, y, ldy, part, M, N, K, epilogue, st);
+        case 8: return launch_r64<8>(p, dg, de, q_tiles, s_rows, y, ldy, part, M, N, K, epilogue, st);
+        default:
+            return launch_r64<16>(p, dg, de, q_tiles, s_rows, y, ldy, part, M, N, K, epilogue, st);
+    }
 }
