@@ -583,6 +583,9 @@ def main():
     ap.add_argument("--kernel-only", action="store_true",
                     help="only the dominant-kernel timing and the copy of known size (for "
                          "rocprofv3 --pmc passes)")
+    ap.add_argument("--section", choices=["config1", "config2", "config3", "prefill"],
+                    help="run only this isolated-kernel section and print its results (for "
+                         "rocprofv3 kernel traces of one workload)")
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-kernels", action="store_true",
                     help="skip the isolated-kernel sections (config 1-3, prefill matmul)")
@@ -613,6 +616,12 @@ def main():
         sys.exit(1)
     hip.check(hip.lib().qlm_set_device(0))
     log("device", hip.device_name())
+
+    if args.section:
+        fn = {"config1": bench_config1, "config2": bench_config2, "config3": bench_config3,
+              "prefill": bench_prefill_matmul}[args.section]
+        print(json.dumps({args.section: fn(hip)}), flush=True)
+        return
 
     if args.kernel_only:
         us = measure_dominant(hip)
