@@ -114,16 +114,18 @@ def gemv_bytes(N, K, M, group):
     return N * K + 4 * N * nb + 4 * M * K + 4 * M * N
 
 
-def tile_major(hip, dq, ds, group, rows, K):
-    """Tile-major copies (qlm_mx_swizzle) of each weight copy; per-row scales
-    keep their layout."""
+def tile_major(hip, dq, ds, group, rows, K, halves=1):
+    """Tile-major copies (qlm_mx_swizzle) of each weight copy (halves = 2: a
+    [gate; up] matrix of 2 x rows, each half tiled on its own); per-row
+    scales keep their layout."""
     qb, sb = C.c_size_t(), C.c_size_t()
-    hip.check(hip.lib().qlm_mx_layout_bytes(rows, K, group, 1, C.byref(qb), C.byref(sb)))
+    hip.check(hip.lib().qlm_mx_layout_bytes(rows, K, group, halves, C.byref(qb), C.byref(sb)))
     out = []
     for q_, s_ in zip(dq, ds):
         qz = hip.DeviceBuffer(qb.value)
         sz = hip.DeviceBuffer(sb.value) if sb.value else s_
-        hip.call("qlm_mx_swizzle", q_, s_, group, rows, K, 1, qz, sz if sb.value else None, None)
+        hip.call("qlm_mx_swizzle", q_, s_, group, rows, K, halves, qz, sz if sb.value else None,
+                 None)
         out.append((qz, sz))
     hip.sync()
     return out
@@ -341,8 +343,9 @@ def bench_config3(hip, n_q=16, n_kv=2, hd=256, ctx_max=32768, Bmax=16):
 # ------------------------------------------------------------ prefill matmul
 def bench_prefill_matmul(hip, M=2047, F=9728, K=2560):
     """The 4B prefill's largest matmul: RMSNorm + gate/up (2F = 19456 int8
-    rows, group-32 scales) + SwiGLU over M prompt rows, bf16 matrix cores;
-    utilisation = 2 M (2F) K / t over the dense bf16 peak."""
+    rows, group-32 scales) + SwiGLU over M prompt rows, bf16 matrix cores, over
+    the tile-major weights the engine holds (qlm_matmul_i8_tm); utilisation =
+    2 M (2F) K / t over the dense bf16 peak."""
     rng = np.random.default_rng(5)
     st = hip.Stream()
     rows = 2 * F
@@ -350,6 +353,8 @@ def bench_prefill_matmul(hip, M=2047, F=9728, K=2560):
     s = rng.uniform(0.001, 0.01, (rows, K // 32)).astype(np.float32)
     ncopy = n_copies(rows * K, lo=2, hi=16)
     dq, ds = dev_copies(hip, q, ncopy), dev_copies(hip, s, ncopy)
+    dz = tile_major(hip, dq, ds, 32, F, K, halves=2)
+    free_all(dq + ds)
     x = hip.DeviceBuffer.from_numpy(rng.standard_normal((M, K)).astype(np.float32))
     nw = hip.DeviceBuffer.from_numpy((rng.standard_normal(K) * 0.02).astype(np.float32))
     y = hip.DeviceBuffer(M * F * 4)
@@ -357,13 +362,15 @@ def bench_prefill_matmul(hip, M=2047, F=9728, K=2560):
     work = hip.DeviceBuffer(nwork)
 
     def launch(i):
-        hip.call("qlm_matmul_i8", x, K, nw, 1e-6, dq[i % ncopy], ds[i % ncopy], 32, y, F, M, F,
-                 K, 2, work, nwork, st.ptr)
+        qz, sz = dz[i % ncopy]
+        hip.call("qlm_matmul_i8_tm", x, K, nw, 1e-6, qz, sz, 32, y, F, M, F, K, 2, work, nwork,
+                 st.ptr)
 
     us = graph_time(hip, st, launch, ncopy, launches=40)
     flops = 2.0 * M * rows * K
-    free_all(dq + ds + [x, nw, y, work])
-    r = {"rows": M, "N": rows, "K": K, "kernel": "qlm_matmul_i8 (RMSNorm + gate/up + SwiGLU)",
+    free_all([t for pair in dz for t in pair] + [x, nw, y, work])
+    r = {"rows": M, "N": rows, "K": K,
+         "kernel": "qlm_matmul_i8_tm (RMSNorm + gate/up + SwiGLU, tile-major weights)",
          "us": round(us, 1), "TFLOPs": round(flops / us / 1e6, 1),
          "mfma_util": round(flops / (us * 1e-6) / BF16_PEAK_FLOPS, 4)}
     log(f"prefill gate/up matmul M={M}: {us:.1f} us, {r['TFLOPs']} TFLOP/s, util "

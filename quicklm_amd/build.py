@@ -32,6 +32,11 @@ HIP_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-command-line-argument", "-I", INCLUDE,
 ]
+# Per-file additions. gemm.hip: MFMA results in ordinary VGPRs; with the
+# default accumulator-register form the group-32 prefill matmul copied every
+# product back (two v_accvgpr_read per MFMA before its scale FMA), at the same
+# register total.
+FILE_FLAGS = {"gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 CXX_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function", "-pthread",
              "-I", INCLUDE, "-I", os.path.join(CSRC, "host")]
 
@@ -52,7 +57,8 @@ def build_hip(jobs: int = 8) -> str:
     for s in srcs:
         o = os.path.join(BUILD, os.path.basename(s) + ".o")
         objs.append(o)
-        cmds.append([HIPCC, *HIP_FLAGS, "-c", s, "-o", o])
+        extra = FILE_FLAGS.get(os.path.basename(s), [])
+        cmds.append([HIPCC, *HIP_FLAGS, *extra, "-c", s, "-o", o])
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         list(ex.map(_run, cmds))
     lib = os.path.join(PKG, "libqlm_hip.so")

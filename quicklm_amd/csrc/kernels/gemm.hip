@@ -420,6 +420,206 @@ __global__ __launch_bounds__(kThreads) void k_mm_i8(const float* __restrict__ x,
 }
 
 // ---------------------------------------------------------------------------
+// Prefill (M > 64) over the tile-major int8 weights and the pre-split
+// activation (bf16 hi plane [M, ldx], lo plane after it): the arithmetic of
+// k_mm_i8<2, 2, 1, 4, 4, ...> (the same operands in the same lane positions,
+// the same per-group MFMA pairs, scale FMAs and order, so the same bits), with
+// the staging rebuilt:
+//   - LDS in operand order: each 16-row x 32-column operand (a 16x16x32 MFMA
+//     input) is 1 KB with lane l's 16 bytes at 16 l, for the activation
+//     hi/lo tiles and the converted weight tiles alike, so every ds_read_b128
+//     and every staging store is lane-contiguous (no bank conflicts; the
+//     padded rows measured a third of the LDS cycles in conflicts);
+//   - two stages, one barrier per 32-column group: group g + 1 is converted
+//     and stored while group g is multiplied, and group g + 2 requested;
+//   - addresses advance by constants (a group is 512 bytes of a weight
+//     fragment and 16 scales), none recomputed in the loop;
+//   - every load unconditional (clamped rows, tiles and groups).
+// Workgroup: 4 waves (2 x 2), each 64 activation rows x 64 staged weight rows
+// (SwiGLU: 32 gate + the matching 32 up rows); 128 x 128 staged per group.
+template <bool RS, int EPI>
+__global__ __launch_bounds__(kThreads, 2) void k_mm_pf(const uint16_t* __restrict__ xh, int ldx,
+                                                       const int8_t* __restrict__ q,
+                                                       const float* __restrict__ sc,
+                                                       float* __restrict__ y, int ldy, int M,
+                                                       int N, int K, TileMap tmap) {
+    constexpr int TM = 4, TN = 4;
+    constexpr int OUT_TN = EPI == EPI_SWIGLU ? TN / 2 : TN;
+    constexpr int BN_OUT = 2 * OUT_TN * 16;
+    constexpr int A_LO = 8192, B_OFS = 16384, STAGE = 24576;
+    __shared__ __attribute__((aligned(16))) unsigned char smem[2 * STAGE];
+    typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int m0 = blockIdx.y * 128;
+    const int nout0 = blockIdx.x * BN_OUT;
+    const int ngrp = K >> 5;
+    const size_t plane = (size_t)M * ldx;
+
+    // staged weight tile t (0..7) -> tile of the tile-major matrix (clamped)
+    auto gtile = [&](int t) -> int {
+        if constexpr (EPI == EPI_SWIGLU) {
+            const int th = min(nout0 / 16 + (t & 3), tmap.tiles_half - 1);
+            return (t >> 2) * tmap.tiles_half + th;
+        } else {
+            return min(nout0 / 16 + t, tmap.tiles_half - 1);
+        }
+    };
+    // a wave's tile tn -> staged tile
+    auto stile = [&](int tn) -> int {
+        if constexpr (EPI == EPI_SWIGLU)
+            return tn < TN / 2 ? wn * (TN / 2) + tn : 4 + wn * (TN / 2) + (tn - TN / 2);
+        else
+            return wn * TN + tn;
+    };
+
+    // activation operand slots s = tid, tid + 256 of 8 tiles x 64 lanes:
+    // row 16 (s >> 6) + (s & 15), columns 8 ((s >> 4) & 3) .. + 7 of a group
+    const uint16_t* ap[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int sl_ = tid + 256 * u;
+        const int row = min(m0 + 16 * (sl_ >> 6) + (sl_ & 15), M - 1);
+        ap[u] = xh + (size_t)row * ldx + 8 * ((sl_ >> 4) & 3);
+    }
+    // weights: thread tid takes staged tile tid >> 5 and the 16 bytes of its
+    // fragment lane 32 (g & 1) + (tid & 31) (row tid & 15, columns 16 ((tid >> 4)
+    // & 1) .. + 15 of the group): group g is at + 512 g
+    const int bt = tid >> 5, bn = tid & 15, bo = 2 * ((tid >> 4) & 1);
+    const int8_t* bp = q + (size_t)gtile(bt) * tmap.nblk64 * 1024 + (size_t)(tid & 31) * 16;
+    // group-32 scales of the wave's tiles, row lane & 15: group g at + 16 g
+    const float* sp[TN];
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn)
+        sp[tn] = sc + (size_t)gtile(stile(tn)) * tmap.nblk64 * 32 + (lane & 15);
+
+    u32x4 xa_h[2], xa_l[2];
+    int4 wb;
+    float sl[TN];
+    auto load = [&](int g) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            xa_h[u] = *reinterpret_cast<const u32x4*>(ap[u] + 32 * g);
+            xa_l[u] = *reinterpret_cast<const u32x4*>(ap[u] + plane + 32 * g);
+        }
+        wb = *reinterpret_cast<const int4*>(bp + (size_t)512 * g);
+        if constexpr (!RS) {
+#pragma unroll
+            for (int tn = 0; tn < TN; ++tn) sl[tn] = sp[tn][16 * g];
+        }
+    };
+    auto store = [&](int stage) {
+        unsigned char* st = smem + stage * STAGE;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            *reinterpret_cast<u32x4*>(st + (tid + 256 * u) * 16) = xa_h[u];
+            *reinterpret_cast<u32x4*>(st + A_LO + (tid + 256 * u) * 16) = xa_l[u];
+        }
+        // 16 int8 -> 16 bf16 (exact): columns 0-7 to operand lane bo*16 + bn,
+        // 8-15 to the next k-octet's lane
+        const int wv[4] = {wb.x, wb.y, wb.z, wb.w};
+        unsigned ow[8];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const unsigned v = (unsigned)wv[j];
+            const int b0 = (int8_t)(v & 0xffu), b1 = (int8_t)((v >> 8) & 0xffu);
+            const int b2 = (int8_t)((v >> 16) & 0xffu), b3 = (int8_t)(v >> 24);
+            ow[2 * j] = (unsigned)i8_bf16(b0) | ((unsigned)i8_bf16(b1) << 16);
+            ow[2 * j + 1] = (unsigned)i8_bf16(b2) | ((unsigned)i8_bf16(b3) << 16);
+        }
+        unsigned char* bd = st + B_OFS + bt * 1024 + (bo * 16 + bn) * 16;
+        *reinterpret_cast<u32x4*>(bd) = u32x4{ow[0], ow[1], ow[2], ow[3]};
+        *reinterpret_cast<u32x4*>(bd + 256) = u32x4{ow[4], ow[5], ow[6], ow[7]};
+    };
+
+    f32x4 acc[TM][TN];
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn) acc[tm][tn] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    float s_cur[TN];
+    load(0);
+    store(0);
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) s_cur[tn] = sl[tn];
+    load(min(1, ngrp - 1));
+    __syncthreads();
+    for (int g = 0; g < ngrp; ++g) {
+        const unsigned char* st = smem + (g & 1) * STAGE;
+        bf16x8 ah[TM], al[TM], bw[TN];
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm) {
+            ah[tm] = *reinterpret_cast<const bf16x8*>(st + (wm * TM + tm) * 1024 + lane * 16);
+            al[tm] = *reinterpret_cast<const bf16x8*>(st + A_LO + (wm * TM + tm) * 1024 + lane * 16);
+        }
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn)
+            bw[tn] = *reinterpret_cast<const bf16x8*>(st + B_OFS + stile(tn) * 1024 + lane * 16);
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+            for (int tn = 0; tn < TN; ++tn) {
+                if constexpr (RS) {
+                    acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[tm], bw[tn], acc[tm][tn], 0, 0, 0);
+                    acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[tm], bw[tn], acc[tm][tn], 0, 0, 0);
+                } else {
+                    f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[tm], bw[tn], d, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[tm], bw[tn], d, 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) acc[tm][tn][i] = fmaf(d[i], s_cur[tn], acc[tm][tn][i]);
+                }
+            }
+        // group g + 1 into the other stage (its last reads ended at the
+        // previous barrier); past the end a copy of the last group nobody reads
+        store((g + 1) & 1);
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn) s_cur[tn] = sl[tn];
+        load(min(g + 2, ngrp - 1));
+        __syncthreads();
+    }
+
+    if constexpr (RS) {
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn) {
+            int r;
+            const int t = stile(tn);
+            if constexpr (EPI == EPI_SWIGLU)
+                r = t < 4 ? min(nout0 + t * 16 + (lane & 15), N - 1)
+                          : N + min(nout0 + (t - 4) * 16 + (lane & 15), N - 1);
+            else
+                r = min(nout0 + t * 16 + (lane & 15), N - 1);
+            const float s = sc[r];
+#pragma unroll
+            for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[tm][tn][i] *= s;
+        }
+    }
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+        for (int tn = 0; tn < OUT_TN; ++tn) {
+            const int n = nout0 + (wn * OUT_TN + tn) * 16 + (lane & 15);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int m = m0 + (wm * TM + tm) * 16 + (lane >> 4) * 4 + i;
+                if (m < M && n < N) {
+                    float* dst = y + (size_t)m * ldy + n;
+                    if constexpr (EPI == EPI_SWIGLU)
+                        *dst = silu_f(acc[tm][tn][i]) * acc[tm][tn + TN / 2][i];
+                    else if constexpr (EPI == EPI_RESID)
+                        *dst += acc[tm][tn][i];
+                    else
+                        *dst = acc[tm][tn][i];
+                }
+            }
+        }
+}
+
+// ---------------------------------------------------------------------------
 // M <= 64 (batched decode): weight streaming with K split across workgroups.
 //
 // A workgroup owns 64 weight rows (wave w: rows 16w..16w+15 as one MFMA
@@ -760,6 +960,16 @@ int launch_mm(const float* x, int ldx, const float* rs, const float* nw, const i
     return qlm_launch_status();
 }
 
+template <bool RS, int EPI>
+int launch_pf(const uint16_t* xh, int ldx, const int8_t* q, const float* sc, float* y, int ldy,
+              int M, int N, int K, const TileMap& tm, hipStream_t st) {
+    constexpr int BN_OUT = EPI == EPI_SWIGLU ? 64 : 128;
+    const dim3 grid((N + BN_OUT - 1) / BN_OUT, (M + 127) / 128);
+    hipLaunchKernelGGL((k_mm_pf<RS, EPI>), grid, dim3(kThreads), 0, st, xh, ldx, q, sc, y, ldy, M,
+                       N, K, tm);
+    return qlm_launch_status();
+}
+
 template <int EPI, bool NORM, bool XS>
 int launch_mm16(const float* x, int ldx, const float* rs, const float* nw, const uint16_t* w,
                 float* y, int ldy, int M, int N, int K, hipStream_t st) {
@@ -821,6 +1031,13 @@ int mm_run(const float* x, int ldx, float* rs, const float* nw, float eps, const
     uint16_t* xh = reinterpret_cast<uint16_t*>(part);
     const int rc = launch_split<NORM>(x, ldx, rs, nw, M, K, xh, st);
     if (rc != QLM_OK) return rc;
+    if constexpr (TL) {  // tile-major weights: the double-buffered operand-order form
+        if (epi == EPI_STORE)
+            return launch_pf<RS, EPI_STORE>(xh, K, q, sc, y, ldy, M, N, K, tm, st);
+        if (epi == EPI_RESID)
+            return launch_pf<RS, EPI_RESID>(xh, K, q, sc, y, ldy, M, N, K, tm, st);
+        return launch_pf<RS, EPI_SWIGLU>(xh, K, q, sc, y, ldy, M, N, K, tm, st);
+    }
     const float* xs = reinterpret_cast<const float*>(xh);
     if (epi == EPI_STORE)
         return launch_mm<2, 2, 1, 4, 4, RS, EPI_STORE, false, true, TL>(
