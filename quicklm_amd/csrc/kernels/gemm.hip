@@ -435,33 +435,38 @@ __global__ __launch_bounds__(kThreads) void k_mm_i8(const float* __restrict__ x,
 //   - addresses advance by constants (a group is 512 bytes of a weight
 //     fragment and 16 scales), none recomputed in the loop;
 //   - every load unconditional (clamped rows, tiles and groups).
-// Workgroup: 4 waves (2 x 2), each 64 activation rows x 64 staged weight rows
-// (SwiGLU: 32 gate + the matching 32 up rows); 128 x 128 staged per group.
-template <bool RS, int EPI>
-__global__ __launch_bounds__(kThreads, 2) void k_mm_pf(const uint16_t* __restrict__ xh, int ldx,
+// Workgroup: 2 x WNW waves, each 64 activation rows x 64 staged weight rows
+// (SwiGLU: 32 gate + the matching 32 up rows); 128 x 64 WNW staged per group
+// (WNW = 4 halves the activation bytes a product against WNW = 2).
+template <bool RS, int EPI, int WNW>
+__global__ __launch_bounds__(128 * WNW, WNW == 2 ? 2 : 1) void k_mm_pf(
+    const uint16_t* __restrict__ xh, int ldx,
                                                        const int8_t* __restrict__ q,
                                                        const float* __restrict__ sc,
                                                        float* __restrict__ y, int ldy, int M,
                                                        int N, int K, TileMap tmap) {
     constexpr int TM = 4, TN = 4;
+    constexpr int NTH = 128 * WNW;            // threads
+    constexpr int NBT = 4 * WNW;              // staged weight tiles
+    constexpr int AS = 512 / NTH;             // activation slots a thread, each plane
     constexpr int OUT_TN = EPI == EPI_SWIGLU ? TN / 2 : TN;
-    constexpr int BN_OUT = 2 * OUT_TN * 16;
-    constexpr int A_LO = 8192, B_OFS = 16384, STAGE = 24576;
+    constexpr int BN_OUT = WNW * OUT_TN * 16;
+    constexpr int A_LO = 8192, B_OFS = 16384, STAGE = 16384 + NBT * 1024;
     __shared__ __attribute__((aligned(16))) unsigned char smem[2 * STAGE];
     typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / WNW, wn = wave % WNW;
     const int m0 = blockIdx.y * 128;
     const int nout0 = blockIdx.x * BN_OUT;
     const int ngrp = K >> 5;
     const size_t plane = (size_t)M * ldx;
 
-    // staged weight tile t (0..7) -> tile of the tile-major matrix (clamped)
+    // staged weight tile t (0..NBT-1) -> tile of the tile-major matrix (clamped)
     auto gtile = [&](int t) -> int {
         if constexpr (EPI == EPI_SWIGLU) {
-            const int th = min(nout0 / 16 + (t & 3), tmap.tiles_half - 1);
-            return (t >> 2) * tmap.tiles_half + th;
+            const int th = min(nout0 / 16 + t % (NBT / 2), tmap.tiles_half - 1);
+            return (t / (NBT / 2)) * tmap.tiles_half + th;
         } else {
             return min(nout0 / 16 + t, tmap.tiles_half - 1);
         }
@@ -469,17 +474,17 @@ __global__ __launch_bounds__(kThreads, 2) void k_mm_pf(const uint16_t* __restric
     // a wave's tile tn -> staged tile
     auto stile = [&](int tn) -> int {
         if constexpr (EPI == EPI_SWIGLU)
-            return tn < TN / 2 ? wn * (TN / 2) + tn : 4 + wn * (TN / 2) + (tn - TN / 2);
+            return tn < TN / 2 ? wn * (TN / 2) + tn : NBT / 2 + wn * (TN / 2) + (tn - TN / 2);
         else
             return wn * TN + tn;
     };
 
-    // activation operand slots s = tid, tid + 256 of 8 tiles x 64 lanes:
+    // activation operand slots s = tid + NTH u of 8 tiles x 64 lanes:
     // row 16 (s >> 6) + (s & 15), columns 8 ((s >> 4) & 3) .. + 7 of a group
-    const uint16_t* ap[2];
+    const uint16_t* ap[AS];
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-        const int sl_ = tid + 256 * u;
+    for (int u = 0; u < AS; ++u) {
+        const int sl_ = tid + NTH * u;
         const int row = min(m0 + 16 * (sl_ >> 6) + (sl_ & 15), M - 1);
         ap[u] = xh + (size_t)row * ldx + 8 * ((sl_ >> 4) & 3);
     }
@@ -494,12 +499,12 @@ __global__ __launch_bounds__(kThreads, 2) void k_mm_pf(const uint16_t* __restric
     for (int tn = 0; tn < TN; ++tn)
         sp[tn] = sc + (size_t)gtile(stile(tn)) * tmap.nblk64 * 32 + (lane & 15);
 
-    u32x4 xa_h[2], xa_l[2];
+    u32x4 xa_h[AS], xa_l[AS];
     int4 wb;
     float sl[TN];
     auto load = [&](int g) {
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
+        for (int u = 0; u < AS; ++u) {
             xa_h[u] = *reinterpret_cast<const u32x4*>(ap[u] + 32 * g);
             xa_l[u] = *reinterpret_cast<const u32x4*>(ap[u] + plane + 32 * g);
         }
@@ -512,9 +517,9 @@ __global__ __launch_bounds__(kThreads, 2) void k_mm_pf(const uint16_t* __restric
     auto store = [&](int stage) {
         unsigned char* st = smem + stage * STAGE;
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            *reinterpret_cast<u32x4*>(st + (tid + 256 * u) * 16) = xa_h[u];
-            *reinterpret_cast<u32x4*>(st + A_LO + (tid + 256 * u) * 16) = xa_l[u];
+        for (int u = 0; u < AS; ++u) {
+            *reinterpret_cast<u32x4*>(st + (tid + NTH * u) * 16) = xa_h[u];
+            *reinterpret_cast<u32x4*>(st + A_LO + (tid + NTH * u) * 16) = xa_l[u];
         }
         // 16 int8 -> 16 bf16 (exact): columns 0-7 to operand lane bo*16 + bn,
         // 8-15 to the next k-octet's lane
@@ -587,8 +592,8 @@ __global__ __launch_bounds__(kThreads, 2) void k_mm_pf(const uint16_t* __restric
             int r;
             const int t = stile(tn);
             if constexpr (EPI == EPI_SWIGLU)
-                r = t < 4 ? min(nout0 + t * 16 + (lane & 15), N - 1)
-                          : N + min(nout0 + (t - 4) * 16 + (lane & 15), N - 1);
+                r = t < NBT / 2 ? min(nout0 + t * 16 + (lane & 15), N - 1)
+                                : N + min(nout0 + (t - NBT / 2) * 16 + (lane & 15), N - 1);
             else
                 r = min(nout0 + t * 16 + (lane & 15), N - 1);
             const float s = sc[r];
@@ -960,13 +965,13 @@ int launch_mm(const float* x, int ldx, const float* rs, const float* nw, const i
     return qlm_launch_status();
 }
 
-template <bool RS, int EPI>
+template <bool RS, int EPI, int WNW = 4>
 int launch_pf(const uint16_t* xh, int ldx, const int8_t* q, const float* sc, float* y, int ldy,
               int M, int N, int K, const TileMap& tm, hipStream_t st) {
-    constexpr int BN_OUT = EPI == EPI_SWIGLU ? 64 : 128;
+    constexpr int BN_OUT = (EPI == EPI_SWIGLU ? 32 : 64) * WNW;
     const dim3 grid((N + BN_OUT - 1) / BN_OUT, (M + 127) / 128);
-    hipLaunchKernelGGL((k_mm_pf<RS, EPI>), grid, dim3(kThreads), 0, st, xh, ldx, q, sc, y, ldy, M,
-                       N, K, tm);
+    hipLaunchKernelGGL((k_mm_pf<RS, EPI, WNW>), grid, dim3(128 * WNW), 0, st, xh, ldx, q, sc, y,
+                       ldy, M, N, K, tm);
     return qlm_launch_status();
 }
 
