@@ -38,6 +38,9 @@ extern "C" {
 
 const char* qlm_error_string(int status);
 int qlm_device_count(int* count);
+/* Makes `device` current and loads every kernel code object of the library
+ * on it (otherwise each kernel file's code object loads at its first launch,
+ * 4-20 ms each, e.g. inside a first prefill). */
 int qlm_set_device(int device);
 int qlm_device_name(char* buf, int len);
 /* Free and total device memory of the current device (hipMemGetInfo). */

@@ -1158,3 +1158,11 @@ extern "C" int qlm_gqa_prefill(float* qkv, int ldqkv, const float* q_norm, const
     }
     return QLM_OK;
 }
+
+// Loads this file's code object on the current device now; the runtime
+// otherwise loads it at the first launch of one of its kernels (4-20 ms,
+// measured inside a first prefill or decode step).
+hipError_t qlm_load_attention() {
+    hipFuncAttributes a;
+    return hipFuncGetAttributes(&a, reinterpret_cast<const void*>((k_attn_combine<128, 1>)));
+}

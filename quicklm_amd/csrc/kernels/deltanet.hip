@@ -582,3 +582,11 @@ extern "C" int qlm_deltanet_prefill(const float* proj, int ldp, int T, float* co
                        H);
     return qlm_launch_status();
 }
+
+// Loads this file's code object on the current device now; the runtime
+// otherwise loads it at the first launch of one of its kernels (4-20 ms,
+// measured inside a first prefill or decode step).
+hipError_t qlm_load_deltanet() {
+    hipFuncAttributes a;
+    return hipFuncGetAttributes(&a, reinterpret_cast<const void*>(k_deltanet_cols));
+}

@@ -496,3 +496,11 @@ extern "C" int qlm_deltanet_prefill_chunked(const float* proj, int ldp, int T, f
                        out, ldo, H, conv_state, p0);
     return qlm_launch_status();
 }
+
+// Loads this file's code object on the current device now; the runtime
+// otherwise loads it at the first launch of one of its kernels (4-20 ms,
+// measured inside a first prefill or decode step).
+hipError_t qlm_load_deltanet_chunk() {
+    hipFuncAttributes a;
+    return hipFuncGetAttributes(&a, reinterpret_cast<const void*>(k_dn_chunk_prep));
+}

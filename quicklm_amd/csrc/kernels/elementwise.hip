@@ -289,3 +289,11 @@ extern "C" int qlm_embed_tokens(const float* table, int vocab, int H, const int*
                        ld_tokens, pos, out, ldo, vocab);
     return qlm_launch_status();
 }
+
+// Loads this file's code object on the current device now; the runtime
+// otherwise loads it at the first launch of one of its kernels (4-20 ms,
+// measured inside a first prefill or decode step).
+hipError_t qlm_load_elementwise() {
+    hipFuncAttributes a;
+    return hipFuncGetAttributes(&a, reinterpret_cast<const void*>(k_fill_u8));
+}

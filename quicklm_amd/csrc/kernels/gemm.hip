@@ -1168,3 +1168,11 @@ extern "C" int qlm_matmul_i8_tm(const float* x, int ldx, const float* norm_w, fl
     return matmul_i8_entry<true>(x, ldx, norm_w, eps, q_tiles, s_tiles, group, y, ldy, M, N, K,
                                  epilogue, work, work_bytes, stream);
 }
+
+// Loads this file's code object on the current device now; the runtime
+// otherwise loads it at the first launch of one of its kernels (4-20 ms,
+// measured inside a first prefill or decode step).
+hipError_t qlm_load_gemm() {
+    hipFuncAttributes a;
+    return hipFuncGetAttributes(&a, reinterpret_cast<const void*>(k_row_rs));
+}

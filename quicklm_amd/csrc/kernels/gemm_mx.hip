@@ -796,3 +796,11 @@ extern "C" int qlm_matmul_i8_rows64(const float* x, int ldx, const float* norm_w
             return launch_r64<16>(p, dg, de, q_tiles, s_rows, y, ldy, part, M, N, K, epilogue, st);
     }
 }
+
+// Loads this file's code object on the current device now; the runtime
+// otherwise loads it at the first launch of one of its kernels (4-20 ms,
+// measured inside a first prefill or decode step).
+hipError_t qlm_load_gemm_mx() {
+    hipFuncAttributes a;
+    return hipFuncGetAttributes(&a, reinterpret_cast<const void*>((k_act_digits<false>)));
+}

@@ -763,3 +763,11 @@ extern "C" int qlm_matmul_i8_t(const float* x, int ldx, const float* norm_w, flo
     return t_run(c, x, ldx, norm_w, eps, q_tiles, s_tiles, y, ldy, M, N, K, epilogue, work,
                  work_bytes, as_stream(stream));
 }
+
+// Loads this file's code object on the current device now; the runtime
+// otherwise loads it at the first launch of one of its kernels (4-20 ms,
+// measured inside a first prefill or decode step).
+hipError_t qlm_load_gemm_t() {
+    hipFuncAttributes a;
+    return hipFuncGetAttributes(&a, reinterpret_cast<const void*>((k_mm_t<8, 8, 1, false>)));
+}

@@ -619,3 +619,11 @@ extern "C" int qlm_matmul_w(const float* x, int ldx, const float* norm_w, float 
                   : w_dispatch<float>(x, ldx, norm_w, eps, static_cast<const float*>(w), y, ldy,
                                       M, N, K, epilogue, work, work_bytes, st);
 }
+
+// Loads this file's code object on the current device now; the runtime
+// otherwise loads it at the first launch of one of its kernels (4-20 ms,
+// measured inside a first prefill or decode step).
+hipError_t qlm_load_gemm_w() {
+    hipFuncAttributes a;
+    return hipFuncGetAttributes(&a, reinterpret_cast<const void*>(k_w_rows));
+}

@@ -1656,3 +1656,11 @@ extern "C" int qlm_lm_head_greedy_mx4(const float* x, const float* norm_w, float
                        greedy_tail(work, tokens, ld_tokens, pos, prompt_len, embed, H, V, h_next),
                        true);
 }
+
+// Loads this file's code object on the current device now; the runtime
+// otherwise loads it at the first launch of one of its kernels (4-20 ms,
+// measured inside a first prefill or decode step).
+hipError_t qlm_load_gemv() {
+    hipFuncAttributes a;
+    return hipFuncGetAttributes(&a, reinterpret_cast<const void*>(k_greedy_finish));
+}

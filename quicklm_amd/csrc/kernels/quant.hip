@@ -171,3 +171,11 @@ extern "C" int qlm_quantize_q4_bf16(const uint16_t* w, int rows, int K, uint8_t*
                                     float* scales, int8_t* q8, void* stream) {
     return quant4_dispatch<uint16_t>(w, rows, K, q4, scales, q8, stream);
 }
+
+// Loads this file's code object on the current device now; the runtime
+// otherwise loads it at the first launch of one of its kernels (4-20 ms,
+// measured inside a first prefill or decode step).
+hipError_t qlm_load_quant() {
+    hipFuncAttributes a;
+    return hipFuncGetAttributes(&a, reinterpret_cast<const void*>((k_quant_g32<float>)));
+}

@@ -31,7 +31,30 @@ extern "C" int qlm_device_count(int* count) {
     return QLM_OK;
 }
 
-extern "C" int qlm_set_device(int device) { return qlm_status(hipSetDevice(device)); }
+// One kernel of each kernel file (defined there): asking for its attributes
+// loads that file's code object.
+hipError_t qlm_load_attention();
+hipError_t qlm_load_deltanet();
+hipError_t qlm_load_deltanet_chunk();
+hipError_t qlm_load_elementwise();
+hipError_t qlm_load_gemm();
+hipError_t qlm_load_gemm_mx();
+hipError_t qlm_load_gemm_t();
+hipError_t qlm_load_gemm_w();
+hipError_t qlm_load_gemv();
+hipError_t qlm_load_quant();
+
+// Selects the device and loads every kernel file's code object on it, so no
+// first launch (of a prefill, a decode step, a graph capture) pays the load.
+extern "C" int qlm_set_device(int device) {
+    hipError_t e = hipSetDevice(device);
+    if (e != hipSuccess) return qlm_status(e);
+    for (hipError_t (*load)() : {qlm_load_attention, qlm_load_deltanet, qlm_load_deltanet_chunk, qlm_load_elementwise, qlm_load_gemm, qlm_load_gemm_mx, qlm_load_gemm_t, qlm_load_gemm_w, qlm_load_gemv, qlm_load_quant}) {
+        e = load();
+        if (e != hipSuccess) return qlm_status(e);
+    }
+    return QLM_OK;
+}
 
 extern "C" int qlm_device_name(char* buf, int len) {
     if (!buf || len <= 0) return QLM_ERR_ARG;
