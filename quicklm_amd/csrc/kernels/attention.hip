@@ -550,6 +550,176 @@ __global__ __launch_bounds__(kThreads) void k_gqa_prep_rows(
     }
 }
 
+// ---- prefill attention, head_dim 128, fp32 cache, on the fp32 matrix cores ----
+//
+// One launch per prefill pass, causal, no per-chunk records and no merge: a
+// workgroup owns 16 consecutive prompt rows and one kv head, wave w the query
+// head g G + w, and walks the keys 0 .. (its last row's position) in tiles of
+// 16 with an online softmax per row (attention.cpp:54-82 per row: the scores
+// q . k / sqrt(hd), softmax, the weighted sum of V). Both products run on
+// v_mfma_f32_16x16x4f32 (A lane l: row l % 16, k l / 16; B lane l: k l / 16,
+// column l % 16; D lane l: rows 4 (l / 16) .. +3, column l % 16):
+//   S^T = K Q^T: A = 16 keys, B = Q^T of the wave's 16 rows, the head's 128
+//     elements split as 32 k-steps of element 32 (l / 16) + s, so a lane
+//     loads 32 contiguous floats of its key (and of its query row, once);
+//     lane (qd, n) then holds the scores of row n for keys 4 qd .. 4 qd + 3;
+//   O^T += V^T P^T: k-step j takes keys 4 qd + j, which is where those
+//     scores already are, so the probabilities feed the B operand from the
+//     registers that computed them; A lane (qd, n) reads V[key][16 c + n].
+// Lane (qd, n) ends with row n's outputs 16 c + 4 qd .. + 3 for c = 0..7.
+// Key rows past the tile's last position are clamped to it (their
+// probabilities are 0 and the cache beyond is not written yet).
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// maximum / sum over lanes l, l ^ 16, l ^ 32, l ^ 48 (the four lane groups of
+// a 16-lane column), on lane swaps instead of LDS permutes
+__device__ __forceinline__ float cols_max(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                    false);
+    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                    false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float cols_sum(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                    false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                    false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+template <int G>
+__global__ __launch_bounds__(G * QLM_WAVE) void k_attn_pf(const float* __restrict__ qkv, int ldq,
+                                                          int qhs, const float* __restrict__ kc,
+                                                          const float* __restrict__ vc, int n_kv,
+                                                          int p0, int T, int gated,
+                                                          float* __restrict__ out, int ldo,
+                                                          float scale) {
+    constexpr int HD = 128;
+    const int t0 = (gridDim.x - 1 - blockIdx.x) * 16;  // longest tiles first
+    const int g = blockIdx.y;
+    const int lane = threadIdx.x & (QLM_WAVE - 1), w = threadIdx.x / QLM_WAVE;
+    const int h = g * G + w;
+    const int qd = lane >> 4, n = lane & 15;
+    const int tq = min(t0 + n, T - 1);  // this lane's row (clamped past the pass)
+    const int qpos = p0 + tq;
+    const int last = p0 + min(t0 + 15, T - 1);  // the tile's last position
+    const int ntiles = last / 16 + 1;
+
+    float qv[32];
+    {
+        const float4* qr =
+            reinterpret_cast<const float4*>(qkv + (size_t)tq * ldq + (size_t)h * qhs + 32 * qd);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float4 x = qr[j];
+            qv[4 * j] = x.x;
+            qv[4 * j + 1] = x.y;
+            qv[4 * j + 2] = x.z;
+            qv[4 * j + 3] = x.w;
+        }
+    }
+    f32x4 o[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) o[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m = -INFINITY, l = 0.0f;
+    const size_t kstride = (size_t)n_kv * HD;
+
+    // K rows (lane: key k0 + n, elements 32 qd ..) and V elements (keys
+    // k0 + 4 qd + j, columns 16 c + n) of a tile; the next tile's are
+    // requested before this one's products
+    float kv[32], vv[4][8];
+    auto load_tile = [&](int k0, float (&kd)[32], float (&vd)[4][8]) {
+        const float4* kr = reinterpret_cast<const float4*>(
+            kc + (size_t)min(k0 + n, last) * kstride + (size_t)g * HD + 32 * qd);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float4 x = kr[j];
+            kd[4 * j] = x.x;
+            kd[4 * j + 1] = x.y;
+            kd[4 * j + 2] = x.z;
+            kd[4 * j + 3] = x.w;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float* vr = vc + (size_t)min(k0 + 4 * qd + j, last) * kstride + (size_t)g * HD + n;
+#pragma unroll
+            for (int c = 0; c < 8; ++c) vd[j][c] = vr[16 * c];
+        }
+    };
+    float kn[32], vn[4][8];
+    // tile kt from (kd, vd) while tile kt + 1 is requested into (kx, vx);
+    // two register sets in turn, so no copy waits for the new loads
+    auto step = [&](int kt, float (&kd)[32], float (&vd)[4][8], float (&kx)[32],
+                    float (&vx)[4][8]) {
+        const int k0 = kt * 16;
+        load_tile(min(k0 + 16, 16 * (ntiles - 1)), kx, vx);  // past the end: the last tile again
+        __builtin_amdgcn_sched_barrier(0);
+        // S^T: two independent chains over the 32 k-steps
+        f32x4 s0 = f32x4{0.f, 0.f, 0.f, 0.f}, s1 = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 32; s += 2) {
+            s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(kd[s], qv[s], s0, 0, 0, 0);
+            s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(kd[s + 1], qv[s + 1], s1, 0, 0, 0);
+        }
+        float sc[4], tm = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int key = k0 + 4 * qd + i;
+            sc[i] = key <= qpos ? (s0[i] + s1[i]) * scale : -INFINITY;
+            tm = fmaxf(tm, sc[i]);
+        }
+        // the row's maximum over the 16 keys (lanes n, n+16, n+32, n+48)
+        tm = cols_max(tm);
+        const float mn = fmaxf(m, tm);
+        const float alpha = expf(m - mn);  // 0 on the first tile
+        float p[4], ps = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            p[i] = expf(sc[i] - mn);
+            ps += p[i];
+        }
+        ps = cols_sum(ps);
+        l = fmaf(l, alpha, ps);
+        m = mn;
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[c][i] *= alpha;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int c = 0; c < 8; ++c)
+                o[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(vd[j][c], p[j], o[c], 0, 0, 0);
+    };
+    load_tile(0, kv, vv);
+    int kt = 0;
+    for (; kt + 2 <= ntiles; kt += 2) {
+        step(kt, kv, vv, kn, vn);
+        step(kt + 1, kn, vn, kv, vv);
+    }
+    if (kt < ntiles) step(kt, kv, vv, kn, vn);
+
+    if (t0 + n >= T) return;
+    const float* grow = qkv + (size_t)tq * ldq + (size_t)h * qhs + HD;
+    float* dst = out + (size_t)tq * ldo + (size_t)h * HD;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+        const int e = 16 * c + 4 * qd;
+        float r[4] = {o[c][0] / l, o[c][1] / l, o[c][2] / l, o[c][3] / l};
+        if (gated) {
+            const float4 gg = *reinterpret_cast<const float4*>(grow + e);
+            r[0] *= 1.0f / (1.0f + expf(-gg.x));
+            r[1] *= 1.0f / (1.0f + expf(-gg.y));
+            r[2] *= 1.0f / (1.0f + expf(-gg.z));
+            r[3] *= 1.0f / (1.0f + expf(-gg.w));
+        }
+        *reinterpret_cast<float4*>(dst + e) = make_float4(r[0], r[1], r[2], r[3]);
+    }
+}
+
 // ---- bf16 K/V on the matrix cores (the isolated attention, kv_dtype 1) ----
 //
 // One wave per workgroup owns a chunk of 32 * spw positions of one (kv head
@@ -1133,6 +1303,21 @@ extern "C" int qlm_gqa_prefill(float* qkv, int ldqkv, const float* q_norm, const
                            n_q, n_kv, p0);
     int rc = qlm_launch_status();
     if (rc != QLM_OK) return rc;
+    if (hd == 128 && (ldqkv % 4) == 0 && (ldo % 4) == 0 && (qstride % 4) == 0) {
+        const dim3 grid((T + 15) / 16, n_kv);
+        const float scale = 1.0f / sqrtf(128.0f);
+#define QLM_ATTN_PF(GG)                                                                         \
+        if (G == GG) {                                                                          \
+            hipLaunchKernelGGL((k_attn_pf<GG>), grid, dim3(GG * QLM_WAVE), 0, st, qkv, ldqkv,   \
+                               qstride, k_cache, v_cache, n_kv, p0, T, gated, out, ldo, scale); \
+            return qlm_launch_status();                                                         \
+        }
+        QLM_ATTN_PF(1)
+        QLM_ATTN_PF(2)
+        QLM_ATTN_PF(4)
+        QLM_ATTN_PF(8)
+#undef QLM_ATTN_PF
+    }
     for (int s0 = 0; s0 < T; s0 += kPrefillSlice) {
         const int rows = T - s0 < kPrefillSlice ? T - s0 : kPrefillSlice;
         float* q = qkv + (size_t)s0 * ldqkv;

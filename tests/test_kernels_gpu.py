@@ -751,10 +751,17 @@ def test_deltanet_prefill_chunked(hip, orc, rng, p0, T):
 
 @pytest.mark.parametrize("n_q,n_kv,hd,rot,gated,p0,T", [(16, 4, 128, 32, 1, 0, 300),
                                                         (16, 4, 128, 32, 1, 37, 90),
-                                                        (16, 2, 256, 64, 0, 10, 40)])
+                                                        (16, 2, 256, 64, 0, 10, 40),
+                                                        (8, 2, 128, 64, 0, 0, 127),
+                                                        (16, 16, 128, 32, 1, 5, 33),
+                                                        (16, 8, 128, 128, 0, 250, 17),
+                                                        (16, 2, 128, 32, 1, 100, 499)])
 def test_gqa_prefill(hip, orc, rng, n_q, n_kv, hd, rot, gated, p0, T):
-    """T prompt rows at positions p0.. (two 256-row slices in the first case)
-    == the oracle row by row: outputs and the cache rows they write."""
+    """T prompt rows at positions p0.. == the oracle row by row: outputs and
+    the cache rows they write. head_dim 128 runs the one-launch tiled form
+    (1, 2, 4 and 8 query heads a kv head, ragged last tiles, passes after
+    earlier ones); 256 the per-row chunks and their merge (two 256-row
+    slices)."""
     max_seq, theta = 600, 1e6
     qs = (2 if gated else 1) * hd
     ld = n_q * qs + 2 * n_kv * hd
