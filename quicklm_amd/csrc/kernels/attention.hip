@@ -627,36 +627,51 @@ __global__ __launch_bounds__(G * QLM_WAVE) void k_attn_pf(const float* __restric
     float m = -INFINITY, l = 0.0f;
     const size_t kstride = (size_t)n_kv * HD;
 
-    // K rows (lane: key k0 + n, elements 32 qd ..) and V elements (keys
-    // k0 + 4 qd + j, columns 16 c + n) of a tile; the next tile's are
-    // requested before this one's products
-    float kv[32], vv[4][8];
-    auto load_tile = [&](int k0, float (&kd)[32], float (&vd)[4][8]) {
-        const float4* kr = reinterpret_cast<const float4*>(
-            kc + (size_t)min(k0 + n, last) * kstride + (size_t)g * HD + 32 * qd);
+    // The workgroup stages each 16-key tile of K and V once in LDS (rows
+    // padded to 132 floats: the 16 lanes of a row read distinct banks), two
+    // buffers: tile kt + 1 goes from registers to the other buffer while tile
+    // kt is multiplied, and tile kt + 2 is requested; one barrier a tile.
+    constexpr int NTH = G * QLM_WAVE, RS = 132, NL = 512 / NTH;
+    __shared__ __align__(16) float kvs[2][2][16 * RS];
+    const int tid = threadIdx.x;
+    f32x4 sk[NL], sv[NL];  // vector types: an aggregate copy to LDS would keep them in scratch
+    auto fetch = [&](int k0) {
+#pragma unroll
+        for (int u = 0; u < NL; ++u) {
+            const int i = tid + NTH * u, key = min(k0 + (i >> 5), last), c4 = i & 31;
+            const size_t off = (size_t)key * kstride + (size_t)g * HD + 4 * c4;
+            sk[u] = *reinterpret_cast<const f32x4*>(kc + off);
+            sv[u] = *reinterpret_cast<const f32x4*>(vc + off);
+        }
+    };
+    auto stage = [&](int buf) {
+#pragma unroll
+        for (int u = 0; u < NL; ++u) {
+            const int i = tid + NTH * u, r = i >> 5, c4 = i & 31;
+            *reinterpret_cast<f32x4*>(&kvs[buf][0][r * RS + 4 * c4]) = sk[u];
+            *reinterpret_cast<f32x4*>(&kvs[buf][1][r * RS + 4 * c4]) = sv[u];
+        }
+    };
+    fetch(0);
+    stage(0);
+    fetch(min(16, 16 * (ntiles - 1)));
+    __syncthreads();
+    for (int kt = 0; kt < ntiles; ++kt) {
+        const int k0 = kt * 16, buf = kt & 1;
+        // K row n of the tile, elements 32 qd .. + 31; V[key 4 qd + j][16 c + n]
+        float kd[32], vd[4][8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            const float4 x = kr[j];
+            const float4 x = *reinterpret_cast<const float4*>(&kvs[buf][0][n * RS + 32 * qd + 4 * j]);
             kd[4 * j] = x.x;
             kd[4 * j + 1] = x.y;
             kd[4 * j + 2] = x.z;
             kd[4 * j + 3] = x.w;
         }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const float* vr = vc + (size_t)min(k0 + 4 * qd + j, last) * kstride + (size_t)g * HD + n;
+        for (int j = 0; j < 4; ++j)
 #pragma unroll
-            for (int c = 0; c < 8; ++c) vd[j][c] = vr[16 * c];
-        }
-    };
-    float kn[32], vn[4][8];
-    // tile kt from (kd, vd) while tile kt + 1 is requested into (kx, vx);
-    // two register sets in turn, so no copy waits for the new loads
-    auto step = [&](int kt, float (&kd)[32], float (&vd)[4][8], float (&kx)[32],
-                    float (&vx)[4][8]) {
-        const int k0 = kt * 16;
-        load_tile(min(k0 + 16, 16 * (ntiles - 1)), kx, vx);  // past the end: the last tile again
-        __builtin_amdgcn_sched_barrier(0);
+            for (int c = 0; c < 8; ++c) vd[j][c] = kvs[buf][1][(4 * qd + j) * RS + 16 * c + n];
         // S^T: two independent chains over the 32 k-steps
         f32x4 s0 = f32x4{0.f, 0.f, 0.f, 0.f}, s1 = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -693,14 +708,10 @@ __global__ __launch_bounds__(G * QLM_WAVE) void k_attn_pf(const float* __restric
 #pragma unroll
             for (int c = 0; c < 8; ++c)
                 o[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(vd[j][c], p[j], o[c], 0, 0, 0);
-    };
-    load_tile(0, kv, vv);
-    int kt = 0;
-    for (; kt + 2 <= ntiles; kt += 2) {
-        step(kt, kv, vv, kn, vn);
-        step(kt + 1, kn, vn, kv, vv);
+        stage(buf ^ 1);  // past the end: a copy of the last tile nobody reads
+        fetch(min(k0 + 32, 16 * (ntiles - 1)));
+        __syncthreads();
     }
-    if (kt < ntiles) step(kt, kv, vv, kn, vn);
 
     if (t0 + n >= T) return;
     const float* grow = qkv + (size_t)tq * ldq + (size_t)h * qhs + HD;
