@@ -1037,11 +1037,19 @@ int mm_run(const float* x, int ldx, float* rs, const float* nw, float eps, const
     const int rc = launch_split<NORM>(x, ldx, rs, nw, M, K, xh, st);
     if (rc != QLM_OK) return rc;
     if constexpr (TL) {  // tile-major weights: the double-buffered operand-order form
+        // 256 weight rows a workgroup where that still gives 256 workgroups
+        // or more, else 128 (the 2560-column projections: 160 workgroups
+        // of the wide form would leave 96 CUs idle)
+        const int bn = epi == EPI_SWIGLU ? 128 : 256;
+        const bool wide = (long)((N + bn - 1) / bn) * ((M + 127) / 128) >= 256;
         if (epi == EPI_STORE)
-            return launch_pf<RS, EPI_STORE>(xh, K, q, sc, y, ldy, M, N, K, tm, st);
+            return wide ? launch_pf<RS, EPI_STORE, 4>(xh, K, q, sc, y, ldy, M, N, K, tm, st)
+                        : launch_pf<RS, EPI_STORE, 2>(xh, K, q, sc, y, ldy, M, N, K, tm, st);
         if (epi == EPI_RESID)
-            return launch_pf<RS, EPI_RESID>(xh, K, q, sc, y, ldy, M, N, K, tm, st);
-        return launch_pf<RS, EPI_SWIGLU>(xh, K, q, sc, y, ldy, M, N, K, tm, st);
+            return wide ? launch_pf<RS, EPI_RESID, 4>(xh, K, q, sc, y, ldy, M, N, K, tm, st)
+                        : launch_pf<RS, EPI_RESID, 2>(xh, K, q, sc, y, ldy, M, N, K, tm, st);
+        return wide ? launch_pf<RS, EPI_SWIGLU, 4>(xh, K, q, sc, y, ldy, M, N, K, tm, st)
+                    : launch_pf<RS, EPI_SWIGLU, 2>(xh, K, q, sc, y, ldy, M, N, K, tm, st);
     }
     const float* xs = reinterpret_cast<const float*>(xh);
     if (epi == EPI_STORE)
