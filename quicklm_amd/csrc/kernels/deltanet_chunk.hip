@@ -314,41 +314,41 @@ __global__ __launch_bounds__(256) void k_dn_chunk_inter(
         const bool tv = tr < nt;
         if (tid < kC) gs[tid] = tid < nt ? pg : 0.0f;
         load_g(cn);
-        // W = U - Wk S: wave w rows 16w..16w+15
-        f32x4 wa = f32x4{0.f, 0.f, 0.f, 0.f}, wb = wa;
+        // W = U - Wk S: wave w rows 16w..16w+15 (four independent chains:
+        // a chain of dependent products waits out each one's latency)
+        f32x4 wc[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) wc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kb = 0; kb < 8; ++kb) {
             const float a[4] = {pw[kb].x, pw[kb].y, pw[kb].z, pw[kb].w};
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const float b = Ss[(16 * kb + 4 * l4 + j) * SP + l16];
-                if (kb & 1)
-                    wb = mma(tv ? a[j] : 0.0f, b, wb);
-                else
-                    wa = mma(tv ? a[j] : 0.0f, b, wa);
+                wc[j] = mma(tv ? a[j] : 0.0f, b, wc[j]);
             }
         }
         load_w(cn);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int t = wave * 16 + l4 * 4 + i;
-            Ws[t * SP + l16] = t < nt ? pu[i] - (wa[i] + wb[i]) : 0.0f;
+            Ws[t * SP + l16] = t < nt ? pu[i] - ((wc[0][i] + wc[1][i]) + (wc[2][i] + wc[3][i])) : 0.0f;
         }
         load_u(cn);
         __syncthreads();
         // O = (gamma_t (Q S) + Mq W) / sqrt(d)
         {
-            f32x4 qa = f32x4{0.f, 0.f, 0.f, 0.f}, qb = qa, mw = qa;
+            f32x4 qc[4], mc[2];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) qc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+            mc[0] = mc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int kb = 0; kb < 8; ++kb) {
                 const float a[4] = {pq[kb].x, pq[kb].y, pq[kb].z, pq[kb].w};
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const float b = Ss[(16 * kb + 4 * l4 + j) * SP + l16];
-                    if (kb & 1)
-                        qb = mma(tv ? a[j] : 0.0f, b, qb);
-                    else
-                        qa = mma(tv ? a[j] : 0.0f, b, qa);
+                    qc[j] = mma(tv ? a[j] : 0.0f, b, qc[j]);
                 }
             }
 #pragma unroll
@@ -356,7 +356,14 @@ __global__ __launch_bounds__(256) void k_dn_chunk_inter(
                 const float a[4] = {pm[kb].x, pm[kb].y, pm[kb].z, pm[kb].w};
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
-                    mw = mma(tv ? a[j] : 0.0f, Ws[(16 * kb + 4 * l4 + j) * SP + l16], mw);
+                    mc[j & 1] = mma(tv ? a[j] : 0.0f, Ws[(16 * kb + 4 * l4 + j) * SP + l16], mc[j & 1]);
+            }
+            f32x4 qa, qb, mw;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                qa[i] = qc[0][i] + qc[2][i];
+                qb[i] = qc[1][i] + qc[3][i];
+                mw[i] = mc[0][i] + mc[1][i];
             }
             load_q(cn);
             load_m(cn);
@@ -376,14 +383,22 @@ __global__ __launch_bounds__(256) void k_dn_chunk_inter(
             for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) sacc[tt][i] *= ge;
+            f32x4 du[2][2];
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) du[tt][0] = du[tt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int s4 = 0; s4 < 16; ++s4) {
                 const int t = 4 * s4 + l4;
                 const bool ok = t < nt;
                 const float b = ok ? Ws[t * SP + l16] * expf(gend - gs[t]) : 0.0f;
 #pragma unroll
-                for (int tt = 0; tt < 2; ++tt) sacc[tt] = mma(ok ? pk[tt][s4] : 0.0f, b, sacc[tt]);
+                for (int tt = 0; tt < 2; ++tt)
+                    du[tt][s4 & 1] = mma(ok ? pk[tt][s4] : 0.0f, b, du[tt][s4 & 1]);
             }
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) sacc[tt][i] += du[tt][0][i] + du[tt][1][i];
             load_k(cn);
         }
         __syncthreads();  // every read of Ss, Ws and gs of this chunk is done
