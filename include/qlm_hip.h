@@ -182,10 +182,12 @@ int qlm_matmul_i8_tm(const float* x, int ldx, const float* norm_w, float eps,
  * activation rows and one scale per weight row (group = K): tile-major
  * weights (qlm_mx_swizzle) and their scales s_rows [N] as quantised. The
  * rows are written as int8 digit planes, x = 2^E (d0 + d1/2^7 + d2/2^14 +
- * d3/2^21) to within 2^-27 max|x| per row (the RMSNorm folded in when
- * norm_w is given), and multiplied on v_mfma_i32_16x16x64_i8 with exact
- * int32 sums over K, combined and scaled once in fp32 (~1e-7 normwise from
- * the fp32 product). epilogue 0 (store) or 1 (y += result); K a multiple of
+ * d3/2^21) per row (the RMSNorm folded in when norm_w is given), and
+ * multiplied on v_mfma_i32_16x16x64_i8 with exact int32 sums over K,
+ * combined and scaled once in fp32: all four digits at 2..8 rows (x to
+ * within 2^-27 max|x|, ~1e-7 normwise from the fp32 product), the first
+ * three at 9..64 rows (x to within 2^-20 max|x|, ~1.3e-6 normwise on N(0,1)
+ * rows). epilogue 0 (store) or 1 (y += result); K a multiple of
  * 64, at most 2^18; QLM_ERR_SHAPE otherwise, for SwiGLU and for M outside
  * 2..64. qlm_matmul_i8_tm takes this form for such calls where measured
  * faster (N >= 8192, or more than 16 rows and K > 4096; its work 256-byte

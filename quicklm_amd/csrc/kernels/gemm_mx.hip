@@ -437,18 +437,25 @@ int launch_gm_mp(const GmConfig& c, const int8_t* dg, const int* de, const int8_
 //
 // y[m, n] = s[n] * sum_k x[m, k] q[n, k]. The rows are written as int8 digit
 // planes by k_act_digits (x_m = 2^E_m (d0 + d1 2^-7 + d2 2^-14 + d3 2^-21),
-// RMSNorm folded in) and multiplied on v_mfma_i32_16x16x64_i8 with
-//   A = 16 digit rows: activation rows 4a .. 4a+3, digits 0..3 (row 4 m' +
-//       d of product a holds digit d of row 4a + m' over the block's 64
-//       columns); MA products cover 4 MA rows;
-//   B = a tile-major weight fragment as stored (lane 16q + n: weight row n,
-//       columns 16q .. 16q+15).
-// D lane (q', n) holds the four digit sums of activation row 4a + q' and
-// weight row n; with one scale per weight row nothing is scaled inside the
-// K loop, so the products accumulate exact int32 sums over all of the
-// workgroup's blocks (|sum| <= 64 * 127 * K < 2^31 for K <= 2^18) and are
-// combined once at the end, in fp32: (D0 + 2^-7 (D1 + 2^-7 (D2 + 2^-7 D3)))
-// 2^E_m s[n].
+// RMSNorm folded in) and multiplied on v_mfma_i32_16x16x64_i8 with B = a
+// tile-major weight fragment as stored (lane 16q + n: weight row n, columns
+// 16q .. 16q+15) and A = 16 digit rows over the block's 64 columns, in one of
+// two orders:
+//   interleaved (2 <= M <= 8): A row 4 m' + d of product a holds digit d of
+//       activation row 4a + m'; NP = 1 or 2 products cover 4 NP rows, all
+//       four digits;
+//   digit-major (9 <= M <= 64): product 3g + d holds digit d of activation
+//       rows 16g .. 16g+15; NP = 3 ceil(M / 16) products, three digits
+//       (x_m to within 2^(E_m - 15), at most 2^-20 of the row's largest
+//       magnitude: a quarter fewer products and digit bytes than four
+//       digits, at the precision of a bf16 hi/lo split).
+// D lane (q', n) then holds, for weight row n, the four digit sums of
+// activation row 4a + q' (interleaved) or digit d's sums of rows 16g + 4q' ..
+// +3 (digit-major, so a row's digits meet in one lane and register slot);
+// with one scale per weight row nothing is scaled inside the K loop, so the
+// products accumulate exact int32 sums over all of the workgroup's blocks
+// (|sum| <= 64 * 127 * K < 2^31 for K <= 2^18) and are combined once at the
+// end, in fp32: (D0 + 2^-7 (D1 + 2^-7 (D2 [+ 2^-7 D3]))) 2^E_m s[n].
 //
 // Work split: a workgroup of 8 waves owns 8 x 2 tiles (16 weight rows each)
 // and one K slice; wave w owns 2 of the tiles, so the waves share
@@ -472,21 +479,21 @@ int launch_gm_mp(const GmConfig& c, const int8_t* dg, const int* de, const int8_
 constexpr int kR64Waves = 8;   // waves per workgroup (two a SIMD)
 constexpr int kR64Tiles = 2;   // tiles per wave
 
-template <int MA, int EPI>
+template <int NP, bool DM, int EPI>
 __global__ __launch_bounds__(kR64Waves * QLM_WAVE) void k_mm_rows64(
     const int8_t* __restrict__ digits, const int* __restrict__ dexp,
     const int8_t* __restrict__ qz, const float* __restrict__ srow, float* __restrict__ y, int ldy,
     float* __restrict__ part, int M, int N, int K, int tiles, int full, int ks, int bps) {
     constexpr int NT = kR64Waves * QLM_WAVE;
-    constexpr int AR = 16 * MA;       // digit rows of a block
+    constexpr int AR = 16 * NP;       // A rows of a block
     constexpr int CH = AR * 4;        // 16-byte chunks of a block
-    // chunks per thread; below 32 rows a block has fewer chunks than threads
-    // (whole waves of them: CH is a multiple of 64): every thread still
-    // loads (chunk index clamped, so the loads stay unconditional) and the
-    // first CH threads store
-    constexpr bool FEW = CH < NT;
-    constexpr int CPT = FEW ? 1 : CH / NT;
-    static_assert(FEW || CH % NT == 0, "digit block must split evenly over the threads");
+    static_assert(!DM || NP % 3 == 0, "digit-major blocks hold three digits a row group");
+    // chunks per thread; when the threads do not divide the chunks (whole
+    // waves of them: CH is a multiple of 64) every thread still loads its
+    // last chunk (index clamped, so the loads stay unconditional) and only
+    // the threads with a chunk there store it
+    constexpr int CPT = (CH + NT - 1) / NT;
+    constexpr bool PART = CH % NT != 0;
     typedef int v4i __attribute__((ext_vector_type(4)));
     __shared__ __align__(16) unsigned char abuf[2][AR * 64];
 
@@ -510,18 +517,20 @@ __global__ __launch_bounds__(kR64Waves * QLM_WAVE) void k_mm_rows64(
     // registers st[j & 3] into LDS buffer j & 1 at the end of iteration j - 1,
     // weight block j into wr[j & 3] (rings of four, so that the slot of every
     // access is a compile-time constant in the loop unrolled by four). Digit
-    // chunk c = tid + NT i is operand lane p = c & 63 (digit row 16 (c >> 6)
-    // + (p & 15), bytes 16 (p >> 4)) of product c >> 6, at LDS byte 16 c.
-    // Vector types: an aggregate copy into LDS would keep the staging array
-    // in scratch memory.
+    // chunk c = tid + NT i is operand lane p = c & 63 (A row p & 15, bytes
+    // 16 (p >> 4)) of product c >> 6, at LDS byte 16 c; A row i of product a
+    // is digit plane 16 a + i (interleaved) or 4 (16 (a / 3) + i) + a % 3
+    // (digit-major) of the [row][digit][K] planes. Vector types: an
+    // aggregate copy into LDS would keep the staging array in scratch memory.
     constexpr int RING = 4;
     v4i st[RING][CPT];
     v4i wr[RING][kR64Tiles];
     auto issue = [&](int slot, int b) {
 #pragma unroll
         for (int i = 0; i < CPT; ++i) {
-            const int c = FEW ? min(tid, CH - 1) : tid + NT * i;
-            const int r = 16 * (c >> 6) + (c & 15);
+            const int c = PART ? min(tid + NT * i, CH - 1) : tid + NT * i;
+            const int a = c >> 6, ar = c & 15;
+            const int r = DM ? 4 * (16 * (a / 3) + ar) + a % 3 : 16 * a + ar;
             st[slot][i] = *reinterpret_cast<const v4i*>(digits + (size_t)r * K + 64 * b +
                                                         16 * ((c >> 4) & 3));
         }
@@ -538,15 +547,15 @@ __global__ __launch_bounds__(kR64Waves * QLM_WAVE) void k_mm_rows64(
 #pragma unroll
         for (int i = 0; i < CPT; ++i) {
             const int c = tid + NT * i;
-            if (!FEW || tid < CH) *reinterpret_cast<v4i*>(&abuf[buf][16 * c]) = st[slot][i];
+            if (!PART || c < CH) *reinterpret_cast<v4i*>(&abuf[buf][16 * c]) = st[slot][i];
         }
     };
 
-    v4i acc[kR64Tiles][MA];
+    v4i acc[kR64Tiles][NP];
 #pragma unroll
     for (int t = 0; t < kR64Tiles; ++t)
 #pragma unroll
-        for (int a = 0; a < MA; ++a) acc[t][a] = v4i{0, 0, 0, 0};
+        for (int a = 0; a < NP; ++a) acc[t][a] = v4i{0, 0, 0, 0};
 
     // iteration i: request block i + 3, multiply block i, stage block i + 1.
     // The requests are unconditional (past the slice they repeat its last
@@ -555,7 +564,7 @@ __global__ __launch_bounds__(kR64Waves * QLM_WAVE) void k_mm_rows64(
     auto mul = [&](int i, int slot) {
         const int buf = i & 1;
 #pragma unroll
-        for (int a = 0; a < MA; ++a) {
+        for (int a = 0; a < NP; ++a) {
             const v4i av = *reinterpret_cast<const v4i*>(&abuf[buf][1024 * a + 16 * lane]);
 #pragma unroll
             for (int t = 0; t < kR64Tiles; ++t)
@@ -600,11 +609,14 @@ __global__ __launch_bounds__(kR64Waves * QLM_WAVE) void k_mm_rows64(
     if (i0 + 1 < nb) tail(i0 + 1, 1);
     if (i0 + 2 < nb) tail(i0 + 2, 2);
 
-    // ---- lane (qd, n): activation rows 4a + qd, weight row 16 tile + n ----
+    // ---- lane (qd, n), weight row 16 tile + n: its activation rows i are
+    // 4 i + qd (interleaved) or 16 (i / 4) + 4 qd + i % 4 (digit-major) ----
+    constexpr int NR = DM ? 4 * (NP / 3) : NP;
+    auto row_m = [&](int i) { return DM ? 16 * (i >> 2) + 4 * qd + (i & 3) : 4 * i + qd; };
     const int row0 = full * kR64Waves * kR64Tiles * 16, nt = N - row0;
-    float ex[MA];
+    float ex[NR];
 #pragma unroll
-    for (int a = 0; a < MA; ++a) ex[a] = ldexpf(1.0f, dexp[min(4 * a + qd, M - 1)]);
+    for (int i = 0; i < NR; ++i) ex[i] = ldexpf(1.0f, dexp[min(row_m(i), M - 1)]);
 #pragma unroll
     for (int t = 0; t < kR64Tiles; ++t) {
         const int tile = tile0 + t;
@@ -612,14 +624,20 @@ __global__ __launch_bounds__(kR64Waves * QLM_WAVE) void k_mm_rows64(
         if (tile >= tiles || row >= N) continue;
         const float sn = srow[row];
 #pragma unroll
-        for (int a = 0; a < MA; ++a) {
-            const int m = 4 * a + qd;
+        for (int i = 0; i < NR; ++i) {
+            const int m = row_m(i);
             if (m >= M) continue;
-            const v4i dd = acc[t][a];
-            const float v =
-                fmaf(fmaf(fmaf((float)dd[3], 0x1p-7f, (float)dd[2]), 0x1p-7f, (float)dd[1]),
-                     0x1p-7f, (float)dd[0]);
-            const float r = (v * ex[a]) * sn;
+            float v;
+            if constexpr (DM) {
+                const int g = i >> 2, j = i & 3;
+                v = fmaf(fmaf((float)acc[t][3 * g + 2][j], 0x1p-7f, (float)acc[t][3 * g + 1][j]),
+                         0x1p-7f, (float)acc[t][3 * g][j]);
+            } else {
+                const v4i dd = acc[t][i];
+                v = fmaf(fmaf(fmaf((float)dd[3], 0x1p-7f, (float)dd[2]), 0x1p-7f, (float)dd[1]),
+                         0x1p-7f, (float)dd[0]);
+            }
+            const float r = (v * ex[i]) * sn;
             if (to_part)  // tail columns only: [slice][m][N - row0]
                 part[((size_t)slice * M + m) * nt + (row - row0)] = r;
             else if constexpr (EPI == EPI_RESID)
@@ -633,7 +651,7 @@ __global__ __launch_bounds__(kR64Waves * QLM_WAVE) void k_mm_rows64(
 constexpr int kR64MaxRows = 64;
 
 struct R64Plan {
-    int ma, groups, full, ks, bps, units;
+    int np, groups, full, ks, bps, units;
 };
 
 // Whole rounds of 256 groups (one workgroup a CU) take whole K; the last
@@ -641,7 +659,9 @@ struct R64Plan {
 // workgroup a CU again).
 R64Plan r64_plan(int M, int N, int K) {
     R64Plan p;
-    p.ma = M <= 4 ? 1 : (M <= 8 ? 2 : (M <= 16 ? 4 : (M <= 32 ? 8 : 16)));  // ceil(M / 4), 2^n
+    // products a block: 4 interleaved rows each up to 8 rows, then three
+    // digit-major products per 16 rows
+    p.np = M <= 4 ? 1 : (M <= 8 ? 2 : 3 * ((M + 15) / 16));
     const int tiles = (N + 15) / 16, nblk = K / 64;
     p.groups = (tiles + kR64Waves * kR64Tiles - 1) / (kR64Waves * kR64Tiles);
     p.full = (p.groups / 256) * 256;
@@ -667,17 +687,17 @@ size_t r64_work_bytes(int M, int N, int K, int epi) {
     return b;
 }
 
-template <int MA>
+template <int NP, bool DM>
 int launch_r64(const R64Plan& p, const int8_t* dg, const int* de, const int8_t* qz,
                const float* sr, float* y, int ldy, float* part, int M, int N, int K, int epi,
                hipStream_t st) {
     const int tiles = (N + 15) / 16;
     if (epi == EPI_RESID)
-        hipLaunchKernelGGL((k_mm_rows64<MA, EPI_RESID>), dim3(p.units), dim3(kR64Waves * QLM_WAVE),
+        hipLaunchKernelGGL((k_mm_rows64<NP, DM, EPI_RESID>), dim3(p.units), dim3(kR64Waves * QLM_WAVE),
                            0, st, dg, de, qz, sr, y, ldy, part, M, N, K, tiles, p.full, p.ks,
                            p.bps);
     else
-        hipLaunchKernelGGL((k_mm_rows64<MA, EPI_STORE>), dim3(p.units), dim3(kR64Waves * QLM_WAVE),
+        hipLaunchKernelGGL((k_mm_rows64<NP, DM, EPI_STORE>), dim3(p.units), dim3(kR64Waves * QLM_WAVE),
                            0, st, dg, de, qz, sr, y, ldy, part, M, N, K, tiles, p.full, p.ks,
                            p.bps);
     int rc = qlm_launch_status();
@@ -778,7 +798,8 @@ extern "C" int qlm_matmul_i8_rows64(const float* x, int ldx, const float* norm_w
     float* part = reinterpret_cast<float*>(reinterpret_cast<char*>(de) +
                                            align256((size_t)kR64MaxRows * sizeof(int)));
     const R64Plan p = r64_plan(M, N, K);
-    const int rows = 4 * p.ma;  // digit rows written (zeros past M)
+    // activation rows the products read (digits of the rows past M are zeros)
+    const int rows = p.np <= 2 ? 4 * p.np : 16 * (p.np / 3);
     if (norm_w)
         hipLaunchKernelGGL(k_act_digits<true>, dim3(rows), dim3(kPrepThreads), 0, st, x, ldx,
                            norm_w, eps, M, K, dg, de);
@@ -787,14 +808,17 @@ extern "C" int qlm_matmul_i8_rows64(const float* x, int ldx, const float* norm_w
                            nullptr, eps, M, K, dg, de);
     int rc = qlm_launch_status();
     if (rc != QLM_OK) return rc;
-    switch (p.ma) {
-        case 1: return launch_r64<1>(p, dg, de, q_tiles, s_rows, y, ldy, part, M, N, K, epilogue, st);
-        case 2: return launch_r64<2>(p, dg, de, q_tiles, s_rows, y, ldy, part, M, N, K, epilogue, st);
-        case 4: return launch_r64<4>(p, dg, de, q_tiles, s_rows, y, ldy, part, M, N, K, epilogue, st);
-        case 8: return launch_r64<8>(p, dg, de, q_tiles, s_rows, y, ldy, part, M, N, K, epilogue, st);
-        default:
-            return launch_r64<16>(p, dg, de, q_tiles, s_rows, y, ldy, part, M, N, K, epilogue, st);
+#define QLM_R64(NP, DM) \
+    return launch_r64<NP, DM>(p, dg, de, q_tiles, s_rows, y, ldy, part, M, N, K, epilogue, st)
+    switch (p.np) {
+        case 1: QLM_R64(1, false);
+        case 2: QLM_R64(2, false);
+        case 3: QLM_R64(3, true);
+        case 6: QLM_R64(6, true);
+        case 9: QLM_R64(9, true);
+        default: QLM_R64(12, true);
     }
+#undef QLM_R64
 }
 
 // Loads this file's code object on the current device now; the runtime
