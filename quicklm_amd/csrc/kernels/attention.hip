@@ -367,8 +367,9 @@ __global__ __launch_bounds__(kThreads) void k_attn(
 // Merge of the chunk records of one (query head, sequence), then the
 // optional sigmoid output gate (attention.cpp:216-227): gate[b*ldg + h*ghs +
 // HD + e]. 256 threads: thread (cg, c4) takes float4 column c4 of the
-// chunks c = cg, cg + NG, ...; the chunks' (m, l) meet in LDS, and the 8 (4
-// at hd 256) chunk groups meet in LDS at the end. Everything the first pass
+// chunks c = cg, cg + NG, ...; the chunk weights meet in LDS (their sum of
+// weighted l as a block reduction), and the NG chunk groups meet at the end
+// (within a wave by shuffles, then across the four waves in LDS). Everything the first pass
 // needs -- (m, l) of chunk tid, the first KB records of the thread's chunks
 // and the gate -- is requested at kernel start with clamped, unconditional
 // loads, so a short context costs one memory round trip. Up to kCombineTile
@@ -387,9 +388,9 @@ __global__ __launch_bounds__(kCombineThreads) void k_attn_combine(
     constexpr int NG = kCombineThreads / C4;      // chunk groups
     constexpr int KB = 8;                         // records per thread per request batch
     constexpr int RS = HD + 4;                    // record stride (floats)
-    __shared__ float fs[kCombineTile], ls_[kCombineTile];
+    __shared__ float fs[kCombineTile];
     __shared__ float4 part[NG][C4];
-    __shared__ float red[kCombineThreads / QLM_WAVE];
+    __shared__ float red[kCombineThreads / QLM_WAVE], red_l[kCombineThreads / QLM_WAVE];
     const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
     const int c4 = tid % C4, cg = tid / C4;
     const int cb = blockIdx.z * C4;  // first float4 column of this workgroup
@@ -431,13 +432,17 @@ __global__ __launch_bounds__(kCombineThreads) void k_attn_combine(
 #pragma unroll
         for (int w = 1; w < kCombineThreads / QLM_WAVE; ++w) mt = fmaxf(mt, red[w]);
         const float Mn = fmaxf(M, mt);
-        if (tid < nt) {
-            fs[tid] = expf(mc - Mn);
-            ls_[tid] = lc;
-        }
+        // chunk weights, and the pass's sum of weighted l over all threads
+        const float fc = tid < nt ? expf(mc - Mn) : 0.0f;
+        if (tid < nt) fs[tid] = fc;
+        float lt = wave_sum(fc * lc);
+        if ((tid & (QLM_WAVE - 1)) == 0) red_l[tid / QLM_WAVE] = lt;
         __syncthreads();
+        lt = red_l[0];
+#pragma unroll
+        for (int w = 1; w < kCombineThreads / QLM_WAVE; ++w) lt += red_l[w];
         const float f0 = expf(M - Mn);  // 0 on the first pass
-        lsum *= f0;
+        lsum = fmaf(lsum, f0, lt);
         o.x *= f0;
         o.y *= f0;
         o.z *= f0;
@@ -457,17 +462,29 @@ __global__ __launch_bounds__(kCombineThreads) void k_attn_combine(
                 o.w = fmaf(f, ov[k].w, o.w);
             }
         }
-        if (cg == 0)
-            for (int c = 0; c < nt; ++c) lsum = fmaf(fs[c], ls_[c], lsum);
         M = Mn;
-        __syncthreads();  // fs/ls_/red are rewritten by the next pass
+        __syncthreads();  // fs/red/red_l are rewritten by the next pass
     }
-    part[cg][c4] = o;
+    // the chunk groups of one wave first (lanes of equal c4, by shuffles),
+    // then the waves' sums in LDS
+    constexpr int NP = C4 < QLM_WAVE ? kCombineThreads / QLM_WAVE : NG;  // partials left
+    if constexpr (C4 < QLM_WAVE) {
+#pragma unroll
+        for (int m = C4; m < QLM_WAVE; m <<= 1) {
+            o.x += __shfl_xor(o.x, m, QLM_WAVE);
+            o.y += __shfl_xor(o.y, m, QLM_WAVE);
+            o.z += __shfl_xor(o.z, m, QLM_WAVE);
+            o.w += __shfl_xor(o.w, m, QLM_WAVE);
+        }
+        if ((tid & (QLM_WAVE - 1)) < C4) part[tid / QLM_WAVE][c4] = o;
+    } else {
+        part[cg][c4] = o;
+    }
     __syncthreads();
     if (cg == 0) {
         float4 t = part[0][c4];
 #pragma unroll
-        for (int g2 = 1; g2 < NG; ++g2) {
+        for (int g2 = 1; g2 < NP; ++g2) {
             const float4 u = part[g2][c4];
             t.x += u.x;
             t.y += u.y;
@@ -1031,7 +1048,8 @@ int launch_mx(int G, const float* q, int ldq, const uint16_t* kc, const uint16_t
     return QLM_ERR_SHAPE;
 }
 
-// cs: workgroups per (head, sequence), each merging HD / cs columns (1, 2 or 4)
+// cs: workgroups per (head, sequence), each merging HD / cs columns (1, 2, 4,
+// 8 or 16)
 template <int HD>
 int launch_combine(const float* work, int nch, int ch, int max_seq, const int* pos, int ctx,
                    int pstep, const float* gate, int ldg, int ghs, float* out, int ldo, int n_q,
@@ -1046,14 +1064,20 @@ int launch_combine(const float* work, int nch, int ch, int max_seq, const int* p
     QLM_COMBINE(1)
     QLM_COMBINE(2)
     QLM_COMBINE(4)
+    QLM_COMBINE(8)
+    QLM_COMBINE(16)
 #undef QLM_COMBINE
     return QLM_ERR_ARG;
 }
 
 // column split of the isolated attention's merge: ~256 workgroups or more
+// (at 16 splits a workgroup holds 4 columns at hd 256, 2 at hd 128, and
+// takes 512 or 1024 records in its first request batch)
 int combine_splits(int n_q, int B) {
     const int pairs = n_q * B;
-    return pairs >= 256 ? 1 : (pairs >= 128 ? 2 : 4);
+    int cs = 1;
+    while (cs < 16 && pairs * cs < 256) cs *= 2;
+    return cs;
 }
 
 }  // namespace
