@@ -40,9 +40,16 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 constexpr int kPrepThreads = 256;
 constexpr int kMaxRows = 16;
 
-// Activation digits of one row per workgroup; rows m >= M (padding up to an
-// even count) are written as zeros. Two passes over the row: sum of squares
-// (RMSNorm) and max|x * (1 + w)|, then the digits.
+// Activation digits of one row per gridDim.y workgroups; rows m >= M
+// (padding up to the products' row count) are written as zeros. Two passes
+// over the row: sum of squares (RMSNorm) and max|x * (1 + w)| over the whole
+// row (by every workgroup of the row), then the digits of this workgroup's
+// share of the columns (blockIdx.y). Each thread keeps kDigitLoads loads in
+// flight (indices clamped, so the loads are unconditional; elements past
+// the row are then dropped); the sum of squares accumulates in the same
+// order for any split.
+constexpr int kDigitLoads = 4;
+
 template <bool NORM>
 __global__ __launch_bounds__(kPrepThreads) void k_act_digits(const float* __restrict__ x,
                                                               int ldx, const float* __restrict__ nw,
@@ -53,31 +60,45 @@ __global__ __launch_bounds__(kPrepThreads) void k_act_digits(const float* __rest
     const int m = blockIdx.x, tid = threadIdx.x, lane = tid & (QLM_WAVE - 1);
     const int wave = tid / QLM_WAVE;
     const int n4 = K >> 2;
+    // float4 columns [c0, c1) get their digits here
+    const int per = (n4 + (int)gridDim.y - 1) / (int)gridDim.y;
+    const int c0 = (int)blockIdx.y * per, c1 = min(n4, c0 + per);
+    constexpr int U = kDigitLoads, STEP = U * kPrepThreads;
     unsigned* planes = reinterpret_cast<unsigned*>(digits + (size_t)m * 4 * K);
     if (m >= M) {
-        for (int i = tid; i < n4; i += kPrepThreads)
+        for (int i = c0 + tid; i < c1; i += kPrepThreads)
 #pragma unroll
             for (int d = 0; d < 4; ++d) planes[(size_t)d * n4 + i] = 0u;
-        if (tid == 0) dexp[m] = 0;
+        if (blockIdx.y == 0 && tid == 0) dexp[m] = 0;
         return;
     }
     const float4* xr = reinterpret_cast<const float4*>(x + (size_t)m * ldx);
     const float4* wr = reinterpret_cast<const float4*>(nw);
     float ss = 0.0f, mx = 0.0f;
-    for (int i = tid; i < n4; i += kPrepThreads) {
-        float4 v = xr[i];
-        if constexpr (NORM) {
-            ss = fmaf(v.x, v.x, ss);
-            ss = fmaf(v.y, v.y, ss);
-            ss = fmaf(v.z, v.z, ss);
-            ss = fmaf(v.w, v.w, ss);
-            const float4 g = wr[i];
-            v.x *= 1.0f + g.x;
-            v.y *= 1.0f + g.y;
-            v.z *= 1.0f + g.z;
-            v.w *= 1.0f + g.w;
+    for (int i = tid; i < n4; i += STEP) {
+        float4 v[U], g[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int k = min(i + u * kPrepThreads, n4 - 1);
+            v[u] = xr[k];
+            if constexpr (NORM) g[u] = wr[k];
         }
-        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (i + u * kPrepThreads >= n4) break;
+            float4 a = v[u];
+            if constexpr (NORM) {
+                ss = fmaf(a.x, a.x, ss);
+                ss = fmaf(a.y, a.y, ss);
+                ss = fmaf(a.z, a.z, ss);
+                ss = fmaf(a.w, a.w, ss);
+                a.x *= 1.0f + g[u].x;
+                a.y *= 1.0f + g[u].y;
+                a.z *= 1.0f + g[u].z;
+                a.w *= 1.0f + g[u].w;
+            }
+            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))));
+        }
     }
     if constexpr (NORM) ss = wave_sum(ss);
     mx = wave_max(mx);
@@ -96,36 +117,55 @@ __global__ __launch_bounds__(kPrepThreads) void k_act_digits(const float* __rest
     int e2 = 0;
     frexpf(mm * rs, &e2);
     const int E = e2 - 6;  // max|x| / 2^E < 64 (one rounding of slack: digits <= 64)
-    if (tid == 0) dexp[m] = E;
-    for (int i = tid; i < n4; i += kPrepThreads) {
-        float4 v = xr[i];
-        if constexpr (NORM) {
-            const float4 g = wr[i];
-            v.x = (v.x * (1.0f + g.x)) * rs;
-            v.y = (v.y * (1.0f + g.y)) * rs;
-            v.z = (v.z * (1.0f + g.z)) * rs;
-            v.w = (v.w * (1.0f + g.w)) * rs;
-        }
-        const float vv[4] = {v.x, v.y, v.z, v.w};
-        unsigned pk[4] = {0u, 0u, 0u, 0u};
+    if (blockIdx.y == 0 && tid == 0) dexp[m] = E;
+    for (int i = c0 + tid; i < c1; i += STEP) {
+        float4 v[U], g[U];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const float u = ldexpf(vv[c], -E);
-            const float d0 = rintf(u);
-            float t = (u - d0) * 128.0f;
-            const float d1 = rintf(t);
-            t = (t - d1) * 128.0f;
-            const float d2 = rintf(t);
-            t = (t - d2) * 128.0f;
-            const float d3 = rintf(t);
-            pk[0] |= ((unsigned)(int)d0 & 0xffu) << (8 * c);
-            pk[1] |= ((unsigned)(int)d1 & 0xffu) << (8 * c);
-            pk[2] |= ((unsigned)(int)d2 & 0xffu) << (8 * c);
-            pk[3] |= ((unsigned)(int)d3 & 0xffu) << (8 * c);
+        for (int u = 0; u < U; ++u) {
+            const int k = min(i + u * kPrepThreads, c1 - 1);
+            v[u] = xr[k];
+            if constexpr (NORM) g[u] = wr[k];
         }
 #pragma unroll
-        for (int d = 0; d < 4; ++d) planes[(size_t)d * n4 + i] = pk[d];
+        for (int u = 0; u < U; ++u) {
+            const int k = i + u * kPrepThreads;
+            if (k >= c1) break;
+            float4 a = v[u];
+            if constexpr (NORM) {
+                a.x = (a.x * (1.0f + g[u].x)) * rs;
+                a.y = (a.y * (1.0f + g[u].y)) * rs;
+                a.z = (a.z * (1.0f + g[u].z)) * rs;
+                a.w = (a.w * (1.0f + g[u].w)) * rs;
+            }
+            const float vv[4] = {a.x, a.y, a.z, a.w};
+            unsigned pk[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const float t0 = ldexpf(vv[c], -E);
+                const float d0 = rintf(t0);
+                float t = (t0 - d0) * 128.0f;
+                const float d1 = rintf(t);
+                t = (t - d1) * 128.0f;
+                const float d2 = rintf(t);
+                t = (t - d2) * 128.0f;
+                const float d3 = rintf(t);
+                pk[0] |= ((unsigned)(int)d0 & 0xffu) << (8 * c);
+                pk[1] |= ((unsigned)(int)d1 & 0xffu) << (8 * c);
+                pk[2] |= ((unsigned)(int)d2 & 0xffu) << (8 * c);
+                pk[3] |= ((unsigned)(int)d3 & 0xffu) << (8 * c);
+            }
+#pragma unroll
+            for (int d = 0; d < 4; ++d) planes[(size_t)d * n4 + k] = pk[d];
+        }
     }
+}
+
+// Workgroups per activation row of k_act_digits: about 256 in all, at most 8
+// a row.
+int act_digit_splits(int rows) {
+    int s = 1;
+    while (s < 8 && rows * s < 256) s *= 2;
+    return s;
 }
 
 // NW waves, T = 2 for the [gate; up] pair of SwiGLU, U >= K / 64 / NW blocks
@@ -751,12 +791,13 @@ extern "C" int qlm_matmul_i8_mx(const float* x, int ldx, const float* norm_w, fl
     int8_t* dg = reinterpret_cast<int8_t*>(work);
     int* de = reinterpret_cast<int*>(reinterpret_cast<char*>(work) + align256(digits_bytes(M, K)));
     const int rows = 2 * mp_for(M);
+    const dim3 dgrid(rows, act_digit_splits(rows));
     if (norm_w)
-        hipLaunchKernelGGL(k_act_digits<true>, dim3(rows), dim3(kPrepThreads), 0, st, x, ldx,
-                           norm_w, eps, M, K, dg, de);
+        hipLaunchKernelGGL(k_act_digits<true>, dgrid, dim3(kPrepThreads), 0, st, x, ldx, norm_w,
+                           eps, M, K, dg, de);
     else
-        hipLaunchKernelGGL(k_act_digits<false>, dim3(rows), dim3(kPrepThreads), 0, st, x, ldx,
-                           nullptr, eps, M, K, dg, de);
+        hipLaunchKernelGGL(k_act_digits<false>, dgrid, dim3(kPrepThreads), 0, st, x, ldx, nullptr,
+                           eps, M, K, dg, de);
     int rc = qlm_launch_status();
     if (rc != QLM_OK) return rc;
 #define QLM_GM_CALL(RS, E) \
@@ -800,12 +841,13 @@ extern "C" int qlm_matmul_i8_rows64(const float* x, int ldx, const float* norm_w
     const R64Plan p = r64_plan(M, N, K);
     // activation rows the products read (digits of the rows past M are zeros)
     const int rows = p.np <= 2 ? 4 * p.np : 16 * (p.np / 3);
+    const dim3 dgrid(rows, act_digit_splits(rows));
     if (norm_w)
-        hipLaunchKernelGGL(k_act_digits<true>, dim3(rows), dim3(kPrepThreads), 0, st, x, ldx,
-                           norm_w, eps, M, K, dg, de);
+        hipLaunchKernelGGL(k_act_digits<true>, dgrid, dim3(kPrepThreads), 0, st, x, ldx, norm_w,
+                           eps, M, K, dg, de);
     else
-        hipLaunchKernelGGL(k_act_digits<false>, dim3(rows), dim3(kPrepThreads), 0, st, x, ldx,
-                           nullptr, eps, M, K, dg, de);
+        hipLaunchKernelGGL(k_act_digits<false>, dgrid, dim3(kPrepThreads), 0, st, x, ldx, nullptr,
+                           eps, M, K, dg, de);
     int rc = qlm_launch_status();
     if (rc != QLM_OK) return rc;
 #define QLM_R64(NP, DM) \
