@@ -719,11 +719,12 @@ template <int NW, int T, int P, bool ROWSCALE, int PRO, int EPI, bool W4>
 __global__ __launch_bounds__(NW * QLM_WAVE) void k_gemv_mx(
     const float* __restrict__ x, const float* __restrict__ nw, float eps,
     const int8_t* __restrict__ q, const float* __restrict__ sc, float* __restrict__ y, int N,
-    int K, int F, int ntiles, GreedyTail tail) {
+    int K, int F, int ntiles, GreedyTail tail, int gtiles) {
     constexpr int XL = (P + 3) / 4;  // activation float4 per lane (16 lanes per block)
     typedef int v4i __attribute__((ext_vector_type(4)));
-    extern __shared__ __align__(16) unsigned char mx_lds[];  // [wave][slot][digit][64 B]
-    __shared__ int red[2][NW][T][16];
+    // dynamic LDS: the digits [wave][slot][digit][64 B], then the partial
+    // sums of gtiles tiles [tile][wave][T][16] (floats)
+    extern __shared__ __align__(16) unsigned char mx_lds[];
     __shared__ float rsum[NW];
 
     const int tid = threadIdx.x, lane = tid & (QLM_WAVE - 1);
@@ -887,58 +888,67 @@ __global__ __launch_bounds__(NW * QLM_WAVE) void k_gemv_mx(
 
     float best_v = -INFINITY;
     int best_i = 0x7fffffff;
-    int par = 0;
-    // Partial sums of the waves meet in LDS (double-buffered by tile parity:
-    // a buffer is rewritten two tiles later, after a barrier wave 0 reaches
-    // only once it has read it); wave 0 reduces them in wave order, applies
-    // 1/rms, the row scale, the epilogue and the stores.
-    auto tile_end = [&](int tile) {
+    // Partial sums of the waves meet in LDS, gtiles tiles at a time: after
+    // each tile a wave parks its partial sums in the tile's slot, and after
+    // the group's last tile one barrier precedes the epilogues, slot s by
+    // wave s % NW (its lanes qd == 0, one output row each), which sums the
+    // waves' partials in wave order and applies 1/rms, the row scale, the
+    // epilogue and the stores. No barrier stands between the tiles of a
+    // group, so a wave whose weights arrived early runs on into the next
+    // tile (and requests the one after).
+    float* red = reinterpret_cast<float*>(mx_lds + (size_t)NW * P * 256);
+    auto park = [&](int slot) {
 #pragma unroll
         for (int tt = 0; tt < T; ++tt) {
             const float p = (accf[tt] + __shfl_xor(accf[tt], 16, QLM_WAVE)) * fx;
-            if (qd == 0) red[par][w][tt][n] = __float_as_int(p);
+            if (qd == 0) red[((slot * NW + w) * T + tt) * 16 + n] = p;
             accf[tt] = 0.0f;
         }
-        __syncthreads();
-        if (w == 0 && qd == 0) {
-            const int o = tile * 16 + n;
-            const bool first = tile == (int)blockIdx.x;
-            float rs = 1.0f;
-            if constexpr (PRO == PRO_RMSNORM) {
-                float tot = rsum[0];
+    };
+    auto epilogue = [&](int tile, int slot) {
+        const int o = tile * 16 + n;
+        const bool first = tile == (int)blockIdx.x;
+        float rs = 1.0f;
+        if constexpr (PRO == PRO_RMSNORM) {
+            float tot = rsum[0];
 #pragma unroll
-                for (int i = 1; i < NW; ++i) tot += rsum[i];
-                rs = 1.0f / sqrtf(tot / (float)K + eps);
-            }
-            float val[T];
+            for (int i = 1; i < NW; ++i) tot += rsum[i];
+            rs = 1.0f / sqrtf(tot / (float)K + eps);
+        }
+        float val[T];
 #pragma unroll
-            for (int tt = 0; tt < T; ++tt) {
-                float v = __int_as_float(red[par][0][tt][n]);
-                for (int ww = 1; ww < NW; ++ww) v += __int_as_float(red[par][ww][tt][n]);
-                if constexpr (PRO == PRO_RMSNORM) v *= rs;
-                if constexpr (ROWSCALE) v *= first ? rsc0[tt] : sc[row_of(tile, tt)];
-                val[tt] = v;
-            }
-            if (o < N) {
-                if constexpr (EPI == EPI_SWIGLU)
-                    y[o] = silu_f(val[0]) * val[1];
-                else if constexpr (EPI == EPI_RESID)
-                    y[o] = (first ? res0 : y[o]) + val[0];
-                else
-                    y[o] = val[0];
-                if constexpr (EPI == EPI_ARGMAX) {
-                    if (val[0] > best_v || (val[0] == best_v && o < best_i)) {
-                        best_v = val[0];
-                        best_i = o;
-                    }
+        for (int tt = 0; tt < T; ++tt) {
+            float v = red[((slot * NW) * T + tt) * 16 + n];
+            for (int ww = 1; ww < NW; ++ww) v += red[((slot * NW + ww) * T + tt) * 16 + n];
+            if constexpr (PRO == PRO_RMSNORM) v *= rs;
+            if constexpr (ROWSCALE) v *= first ? rsc0[tt] : sc[row_of(tile, tt)];
+            val[tt] = v;
+        }
+        if (o < N) {
+            if constexpr (EPI == EPI_SWIGLU)
+                y[o] = silu_f(val[0]) * val[1];
+            else if constexpr (EPI == EPI_RESID)
+                y[o] = (first ? res0 : y[o]) + val[0];
+            else
+                y[o] = val[0];
+            if constexpr (EPI == EPI_ARGMAX) {
+                if (val[0] > best_v || (val[0] == best_v && o < best_i)) {
+                    best_v = val[0];
+                    best_i = o;
                 }
             }
         }
-        par ^= 1;
+    };
+    // the epilogues of slots [0, count) of the group starting at tile0
+    auto flush = [&](int tile0, int count) {
+        __syncthreads();
+        if (qd == 0)
+            for (int sl = w; sl < count; sl += NW) epilogue(tile0 + sl * (int)gridDim.x, sl);
     };
 
     // ---- tiles: consume the P slots in order (each refilled with the next
-    // tile's block when there is one), then the cross-wave epilogue
+    // tile's block when there is one); the cross-wave epilogues per group
+    int slot = 0, tile0 = blockIdx.x;
     for (int tile = blockIdx.x;; tile += gridDim.x) {
         const int next = tile + (int)gridDim.x;
         // the digit reads stay in the loop (hoisted, P fragments would stay
@@ -954,20 +964,36 @@ __global__ __launch_bounds__(NW * QLM_WAVE) void k_gemv_mx(
 #pragma unroll
             for (int u = 0; u < P; ++u) consume(u);
         }
-        tile_end(tile);
-        if (next >= ntiles) break;
+        park(slot);
+        ++slot;
+        if (next >= ntiles) {
+            flush(tile0, slot);
+            break;
+        }
+        if (slot == gtiles) {
+            flush(tile0, slot);
+            __syncthreads();  // the group's slots are read before they are rewritten
+            slot = 0;
+            tile0 = next;
+        }
     }
 
     if constexpr (EPI == EPI_ARGMAX) {
-        if (w == 0) {
-            unsigned long long k = argmax_key(best_v, best_i);
-            if (best_i == 0x7fffffff) k = 0ull;
+        // each wave's best over its rows, then the workgroup's
+        __shared__ unsigned long long wkey[NW];
+        unsigned long long k = argmax_key(best_v, best_i);
+        if (best_i == 0x7fffffff) k = 0ull;
 #pragma unroll
-            for (int mm = 32; mm >= 1; mm >>= 1) {
-                const unsigned long long o = __shfl_xor(k, mm, QLM_WAVE);
-                k = o > k ? o : k;
-            }
-            if (lane == 0) tail.keys[blockIdx.x] = k;
+        for (int mm = 32; mm >= 1; mm >>= 1) {
+            const unsigned long long o = __shfl_xor(k, mm, QLM_WAVE);
+            k = o > k ? o : k;
+        }
+        if (lane == 0) wkey[w] = k;
+        __syncthreads();
+        if (tid == 0) {
+#pragma unroll
+            for (int i = 0; i < NW; ++i) k = wkey[i] > k ? wkey[i] : k;
+            tail.keys[blockIdx.x] = k;
         }
     }
 }
@@ -1159,6 +1185,8 @@ struct MxConfig {
 
 // Dynamic LDS of k_gemv_mx: per wave and slot, four 64-byte digit planes.
 size_t mx_lds_bytes(int nw, int ring) { return (size_t)nw * ring * 256; }
+// dynamic LDS of a k_gemv_mx workgroup, digits and parked partial sums
+constexpr size_t kMxLdsMax = 60 * 1024;
 
 // Instantiated (waves per workgroup, slots per wave) pairs; slots =
 // ceil(K / 64 / waves), so each pair serves a range of K.
@@ -1226,9 +1254,15 @@ int launch_mx(const MxConfig& c, const float* x, const float* nw, float eps, con
     const int ntiles = (N + 15) / 16;
     int grid = c.grid < ntiles ? c.grid : ntiles;
     if (grid < 1) grid = 1;
+    // tiles whose partial sums wait in LDS together: all of a workgroup's
+    // tiles where they fit
+    const int tpw = (ntiles + grid - 1) / grid;
+    const size_t per_tile = (size_t)NW * T * 16 * sizeof(float);
+    int gtiles = (int)((kMxLdsMax - mx_lds_bytes(NW, P)) / per_tile);
+    gtiles = gtiles < 1 ? 1 : (gtiles > tpw ? tpw : gtiles);
     hipLaunchKernelGGL((k_gemv_mx<NW, T, P, ROWSCALE, PRO, EPI, W4>), dim3(grid),
-                       dim3(NW * QLM_WAVE), mx_lds_bytes(NW, P), st, x, nw, eps, q, sc, y, N, K, F,
-                       ntiles, tail);
+                       dim3(NW * QLM_WAVE), mx_lds_bytes(NW, P) + gtiles * per_tile, st, x, nw, eps,
+                       q, sc, y, N, K, F, ntiles, tail, gtiles);
     if constexpr (EPI == EPI_ARGMAX) {
         const int rc = qlm_launch_status();
         if (rc != QLM_OK) return rc;
