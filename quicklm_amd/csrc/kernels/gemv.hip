@@ -539,6 +539,8 @@ __global__ __launch_bounds__(kThreads) void k_greedy_finish(GreedyTail tail, int
     __shared__ unsigned long long wk[kWaves];
     __shared__ int tok;
     const int tid = threadIdx.x, lane = tid & (QLM_WAVE - 1), wave = tid / QLM_WAVE;
+    // the position and prompt length travel with the keys (one round trip)
+    const int p = tail.pos[0], plen = tail.prompt_len[0];
     // nkeys <= kMaxXsGrid: every slot is requested before any is compared
     unsigned long long v[kMaxXsGrid / kThreads];
 #pragma unroll
@@ -561,9 +563,10 @@ __global__ __launch_bounds__(kThreads) void k_greedy_finish(GreedyTail tail, int
         for (int w2 = 1; w2 < kWaves; ++w2) m = wk[w2] > m ? wk[w2] : m;
         int idx = m ? (int)(0xFFFFFFFFu - (unsigned)(m & 0xFFFFFFFFull)) : 0;
         if (idx < 0 || idx >= N) idx = 0;
-        const int p = tail.pos[0];
-        if (p + 1 < tail.ld_tokens && p + 1 >= tail.prompt_len[0]) tail.tokens[p + 1] = idx;
-        int t = (p + 1 < tail.ld_tokens) ? tail.tokens[p + 1] : idx;
+        if (p + 1 < tail.ld_tokens && p + 1 >= plen) tail.tokens[p + 1] = idx;
+        // the token now at p + 1: the prompt's there, else the pick (no
+        // reload of what was just stored)
+        int t = (p + 1 < tail.ld_tokens && p + 1 < plen) ? tail.tokens[p + 1] : idx;
         t = t < 0 ? 0 : (t >= tail.vocab ? tail.vocab - 1 : t);
         tok = t;
         tail.pos[0] = p + 1;
