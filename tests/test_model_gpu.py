@@ -104,6 +104,41 @@ def test_graph_replay_equals_eager(engine, golden):
     assert np.array_equal(la, lb)
 
 
+ROWS = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "tiny_greedy_rows.npz")
+
+
+def test_tiny_batch16_rows_match_reference(hip, tiny_dir, golden, engine):
+    """Config 0 at batch 16 (the batched kernels: bf16 matrix-core matmuls,
+    one workgroup a DeltaNet head, 16-sequence attention): the 16 prompts of
+    seed 0 decoded together for 64 steps. Rows 0-2 have reference streams
+    (tiny_greedy.npz is row 0, tiny_greedy_rows.npz rows 1 and 2, the IEEE
+    build) and must equal them; rows 3-15 must equal the batch-1 engine's
+    streams of the same prompts."""
+    from quicklm_amd import synth
+    from quicklm_amd.engine import Engine
+
+    rows = np.load(ROWS)
+    prompts = synth.prompt_tokens(128, seed=0, batch=16)
+    assert np.array_equal(prompts[0], golden["prompt"])
+    ref = {0: golden["tokens"]}
+    for i, r in enumerate(rows["rows"]):
+        assert np.array_equal(prompts[int(r)], rows["prompt"][i])
+        ref[int(r)] = rows["tokens"][i]
+    e16 = Engine(tiny_dir, max_seq_len=256, max_batch=16, precision="int8")
+    try:
+        out16, _, _ = e16.generate(prompts, 64, batched_prefill=True)
+    finally:
+        e16.close()
+    for r, toks in ref.items():
+        d = np.nonzero(out16[r] != toks)[0]
+        say(f"batch 16 row {r}: first divergence from the reference",
+            int(d[0]) if d.size else None)
+        assert d.size == 0, (r, int(d[0]))
+    for b in range(3, 16):
+        one, _, _ = engine.generate(prompts[b][None, :], 64, batched_prefill=True)
+        assert np.array_equal(out16[b], one[0]), b
+
+
 def test_batch_rows_equal_single(engine, golden):
     """Two sequences in one batch give exactly the single-sequence results."""
     p0 = golden["prompt"][:48]
