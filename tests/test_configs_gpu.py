@@ -5,9 +5,11 @@ decode attention at long contexts, each against the CPU oracle.
   int8 matmul      N x K in {4096x4096, 12288x4096, 4096x12288, 151936x2560},
                    Wq int8 U{-127..127}, per-row scales U(0.001, 0.01) (and
                    group-32 scales for the tile-major forms), x N(0,1), at
-                   M = 1, 16, 64 (math_ops.cpp:820-900). The 151936-row case
-                   is scored on a sample of rows (every output row is an
-                   independent dot product).
+                   M = 1, 4, 16, 64 (math_ops.cpp:820-900), through the
+                   row-major entry point and through exactly the kernel
+                   bench.py times at each M. The 151936-row case is scored on
+                   a sample of rows (every output row is an independent dot
+                   product).
   DeltaNet         decode step at B = 32, 32 heads, d = 128: S N(0, 0.01),
                    q, k L2-normalised N(0,1), v N(0,1), decay =
                    sigmoid(N(0,1) + 2), beta = sigmoid(N(0,1))
@@ -64,7 +66,7 @@ def swizzle(hip, dq, ds, group, N, K):
 
 
 @pytest.mark.parametrize("N,K", SHAPES)
-@pytest.mark.parametrize("M", [1, 16, 64])
+@pytest.mark.parametrize("M", [1, 4, 16, 64])
 def test_cfg1_matmul_row_scales(hip, orc, rng, N, K, M):
     """Per-row scales (G = K): M = 1 on the int8 matrix cores over the
     tile-major copy (the decode GEMV), M = 16 and 64 through qlm_matmul_i8."""
@@ -103,6 +105,48 @@ def test_cfg1_matmul_tile_major_m16(hip, orc, rng, N, K):
     say(f"cfg1 tile-major {N}x{K} M=16")
     hip.call("qlm_matmul_i8_t", dev(hip, x), K, None, 0.0, qz, sz, 32, dy, N, M, N, K, 0, work,
              nbytes, None)
+    assert rel_err(dy.to_numpy((M, N), np.float32)[:, rows], ref) < 1e-5
+
+
+@pytest.fixture(scope="module")
+def cfg1_cache():
+    """One weight draw per (shape, scale group), on the host and on the
+    device in the tile-major layout, shared by the M cases below."""
+    return {}
+
+
+@pytest.mark.parametrize("N,K", SHAPES)
+@pytest.mark.parametrize("group", ["row", 32])
+@pytest.mark.parametrize("M", [4, 16, 64])
+def test_cfg1_bench_kernels(hip, orc, cfg1_cache, N, K, group, M):
+    """The kernel bench.py times at each M over the tile-major weights, at the
+    workload's own shapes: group-32 scales at 4 and 16 rows qlm_matmul_i8_t,
+    every other case qlm_matmul_i8_tm (which takes its int8-digit form,
+    k_act_digits + k_mm_rows64, for per-row scales at N >= 8192 or more than
+    16 rows with K > 4096, and the bf16 matrix-core form elsewhere)."""
+    g = K if group == "row" else 32
+    key = (N, K, g)
+    if key not in cfg1_cache:
+        cfg1_cache.clear()  # one shape's weights resident at a time
+        wr = np.random.default_rng(N * 31 + K + g)
+        q, s = cfg1_weights(wr, N, K, g)
+        qz, sz = swizzle(hip, dev(hip, q), dev(hip, s), g, N, K)
+        cfg1_cache[key] = (q, s, qz, sz)
+    q, s, qz, sz = cfg1_cache[key]
+    rng = np.random.default_rng(N + K + M)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    rows = sample_rows(N)
+    ref = orc.matmul_i8(x, np.ascontiguousarray(q[rows]), np.ascontiguousarray(s[rows]), g)
+    dy = hip.DeviceBuffer(M * N * 4)
+    if M <= 16 and g == 32:
+        kern = "qlm_matmul_i8_t"
+        nbytes = hip.lib().qlm_matmul_i8_t_workspace_bytes(M, N, K, 0)
+    else:
+        kern = "qlm_matmul_i8_tm"
+        nbytes = hip.lib().qlm_matmul_i8_workspace_bytes(M, N, K, 0)
+    work = hip.DeviceBuffer(nbytes)
+    say(f"cfg1 bench kernel {kern} {N}x{K} M={M} group={group}")
+    hip.call(kern, dev(hip, x), K, None, 0.0, qz, sz, g, dy, N, M, N, K, 0, work, nbytes, None)
     assert rel_err(dy.to_numpy((M, N), np.float32)[:, rows], ref) < 1e-5
 
 
