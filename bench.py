@@ -10,8 +10,10 @@ Workload of `value` (one "step" = one greedy decode step of every sequence):
   prompts (batched prefill of positions 0..2046, untimed), greedy decode; the
   whole step is one replayed hipGraph. `value` = batch-1 decode tokens/s over
   exactly --steps timed steps after --warmup untimed steps; batch 16 beside it.
-  `parity` compares the batch-1 stream with the reference's IEEE build on the
-  same checkpoint and prompt (tests/golden/4b_greedy.npz, 128 steps).
+  `parity` compares greedy streams with the reference's IEEE build on the same
+  checkpoint and prompts (tests/golden/4b_greedy.npz, 4b_greedy_seq1.npz:
+  sequences 0 and 1 of the batch, 256 steps each), at batch 1 and as rows of
+  the batch-16 run, from generate runs of their own outside the timed region.
 
 Isolated kernels (every launch timed with HIP events around graph replays of
 back-to-back launches on the launching stream, operands cycled over copies
@@ -37,6 +39,7 @@ Usage: python bench.py [--gpus 1] [--steps 256] [--warmup 8] [--kernel-only]
 from __future__ import annotations
 
 import argparse
+import hashlib
 import ctypes as C
 import json
 import os
@@ -55,6 +58,11 @@ BF16_PEAK_FLOPS = 2.5e15   # dense bf16 matrix-core peak of MI355X
 FP32_MFMA_PEAK_FLOPS = 157.3e12  # dense fp32 matrix-core peak of MI355X
 METRIC = "decode tokens/sec at batch 1 and 16 (4B int8); int8 GEMV achieved HBM GB/s"
 GOLDEN_4B = os.path.join(ROOT, "tests", "golden", "4b_greedy.npz")
+GOLDEN_4B_SEQ1 = os.path.join(ROOT, "tests", "golden", "4b_greedy_seq1.npz")
+# the dominant kernel's source: a PMC record is this build's only if it
+# carries the same hash
+DOM_SOURCES = [os.path.join(ROOT, "quicklm_amd", "csrc", "kernels", f)
+               for f in ("gemv.hip", "common.hpp")]
 POOL_BYTES = 1 << 30  # operands cycled over at least this many bytes
 
 
@@ -399,6 +407,15 @@ DOM_NAME = ("k_gemv_mx<8, 2, 5, false, 1, 2, false> (RMSNorm + gate/up GEMV + Sw
 PMC_FILE = os.path.join(ROOT, "profiles", "gemv_gate_up_4b_pmc.json")
 
 
+def dominant_source_sha():
+    """sha256 over the dominant kernel's source files, in order."""
+    h = hashlib.sha256()
+    for path in DOM_SOURCES:
+        with open(path, "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()
+
+
 def dominant_bytes():
     """Algorithmic HBM bytes of one launch: int8 weights, group scales, x and
     the norm gain read once, the F outputs written once."""
@@ -476,28 +493,47 @@ def run_decode(eng, prompts, warmup, steps, graph=True):
             "tokens": toks}
 
 
-def ieee_parity(prompt, tokens):
-    """The batch-1 stream against the reference's IEEE build on the same
-    checkpoint and prompt (committed fixture, 128 steps): first divergence and
-    the reference's top-2 logit margin there."""
-    if not os.path.exists(GOLDEN_4B):
+def ieee_parity(eng, prompts, batch):
+    """Greedy streams against the reference's IEEE build on the same
+    checkpoint and prompts (committed fixtures: sequences 0 and 1 of the
+    batch, 256 steps each), from generate runs of their own outside the timed
+    region: each sequence at batch 1, and rows 0 and 1 of a batch-`batch`
+    run. Per stream: the length of the prefix equal to the reference's and
+    the reference's top-2 margin where it first differs."""
+    gold = []
+    for k, path in ((0, GOLDEN_4B), (1, GOLDEN_4B_SEQ1)):
+        if not os.path.exists(path):
+            continue
+        g = np.load(path)
+        if prompts.shape[1] != len(g["prompt"]) or not np.array_equal(prompts[k], g["prompt"]):
+            return {"note": "prompts differ from the fixtures' (non-default --prompt-len)"}
+        gold.append((k, g))
+    if not gold:
         return None
-    g = np.load(GOLDEN_4B)
-    if len(prompt) != len(g["prompt"]) or not np.array_equal(prompt, g["prompt"]):
-        return {"note": "prompt differs from the fixture's (non-default --prompt-len)"}
-    ref = g["tokens"]
-    got = tokens[: len(ref)]
-    diff = np.nonzero(got != ref[: len(got)])[0]
-    first = int(diff[0]) if diff.size else int(len(got))
-    fast = g["tokens_fast"]
-    fd = np.nonzero(fast != ref)[0]
-    margin = g["margin"]
-    return {"reference": "reference sources built with IEEE flags, same checkpoint and prompt "
-                         "(tests/golden/4b_greedy.npz)",
-            "steps_compared": int(len(got)), "gpu_tokens_match_prefix_ieee": first,
-            "margin_at_divergence": float(margin[first]) if first < len(got) else None,
-            "min_margin_in_prefix": float(margin[:first].min()) if first else None,
-            "reference_fast_math_matches_ieee_prefix": int(fd[0]) if fd.size else int(len(ref))}
+
+    def cmp(got, g):
+        ref = g["tokens"]
+        diff = np.nonzero(got[:len(ref)] != ref)[0]
+        first = int(diff[0]) if diff.size else int(len(ref))
+        return {"steps_compared": int(len(ref)), "match_prefix": first,
+                "margin_at_divergence": float(g["margin"][first]) if first < len(ref) else None,
+                "min_margin_in_prefix": float(g["margin"][:first].min()) if first else None}
+
+    res = {"reference": "reference sources built with IEEE flags, same checkpoint and prompts "
+                        "(tests/golden/4b_greedy.npz, 4b_greedy_seq1.npz)", "batch1": {},
+           "batch" + str(batch): {}}
+    n = max(len(g["tokens"]) for _, g in gold)
+    for k, g in gold:
+        out, _, _ = eng.generate(prompts[k:k + 1], n)
+        res["batch1"][f"seq{k}"] = cmp(out[0], g)
+    if batch > 1:
+        out, _, _ = eng.generate(prompts[:batch], n)
+        for k, g in gold:
+            res["batch" + str(batch)][f"seq{k}"] = cmp(out[k], g)
+    g0 = gold[0][1]
+    fd = np.nonzero(g0["tokens_fast"] != g0["tokens"])[0]
+    res["reference_fast_math_matches_ieee_prefix"] = int(fd[0]) if fd.size else len(fd)
+    return res
 
 
 def run_spec(target, draft, prompt, n_new, K, name):
@@ -584,9 +620,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--prompt-len", type=int, default=2048)
     ap.add_argument("--batch", type=int, default=16, help="second batch size (0 to skip)")
-    ap.add_argument("--cpu-prompt", type=int, default=512,
-                    help="prompt ids prefilled by the CPU baseline (a prefix of the 2048)")
-    ap.add_argument("--cpu-decode", type=int, default=128)
+    ap.add_argument("--cpu-prompt", type=int, default=2048,
+                    help="prompt ids of the CPU baseline (a prefix of the benchmark prompt; its "
+                         "first n-1 are prefilled untimed)")
+    ap.add_argument("--cpu-decode", type=int, default=64)
     ap.add_argument("--kernel-only", action="store_true",
                     help="only the dominant-kernel timing and the copy of known size (for "
                          "rocprofv3 --pmc passes)")
@@ -648,7 +685,8 @@ def main():
         if own_dir:
             synth.write_model(mdir, "4b")
         log(f"4B checkpoint written in {time.perf_counter() - t0:.1f}s ({mdir})")
-        max_seq = args.prompt_len + args.warmup + args.steps
+        # room for the parity runs' 256 steps after the prompt too
+        max_seq = args.prompt_len + max(args.warmup + args.steps, 256) + 8
         Bmax = max(1, args.batch)
         t0 = time.perf_counter()
         eng = Engine(mdir, max_seq_len=max_seq, max_batch=Bmax, precision="int8")
@@ -659,9 +697,6 @@ def main():
         r1 = run_decode(eng, prompts[:1], args.warmup, args.steps, graph)
         log(f"batch 1: {r1['tok_s']:.1f} tok/s ({r1['ms_per_step']:.3f} ms/step), prefill "
             f"{r1['prefill_s']:.3f}s, kernels/step {eng.kernels_per_step()}")
-        parity = ieee_parity(prompts[0], r1["tokens"][0])
-        if parity:
-            log(f"IEEE reference parity: {parity}")
         rB = None
         if args.batch > 1:
             rB = run_decode(eng, prompts[:args.batch], args.warmup, args.steps, graph)
@@ -670,11 +705,14 @@ def main():
             same = len(a0) if np.array_equal(a0, b0) else int(np.argmax(a0 != b0))
             rB["row0_matches_batch1"] = same
             log(f"batch row 0 matches the batch-1 stream for {same}/{len(a0)} tokens")
+        parity = ieee_parity(eng, prompts, args.batch)
+        if parity:
+            log(f"IEEE reference parity: {parity}")
 
         cpu = None
         if not args.skip_cpu:
             cpu = cpu_baseline(mdir, prompts[0], args.cpu_prompt, args.cpu_decode)
-            # the same short prompt on the GPU: the fast-math build's stream beside it
+            # the same prompt on the GPU: the fast-math build's stream beside it
             g, _, _ = eng.generate(prompts[:1, :args.cpu_prompt], args.cpu_decode)
             match = int(np.argmax(g[0] != cpu["tokens"])) if not np.array_equal(
                 g[0], cpu["tokens"]) else args.cpu_decode
@@ -803,8 +841,11 @@ def main():
     if os.path.exists(PMC_FILE):
         with open(PMC_FILE) as f:
             pmc = json.load(f)
-        if pmc.get("bytes") == dom_b:
+        if pmc.get("bytes") == dom_b and pmc.get("kernel_source_sha256") == dominant_source_sha():
             traffic, traffic_src = pmc.get("traffic_bytes"), os.path.relpath(PMC_FILE, ROOT)
+        else:
+            log("PMC record is not of this build's dominant kernel (source hash differs): "
+                "traffic left null")
     achieved = dom_b / dom_us / 1e3
     result["roofline"] = {"kernel": DOM_NAME, "bound": "hbm", "achieved": round(achieved, 1),
                           "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -816,6 +857,14 @@ def main():
             f"4B checkpoint, batch 1: prefill (untimed) of the first {args.cpu_prompt - 1} ids "
             f"of the same 2048-token prompt, then {args.cpu_decode} greedy decode steps (timed) "
             f"at context {args.cpu_prompt}-{args.cpu_prompt + args.cpu_decode}"))
+        if args.batch > 1:
+            # the reference decodes one sequence at a time: a batch of B is B
+            # sequential runs, B * n tokens in B times one run's decode time
+            result["cpu_baseline"]["batch" + str(args.batch)] = {
+                "value": cpu["value"], "unit": "tokens/s",
+                "derivation": f"{args.batch} sequential single-sequence runs (the reference "
+                              f"has no batched decode): {args.batch}x the tokens in "
+                              f"{args.batch}x the time of the measured run above"}
     print(json.dumps(result), flush=True)
 
 

@@ -435,8 +435,12 @@ int qlm_attention_decode(const float* q, const void* k_cache, const void* v_cach
  * positions at hd 128 and 32 to 256 at hd 256, or at most min(256,
  * ceil(ctx / 64)) at hd 128 and min(256, ceil(ctx / 32)) at hd 256 for a
  * bf16 cache; the larger of the two) and returns QLM_ERR_SCRATCH, launching
- * nothing, when the call's records exceed the maximum. The call allocates nothing; its first call on a
- * device looks the array's address up once. Every call on one GPU shares
+ * nothing, when the call's records exceed the maximum. The call allocates
+ * nothing. qlm_set_device looks the array's address up on that device, so a
+ * first call after it (under graph capture included) makes no runtime
+ * query; without it, the first call on a device does the lookup (a
+ * hipGetSymbolAddress, which should then run outside any capture). Every
+ * call on one GPU shares
  * that GPU's array: calls that may overlap on one GPU (different streams,
  * different host threads) race, so order them on one stream. Nothing in the
  * array needs clearing between calls. */

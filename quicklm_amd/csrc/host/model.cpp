@@ -360,7 +360,8 @@ void DecoderModel::enqueue_step(int B) {
     int dn_i = 0, at_i = 0;
     for (auto& w : layers_) {
         Tensor in_ln({H}, w.in_ln.get<float>()), post_ln({H}, w.post_ln.get<float>());
-        if (w.linear && B == 1 && math::headnorm_supported(w.dn_out.view())) {
+        // the column-split mixer reads proj rows as float4 (stride % 4 == 0)
+        if (w.linear && B == 1 && Pmax % 4 == 0 && math::headnorm_supported(w.dn_out.view())) {
             // one sequence: the mixer over H x 8 workgroups, its head RMSNorm
             // applied by the out-projection's prologue
             Tensor proj({B, PD_}, proj_.get<float>());
@@ -421,8 +422,15 @@ void DecoderModel::enqueue_step(int B) {
     // Step tail: final norm + lm_head + greedy sample + advance, then the
     // embedding of the token now at pos (the next step's input, or the next
     // prompt token) -- model.cpp:193-199, :263-274, :157-164.
-    if (B == 1 && !native_) {
-        const Tensor lm = lm_head_.view();
+    const Tensor lm = lm_head_.view();
+    // the fused greedy tail needs a one-row GEMV shape for the lm_head (the
+    // tile-major mx forms, or the row-major GEMV when the model kept rows)
+    int tail_waves = 0, tail_ring = 0, tail_grid = 0;
+    const bool fused_tail =
+        B == 1 && !native_ &&
+        (lm.int8_data ||
+         qlm_gemv_i8_mx_shape(V, H, 0, &tail_waves, &tail_ring, &tail_grid) == QLM_OK);
+    if (fused_tail) {
         int rc = QLM_ERR_SHAPE;
         if (lm.int4_tiles)
             rc = qlm_lm_head_greedy_mx4(h_.get<float>(), final_norm_.get<float>(), eps,
@@ -436,7 +444,7 @@ void DecoderModel::enqueue_step(int B) {
                                        H, tail_work_.get(), tokens_.get<int>(), ld_tokens_,
                                        pos_.get<int>(), prompt_len_.get<int>(), embed_.get<float>(),
                                        H, h_.get<float>(), stream_);
-        if (rc == QLM_ERR_SHAPE)
+        if (rc == QLM_ERR_SHAPE && lm.int8_data)
             rc = qlm_lm_head_greedy(h_.get<float>(), final_norm_.get<float>(), eps,
                                     lm_head_.q.get<int8_t>(), lm_head_.s.get<float>(),
                                     lm_head_.group, logits_.get<float>(), V, H, tail_work_.get(),

@@ -1384,5 +1384,12 @@ extern "C" int qlm_gqa_prefill(float* qkv, int ldqkv, const float* q_norm, const
 // measured inside a first prefill or decode step).
 hipError_t qlm_load_attention() {
     hipFuncAttributes a;
-    return hipFuncGetAttributes(&a, reinterpret_cast<const void*>((k_attn_combine<128, 1>)));
+    hipError_t e = hipFuncGetAttributes(&a, reinterpret_cast<const void*>((k_attn_combine<128, 1>)));
+    if (e != hipSuccess) return e;
+    // the no-allocation entry point's scratch address on this device, so
+    // that its first call (possibly under graph capture) makes no runtime
+    // query
+    float* w = nullptr;
+    const int rc = scratch_ptr(&w);
+    return rc == QLM_OK ? hipSuccess : (rc > 0 ? (hipError_t)rc : hipErrorInvalidValue);
 }

@@ -204,9 +204,11 @@ def test_matmul_t_refuses(hip, orc, rng):
     """M > 16, K not a multiple of 64, group K, an unbuilt shape and a slice
     longer than 64 blocks return an error before any launch."""
     lib = hip.lib()
-    q, s = _weights(orc, rng, 64, 4096, 32)
+    # buffers sized for the largest call below (64 rows, K up to 4160, 17
+    # activation rows), so not even a regressed check could read past them
+    q, s = _weights(orc, rng, 64, 4160, 32)
     dq, ds = dev(hip, q), dev(hip, s)
-    x = dev(hip, rng.standard_normal((17, 4096)).astype(np.float32))
+    x = dev(hip, rng.standard_normal((17, 4160)).astype(np.float32))
     y = hip.DeviceBuffer(17 * 64 * 4)
     work = hip.DeviceBuffer(1 << 22)
     for M, K, g in ((17, 2560, 32), (4, 2560 + 32, 32), (4, 2560, 2560)):
@@ -328,13 +330,3 @@ def test_matmul_i8_rows64_rounds(hip, orc, rng, M, N, K, epi):
     assert rel_err(dy.to_numpy((M, N), np.float32), ref) < 1e-5
 
 
-def test_matmul_i8_rows64_rejects(hip):
-    """Shapes outside the form are refused with QLM_ERR_SHAPE (-2) before any
-    launch: 1 or 65 rows, SwiGLU, K not a multiple of 64."""
-    lib = hip.lib()
-    fake = 4096
-    for M, K, e in ((1, 256, 0), (65, 256, 0), (32, 256, 2), (32, 200, 0)):
-        assert lib.qlm_matmul_i8_rows64(fake, K, None, C.c_float(0.0), fake, fake, fake, 64, M,
-                                        64, K, e, fake, C.c_size_t(1 << 30), None) == -2
-    assert lib.qlm_matmul_i8_rows64_workspace_bytes(1, 64, 256, 0) == 0
-    assert lib.qlm_matmul_i8_rows64_workspace_bytes(33, 64, 256, 2) == 0

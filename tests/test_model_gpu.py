@@ -260,3 +260,36 @@ def test_one_weight_copy(hip, tiny_dir, precision):
     say(f"{precision}: device bytes {used / 1e9:.3f} GB, tile-major weights {tiles / 1e9:.3f} GB, "
         f"embedding {embed / 1e9:.3f} GB")
     assert used < tiles + embed + 450e6
+
+
+def test_shapes_without_fast_forms_fall_back(hip, tmp_path):
+    """A model whose hidden size has no launch shape of the matrix-core
+    one-row GEMV (3072 = 48 blocks of 64: no instantiated (waves, ring) pair)
+    and an odd DeltaNet head count (3 heads: the projection row of 4 * 384 +
+    6 = 1542 floats is not a multiple of 4, which the column-split mixer
+    needs): the decode step takes the general forms instead (the lm_head
+    through the matrix-core matmul and the two-pass argmax, the one-workgroup-
+    a-head mixer), at batch 1 and 2, and the greedy stream equals the oracle
+    model's."""
+    from oracle.oracle import Oracle, OracleModel
+    from quicklm_amd import synth
+    from quicklm_amd.engine import Engine
+
+    cfg = dict(synth.MICRO, name="odd", index=10, hidden_size=3072, linear_num_heads=3,
+               intermediate_size=1024)
+    d = str(tmp_path)
+    synth.write_model(d, cfg)
+    prompt = synth.prompt_tokens(20, seed=6, vocab=4096)[0]
+    eng = Engine(d, max_seq_len=64, max_batch=2, precision="int8")
+    try:
+        got, _, _ = eng.generate(prompt[None, :], 12)
+        lg = eng.last_logits(0)
+        both, _, _ = eng.generate(np.stack([prompt, prompt[::-1].copy()]), 12)
+    finally:
+        eng.close()
+    want, wlg = OracleModel(d, 64, Oracle()).generate(prompt, 12, keep_logits=True)
+    err = float(np.abs(lg - wlg[-1]).max() / np.abs(wlg[-1]).max())
+    say("odd-shaped micro: last-step logit rel err", err, "tokens", got[0][:6], want[:6])
+    assert np.array_equal(got[0], want)
+    assert np.array_equal(both[0], got[0])
+    assert err < 1e-3
