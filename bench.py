@@ -692,7 +692,7 @@ def main():
         eng = Engine(mdir, max_seq_len=max_seq, max_batch=Bmax, precision="int8")
         log(f"engine load + device quantisation {time.perf_counter() - t0:.1f}s, "
             f"{eng.weight_bytes / 1e9:.3f} GB of int8 weights+scales")
-        prompts = synth.prompt_tokens(args.prompt_len, seed=4, batch=Bmax)
+        prompts = synth.prompt_tokens(args.prompt_len, seed=4, batch=max(2, Bmax))
         graph = not args.eager
         r1 = run_decode(eng, prompts[:1], args.warmup, args.steps, graph)
         log(f"batch 1: {r1['tok_s']:.1f} tok/s ({r1['ms_per_step']:.3f} ms/step), prefill "
