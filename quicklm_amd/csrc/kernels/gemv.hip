@@ -1209,34 +1209,39 @@ bool mx_fits(int K, int nw, int ring) {
 
 // Measured launch shapes of the 4B hybrid's decode projections (N, K,
 // epilogue -> waves per workgroup, ring depth, grid), graph replays on MI355X.
+// group: the scale group an entry is for (0: either).
 struct MxTuned {
-    int N, K, epi, nw, ring, grid;
+    int N, K, epi, group, nw, ring, grid;
 };
 constexpr MxTuned kMxTuned[] = {
-    {9728, 2560, EPI_SWIGLU, 8, 5, 203},     // gate/up (3 tiles per workgroup)
-    {2560, 9728, EPI_RESID, 16, 10, 160},    // down
-    {8224, 2560, EPI_STORE, 8, 5, 512},      // DeltaNet in_proj [qkv|z|b|a]
-    {5120, 2560, EPI_STORE, 8, 5, 320},      // GQA q(+gate)/k/v
-    {2560, 2048, EPI_RESID, 8, 4, 160},      // out_proj / o_proj
-    {151936, 2560, EPI_STORE, 8, 5, 256},    // lm_head (also its greedy form)
+    {9728, 2560, EPI_SWIGLU, 0, 8, 5, 203},     // gate/up (3 tiles per workgroup)
+    {2560, 9728, EPI_RESID, 0, 16, 10, 160},    // down
+    {8224, 2560, EPI_STORE, 0, 8, 5, 512},      // DeltaNet in_proj [qkv|z|b|a]
+    {5120, 2560, EPI_STORE, 0, 8, 5, 320},      // GQA q(+gate)/k/v
+    {2560, 2048, EPI_RESID, 0, 8, 4, 160},      // out_proj / o_proj
+    {151936, 2560, EPI_STORE, 0, 8, 5, 192},  // lm_head (also its greedy form)
+    {12288, 4096, EPI_STORE, 32, 16, 4, 768},   // 12288 x 4096, group-32 scales
 };
 
 // Where int4 weights (half the bytes) measured a different best shape.
 constexpr MxTuned kMx4Tuned[] = {
-    {151936, 2560, EPI_STORE, 8, 5, 512},    // lm_head
+    {151936, 2560, EPI_STORE, 0, 8, 5, 512},    // lm_head
 };
 
 // Launch shape: the tuned table (int4 overrides first), else the fewest
 // waves per workgroup that give >= 2048 waves in all (each a K-slice of a
 // tile) among the instantiated pairs, and one tile per workgroup up to the
 // greedy tail's key slots. nw = 0 when no pair fits K.
-MxConfig mx_config(int N, int K, int epi, bool w4 = false) {
+MxConfig mx_config(int N, int K, int epi, bool w4 = false, int group = 0) {
     const int e = epi == EPI_ARGMAX ? EPI_STORE : epi;
+    auto match = [&](const MxTuned& t) {
+        return t.N == N && t.K == K && t.epi == e && (t.group == 0 || t.group == group);
+    };
     if (w4)
         for (const MxTuned& t : kMx4Tuned)
-            if (t.N == N && t.K == K && t.epi == e) return MxConfig{t.nw, t.ring, t.grid};
+            if (match(t)) return MxConfig{t.nw, t.ring, t.grid};
     for (const MxTuned& t : kMxTuned)
-        if (t.N == N && t.K == K && t.epi == e) return MxConfig{t.nw, t.ring, t.grid};
+        if (match(t)) return MxConfig{t.nw, t.ring, t.grid};
     const int tiles = (N + 15) / 16, nblk = K / 64;
     MxConfig c{0, 0, tiles < kMaxXsGrid ? tiles : kMaxXsGrid};
     for (int nw = 4; nw <= 16; nw *= 2) {
@@ -1536,7 +1541,7 @@ extern "C" int qlm_lm_head_greedy_mx(const float* x, const float* norm_w, float 
     if (!rowscale && group != 32) return QLM_ERR_SHAPE;
     if (((uintptr_t)x | (uintptr_t)q_tiles | (uintptr_t)norm_w | (uintptr_t)work) & 15u)
         return QLM_ERR_SHAPE;
-    const MxConfig c = mx_config(V, K, EPI_ARGMAX);
+    const MxConfig c = mx_config(V, K, EPI_ARGMAX, false, group);
     if (c.nw == 0) return QLM_ERR_SHAPE;
     return mx_dispatch(PRO_RMSNORM, EPI_ARGMAX, c, x, norm_w, eps, q_tiles, s_tiles, rowscale,
                        logits, V, K, as_stream(stream),
@@ -1565,7 +1570,7 @@ extern "C" int qlm_gemv_i8_mx(const float* x, const float* norm_w, float eps,
     const int pro = norm_w ? PRO_RMSNORM : PRO_NONE;
     if (epilogue == EPI_SWIGLU && !norm_w) return QLM_ERR_ARG;
     if (epilogue == EPI_RESID && pro == PRO_RMSNORM) return QLM_ERR_ARG;
-    const MxConfig c = mx_config(N, K, epilogue);
+    const MxConfig c = mx_config(N, K, epilogue, false, group);
     if (c.nw == 0) return QLM_ERR_SHAPE;
     return mx_dispatch(pro, epilogue, c, x, norm_w, eps, q_tiles, s_tiles, rowscale, y, N, K,
                        as_stream(stream));
