@@ -406,6 +406,67 @@ __global__ __launch_bounds__(kColThreads) void k_deltanet_cols(
     }
 }
 
+// Column split of the isolated step, for few (sequence, head) pairs: the
+// 128 value columns of a head over kSplit workgroups of kColW columns (the
+// recurrence is independent per value column, attention.cpp:513-569), so
+// B = 1 x 32 heads runs 256 workgroups instead of 32. Thread (rg, j) owns
+// rows rg*8 .. rg*8+7 of column 16 s + j; the sums over rows meet by lane
+// shuffles within a wave and through LDS across the 4 waves.
+__global__ __launch_bounds__(kColThreads) void k_gated_delta_step_cols(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+    const float* __restrict__ decay, const float* __restrict__ beta, float* __restrict__ state,
+    float* __restrict__ out, int H) {
+    constexpr int NWV = kColThreads / QLM_WAVE;
+    __shared__ float qs[kD], ks[kD], dl[kColW];
+    __shared__ float red[NWV][kColW];
+    const int bh = blockIdx.x / kSplit, sp = blockIdx.x % kSplit;  // bh = b*H + h
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int j = tid & (kColW - 1), rg = tid / kColW;
+    const int col = sp * kColW + j;
+    float* Sh = state + (size_t)bh * kD * kD;
+    // operands, unconditional: this thread's q or k element, v of its
+    // column, the gates, then its state rows
+    const float qk = tid < kD ? q[(size_t)bh * kD + tid] : k[(size_t)bh * kD + tid - kD];
+    const float vj = v[(size_t)bh * kD + col];
+    const float dec = decay[bh], bt = beta[bh];
+    float sr[kColRows];
+#pragma unroll
+    for (int r = 0; r < kColRows; ++r) sr[r] = Sh[(size_t)(rg * kColRows + r) * kD + col];
+    if (tid < kD) qs[tid] = qk;
+    else ks[tid - kD] = qk;
+    __syncthreads();
+    // (1) decay and kv[col] = k . S_decayed[:, col]
+    float kv = 0.0f;
+#pragma unroll
+    for (int r = 0; r < kColRows; ++r) {
+        sr[r] *= dec;
+        kv = fmaf(ks[rg * kColRows + r], sr[r], kv);
+    }
+    kv += __shfl_xor(kv, 16, QLM_WAVE);
+    kv += __shfl_xor(kv, 32, QLM_WAVE);
+    if (lane < kColW) red[wave][lane] = kv;
+    __syncthreads();
+    if (tid < kColW) dl[tid] = vj - ((red[0][tid] + red[1][tid]) + (red[2][tid] + red[3][tid]));
+    __syncthreads();
+    // (2) S += (beta k) delta^T ; (3) o[col] = q . S_new[:, col]
+    const float dj = dl[j];
+    float o = 0.0f;
+#pragma unroll
+    for (int r = 0; r < kColRows; ++r) {
+        const int i = rg * kColRows + r;
+        sr[r] = fmaf(bt * ks[i], dj, sr[r]);
+        o = fmaf(qs[i], sr[r], o);
+        Sh[(size_t)i * kD + col] = sr[r];
+    }
+    o += __shfl_xor(o, 16, QLM_WAVE);
+    o += __shfl_xor(o, 32, QLM_WAVE);
+    if (lane < kColW) red[wave][lane] = o;  // red's kv sums were read before the last barrier
+    __syncthreads();
+    if (tid < kColW)
+        out[(size_t)bh * kD + col] = ((red[0][tid] + red[1][tid]) + (red[2][tid] + red[3][tid])) *
+                                     (1.0f / sqrtf((float)kD));
+}
+
 // Prefill of one sequence over T consecutive rows of proj (positions
 // p0 .. p0+T-1), one workgroup per head: the reference processes the rows of
 // a prompt one after another through the same recurrence
@@ -531,8 +592,15 @@ extern "C" int qlm_gated_delta_step(const float* q, const float* k, const float*
     if (!q || !k || !v || !decay || !beta || !state || !out || B <= 0 || H <= 0)
         return QLM_ERR_ARG;
     if (d != kD) return QLM_ERR_SHAPE;
-    hipLaunchKernelGGL(k_gated_delta_step, dim3(B * H), dim3(kThreads), 0, as_stream(stream), q, k,
-                       v, decay, beta, state, out, H);
+    // few (sequence, head) pairs: the column split keeps more of the GPU busy
+    // (measured at 32 heads: B = 1 and 4 faster split, B >= 8 one workgroup
+    // a head)
+    if (B <= 4)
+        hipLaunchKernelGGL(k_gated_delta_step_cols, dim3(B * H * kSplit), dim3(kColThreads), 0,
+                           as_stream(stream), q, k, v, decay, beta, state, out, H);
+    else
+        hipLaunchKernelGGL(k_gated_delta_step, dim3(B * H), dim3(kThreads), 0, as_stream(stream),
+                           q, k, v, decay, beta, state, out, H);
     return qlm_launch_status();
 }
 

@@ -158,9 +158,11 @@ def _sig(x):
     return (1 / (1 + np.exp(-x))).astype(np.float32)
 
 
-def test_cfg2_delta_step_b32(hip, orc, rng):
-    """The recurrent step at batch 32, 32 heads, three steps in a row."""
-    B, H, d = 32, 32, 128
+@pytest.mark.parametrize("B", [1, 8, 32])
+def test_cfg2_delta_step(hip, orc, rng, B):
+    """The recurrent step at the workload's batches (1, 8, 32 sequences), 32
+    heads, three steps in a row."""
+    H, d = 32, 128
     S = (rng.standard_normal((B, H, d, d)) * 0.01).astype(np.float32)
     dS, Sref = dev(hip, S), S.copy()
     for step in range(3):
@@ -171,7 +173,7 @@ def test_cfg2_delta_step_b32(hip, orc, rng):
         b = _sig(rng.standard_normal((B, H)))
         o_ref, Sref = orc.gated_delta_step(q, k, v, a, b, Sref)
         do = hip.DeviceBuffer(q.nbytes)
-        say("cfg2 delta step B=32 H=32 step", step)
+        say(f"cfg2 delta step B={B} H=32 step", step)
         hip.call("qlm_gated_delta_step", dev(hip, q), dev(hip, k), dev(hip, v), dev(hip, a),
                  dev(hip, b), dS, do, B, H, d, None)
         assert rel_err(do.to_numpy(q.shape, np.float32), o_ref) < 1e-5

@@ -618,8 +618,10 @@ def _l2n(x):
     return (x / np.linalg.norm(x, axis=-1, keepdims=True)).astype(np.float32)
 
 
-@pytest.mark.parametrize("B,H", [(1, 32), (8, 32), (3, 5)])
+@pytest.mark.parametrize("B,H", [(1, 32), (4, 32), (8, 32), (3, 5)])
 def test_gated_delta_step(hip, orc, rng, B, H):
+    """The isolated step over 3 steps: column-split workgroups at B <= 4, one
+    workgroup a head above."""
     d = 128
     S = (rng.standard_normal((B, H, d, d)) * 0.01).astype(np.float32)
     dS = dev(hip, S)
