@@ -16,16 +16,16 @@
 // Every decay factor is exp of a non-positive number (ratios, never 1/gamma).
 //
 // Kernels (one stream, in order):
-//   k_dn_chunk_prep   per (row, head): conv taps from the prompt rows or the
-//                     ring (positions before p0), SiLU, L2 norms, gates --
+//   k_dn_chunk_prep   per (16 rows, head): conv taps from the prompt rows or
+//                     the ring (positions before p0), SiLU, L2 norms, gates --
 //                     the decode step's arithmetic;
-//   k_dn_chunk_intra  per (chunk, head): K K^T on the matrix cores, the
-//                     triangular solve for T (one column per lane, unrolled),
-//                     U, Wk and the masked, decayed Q K^T on the matrix cores;
+//   k_dn_chunk_intra  per (chunk, head): K K^T and the masked, decayed Q K^T
+//                     on the matrix cores, the triangular solve for T (one
+//                     column per lane, unrolled), U and Wk on the matrix cores;
 //   k_dn_chunk_inter  per (head, 16 value columns): chunks in order; W, O and
 //                     the state update on the matrix cores, the state slice
 //                     living in the accumulators;
-//   k_dn_chunk_post   per (row, head): head RMSNorm + SiLU(z) gate (decode
+//   k_dn_chunk_post   per (16 rows, head): head RMSNorm + SiLU(z) gate (decode
 //                     arithmetic) and the conv ring rows of the last positions.
 
 #include "common.hpp"
@@ -49,60 +49,84 @@ __device__ __forceinline__ f32x4 mma(float a, float b, f32x4 c) {
 
 __device__ __forceinline__ size_t rix(int t, int h, int H) { return ((size_t)t * H + h) * kD; }
 
+// Rows a prep or post workgroup handles (a conv window slides down them).
+constexpr int kPR = 16;
+
+// Per (16 rows, head): thread (section, column) slides the conv window down
+// the rows, the q and k outputs wait in LDS for their row norms (6 waves, a
+// norm each at a time), v goes straight out.
 __global__ __launch_bounds__(3 * kD) void k_dn_chunk_prep(
     const float* __restrict__ proj, int ldp, int T, const float* __restrict__ conv_state,
     const float* __restrict__ wt, const float* __restrict__ A_log,
     const float* __restrict__ dt_bias, int p0, int H, float* __restrict__ qn,
     float* __restrict__ kn, float* __restrict__ vv, float* __restrict__ alpha,
     float* __restrict__ beta) {
-    __shared__ float sq[kD], sk[kD];
-    const int t = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+    __shared__ float ys[2][kPR][kD];
+    const int t0 = blockIdx.x * kPR, h = blockIdx.y, tid = threadIdx.x;
+    const int nt = min(kPR, T - t0);
     const int lane = tid & 63, wave = tid >> 6;
     const int HD = H * kD, C = 3 * HD;
     const int sec = tid / kD, tt = tid % kD, ch = sec * HD + h * kD + tt;
-    float xs[3];
+    const float w0 = wt[ch], w1 = wt[(size_t)C + ch], w2 = wt[(size_t)2 * C + ch],
+                w3 = wt[(size_t)3 * C + ch];
+    // inputs of positions t-3, t-2, t-1; positions before p0 come from the
+    // ring, row (position mod 3), as the decode step reads it (zero rows on a
+    // fresh sequence)
+    float xw[3];
 #pragma unroll
     for (int j = 0; j < 3; ++j) {
-        const int r = t - 3 + j;
+        const int r = t0 - 3 + j;
         if (r >= 0) {
-            xs[j] = proj[(size_t)r * ldp + ch];
+            xw[j] = proj[(size_t)r * ldp + ch];
         } else {
-            // positions before p0 come from the ring, row (position mod 3), as
-            // the decode step reads it (zero rows on a fresh sequence)
             const int row = ((p0 + r) % 3 + 3) % 3;
-            xs[j] = conv_state[(size_t)row * C + ch];
+            xw[j] = conv_state[(size_t)row * C + ch];
         }
     }
-    const float x = proj[(size_t)t * ldp + ch];
-    float acc = 0.0f;
-    acc = nc_add_mul(acc, xs[0], wt[ch]);
-    acc = nc_add_mul(acc, xs[1], wt[(size_t)C + ch]);
-    acc = nc_add_mul(acc, xs[2], wt[(size_t)2 * C + ch]);
-    acc = nc_add_mul(acc, x, wt[(size_t)3 * C + ch]);
-    const float y = silu_f(acc);
-    if (sec == 0) sq[tt] = y;
-    else if (sec == 1) sk[tt] = y;
-    else vv[rix(t, h, H) + tt] = y;
-    __syncthreads();
-    if (wave < 2) {
-        const float* v = wave == 0 ? sq : sk;
-        const float a0 = v[lane], a1 = v[lane + 64];
-        float ss = fmaf(a0, a0, a1 * a1);
-        ss = wave_sum(ss);
-        const float nrm = sqrtf(ss + 1e-6f);
-        float* dst = (wave == 0 ? qn : kn) + rix(t, h, H);
-        dst[lane] = a0 / nrm;
-        dst[lane + 64] = a1 / nrm;
-    } else if (wave == 2 && lane == 0) {
+    float xr[kPR];  // rows past T read row T-1 and are never stored
+#pragma unroll
+    for (int r = 0; r < kPR; ++r) xr[r] = proj[(size_t)min(t0 + r, T - 1) * ldp + ch];
+#pragma unroll
+    for (int r = 0; r < kPR; ++r) {
+        float acc = 0.0f;
+        acc = nc_add_mul(acc, xw[0], w0);
+        acc = nc_add_mul(acc, xw[1], w1);
+        acc = nc_add_mul(acc, xw[2], w2);
+        acc = nc_add_mul(acc, xr[r], w3);
+        const float y = silu_f(acc);
+        if (sec < 2) ys[sec][r][tt] = y;
+        else if (r < nt) vv[rix(t0 + r, h, H) + tt] = y;
+        xw[0] = xw[1];
+        xw[1] = xw[2];
+        xw[2] = xr[r];
+    }
+    if (tid >= 2 * kD && tid - 2 * kD < nt) {
+        const int t = t0 + tid - 2 * kD;
         const float* pr = proj + (size_t)t * ldp;
         const float dt = pr[4 * HD + H + h] + dt_bias[h];
         const float sp = dt > 20.0f ? dt : log1pf(expf(dt));
         alpha[(size_t)t * H + h] = -expf(A_log[h]) * sp;
         beta[(size_t)t * H + h] = 1.0f / (1.0f + expf(-pr[4 * HD + h]));
     }
+    __syncthreads();
+    for (int i = wave; i < 2 * kPR; i += 3 * kD / 64) {
+        const int which = i & 1, r = i >> 1;
+        if (r >= nt) break;
+        const float a0 = ys[which][r][lane], a1 = ys[which][r][lane + 64];
+        float ss = fmaf(a0, a0, a1 * a1);
+        ss = wave_sum(ss);
+        const float nrm = sqrtf(ss + 1e-6f);
+        float* dst = (which == 0 ? qn : kn) + rix(t0 + r, h, H);
+        dst[lane] = a0 / nrm;
+        dst[lane + 64] = a1 / nrm;
+    }
 }
 
-__global__ __launch_bounds__(256) void k_dn_chunk_intra(
+// Global operands that feed the matrix cores straight from registers (the
+// wave's q rows for Q K^T, its 32 value columns for U = T V) are loaded at
+// the start, so their latency passes under the K staging, K K^T and the
+// solve instead of stalling each product step.
+__global__ __launch_bounds__(256, 2) void k_dn_chunk_intra(
     const float* __restrict__ qn, const float* __restrict__ kn, const float* __restrict__ vv,
     const float* __restrict__ alpha, const float* __restrict__ beta, int T, int H,
     float* __restrict__ U, float* __restrict__ Wk, float* __restrict__ Mq,
@@ -115,7 +139,24 @@ __global__ __launch_bounds__(256) void k_dn_chunk_intra(
     const int l16 = lane & 15, l4 = lane >> 4;
     const int t0 = c * kC;
     const int nt = min(kC, T - t0);
+    auto row = [&](int t) { return rix(t0 + min(t, nt - 1), h, H); };  // clamped; masked at use
 
+    // q[tq][k0 + l4] for k0 = 0, 4, .., 124 (rows of Q K^T)
+    const int tq = wave * 16 + l16;
+    float qv[kD / 4];
+    {
+        const float* qrow = qn + row(tq);
+#pragma unroll
+        for (int i = 0; i < kD / 4; ++i) qv[i] = qrow[4 * i + l4];
+    }
+    // V[k0 + l4][32 wave + 16 ct + l16] for k0 = 0, 4, .., 60 (columns of U)
+    float vr[kC / 4][2];
+#pragma unroll
+    for (int i = 0; i < kC / 4; ++i) {
+        const float* vrow = vv + row(4 * i + l4) + 32 * wave + l16;
+        vr[i][0] = vrow[0];
+        vr[i][1] = vrow[16];
+    }
     for (int i = tid; i < kC * (kD / 4); i += 256) {
         const int r = i / (kD / 4), c4 = i % (kD / 4);
         float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -158,6 +199,28 @@ __global__ __launch_bounds__(256) void k_dn_chunk_intra(
                 Ts[t * TP + s] = s < t ? bs[t] * expf(gs[t] - gs[s]) * acc[tc][i] : 0.0f;
             }
     }
+
+    // Mq[t][s] = (gamma_t/gamma_s) q_t . k_s for s <= t; wave w: rows 16w..
+    {
+        f32x4 m[4];
+#pragma unroll
+        for (int tc = 0; tc < 4; ++tc) m[tc] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < kD / 4; ++i) {
+            const float a = tq < nt ? qv[i] : 0.0f;
+#pragma unroll
+            for (int tc = 0; tc < 4; ++tc)
+                m[tc] = mma(a, Ks[(tc * 16 + l16) * KP + 4 * i + l4], m[tc]);
+        }
+        float* mq = Mq + ((size_t)c * H + h) * kC * kC;
+#pragma unroll
+        for (int tc = 0; tc < 4; ++tc)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int t = wave * 16 + l4 * 4 + i, s = tc * 16 + l16;
+                mq[t * kC + s] = (s <= t && t < nt) ? expf(gs[t] - gs[s]) * m[tc][i] : 0.0f;
+            }
+    }
     __syncthreads();
 
     // T = (I + A)^-1 diag(beta) by forward substitution; lane s < 64 owns
@@ -179,57 +242,47 @@ __global__ __launch_bounds__(256) void k_dn_chunk_intra(
     }
     __syncthreads();
 
-    // Wk = T diag(gamma) K and U = T V: wave w rows 16w.., 8 column tiles
+    // Wk = T diag(gamma) K and U = T V: wave w columns 32w..32w+31, all 64
+    // rows (four row tiles)
     {
-        f32x4 wk[8], u[8];
+        f32x4 wk[4][2], u[4][2];
 #pragma unroll
-        for (int ct = 0; ct < 8; ++ct) {
-            wk[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
-            u[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
-        }
-        for (int k0 = 0; k0 < kC; k0 += 4) {
-            const int s = k0 + l4;
-            const float tv = Ts[(wave * 16 + l16) * TP + s];
-            const float tg = tv * gam[s];
-            const float* vrow = vv + rix(t0 + (s < nt ? s : 0), h, H);
+        for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
-            for (int ct = 0; ct < 8; ++ct) {
-                wk[ct] = mma(tg, Ks[s * KP + ct * 16 + l16], wk[ct]);
-                u[ct] = mma(tv, s < nt ? vrow[ct * 16 + l16] : 0.0f, u[ct]);
+            for (int ct = 0; ct < 2; ++ct) {
+                wk[rt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+                u[rt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+#pragma unroll
+        for (int i = 0; i < kC / 4; ++i) {
+            const int s = 4 * i + l4;
+            const bool ok = s < nt;
+            const float g = gam[s];
+            const float kb0 = Ks[s * KP + 32 * wave + l16], kb1 = Ks[s * KP + 32 * wave + 16 + l16];
+            const float vb0 = ok ? vr[i][0] : 0.0f, vb1 = ok ? vr[i][1] : 0.0f;
+#pragma unroll
+            for (int rt = 0; rt < 4; ++rt) {
+                const float tv = Ts[(rt * 16 + l16) * TP + s];
+                const float tg = tv * g;
+                wk[rt][0] = mma(tg, kb0, wk[rt][0]);
+                wk[rt][1] = mma(tg, kb1, wk[rt][1]);
+                u[rt][0] = mma(tv, vb0, u[rt][0]);
+                u[rt][1] = mma(tv, vb1, u[rt][1]);
             }
         }
 #pragma unroll
-        for (int ct = 0; ct < 8; ++ct)
+        for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int t = wave * 16 + l4 * 4 + i;
-                if (t < nt) {
-                    Wk[rix(t0 + t, h, H) + ct * 16 + l16] = wk[ct][i];
-                    U[rix(t0 + t, h, H) + ct * 16 + l16] = u[ct][i];
+            for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int t = rt * 16 + l4 * 4 + i;
+                    if (t < nt) {
+                        const size_t o = rix(t0 + t, h, H) + 32 * wave + 16 * ct + l16;
+                        Wk[o] = wk[rt][ct][i];
+                        U[o] = u[rt][ct][i];
+                    }
                 }
-            }
-    }
-
-    // Mq[t][s] = (gamma_t/gamma_s) q_t . k_s for s <= t
-    {
-        f32x4 m[4];
-#pragma unroll
-        for (int tc = 0; tc < 4; ++tc) m[tc] = f32x4{0.f, 0.f, 0.f, 0.f};
-        const int tq = wave * 16 + l16;
-        const float* qrow = qn + rix(t0 + (tq < nt ? tq : 0), h, H);
-        for (int k0 = 0; k0 < kD; k0 += 4) {
-            const float a = tq < nt ? qrow[k0 + l4] : 0.0f;
-#pragma unroll
-            for (int tc = 0; tc < 4; ++tc) m[tc] = mma(a, Ks[(tc * 16 + l16) * KP + k0 + l4], m[tc]);
-        }
-        float* mq = Mq + ((size_t)c * H + h) * kC * kC;
-#pragma unroll
-        for (int tc = 0; tc < 4; ++tc)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int t = wave * 16 + l4 * 4 + i, s = tc * 16 + l16;
-                mq[t * kC + s] = (s <= t && t < nt) ? expf(gs[t] - gs[s]) * m[tc][i] : 0.0f;
-            }
     }
 }
 
@@ -415,28 +468,33 @@ __global__ __launch_bounds__(256) void k_dn_chunk_inter(
             Sg[(size_t)((2 * wave + tt) * 16 + l4 * 4 + i) * kD + jb + l16] = sacc[tt][i];
 }
 
-__global__ __launch_bounds__(kD) void k_dn_chunk_post(
+// Per (16 rows, head): a wave a row at a time (its two 64-column halves
+// summed as the decode step's two waves are), and the conv ring rows of the
+// last three positions.
+__global__ __launch_bounds__(256) void k_dn_chunk_post(
     const float* __restrict__ O, const float* __restrict__ proj, int ldp, int T,
     const float* __restrict__ norm_w, float* __restrict__ out, int ldo, int H,
     float* __restrict__ conv_state, int p0) {
-    __shared__ float sc[2];
-    const int t = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
+    const int t0 = blockIdx.x * kPR, h = blockIdx.y;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int nt = min(kPR, T - t0);
     const int HD = H * kD, C = 3 * HD;
-    const float* pr = proj + (size_t)t * ldp;
-    const float o = O[rix(t, h, H) + tid];
-    const float ss = wave_sum(o * o);
-    if (lane == 0) sc[wave] = ss;
-    __syncthreads();
-    const float tot = sc[0] + sc[1];
-    const float sn = 1.0f / sqrtf(tot / (float)kD + 1e-6f);
-    const float r = (o * sn) * norm_w[tid];
-    out[(size_t)t * ldo + h * kD + tid] = r * silu_f(pr[3 * HD + h * kD + tid]);
-    if (t >= T - 3) {  // ring row of position p0 + t keeps its conv input
-        const int row = (p0 + t) % 3;
-        for (int i = tid; i < 3 * kD; i += kD) {
-            const int ch = (i / kD) * HD + h * kD + i % kD;
-            conv_state[(size_t)row * C + ch] = pr[ch];
+    const float nw0 = norm_w[lane], nw1 = norm_w[lane + 64];
+    for (int r = wave; r < nt; r += 4) {
+        const int t = t0 + r;
+        const float* pr = proj + (size_t)t * ldp;
+        const float o0 = O[rix(t, h, H) + lane], o1 = O[rix(t, h, H) + lane + 64];
+        const float z0 = pr[3 * HD + h * kD + lane], z1 = pr[3 * HD + h * kD + lane + 64];
+        const float tot = wave_sum(o0 * o0) + wave_sum(o1 * o1);
+        const float sn = 1.0f / sqrtf(tot / (float)kD + 1e-6f);
+        out[(size_t)t * ldo + h * kD + lane] = ((o0 * sn) * nw0) * silu_f(z0);
+        out[(size_t)t * ldo + h * kD + lane + 64] = ((o1 * sn) * nw1) * silu_f(z1);
+        if (t >= T - 3) {  // ring row of position p0 + t keeps its conv input
+            const int row = (p0 + t) % 3;
+            for (int i = lane; i < 3 * kD; i += 64) {
+                const int ch = (i / kD) * HD + h * kD + i % kD;
+                conv_state[(size_t)row * C + ch] = pr[ch];
+            }
         }
     }
 }
@@ -495,7 +553,8 @@ extern "C" int qlm_deltanet_prefill_chunked(const float* proj, int ldp, int T, f
     if (work_bytes < w.bytes || ((uintptr_t)work & 255u)) return QLM_ERR_ARG;
     hipStream_t st = as_stream(stream);
     const int nch = (T + kC - 1) / kC;
-    hipLaunchKernelGGL(k_dn_chunk_prep, dim3(T, H), dim3(3 * kD), 0, st, proj, ldp, T, conv_state,
+    const int nrb = (T + kPR - 1) / kPR;
+    hipLaunchKernelGGL(k_dn_chunk_prep, dim3(nrb, H), dim3(3 * kD), 0, st, proj, ldp, T, conv_state,
                        conv_w_t, A_log, dt_bias, p0, H, w.qn, w.kn, w.vv, w.alpha, w.beta);
     int rc = qlm_launch_status();
     if (rc != QLM_OK) return rc;
@@ -507,7 +566,7 @@ extern "C" int qlm_deltanet_prefill_chunked(const float* proj, int ldp, int T, f
                        w.Wk, w.Mq, w.Gc, T, H, state, w.O);
     rc = qlm_launch_status();
     if (rc != QLM_OK) return rc;
-    hipLaunchKernelGGL(k_dn_chunk_post, dim3(T, H), dim3(kD), 0, st, w.O, proj, ldp, T, norm_w,
+    hipLaunchKernelGGL(k_dn_chunk_post, dim3(nrb, H), dim3(256), 0, st, w.O, proj, ldp, T, norm_w,
                        out, ldo, H, conv_state, p0);
     return qlm_launch_status();
 }
