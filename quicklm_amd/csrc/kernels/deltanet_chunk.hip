@@ -22,9 +22,10 @@
 //   k_dn_chunk_intra  per (chunk, head): K K^T and the masked, decayed Q K^T
 //                     on the matrix cores, the triangular solve for T (one
 //                     column per lane, unrolled), U and Wk on the matrix cores;
-//   k_dn_chunk_inter  per (head, 16 value columns): chunks in order; W, O and
+//   k_dn_chunk_inter  per (head, 16 value columns): chunks in order; W and
 //                     the state update on the matrix cores, the state slice
-//                     living in the accumulators;
+//                     living in the accumulators, and on other waves O of
+//                     the chunk before;
 //   k_dn_chunk_post   per (16 rows, head): head RMSNorm + SiLU(z) gate (decode
 //                     arithmetic) and the conv ring rows of the last positions.
 
@@ -39,7 +40,15 @@ constexpr int kC = 64;       // chunk rows
 constexpr int KP = kD + 4;   // padded LDS row of a [64][128] tile
 constexpr int TP = kC + 4;   // padded LDS row of a [64][64] tile
 constexpr int CB = 16;       // value columns per inter-chunk workgroup
-constexpr int SP = CB + 4;   // padded LDS row of a [*][16] tile
+
+// Makes the compiler wait here for the load that produced v.
+__device__ __forceinline__ void landed(float v) { asm volatile("" ::"v"(v)); }
+__device__ __forceinline__ void landed(const float4& v) {
+    landed(v.x);
+    landed(v.y);
+    landed(v.z);
+    landed(v.w);
+}
 
 // D += A B on a 16x16 tile, K = 4: lane l supplies A[l%16][l/16] and
 // B[l/16][l%16]; it holds D[(l/16)*4 + i][l%16].
@@ -286,186 +295,253 @@ __global__ __launch_bounds__(256, 2) void k_dn_chunk_intra(
     }
 }
 
-// The chunk operands (Wk, q and Mq rows, U, k columns, the cumulative gates)
-// do not depend on the state: each is reloaded for the next chunk right after
-// its last use in this one, so only the state chain is serial. Contractions
-// whose A operand is a row (Wk S, Q S, Mq W) take the row as float4s, lane
-// (l16, l4) holding columns 16kb + 4 l4 + j, and the LDS operand is read in
-// the same K order.
-__global__ __launch_bounds__(256) void k_dn_chunk_inter(
+// Per (head, 16 value columns), chunks in order, with two roles a SIMD:
+// waves 0-3 run the state chain of chunk c,
+//   W = U - Wk S,  S = gamma_end S + K^T diag(gamma_end / gamma) W,
+// the only products that depend on the state (wave w: W rows 16w.., state
+// rows 32w..); waves 4-7 meanwhile form the outputs of chunk c-1,
+//   O = (gamma_t (Q S) + Mq W) / sqrt(d),
+// Q S beside the chain's W and Mq W beside its state update, from the state
+// and W that chunk left in LDS, so that work fills the chain's waits instead
+// of lengthening it. The output waves also stage each chunk's k rows in LDS
+// (whole rows, 16-byte loads) for the state update. The state is kept in
+// three LDS slots (S_c read by the chain, S_{c+1} written, S_{c-1} read by
+// the output waves), W and the cumulative gates in two. The chunk operands
+// do not depend on the state: each is loaded for the next chunk right after
+// its last use in this one, from buffers padded to whole chunks (rows past T
+// are never used: every operand from them is replaced by zero with a
+// select). Every product runs its K index as 16 kb + 4 l4 + j on lane
+// (l16, l4), so the LDS operand of four consecutive products is one 16-byte
+// read: the state and W slices are stored transposed ([16][K + 4]).
+constexpr int KT = kD + 4;  // pitch of a transposed state slice
+constexpr int TT = kC + 4;  // pitch of a transposed W slice
+
+__global__ __launch_bounds__(512) void k_dn_chunk_inter(
     const float* __restrict__ qn, const float* __restrict__ kn, const float* __restrict__ U,
     const float* __restrict__ Wk, const float* __restrict__ Mq, const float* __restrict__ Gc,
     int T, int H, float* __restrict__ state, float* __restrict__ O) {
-    __shared__ float Ss[kD * SP];
-    __shared__ float Ws[kC * SP];
-    __shared__ float gs[kC];
+    __shared__ __attribute__((aligned(16))) float St[3][CB * KT];
+    __shared__ __attribute__((aligned(16))) float Wt[2][CB * TT];
+    __shared__ __attribute__((aligned(16))) float gs[2][kC];
+    __shared__ __attribute__((aligned(16))) float dec[kC];
+    __shared__ __attribute__((aligned(16))) float Ks[kC * KP];
     const int h = blockIdx.x, jb = blockIdx.y * CB;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: the roles branch on it
     const int l16 = lane & 15, l4 = lane >> 4;
-    float* Sg = state + (size_t)h * kD * kD;
-    const float rsd = 1.0f / sqrtf((float)kD);
+    const int w4 = wave & 3;
     const int nch = (T + kC - 1) / kC;
-    const int tr = wave * 16 + l16;  // A-operand row of this wave's tiles
+    const size_t RS = (size_t)H * kD;  // a row of every head
+    const size_t CS = kC * RS;         // a chunk of rows
+    const int tr = w4 * 16 + l16;      // A-operand row of this wave's tiles
+    auto lds4 = [](const float* p) { return *reinterpret_cast<const float4*>(p); };
+    auto sto4 = [](float* p, f32x4 v) { *reinterpret_cast<f32x4*>(p) = v; };
 
-    // state rows 32w .. 32w+31 (two 16-row tiles), columns jb .. jb+15
-    f32x4 sacc[2];
+    // Each role runs its own loop (so each loop's load waits count only its
+    // own loads); both pass two barriers a round for nch + 1 rounds.
+    if (wave < 4) {
+        // state rows 32w .. 32w+31 (two 16-row tiles), columns jb .. jb+15
+        float* Sg = state + (size_t)h * kD * kD;
+        f32x4 sacc[2];
+        float4 pw[8];
+        float pu[4], pg = 0.0f, pge = 0.0f;
+        const float* wk_b = Wk + tr * RS + h * kD + 4 * l4;
+        const float* u_b = U + (w4 * 16 + l4 * 4) * RS + h * kD + jb + l16;
+        auto load_g = [&](int c) {
+            pg = Gc[((size_t)c * kC + lane) * H + h];  // row lane of the chunk (wave 0 uses it)
+            pge = Gc[((size_t)c * kC + min(kC, T - c * kC) - 1) * H + h];
+        };
+        auto load_wu = [&](int c) {
+            const size_t cs = (size_t)c * CS;
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt)
+            for (int kb = 0; kb < 8; ++kb) pw[kb] = *reinterpret_cast<const float4*>(wk_b + cs + 16 * kb);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int row = (2 * wave + tt) * 16 + l4 * 4 + i;
-            sacc[tt][i] = Sg[(size_t)row * kD + jb + l16];
-            Ss[row * SP + l16] = sacc[tt][i];
+            for (int i = 0; i < 4; ++i) pu[i] = u_b[cs + i * RS];
+        };
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+            const int r0 = (2 * w4 + tt) * 16 + l4 * 4;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sacc[tt][i] = Sg[(size_t)(r0 + i) * kD + jb + l16];
+            sto4(&St[0][l16 * KT + r0], sacc[tt]);
         }
-
-    // chunk operands in registers (rows clamped into [0, T); masked at use)
-    float4 pw[8], pq[8], pm[4];
-    float pu[4], pk[2][16], pg = 0.0f;
-    auto row_of = [&](int c, int t) { return min(c * kC + t, T - 1); };
-    auto load_w = [&](int c) {
-        const float4* r = reinterpret_cast<const float4*>(Wk + rix(row_of(c, tr), h, H));
+        load_g(0);
+        load_wu(0);
+        // Every load of the preamble lands before the loop: the wait counts
+        // inside it then follow the loop's own load order (entered with the
+        // preamble's loads pending, in another order, they wait for all).
+        landed(pg);
+        landed(pge);
 #pragma unroll
-        for (int kb = 0; kb < 8; ++kb) pw[kb] = r[4 * kb + l4];
-    };
-    auto load_q = [&](int c) {
-        const float4* r = reinterpret_cast<const float4*>(qn + rix(row_of(c, tr), h, H));
+        for (int kb = 0; kb < 8; ++kb) landed(pw[kb]);
 #pragma unroll
-        for (int kb = 0; kb < 8; ++kb) pq[kb] = r[4 * kb + l4];
-    };
-    auto load_m = [&](int c) {
-        const float4* r =
-            reinterpret_cast<const float4*>(Mq + (((size_t)c * H + h) * kC + tr) * kC);
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb) pm[kb] = r[4 * kb + l4];
-    };
-    auto load_u = [&](int c) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) pu[i] = U[rix(row_of(c, wave * 16 + l4 * 4 + i), h, H) + jb + l16];
-    };
-    auto load_k = [&](int c) {
-#pragma unroll
-        for (int s4 = 0; s4 < 16; ++s4) {
-            const float* kr = kn + rix(row_of(c, 4 * s4 + l4), h, H);
-#pragma unroll
-            for (int tt = 0; tt < 2; ++tt) pk[tt][s4] = kr[(2 * wave + tt) * 16 + l16];
-        }
-    };
-    auto load_g = [&](int c) {
-        if (tid < kC) pg = Gc[(size_t)row_of(c, tid) * H + h];
-    };
-    load_g(0);
-    load_w(0);
-    load_u(0);
-    load_q(0);
-    load_m(0);
-    load_k(0);
-    __syncthreads();
-
-    for (int c = 0; c < nch; ++c) {
-        const int cn = min(c + 1, nch - 1);
-        const int nt = min(kC, T - c * kC);
-        const bool tv = tr < nt;
-        if (tid < kC) gs[tid] = tid < nt ? pg : 0.0f;
-        load_g(cn);
-        // W = U - Wk S: wave w rows 16w..16w+15 (four independent chains:
-        // a chain of dependent products waits out each one's latency)
-        f32x4 wc[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) wc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int kb = 0; kb < 8; ++kb) {
-            const float a[4] = {pw[kb].x, pw[kb].y, pw[kb].z, pw[kb].w};
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float b = Ss[(16 * kb + 4 * l4 + j) * SP + l16];
-                wc[j] = mma(tv ? a[j] : 0.0f, b, wc[j]);
-            }
-        }
-        load_w(cn);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int t = wave * 16 + l4 * 4 + i;
-            Ws[t * SP + l16] = t < nt ? pu[i] - ((wc[0][i] + wc[1][i]) + (wc[2][i] + wc[3][i])) : 0.0f;
-        }
-        load_u(cn);
+        for (int i = 0; i < 4; ++i) landed(pu[i]);
         __syncthreads();
-        // O = (gamma_t (Q S) + Mq W) / sqrt(d)
-        {
-            f32x4 qc[4], mc[2];
+        for (int c = 0; c < nch; ++c) {
+            const int cn = min(c + 1, nch - 1);
+            const int nt = min(kC, T - c * kC);
+            const bool tv = tr < nt;
+            const float* Sc = St[c % 3] + l16 * KT + 4 * l4;
+            if (wave == 0) {
+                gs[c & 1][lane] = lane < nt ? pg : 0.0f;
+                dec[lane] = lane < nt ? expf(pge - pg) : 0.0f;  // gamma_end / gamma_t
+            }
+            const float ge = expf(pge);
+            load_g(cn);
+            // W = U - Wk S (four independent chains: a chain of dependent
+            // products waits out each one's latency)
+            f32x4 wc[4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) qc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
-            mc[0] = mc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int r = 0; r < 4; ++r) wc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int kb = 0; kb < 8; ++kb) {
-                const float a[4] = {pq[kb].x, pq[kb].y, pq[kb].z, pq[kb].w};
+                const float a[4] = {pw[kb].x, pw[kb].y, pw[kb].z, pw[kb].w};
+                const float4 b4 = lds4(Sc + 16 * kb);
+                const float b[4] = {b4.x, b4.y, b4.z, b4.w};
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const float b = Ss[(16 * kb + 4 * l4 + j) * SP + l16];
-                    qc[j] = mma(tv ? a[j] : 0.0f, b, qc[j]);
-                }
+                for (int j = 0; j < 4; ++j) wc[j] = mma(tv ? a[j] : 0.0f, b[j], wc[j]);
             }
-#pragma unroll
-            for (int kb = 0; kb < 4; ++kb) {
-                const float a[4] = {pm[kb].x, pm[kb].y, pm[kb].z, pm[kb].w};
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    mc[j & 1] = mma(tv ? a[j] : 0.0f, Ws[(16 * kb + 4 * l4 + j) * SP + l16], mc[j & 1]);
-            }
-            f32x4 qa, qb, mw;
+            f32x4 wv;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                qa[i] = qc[0][i] + qc[2][i];
-                qb[i] = qc[1][i] + qc[3][i];
-                mw[i] = mc[0][i] + mc[1][i];
+                const int t = w4 * 16 + l4 * 4 + i;
+                wv[i] = t < nt ? pu[i] - ((wc[0][i] + wc[1][i]) + (wc[2][i] + wc[3][i])) : 0.0f;
             }
-            load_q(cn);
-            load_m(cn);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int t = wave * 16 + l4 * 4 + i;
-                if (t < nt)
-                    O[rix(c * kC + t, h, H) + jb + l16] =
-                        (expf(gs[t]) * (qa[i] + qb[i]) + mw[i]) * rsd;
-            }
-        }
-        // S = gamma_end S + K^T diag(gamma_end / gamma) W
-        {
-            const float gend = gs[nt - 1];
-            const float ge = expf(gend);
-#pragma unroll
-            for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) sacc[tt][i] *= ge;
+            sto4(&Wt[c & 1][l16 * TT + w4 * 16 + l4 * 4], wv);
+            load_wu(cn);
+            __syncthreads();  // W of chunk c and its gates are in LDS
+            // S = gamma_end S + K^T diag(gamma_end / gamma) W
+            const float* Wc = Wt[c & 1] + l16 * TT + 4 * l4;
+            const float* Kc = Ks + 4 * l4 * KP + 2 * w4 * 16 + l16;
             f32x4 du[2][2];
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt) du[tt][0] = du[tt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int s4 = 0; s4 < 16; ++s4) {
-                const int t = 4 * s4 + l4;
-                const bool ok = t < nt;
-                const float b = ok ? Ws[t * SP + l16] * expf(gend - gs[t]) : 0.0f;
+            for (int kb = 0; kb < 4; ++kb) {
+                const float4 w4v = lds4(Wc + 16 * kb);
+                const float4 d4 = lds4(&dec[16 * kb + 4 * l4]);
+                const float b[4] = {w4v.x * d4.x, w4v.y * d4.y, w4v.z * d4.z, w4v.w * d4.w};
 #pragma unroll
-                for (int tt = 0; tt < 2; ++tt)
-                    du[tt][s4 & 1] = mma(ok ? pk[tt][s4] : 0.0f, b, du[tt][s4 & 1]);
+                for (int j = 0; j < 4; ++j) {
+                    const bool ok = 16 * kb + 4 * l4 + j < nt;
+#pragma unroll
+                    for (int tt = 0; tt < 2; ++tt) {
+                        const float kv = Kc[(16 * kb + j) * KP + 16 * tt];
+                        du[tt][j & 1] = mma(ok ? kv : 0.0f, b[j], du[tt][j & 1]);
+                    }
+                }
             }
+            float* Sn = St[(c + 1) % 3];
 #pragma unroll
-            for (int tt = 0; tt < 2; ++tt)
+            for (int tt = 0; tt < 2; ++tt) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) sacc[tt][i] += du[tt][0][i] + du[tt][1][i];
-            load_k(cn);
+                for (int i = 0; i < 4; ++i)
+                    sacc[tt][i] = sacc[tt][i] * ge + (du[tt][0][i] + du[tt][1][i]);
+                sto4(&Sn[l16 * KT + (2 * w4 + tt) * 16 + l4 * 4], sacc[tt]);
+            }
+            __syncthreads();  // S of chunk c+1 is in LDS; this round's slot reads are done
         }
-        __syncthreads();  // every read of Ss, Ws and gs of this chunk is done
+        __syncthreads();  // the output waves' last round
+        __syncthreads();
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) Ss[((2 * wave + tt) * 16 + l4 * 4 + i) * SP + l16] = sacc[tt][i];
+            for (int i = 0; i < 4; ++i)
+                Sg[(size_t)((2 * w4 + tt) * 16 + l4 * 4 + i) * kD + jb + l16] = sacc[tt][i];
+    } else {
+        // outputs of the chunk before: q and Mq rows 16w'.. of it
+        const float rsd = 1.0f / sqrtf((float)kD);
+        const size_t MS = (size_t)H * kC * kC;
+        float4 pq[8], pm[4];
+        const float* q_b = qn + tr * RS + h * kD + 4 * l4;
+        const float* m_b = Mq + ((size_t)h * kC + tr) * kC + 4 * l4;
+        auto load_out = [&](int c) {
+#pragma unroll
+            for (int kb = 0; kb < 8; ++kb)
+                pq[kb] = *reinterpret_cast<const float4*>(q_b + (size_t)c * CS + 16 * kb);
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb)
+                pm[kb] = *reinterpret_cast<const float4*>(m_b + (size_t)c * MS + 16 * kb);
+        };
+        // k rows of a chunk: thread o = tid - 256 moves float4 o + 256 i
+        float4 pkk[8];
+        const int o = tid - 256;
+        auto load_kk = [&](int c) {
+            const float* base = kn + (size_t)c * CS + h * kD;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int e = o + 256 * i;
+                pkk[i] = *reinterpret_cast<const float4*>(base + (e >> 5) * RS + (e & 31) * 4);
+            }
+        };
+        auto store_kk = [&]() {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int e = o + 256 * i;
+                *reinterpret_cast<float4*>(&Ks[(e >> 5) * KP + (e & 31) * 4]) = pkk[i];
+            }
+        };
+        load_out(0);
+        load_kk(0);
+        store_kk();
+        if (nch > 1) load_kk(1);
+#pragma unroll
+        for (int kb = 0; kb < 8; ++kb) landed(pq[kb]);
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) landed(pm[kb]);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) landed(pkk[i]);
         __syncthreads();
+        for (int c = 0; c <= nch; ++c) {
+            const int cp = c - 1;
+            const int nt = min(kC, T - cp * kC);
+            const bool tv = tr < nt;
+            f32x4 qc[4];
+            if (c > 0 && c < nch) {  // k rows of chunk c for its state update
+                store_kk();
+                if (c + 1 < nch) load_kk(c + 1);
+            }
+            if (c > 0) {  // Q S, beside the chain's W = U - Wk S
+                const float* Sp = St[cp % 3] + l16 * KT + 4 * l4;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) qc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int kb = 0; kb < 8; ++kb) {
+                    const float a[4] = {pq[kb].x, pq[kb].y, pq[kb].z, pq[kb].w};
+                    const float4 b4 = lds4(Sp + 16 * kb);
+                    const float b[4] = {b4.x, b4.y, b4.z, b4.w};
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) qc[j] = mma(tv ? a[j] : 0.0f, b[j], qc[j]);
+                }
+            }
+            __syncthreads();
+            if (c > 0) {  // Mq W and the outputs, beside the chain's state update
+                const float* Wp = Wt[cp & 1] + l16 * TT + 4 * l4;
+                f32x4 mc[2];
+                mc[0] = mc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int kb = 0; kb < 4; ++kb) {
+                    const float a[4] = {pm[kb].x, pm[kb].y, pm[kb].z, pm[kb].w};
+                    const float4 b4 = lds4(Wp + 16 * kb);
+                    const float b[4] = {b4.x, b4.y, b4.z, b4.w};
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) mc[j & 1] = mma(tv ? a[j] : 0.0f, b[j], mc[j & 1]);
+                }
+                if (c < nch) load_out(c);
+                const float4 g4 = lds4(&gs[cp & 1][w4 * 16 + l4 * 4]);
+                const float g[4] = {g4.x, g4.y, g4.z, g4.w};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int t = w4 * 16 + l4 * 4 + i;
+                    if (t < nt)
+                        O[((size_t)cp * kC + t) * RS + h * kD + jb + l16] =
+                            (expf(g[i]) * ((qc[0][i] + qc[2][i]) + (qc[1][i] + qc[3][i])) +
+                             (mc[0][i] + mc[1][i])) * rsd;
+                }
+            }
+            __syncthreads();
+        }
     }
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            Sg[(size_t)((2 * wave + tt) * 16 + l4 * 4 + i) * kD + jb + l16] = sacc[tt][i];
 }
 
 // Per (16 rows, head): a wave a row at a time (its two 64-column halves
@@ -508,9 +584,11 @@ struct ChunkWork {
 
 ChunkWork carve(void* base, int T, int H) {
     ChunkWork w{};
-    const size_t rows = a256((size_t)T * H * kD * sizeof(float));
-    const size_t sc = a256((size_t)T * H * sizeof(float));
+    // rows and gates padded to whole chunks: the state chain reads a whole
+    // chunk's operands and masks the rows past T
     const int nch = (T + kC - 1) / kC;
+    const size_t rows = a256((size_t)nch * kC * H * kD * sizeof(float));
+    const size_t sc = a256((size_t)nch * kC * H * sizeof(float));
     char* p = reinterpret_cast<char*>(base);
     auto take = [&](size_t b) {
         float* r = reinterpret_cast<float*>(p);
@@ -562,7 +640,7 @@ extern "C" int qlm_deltanet_prefill_chunked(const float* proj, int ldp, int T, f
                        w.alpha, w.beta, T, H, w.U, w.Wk, w.Mq, w.Gc);
     rc = qlm_launch_status();
     if (rc != QLM_OK) return rc;
-    hipLaunchKernelGGL(k_dn_chunk_inter, dim3(H, kD / CB), dim3(256), 0, st, w.qn, w.kn, w.U,
+    hipLaunchKernelGGL(k_dn_chunk_inter, dim3(H, kD / CB), dim3(512), 0, st, w.qn, w.kn, w.U,
                        w.Wk, w.Mq, w.Gc, T, H, state, w.O);
     rc = qlm_launch_status();
     if (rc != QLM_OK) return rc;
