@@ -19,7 +19,7 @@ static inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream
 // operand modifier, no LDS round trip): xor 1 and xor 2 as quad permutes;
 // once every lane of a quad holds the same value, the row half-mirror
 // (lane i <-> 7-i) and mirror (i <-> 15-i) pair quads and half-rows exactly
-// as xor 4 and xor 8 would. Across rows, xor 16 and 32 are lane shuffles.
+// as xor 4 and xor 8 would. Across rows, xor 16 and 32 are lane swaps.
 // Callers keep every lane of the wave active (the reductions read all of
 // them).
 constexpr int kDppXor1 = 0xB1;        // quad_perm [1, 0, 3, 2]
@@ -32,6 +32,31 @@ __device__ __forceinline__ float dpp_mov(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
 }
 
+// Across rows: v(l) op v(l ^ 16) and v(l) op v(l ^ 32) on every lane, by
+// v_permlane16_swap / v_permlane32_swap (VALU lane swaps, no LDS permute).
+// With both operands v, the swap's two results hold, on every lane, the
+// values of the lane pair in either order; op is commutative.
+__device__ __forceinline__ float xor16_add(float v) {
+    const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                    false);
+    return __uint_as_float(s[0]) + __uint_as_float(s[1]);
+}
+__device__ __forceinline__ float xor32_add(float v) {
+    const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                    false);
+    return __uint_as_float(s[0]) + __uint_as_float(s[1]);
+}
+__device__ __forceinline__ float xor16_max(float v) {
+    const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                    false);
+    return fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
+}
+__device__ __forceinline__ float xor32_max(float v) {
+    const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                    false);
+    return fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
+}
+
 // Sum over aligned groups of `width` lanes (a power of two, 2..64); every
 // lane of a group gets the group total.
 template <int width>
@@ -41,8 +66,8 @@ __device__ __forceinline__ float group_sum(float v) {
     if constexpr (width >= 4) v += dpp_mov<kDppXor2>(v);
     if constexpr (width >= 8) v += dpp_mov<kDppHalfMirror>(v);
     if constexpr (width >= 16) v += dpp_mov<kDppMirror>(v);
-    if constexpr (width >= 32) v += __shfl_xor(v, 16, QLM_WAVE);
-    if constexpr (width >= 64) v += __shfl_xor(v, 32, QLM_WAVE);
+    if constexpr (width >= 32) v = xor16_add(v);
+    if constexpr (width >= 64) v = xor32_add(v);
     return v;
 }
 
@@ -54,8 +79,7 @@ __device__ __forceinline__ float wave_max(float v) {
     v = fmaxf(v, dpp_mov<kDppXor2>(v));
     v = fmaxf(v, dpp_mov<kDppHalfMirror>(v));
     v = fmaxf(v, dpp_mov<kDppMirror>(v));
-    v = fmaxf(v, __shfl_xor(v, 16, QLM_WAVE));
-    return fmaxf(v, __shfl_xor(v, 32, QLM_WAVE));
+    return xor32_max(xor16_max(v));
 }
 
 // Block-wide sum for blockDim.x a multiple of 64 (<= 1024). `red` is LDS

@@ -259,11 +259,26 @@ __global__ __launch_bounds__(kThreads) void k_deltanet_decode(
 // dividing 2^32). The L2 norms of q and k enter as the scalars 1/|q| and
 // 1/|k| on the reductions (the reference divides each element; the same
 // value to rounding).
+//
+// Thread (rg, j) owns state rows rg*8 .. rg*8+7 of column 16 s + j and
+// computes one q or k channel of those rows (lanes j < 8 of its 16-lane row
+// q, lanes j >= 8 k), so every q and k value a thread needs is a row
+// broadcast away (DPP, no LDS): the sums of squares and the kv partial sums
+// meet in one LDS round, the output sums in a second. Every thread forms
+// its own column's v channel and the gates.
 constexpr int kColW = 16;                       // value columns per workgroup
 constexpr int kSplit = kD / kColW;              // workgroups per head
 constexpr int kColThreads = 256;
 constexpr int kColRG = kColThreads / kColW;     // row groups
 constexpr int kColRows = kD / kColRG;           // state rows per thread
+static_assert(kColRows == 8 && kColW == 16, "a row group is one 16-lane DPP row: 8 q + 8 k");
+
+// lane n of this lane's 16-lane row
+template <int n>
+__device__ __forceinline__ float row_lane(float v) {
+    return __int_as_float(
+        __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150 + n, 0xf, 0xf, false));
+}
 
 __global__ __launch_bounds__(kColThreads) void k_deltanet_cols(
     const float* __restrict__ proj, int ldp, float* __restrict__ conv_state,
@@ -272,9 +287,8 @@ __global__ __launch_bounds__(kColThreads) void k_deltanet_cols(
     float* __restrict__ state, const int* __restrict__ pos, float* __restrict__ u, int ldu,
     float* __restrict__ ss, unsigned* __restrict__ ticket, int H) {
     constexpr int NWV = kColThreads / QLM_WAVE;
-    __shared__ float qs[kD], ks[kD], vs[kColW], dl[kColW];
-    __shared__ float red[NWV][kColW];
-    __shared__ float ssq[NWV], gsc[2];
+    __shared__ float red[NWV][kColW], red2[NWV][kColW];
+    __shared__ float ssq[NWV][2];
     const int h = blockIdx.x / kSplit, sp = blockIdx.x % kSplit;
     const int b = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -285,12 +299,13 @@ __global__ __launch_bounds__(kColThreads) void k_deltanet_cols(
     float* Sh = state + ((size_t)b * H + h) * kD * kD;
     const int j = tid & (kColW - 1), rg = tid / kColW;
     const int col = sp * kColW + j;  // value column of this thread
+    const bool isk = j >= 8;
 
-    // Operands, all unconditional: the position, thread tid's q/k channel
-    // (q_h for tid < d, else k_h), the v channel of column col, z, gain and
+    // Operands, all unconditional: the position, this thread's q/k channel
+    // (row rg*8 + j%8 of q or k), the v channel of column col, z, gain and
     // gates, then the state slice rows rg*8 .. rg*8+7 of column col.
     const int pb = pos ? pos[b] : 0;
-    const int chqk = h * kD + tid + (tid < kD ? 0 : HD - kD);
+    const int chqk = (isk ? HD : 0) + h * kD + rg * kColRows + (j & 7);
     const int chv = 2 * HD + h * kD + col;
     float rq[3], wq[4], rv[3], wv[4];
 #pragma unroll
@@ -312,10 +327,7 @@ __global__ __launch_bounds__(kColThreads) void k_deltanet_cols(
 #pragma unroll
     for (int r = 0; r < kColRows; ++r) sr[r] = Sh[(size_t)(rg * kColRows + r) * kD + col];
 
-    // conv1d (taps chronological from the oldest ring row) + SiLU; the
-    // sums of squares of q (waves 0-1) and k (waves 2-3) and the gates are
-    // formed in the same phase: the L2 norms enter the recurrence as the
-    // scalars 1/|q| and 1/|k| (attention.cpp:463-470)
+    // conv1d (taps chronological from the oldest ring row) + SiLU
     const int oldest = pb % 3;
     auto conv = [&](const float (&ring)[3], const float (&w)[4], float x) {
         float acc = 0.0f;
@@ -330,71 +342,79 @@ __global__ __launch_bounds__(kColThreads) void k_deltanet_cols(
     };
     const float yq = conv(rq, wq, xq);
     const float yv = conv(rv, wv, xv);
-    if (tid < kD) qs[tid] = yq;
-    else ks[tid - kD] = yq;
-    const float wsq = wave_sum(yq * yq);
-    if (lane == 0) ssq[wave] = wsq;
-    if (tid < kColW) {
-        vs[tid] = yv;
-        cs[(size_t)oldest * C + chv] = xv;  // this workgroup's own v channels
-    }
-    if (tid == kColThreads - 1) {  // gates (attention.cpp:472-483)
-        const float dt = ga + gdt;
-        const float sp_ = dt > 20.0f ? dt : log1pf(expf(dt));
-        const float alpha = -expf(galog) * sp_;
-        gsc[0] = expf(alpha);
-        gsc[1] = 1.0f / (1.0f + expf(-gb));
-    }
-    __syncthreads();  // every thread's ring values have arrived
-    // Ticket, taken now; its value is needed only at the end. The workgroup
-    // drawing the last ticket of the head overwrites the q/k ring row.
-    unsigned t0 = 0;
-    if (tid == 0) t0 = atomicAdd(&ticket[((size_t)b * H + h) * QLM_DN_TICKET_STRIDE], 1u);
+    // gates (attention.cpp:472-483), in every thread
+    const float dt = ga + gdt;
+    const float spl = dt > 20.0f ? dt : log1pf(expf(dt));
+    const float dec = expf(-expf(galog) * spl);
+    const float beta = 1.0f / (1.0f + expf(-gb));
 
-    const float rqn = 1.0f / sqrtf((ssq[0] + ssq[1]) + 1e-6f);
-    const float rkn = 1.0f / sqrtf((ssq[2] + ssq[3]) + 1e-6f);
-    const float dec = gsc[0], beta = gsc[1];
+    // this row group's k and q values
+    float kr[kColRows], qr[kColRows];
+    kr[0] = row_lane<8>(yq);
+    kr[1] = row_lane<9>(yq);
+    kr[2] = row_lane<10>(yq);
+    kr[3] = row_lane<11>(yq);
+    kr[4] = row_lane<12>(yq);
+    kr[5] = row_lane<13>(yq);
+    kr[6] = row_lane<14>(yq);
+    kr[7] = row_lane<15>(yq);
+    qr[0] = row_lane<0>(yq);
+    qr[1] = row_lane<1>(yq);
+    qr[2] = row_lane<2>(yq);
+    qr[3] = row_lane<3>(yq);
+    qr[4] = row_lane<4>(yq);
+    qr[5] = row_lane<5>(yq);
+    qr[6] = row_lane<6>(yq);
+    qr[7] = row_lane<7>(yq);
 
-    // (1) decay and kv[col] = k . S_decayed[:, col]
+    // (1) decay and kv[col] = k . S_decayed[:, col] (k not yet normalised),
+    // with the wave's q and k sums of squares
     float kv = 0.0f;
 #pragma unroll
     for (int r = 0; r < kColRows; ++r) {
         sr[r] *= dec;
-        kv = fmaf(ks[rg * kColRows + r], sr[r], kv);
+        kv = fmaf(kr[r], sr[r], kv);
     }
     // the 4 row groups of a wave share column j at lanes j, j+16, j+32, j+48
-    kv += __shfl_xor(kv, 16, QLM_WAVE);
-    kv += __shfl_xor(kv, 32, QLM_WAVE);
+    kv = xor32_add(xor16_add(kv));
+    const float sq = wave_sum(isk ? 0.0f : yq * yq), sk = wave_sum(isk ? yq * yq : 0.0f);
     if (lane < kColW) red[wave][lane] = kv;
-    __syncthreads();
-    if (tid < kColW)
-        dl[tid] = vs[tid] - ((red[0][tid] + red[1][tid]) + (red[2][tid] + red[3][tid])) * rkn;
-    __syncthreads();
+    if (lane == 0) {
+        ssq[wave][0] = sq;
+        ssq[wave][1] = sk;
+    }
+    __syncthreads();  // every thread's ring values have arrived
+    if (tid < kColW) cs[(size_t)oldest * C + chv] = xv;  // this workgroup's own v channels
+    // Ticket, taken now; its value is needed only at the end. The workgroup
+    // drawing the last ticket of the head overwrites the q/k ring row.
+    unsigned t0 = 0;
+    if (tid == 0) t0 = atomicAdd(&ticket[((size_t)b * H + h) * QLM_DN_TICKET_STRIDE], 1u);
+    const float rqn = 1.0f / sqrtf(((ssq[0][0] + ssq[1][0]) + (ssq[2][0] + ssq[3][0])) + 1e-6f);
+    const float rkn = 1.0f / sqrtf(((ssq[0][1] + ssq[1][1]) + (ssq[2][1] + ssq[3][1])) + 1e-6f);
+    const float dj = yv - ((red[0][j] + red[1][j]) + (red[2][j] + red[3][j])) * rkn;
 
     // (2) S += (beta k) delta^T ; (3) o[col] = q . S_new[:, col]
-    const float dj = dl[j];
     const float bk = beta * rkn;
     float o = 0.0f;
 #pragma unroll
     for (int r = 0; r < kColRows; ++r) {
         const int i = rg * kColRows + r;
-        sr[r] = fmaf(bk * ks[i], dj, sr[r]);
-        o = fmaf(qs[i], sr[r], o);
+        sr[r] = fmaf(bk * kr[r], dj, sr[r]);
+        o = fmaf(qr[r], sr[r], o);
         Sh[(size_t)i * kD + col] = sr[r];
     }
-    o += __shfl_xor(o, 16, QLM_WAVE);
-    o += __shfl_xor(o, 32, QLM_WAVE);
-    if (lane < kColW) red[wave][lane] = o;  // red's kv sums were read before the last barrier
+    o = xor32_add(xor16_add(o));
+    if (lane < kColW) red2[wave][lane] = o;
     __syncthreads();
     if (wave == 0) {
         float oj = 0.0f;
         if (lane < kColW) {
-            oj = ((red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane])) *
+            oj = ((red2[0][lane] + red2[1][lane]) + (red2[2][lane] + red2[3][lane])) *
                  (rqn * (1.0f / sqrtf((float)kD)));
             u[(size_t)b * ldu + h * kD + col] = (oj * nwj) * silu_f(zj);
         }
-        const float sq = group_sum<kColW>(oj * oj);
-        if (lane == 0) ss[((size_t)b * H + h) * kSplit + sp] = sq;
+        const float sq2 = group_sum<kColW>(oj * oj);
+        if (lane == 0) ss[((size_t)b * H + h) * kSplit + sp] = sq2;
         // the last workgroup of the head to have read the q/k ring row
         // overwrites it with this step's inputs (lane l copies 4 of the 256)
         t0 = __shfl(t0, 0, QLM_WAVE);
@@ -442,8 +462,7 @@ __global__ __launch_bounds__(kColThreads) void k_gated_delta_step_cols(
         sr[r] *= dec;
         kv = fmaf(ks[rg * kColRows + r], sr[r], kv);
     }
-    kv += __shfl_xor(kv, 16, QLM_WAVE);
-    kv += __shfl_xor(kv, 32, QLM_WAVE);
+    kv = xor32_add(xor16_add(kv));
     if (lane < kColW) red[wave][lane] = kv;
     __syncthreads();
     if (tid < kColW) dl[tid] = vj - ((red[0][tid] + red[1][tid]) + (red[2][tid] + red[3][tid]));
@@ -458,8 +477,7 @@ __global__ __launch_bounds__(kColThreads) void k_gated_delta_step_cols(
         o = fmaf(qs[i], sr[r], o);
         Sh[(size_t)i * kD + col] = sr[r];
     }
-    o += __shfl_xor(o, 16, QLM_WAVE);
-    o += __shfl_xor(o, 32, QLM_WAVE);
+    o = xor32_add(xor16_add(o));
     if (lane < kColW) red[wave][lane] = o;  // red's kv sums were read before the last barrier
     __syncthreads();
     if (tid < kColW)

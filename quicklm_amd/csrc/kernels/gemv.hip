@@ -903,7 +903,7 @@ __global__ __launch_bounds__(NW * QLM_WAVE) void k_gemv_mx(
     auto park = [&](int slot) {
 #pragma unroll
         for (int tt = 0; tt < T; ++tt) {
-            const float p = (accf[tt] + __shfl_xor(accf[tt], 16, QLM_WAVE)) * fx;
+            const float p = xor16_add(accf[tt]) * fx;
             if (qd == 0) red[((slot * NW + w) * T + tt) * 16 + n] = p;
             accf[tt] = 0.0f;
         }
