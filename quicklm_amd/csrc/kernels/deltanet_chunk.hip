@@ -338,7 +338,7 @@ __global__ __launch_bounds__(512) void k_dn_chunk_inter(
     auto sto4 = [](float* p, f32x4 v) { *reinterpret_cast<f32x4*>(p) = v; };
 
     // Each role runs its own loop (so each loop's load waits count only its
-    // own loads); both pass two barriers a round for nch + 1 rounds.
+    // own loads); both meet two barriers a pass, nch + 1 passes.
     if (wave < 4) {
         // state rows 32w .. 32w+31 (two 16-row tiles), columns jb .. jb+15
         float* Sg = state + (size_t)h * kD * kD;
@@ -439,9 +439,9 @@ __global__ __launch_bounds__(512) void k_dn_chunk_inter(
                     sacc[tt][i] = sacc[tt][i] * ge + (du[tt][0][i] + du[tt][1][i]);
                 sto4(&Sn[l16 * KT + (2 * w4 + tt) * 16 + l4 * 4], sacc[tt]);
             }
-            __syncthreads();  // S of chunk c+1 is in LDS; this round's slot reads are done
+            __syncthreads();  // S of chunk c+1 is in LDS; this pass's slot reads are done
         }
-        __syncthreads();  // the output waves' last round
+        __syncthreads();  // the output waves' last pass
         __syncthreads();
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt)
