@@ -711,12 +711,13 @@ def test_deltanet_prefill(hip, orc, rng, p0, T):
                           dconv2.to_numpy(conv.shape, np.float32))
 
 
-@pytest.mark.parametrize("p0,T", [(0, 64), (0, 200), (5, 130), (1, 2), (0, 1024), (0, 4096),
-                                  (9, 3001)])
+@pytest.mark.parametrize("p0,T", [(0, 64), (0, 200), (5, 130), (1, 2), (3, 65), (2, 1),
+                                  (0, 1024), (0, 4096), (9, 3001)])
 def test_deltanet_prefill_chunked(hip, orc, rng, p0, T):
     """Chunked (WY, matrix-core) prefill == the row-by-row recurrence: outputs
     against the oracle, state and conv ring against the sequential kernel
-    (ragged last chunk, continuation from p0 > 0, T < 3)."""
+    (ragged last chunk, a last chunk of one row, continuation from p0 > 0,
+    T < 3, one row)."""
     H, d = 16, 128
     HD = H * d
     ldp = 4 * HD + 2 * H
