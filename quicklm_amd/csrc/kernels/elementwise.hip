@@ -102,12 +102,12 @@ __global__ void k_fill_u8(uint8_t* __restrict__ p, uint8_t v, size_t n) {
 // wins (strict >), matching DecoderModel::sample (model.cpp:263-274).
 constexpr int kArgThreads = 256;
 constexpr int kArgSlice = 4096;
+constexpr int kArgPer = kArgSlice / kArgThreads;  // logits per thread
 
 __device__ __forceinline__ void arg_better(float& bv, int& bi, float v, int i) {
-    if (v > bv || (v == bv && i < bi)) {
-        bv = v;
-        bi = i;
-    }
+    const bool better = v > bv || (v == bv && i < bi);  // selects, no branch
+    bv = better ? v : bv;
+    bi = better ? i : bi;
 }
 
 __global__ __launch_bounds__(kArgThreads) void k_argmax_partial(const float* __restrict__ lg,
@@ -121,7 +121,18 @@ __global__ __launch_bounds__(kArgThreads) void k_argmax_partial(const float* __r
     const int hi = min(n, lo + kArgSlice);
     float bv = -INFINITY;
     int bi = 0x7fffffff;
-    for (int i = lo + threadIdx.x; i < hi; i += kArgThreads) arg_better(bv, bi, row[i], i);
+    // the slice's logits are all requested before the first comparison (a
+    // strided loop with a runtime bound would wait for each load in turn);
+    // indices past the row are clamped and left out
+    float v[kArgPer];
+#pragma unroll
+    for (int j = 0; j < kArgPer; ++j)
+        v[j] = row[min(lo + (int)threadIdx.x + j * kArgThreads, hi - 1)];
+#pragma unroll
+    for (int j = 0; j < kArgPer; ++j) {
+        const int i = lo + (int)threadIdx.x + j * kArgThreads;
+        if (i < hi) arg_better(bv, bi, v[j], i);
+    }
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) {
         const float ov = __shfl_xor(bv, m, QLM_WAVE);

@@ -49,6 +49,7 @@ enum { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_ARGMAX = 3 };
 // invalidates its XCD's L2, ~0.3 us apiece over a 2048-workgroup grid).
 // One 64-bit key slot per workgroup of the logits GEMV (grid <= kMaxXsGrid).
 constexpr int kMaxXsGrid = 2048;
+constexpr int kEmbPer = 4;  // float4 of the next embedding row per thread and round
 
 struct GreedyTail {
     unsigned long long* keys;
@@ -572,8 +573,25 @@ __global__ __launch_bounds__(kThreads) void k_greedy_finish(GreedyTail tail, int
         tail.pos[0] = p + 1;
     }
     __syncthreads();
+    // the embedding row: every float4 of a round (kEmbPer a thread) is
+    // requested before any is stored; a strided copy loop with a runtime
+    // bound waits for each load before issuing the next
     const float* src = tail.embed + (size_t)tok * tail.H;
-    for (int i = tid; i < tail.H; i += kThreads) tail.h[i] = src[i];
+    if ((tail.H & 3) == 0) {
+        const int H4 = tail.H >> 2;
+        const float4* s4 = reinterpret_cast<const float4*>(src);
+        float4* d4 = reinterpret_cast<float4*>(tail.h);
+        for (int i0 = 0; i0 < H4; i0 += kEmbPer * kThreads) {
+            float4 v[kEmbPer];
+#pragma unroll
+            for (int j = 0; j < kEmbPer; ++j) v[j] = s4[min(i0 + j * kThreads + tid, H4 - 1)];
+#pragma unroll
+            for (int j = 0; j < kEmbPer; ++j)
+                if (i0 + j * kThreads + tid < H4) d4[i0 + j * kThreads + tid] = v[j];
+        }
+    } else {
+        for (int i = tid; i < tail.H; i += kThreads) tail.h[i] = src[i];
+    }
 }
 
 // ---------------------------------------------------------------------------
