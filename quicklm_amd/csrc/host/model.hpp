@@ -169,7 +169,9 @@ class DecoderModel : public GreedyModel {
     void ensure_prefill_buffers(int rows);
     size_t matmul_workspace(int M) const;
     void embed_current(int B);
-    void* graph_for(int B);
+    // the decode step of batch B captured n times in a row as one graph
+    // (cached per (B, n))
+    void* graph_for(int B, int n = 1);
     void quantize_into(LinearI8& lin, int row_off, const std::string& name);
     void upload_f32(DeviceBuffer& dst, const std::string& name, int64_t expect);
     void alloc_linear(LinearI8& lin, int N, int K);
@@ -212,7 +214,7 @@ class DecoderModel : public GreedyModel {
     bool have_snapshot_ = false;
     DeviceBuffer lm_pf_, lm_pf_idx_, lm_pf_work_;
 
-    std::map<int, void*> graphs_;
+    std::map<std::pair<int, int>, void*> graphs_;
     int run_B_ = 0, run_n_ = 0, run_steps_ = 0;
 };
 
