@@ -1235,7 +1235,7 @@ constexpr MxTuned kMxTuned[] = {
     {9728, 2560, EPI_SWIGLU, 0, 8, 5, 203},     // gate/up (3 tiles per workgroup)
     {2560, 9728, EPI_RESID, 0, 16, 10, 160},    // down
     {8224, 2560, EPI_STORE, 0, 8, 5, 512},      // DeltaNet in_proj [qkv|z|b|a]
-    {5120, 2560, EPI_STORE, 0, 8, 5, 320},      // GQA q(+gate)/k/v
+    {5120, 2560, EPI_STORE, 0, 8, 5, 160},      // GQA q(+gate)/k/v (2 tiles per workgroup)
     {2560, 2048, EPI_RESID, 0, 8, 4, 160},      // out_proj / o_proj
     {151936, 2560, EPI_STORE, 0, 8, 5, 192},  // lm_head (also its greedy form)
     {12288, 4096, EPI_STORE, 32, 16, 4, 768},   // 12288 x 4096, group-32 scales
