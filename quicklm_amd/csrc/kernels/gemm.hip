@@ -864,15 +864,24 @@ int launch_split(const float* x, int ldx, const float* rs, const float* nw, int 
 }
 
 // K slices for the M <= 64 path: the fewest that divide the 128-column
-// chunk count, leave each workgroup at most 4 chunks (one ring) and give at
-// least ~640 workgroups; a tall matrix (>= 1024 row tiles) is one slice.
-int sk_splits(int NR, int K) {
+// chunk count and give each workgroup at most 6 chunks and the launch at
+// least ~640 workgroups (up to 16 rows); above 16 rows (four times the work
+// a workgroup) at most 8 chunks a workgroup, ~320 workgroups and at least 8
+// slices. A tall matrix (>= 1024 row tiles) is one slice. Measured on the
+// config-1 shapes (graph replays): 4096 x 12288 at 4 / 16 rows 21.4 / 23.1
+// us with the former rule (at most 4 chunks a workgroup) against 18.2 /
+// 20.4 us; 64 rows 40.9 against 38.5 us; 4096 x 4096 at 64 rows 22.4
+// against 20.7 us; 12288 x 4096 at 64 rows 42.6 us in 8 slices, 43.1 in 4.
+int sk_splits(int M, int NR, int K) {
     const int nt = (NR + kSkRows - 1) / kSkRows;
     const int nch = K / kSkKc;
     if (nt >= 1024) return 1;
-    const int need_ring = (nch + 3) / 4;
-    const int need_wgs = (640 + nt - 1) / nt;
-    const int want = need_ring > need_wgs ? need_ring : need_wgs;
+    const bool tall = M > 16;
+    const int per = tall ? 8 : 6;
+    const int wgs = tall ? 320 : 640;
+    int want = (nch + per - 1) / per;
+    want = want > (wgs + nt - 1) / nt ? want : (wgs + nt - 1) / nt;
+    if (tall && want < 8) want = 8;
     for (int d = 1; d <= nch; ++d)
         if (nch % d == 0 && d >= want) return d;
     return nch;
@@ -904,7 +913,7 @@ size_t mm_workspace(int M, int N, int K, int epi) {
     size_t b = align256((size_t)M * sizeof(float));  // row scales
     if (use_sk(M, K)) {
         const int NR = epi == EPI_SWIGLU ? 2 * N : N;
-        const int ks = sk_splits(NR, K);
+        const int ks = sk_splits(M, NR, K);
         if (!(ks == 1 && epi == EPI_STORE)) b += (size_t)ks * M * NR * sizeof(float);
     } else {
         b += align256((size_t)4 * M * K);  // the split activation (bf16 hi, lo)
@@ -1001,7 +1010,7 @@ int mm_run(const float* x, int ldx, float* rs, const float* nw, float eps, const
     const TileMap tm{N, (N + 15) / 16, K / 64};  // a SwiGLU matrix: gate rows, then up rows
     if (use_sk(M, K)) {
         const int NR = epi == EPI_SWIGLU ? 2 * N : N;
-        const int ks = sk_splits(NR, K);
+        const int ks = sk_splits(M, NR, K);
         const bool direct = ks == 1 && epi == EPI_STORE;
         float* dst = direct ? y : part;
         const int ldp = direct ? ldy : NR;
