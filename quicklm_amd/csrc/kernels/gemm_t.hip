@@ -462,6 +462,8 @@ constexpr TTuned kTTuned[] = {
     {5120, 2560, EPI_STORE, {8, 4, 2, 3}},   // attention q/k/v: 11.3 us (14.0)
     {2560, 2048, EPI_RESID, {8, 2, 2, 2}},   // output projections: 7.2 us (7.9)
     {151936, 2560, EPI_STORE, {4, 8, 1, 1}}, // lm_head: 110 us (180)
+    // config-1 4096 x 12288: 17.0 / 18.2 us at 4 / 16 rows (19.2 / 19.4)
+    {4096, 12288, EPI_STORE, {8, 8, 1, 8}},
 };
 
 TConfig t_config(int N, int K, int epi) {
@@ -583,6 +585,11 @@ constexpr BTuned kBTuned[] = {
     {8224, 2560, EPI_STORE, {8, 1, 256, 1}},    // DeltaNet in-projection: 13.8 us (15.5)
     {2560, 2048, EPI_RESID, {16, 1, 160, 1}},   // output projections: 6.5 us (7.9)
     {151936, 2560, EPI_STORE, {8, 2, 256, 1}},  // lm_head: 87.9 us (113.5)
+    // the config-1 shapes with K = 4096, in 4 K slices (then the ordered
+    // reduction), at 4 / 16 rows: 4096 x 4096 8.7 / 10.0 us (K-sliced form
+    // 11.6 / 13.0), 12288 x 4096 14.7 / 17.6 us (21.8 / 23.3)
+    {4096, 4096, EPI_STORE, {8, 2, 128, 4}},
+    {12288, 4096, EPI_STORE, {8, 2, 128, 4}},
 };
 
 bool b_lookup(int N, int K, int epi, BConfig* c) {
