@@ -1046,11 +1046,14 @@ int mm_run(const float* x, int ldx, float* rs, const float* nw, float eps, const
     const int rc = launch_split<NORM>(x, ldx, rs, nw, M, K, xh, st);
     if (rc != QLM_OK) return rc;
     if constexpr (TL) {  // tile-major weights: the double-buffered operand-order form
-        // 256 weight rows a workgroup where that still gives 256 workgroups
-        // or more, else 128 (the 2560-column projections: 160 workgroups
-        // of the wide form would leave 96 CUs idle)
+        // 256 weight rows a workgroup where that still gives 1024 workgroups
+        // or more (four rounds of the GPU), else 128, two workgroups a CU.
+        // Measured at 2047 rows (graph replays): gate/up 509 us wide against
+        // 515 narrow; the DeltaNet in-projection 306 against 278 us (528
+        // workgroups wide: two rounds and 16 more), attention q/k/v 213
+        // against 197, down 415 against 360 us
         const int bn = epi == EPI_SWIGLU ? 128 : 256;
-        const bool wide = (long)((N + bn - 1) / bn) * ((M + 127) / 128) >= 256;
+        const bool wide = (long)((N + bn - 1) / bn) * ((M + 127) / 128) >= 1024;
         if (epi == EPI_STORE)
             return wide ? launch_pf<RS, EPI_STORE, 4>(xh, K, q, sc, y, ldy, M, N, K, tm, st)
                         : launch_pf<RS, EPI_STORE, 2>(xh, K, q, sc, y, ldy, M, N, K, tm, st);
