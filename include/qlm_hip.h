@@ -149,6 +149,34 @@ int qlm_gemv_i4_mx_headnorm(const float* u, const float* ss, float eps, const ui
  * wave, workgroups), or QLM_ERR_SHAPE. Host only. */
 int qlm_gemv_i8_mx_shape(int N, int K, int epilogue, int* waves, int* ring, int* grid);
 
+/* ---- L2 prefetch plans (no reference counterpart: an MI355X scheduling aid) ----
+ * MI355X runs workgroup i of a launch on XCD i % 8, and each XCD's 4 MB L2
+ * keeps what one kernel read for the kernels after it. A plan lists a later
+ * kernel's operands by tile: segment s of tile t is bytes[s] bytes at
+ * base[s] + t * stride[s], read later by a workgroup on XCD t % 8, for
+ * t < tiles[s]. The entry points that take a plan (qlm_deltanet_decode_cols_pf)
+ * append workgroups that load every tile into the L2 of its XCD while their
+ * own latency-bound work runs. A plan changes no result, only where the later
+ * kernel finds its operands. Zero-initialise, then append. */
+#define QLM_L2_PLAN_SEGMENTS 8
+typedef struct qlm_l2_plan {
+    const void* base[QLM_L2_PLAN_SEGMENTS];
+    long long stride[QLM_L2_PLAN_SEGMENTS];
+    int bytes[QLM_L2_PLAN_SEGMENTS]; /* a multiple of 16, > 0 */
+    int tiles[QLM_L2_PLAN_SEGMENTS];
+    int nseg;
+} qlm_l2_plan;
+
+/* Appends the tiles that the workgroups of the tile-major M = 1 GEMV
+ * (qlm_gemv_i8_mx and its headnorm form with epilogue 0-2; the int4 forms
+ * when int4 != 0) over q_tiles / s_tiles read first: 16-row tile t (of each
+ * half, for SwiGLU) is read by workgroup t for t < that launch's grid, and
+ * tiles 0 .. min(max_tiles, grid) - 1 are appended, weights and group-32
+ * scales (per-row scales, 64 bytes a tile, are left out). QLM_ERR_SHAPE when
+ * no launch shape fits or the plan has no room for the segments. Host only. */
+int qlm_gemv_mx_l2_plan(const void* q_tiles, const float* s_tiles, int group, int int4, int N,
+                        int K, int epilogue, int max_tiles, qlm_l2_plan* plan);
+
 /* A4: the same matmul for M > 1 on the matrix cores (batched decode, prefill;
  * math_ops.cpp:845-871). Weights stay exact (int8 in bf16); each activation
  * is split into bf16 hi + lo and the per-group products are scaled in fp32,
@@ -357,6 +385,14 @@ int qlm_deltanet_decode_cols(const float* proj, int ldp, float* conv_state,
                              const float* conv_w_t, const float* A_log, const float* dt_bias,
                              const float* norm_w, float* state, const int* pos, float* u, int ldu,
                              float* ss, unsigned* ticket, int B, int H, int d, void* stream);
+/* The same, carrying out an L2 prefetch plan (see qlm_l2_plan; NULL or empty:
+ * none) in workgroups of its own beside the mixer's. A non-empty plan needs
+ * B = 1. Same results as qlm_deltanet_decode_cols. */
+int qlm_deltanet_decode_cols_pf(const float* proj, int ldp, float* conv_state,
+                                const float* conv_w_t, const float* A_log, const float* dt_bias,
+                                const float* norm_w, float* state, const int* pos, float* u,
+                                int ldu, float* ss, unsigned* ticket, int B, int H, int d,
+                                const qlm_l2_plan* plan, void* stream);
 
 /* ---- A13: DeltaNet prefill of one sequence -----------------------------------
  * Qwen3_5GatedDeltaNet::forward_chunk (attention.cpp:600-758): the mixer of

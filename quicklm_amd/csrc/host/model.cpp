@@ -3,6 +3,7 @@
 #include <algorithm>
 #include <chrono>
 #include <climits>
+#include <cstdlib>
 #include <cstring>
 #include <stdexcept>
 
@@ -176,6 +177,7 @@ void DecoderModel::load(const std::string& dir, int max_seq_len, const std::stri
     ws_ = std::make_unique<WeightStore>(dir);
     max_seq_ = max_seq_len;
     max_batch_ = max_batch;
+    if (const char* e = std::getenv("QLM_L2_PREFETCH")) l2_plan_ = std::atoi(e) != 0;
     check(qlm_stream_create(&stream_), "stream");
     math::set_stream(stream_);
 
@@ -347,6 +349,19 @@ void DecoderModel::reset_states() {
     check(qlm_stream_sync(stream_), "sync");
 }
 
+// Appends to `plan` the tiles that the one-row GEMV over weight B (N outputs,
+// K inputs, epilogue as qlm_gemv_i8_mx) reads first, where B has a
+// tile-major copy; nothing where no launch shape fits.
+static void plan_gemv_tiles(const Tensor& B, int N, int K, int epi, int max_tiles,
+                            qlm_l2_plan& plan) {
+    const void* q = B.int4_tiles ? static_cast<const void*>(B.int4_tiles)
+                                 : static_cast<const void*>(B.int8_tiles);
+    if (!q || B.is_native()) return;
+    const int rc = qlm_gemv_mx_l2_plan(q, B.int8_tile_scales, B.int8_group, B.int4_tiles ? 1 : 0,
+                                       N, K, epi, max_tiles, &plan);
+    if (rc != QLM_OK && rc != QLM_ERR_SHAPE) check(rc, "qlm_gemv_mx_l2_plan");
+}
+
 // One decode step for sequences [0, B): the forward of DecoderModel::forward
 // (model.cpp:151-199) with every layer's elementwise work fused into the
 // projections, followed by greedy sampling and the position advance.
@@ -371,12 +386,18 @@ void DecoderModel::enqueue_step(int B) {
             Tensor proj({B, PD_}, proj_.get<float>());
             proj.strides = {Pmax, 1};
             math::matmul_rmsnorm(hx, in_ln, eps, w.dn_in.view(), proj);
-            check(qlm_deltanet_decode_cols(proj_.get<float>(), Pmax, conv_state_[dn_i].get<float>(),
-                                           w.conv_wt.get<float>(), w.A_log.get<float>(),
-                                           w.dt_bias.get<float>(), w.dn_norm.get<float>(),
-                                           dn_state_[dn_i].get<float>(), pos_.get<int>(),
-                                           core_.get<float>(), CORE_, dn_ss_.get<float>(),
-                                           dn_ticket_.get<unsigned>(), 1, nh, d, stream_),
+            // the mixer leaves HBM mostly idle: its extra workgroups bring the
+            // out-projection's tiles into the L2 of the XCDs that will read them
+            qlm_l2_plan plan{};
+            if (l2_plan_) plan_gemv_tiles(w.dn_out.view(), H, HD_, 1, 1 << 30, plan);
+            check(qlm_deltanet_decode_cols_pf(proj_.get<float>(), Pmax,
+                                              conv_state_[dn_i].get<float>(),
+                                              w.conv_wt.get<float>(), w.A_log.get<float>(),
+                                              w.dt_bias.get<float>(), w.dn_norm.get<float>(),
+                                              dn_state_[dn_i].get<float>(), pos_.get<int>(),
+                                              core_.get<float>(), CORE_, dn_ss_.get<float>(),
+                                              dn_ticket_.get<unsigned>(), 1, nh, d, &plan,
+                                              stream_),
                   "deltanet");
             Tensor core({B, HD_}, core_.get<float>());
             core.strides = {CORE_, 1};

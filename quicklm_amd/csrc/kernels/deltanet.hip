@@ -17,6 +17,7 @@
 // one launch replaces steps 2-9 of the reference forward.
 
 #include "common.hpp"
+#include "l2_prefetch.hpp"
 
 namespace {
 
@@ -272,6 +273,7 @@ constexpr int kColThreads = 256;
 constexpr int kColRG = kColThreads / kColW;     // row groups
 constexpr int kColRows = kD / kColRG;           // state rows per thread
 static_assert(kColRows == 8 && kColW == 16, "a row group is one 16-lane DPP row: 8 q + 8 k");
+static_assert(kSplit % 8 == 0, "prefetching workgroups start on XCD 0");
 
 // lane n of this lane's 16-lane row
 template <int n>
@@ -285,7 +287,15 @@ __global__ __launch_bounds__(kColThreads) void k_deltanet_cols(
     const float* __restrict__ wt, const float* __restrict__ A_log,
     const float* __restrict__ dt_bias, const float* __restrict__ norm_w,
     float* __restrict__ state, const int* __restrict__ pos, float* __restrict__ u, int ldu,
-    float* __restrict__ ss, unsigned* __restrict__ ticket, int H) {
+    float* __restrict__ ss, unsigned* __restrict__ ticket, int H, qlm_l2_plan plan) {
+    // workgroups past the mixer's carry out the L2 plan (B = 1: blockIdx.x
+    // is the dispatch order; H * kSplit is a multiple of 8, so prefetching
+    // workgroup p sits on XCD p % 8)
+    if ((int)blockIdx.x >= H * kSplit) {
+        const int p = (int)blockIdx.x - H * kSplit;
+        l2_prefetch(plan, p % 8, p / 8, ((int)gridDim.x - H * kSplit) / 8);
+        return;
+    }
     constexpr int NWV = kColThreads / QLM_WAVE;
     __shared__ float red[NWV][kColW], red2[NWV][kColW];
     __shared__ float ssq[NWV][2];
@@ -636,11 +646,12 @@ extern "C" int qlm_deltanet_decode(const float* proj, int ldp, float* conv_state
     return qlm_launch_status();
 }
 
-extern "C" int qlm_deltanet_decode_cols(const float* proj, int ldp, float* conv_state,
-                                        const float* conv_w_t, const float* A_log,
-                                        const float* dt_bias, const float* norm_w, float* state,
-                                        const int* pos, float* u, int ldu, float* ss,
-                                        unsigned* ticket, int B, int H, int d, void* stream) {
+extern "C" int qlm_deltanet_decode_cols_pf(const float* proj, int ldp, float* conv_state,
+                                           const float* conv_w_t, const float* A_log,
+                                           const float* dt_bias, const float* norm_w,
+                                           float* state, const int* pos, float* u, int ldu,
+                                           float* ss, unsigned* ticket, int B, int H, int d,
+                                           const qlm_l2_plan* plan, void* stream) {
     if (!proj || !conv_state || !conv_w_t || !A_log || !dt_bias || !norm_w || !state || !u ||
         !ss || !ticket || B <= 0 || H <= 0)
         return QLM_ERR_ARG;
@@ -648,10 +659,26 @@ extern "C" int qlm_deltanet_decode_cols(const float* proj, int ldp, float* conv_
     if (ldp < 4 * H * d + 2 * H || ldu < H * d) return QLM_ERR_SHAPE;
     // the last workgroup copies the q/k inputs into the ring as float4
     if (ldp % 4 != 0 || (((uintptr_t)proj | (uintptr_t)conv_state) & 15u)) return QLM_ERR_SHAPE;
-    hipLaunchKernelGGL(k_deltanet_cols, dim3(H * kSplit, B), dim3(kColThreads), 0,
+    qlm_l2_plan pl{};
+    if (plan) {
+        if (!l2_plan_valid(*plan)) return QLM_ERR_ARG;
+        pl = *plan;
+    }
+    const int npf = l2_plan_workgroups(pl);
+    if (npf > 0 && B != 1) return QLM_ERR_SHAPE;  // XCD placement assumes a 1-D grid
+    hipLaunchKernelGGL(k_deltanet_cols, dim3(H * kSplit + npf, B), dim3(kColThreads), 0,
                        as_stream(stream), proj, ldp, conv_state, conv_w_t, A_log, dt_bias, norm_w,
-                       state, pos, u, ldu, ss, ticket, H);
+                       state, pos, u, ldu, ss, ticket, H, pl);
     return qlm_launch_status();
+}
+
+extern "C" int qlm_deltanet_decode_cols(const float* proj, int ldp, float* conv_state,
+                                        const float* conv_w_t, const float* A_log,
+                                        const float* dt_bias, const float* norm_w, float* state,
+                                        const int* pos, float* u, int ldu, float* ss,
+                                        unsigned* ticket, int B, int H, int d, void* stream) {
+    return qlm_deltanet_decode_cols_pf(proj, ldp, conv_state, conv_w_t, A_log, dt_bias, norm_w,
+                                       state, pos, u, ldu, ss, ticket, B, H, d, nullptr, stream);
 }
 
 extern "C" int qlm_deltanet_prefill(const float* proj, int ldp, int T, float* conv_state,

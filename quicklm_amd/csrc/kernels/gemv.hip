@@ -1577,6 +1577,41 @@ extern "C" int qlm_gemv_i8_mx_shape(int N, int K, int epilogue, int* waves, int*
     return QLM_OK;
 }
 
+extern "C" int qlm_gemv_mx_l2_plan(const void* q_tiles, const float* s_tiles, int group, int int4,
+                                   int N, int K, int epilogue, int max_tiles, qlm_l2_plan* plan) {
+    if (!q_tiles || !plan || N <= 0 || K <= 0 || max_tiles < 0) return QLM_ERR_ARG;
+    if (epilogue < EPI_STORE || epilogue > EPI_SWIGLU) return QLM_ERR_ARG;
+    const bool rowscale = (group == K);
+    if (!rowscale && (group != 32 || !s_tiles)) return QLM_ERR_SHAPE;
+    if (int4 && rowscale) return QLM_ERR_SHAPE;
+    const MxConfig c = mx_config(N, K, epilogue, int4 != 0, group);
+    if (c.nw == 0 || K % 64 != 0) return QLM_ERR_SHAPE;
+    const int ntiles = (N + 15) / 16, nblk = K / 64, T = epilogue == EPI_SWIGLU ? 2 : 1;
+    const int grid = c.grid < ntiles ? c.grid : ntiles;  // as launch_mx
+    const int tiles = max_tiles < grid ? max_tiles : grid;
+    const int nseg = T * (rowscale ? 1 : 2);
+    if (plan->nseg < 0 || plan->nseg + nseg > QLM_L2_PLAN_SEGMENTS) return QLM_ERR_SHAPE;
+    if (tiles == 0) return QLM_OK;
+    // fragment (tile t of half tt, block b) at (t + tt * ntiles) * nblk + b:
+    // 1 KB of int8 (512 B of int4) and 32 scales
+    const long long fq = int4 ? 512 : 1024, fs = 32 * sizeof(float);
+    for (int tt = 0; tt < T; ++tt) {
+        const long long f0 = (long long)tt * ntiles * nblk;
+        int s = plan->nseg++;
+        plan->base[s] = static_cast<const char*>(q_tiles) + f0 * fq;
+        plan->stride[s] = nblk * fq;
+        plan->bytes[s] = (int)(nblk * fq);
+        plan->tiles[s] = tiles;
+        if (rowscale) continue;
+        s = plan->nseg++;
+        plan->base[s] = reinterpret_cast<const char*>(s_tiles) + f0 * fs;
+        plan->stride[s] = nblk * fs;
+        plan->bytes[s] = (int)(nblk * fs);
+        plan->tiles[s] = tiles;
+    }
+    return QLM_OK;
+}
+
 extern "C" int qlm_gemv_i8_mx(const float* x, const float* norm_w, float eps,
                               const int8_t* q_tiles, const float* s_tiles, int group, float* y,
                               int N, int K, int epilogue, void* stream) {

@@ -22,6 +22,13 @@ class HipError(RuntimeError):
     pass
 
 
+class L2Plan(C.Structure):
+    """qlm_l2_plan: a later kernel's operands by tile (segment s of tile t:
+    bytes[s] bytes at base[s] + t * stride[s], for t < tiles[s])."""
+    _fields_ = [("base", C.c_void_p * 8), ("stride", C.c_longlong * 8), ("bytes", C.c_int * 8),
+                ("tiles", C.c_int * 8), ("nseg", C.c_int)]
+
+
 # name -> (restype, argtypes)
 _SIGS = {
     "qlm_error_string": (C.c_char_p, [_i]),
@@ -100,6 +107,9 @@ _SIGS = {
                                  _i, _vp]),
     "qlm_deltanet_decode_cols": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp,
                                       _vp, _i, _i, _i, _vp]),
+    "qlm_deltanet_decode_cols_pf": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i,
+                                         _vp, _vp, _i, _i, _i, C.POINTER(L2Plan), _vp]),
+    "qlm_gemv_mx_l2_plan": (_i, [_vp, _vp, _i, _i, _i, _i, _i, _i, C.POINTER(L2Plan)]),
     "qlm_gemv_i8_mx_headnorm": (_i, [_vp, _vp, _f, _vp, _vp, _i, _vp, _i, _i, _i, _vp]),
     "qlm_gemv_i4_mx_headnorm": (_i, [_vp, _vp, _f, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "qlm_gqa_workspace_bytes": (_sz, [_i, _i, _i, _i]),

@@ -85,3 +85,77 @@ def test_noalloc_attention_rejects_oversize_on_host():
                                           None) == -1  # ctx > max_seq
     assert L.qlm_attention_decode_noalloc(fake, fake, fake, 1, 100, 50, fake, 1, 16, 2, 96,
                                           None) == -2  # head dim
+
+
+def test_l2_plan_of_the_4b_projections():
+    """qlm_gemv_mx_l2_plan (host only) lists, per half, the tiles the
+    one-row GEMV's workgroups read first: tile t of the tile-major copy at
+    t * (K / 64) fragments, the plan of a whole matrix ending exactly where
+    the layout's bytes end, and never more tiles than the launch has
+    workgroups."""
+    from quicklm_amd import hip
+
+    L = hip.lib()
+    q, s = 1 << 32, 1 << 36  # never dereferenced: the builder only does arithmetic
+
+    def layout(rows, K, group, halves):
+        qb, sb = ctypes.c_size_t(), ctypes.c_size_t()
+        assert L.qlm_mx_layout_bytes(rows, K, group, halves, ctypes.byref(qb),
+                                     ctypes.byref(sb)) == 0
+        return qb.value, sb.value
+
+    def grid(N, K, epi):
+        w, r, g = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+        assert L.qlm_gemv_i8_mx_shape(N, K, epi, ctypes.byref(w), ctypes.byref(r),
+                                      ctypes.byref(g)) == 0
+        return g.value
+
+    # out-projection 2560 x 2048, residual epilogue, group-32 scales
+    p = hip.L2Plan()
+    assert L.qlm_gemv_mx_l2_plan(q, s, 32, 0, 2560, 2048, 1, 1 << 30, ctypes.byref(p)) == 0
+    qb, sb = layout(2560, 2048, 32, 1)
+    assert p.nseg == 2 and list(p.tiles[:2]) == [160, 160] and grid(2560, 2048, 1) >= 160
+    assert (p.base[0], p.base[1]) == (q, s)
+    assert p.base[0] + p.tiles[0] * p.stride[0] == q + qb and p.bytes[0] == p.stride[0]
+    assert p.base[1] + p.tiles[1] * p.stride[1] == s + sb and p.bytes[1] == p.stride[1]
+
+    # gate/up [2F, K]: both halves, first tiles only (one per workgroup)
+    F, H = 9728, 2560
+    g = grid(F, H, 2)
+    assert L.qlm_gemv_mx_l2_plan(q, s, 32, 0, F, H, 2, 1 << 30, ctypes.byref(p)) == 0
+    qb, sb = layout(F, H, 32, 2)
+    assert p.nseg == 6 and list(p.tiles[2:6]) == [g] * 4 and g < F // 16
+    assert p.base[2] == q and p.base[4] == q + qb // 2  # half 1 starts mid-layout
+    assert p.base[3] == s and p.base[5] == s + sb // 2
+    assert p.stride[2] == (H // 64) * 1024 and p.stride[3] == (H // 64) * 128
+
+    # no room for four more segments: refused, the plan unchanged
+    assert L.qlm_gemv_mx_l2_plan(q, s, 32, 0, F, H, 2, 1 << 30, ctypes.byref(p)) == -2
+    assert p.nseg == 6
+
+    # fewer tiles on request; int4 halves the weight bytes; per-row scales
+    # add no segment
+    p = hip.L2Plan()
+    assert L.qlm_gemv_mx_l2_plan(q, s, 32, 1, 2560, 2048, 1, 24, ctypes.byref(p)) == 0
+    assert p.nseg == 2 and p.tiles[0] == 24 and p.bytes[0] == 32 * 512
+    p = hip.L2Plan()
+    assert L.qlm_gemv_mx_l2_plan(q, s, 2048, 0, 2560, 2048, 1, 1 << 30, ctypes.byref(p)) == 0
+    assert p.nseg == 1 and p.bytes[0] == 32 * 1024
+    assert L.qlm_gemv_mx_l2_plan(q, s, 32, 0, 2560, 2000, 1, 8, ctypes.byref(p)) == -2  # K % 64
+
+
+def test_mixer_plan_checks_run_before_any_launch():
+    """qlm_deltanet_decode_cols_pf rejects a malformed plan (-1) and a plan
+    with B > 1 (-2) on the host."""
+    from quicklm_amd import hip
+
+    L = hip.lib()
+    fake = 4096
+    p = hip.L2Plan()
+    p.nseg, p.base[0], p.stride[0], p.bytes[0], p.tiles[0] = 1, fake, 1024, 1000, 8  # 1000 % 16
+    H, d = 16, 128
+    args = (fake, 4 * H * d + 2 * H, fake, fake, fake, fake, fake, fake, fake, fake, H * d, fake,
+            fake)
+    assert L.qlm_deltanet_decode_cols_pf(*args, 1, H, d, ctypes.byref(p), None) == -1
+    p.bytes[0] = 1024
+    assert L.qlm_deltanet_decode_cols_pf(*args, 2, H, d, ctypes.byref(p), None) == -2

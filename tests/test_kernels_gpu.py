@@ -926,6 +926,59 @@ def test_deltanet_decode_cols(hip, orc, rng, B, H):
         assert np.all(tk[:, 0] == 8 * (step + 1)) and not tk[:, 1:].any()
 
 
+@pytest.mark.parametrize("plan_kind", ["out", "out+gate_up"])
+def test_deltanet_decode_cols_with_l2_plan(hip, rng, plan_kind):
+    """The mixer carrying an L2 prefetch plan (the 4B out-projection's tiles,
+    and the gate/up projection's first tiles, as the engine passes them)
+    writes the same bits as without one: u, the partial sums, the state, the
+    conv ring and the tickets, over 3 steps of two copies of the inputs."""
+    H, d = 16, 128
+    HD = H * d
+    ldp = 4 * HD + 2 * H
+    Hm, F = 2560, 9728
+    plan = hip.L2Plan()
+    keep = []
+    for N, K, epi, halves in [(Hm, HD, 1, 1), (F, Hm, 2, 2)][:1 if plan_kind == "out" else 2]:
+        qb, sb = C.c_size_t(), C.c_size_t()
+        hip.check(hip.lib().qlm_mx_layout_bytes(N, K, 32, halves, C.byref(qb), C.byref(sb)))
+        qz, sz = hip.DeviceBuffer(qb.value), hip.DeviceBuffer(sb.value)
+        qz.zero()
+        sz.zero()
+        keep += [qz, sz]
+        hip.call("qlm_gemv_mx_l2_plan", qz, sz, 32, 0, N, K, epi, 1 << 30, C.byref(plan))
+    assert plan.nseg == (2 if plan_kind == "out" else 6)
+    wt = (rng.standard_normal((4, 3 * HD)) * 0.3).astype(np.float32)
+    A_log = np.log(rng.uniform(1, 16, H)).astype(np.float32)
+    dtb = (rng.standard_normal(H) * 0.5 - 4).astype(np.float32)
+    nw = (1 + rng.standard_normal(d) * 0.02).astype(np.float32)
+    conv = (rng.standard_normal((1, 3, 3 * HD)) * 0.5).astype(np.float32)
+    S = (rng.standard_normal((1, H, d, d)) * 0.01).astype(np.float32)
+    dwt, dA, ddt, dnw = dev(hip, wt), dev(hip, A_log), dev(hip, dtb), dev(hip, nw)
+    runs = []
+    for _ in range(2):
+        tk = hip.DeviceBuffer(H * 32 * 4)
+        tk.zero()
+        runs.append(dict(conv=dev(hip, conv), S=dev(hip, S), u=hip.DeviceBuffer(HD * 4),
+                         ss=hip.DeviceBuffer(H * 8 * 4), tk=tk))
+    for step in range(3):
+        proj = dev(hip, (rng.standard_normal((1, ldp)) * 0.6).astype(np.float32))
+        pos = dev(hip, np.array([step + 5], np.int32))
+        say("deltanet_decode_cols l2 plan", plan_kind, step)
+        for r, pl in zip(runs, (None, C.byref(plan))):
+            hip.call("qlm_deltanet_decode_cols_pf", proj, ldp, r["conv"], dwt, dA, ddt, dnw,
+                     r["S"], pos, r["u"], HD, r["ss"], r["tk"], 1, H, d, pl, None)
+        a, b = runs
+        assert np.array_equal(a["u"].to_numpy(HD, np.float32), b["u"].to_numpy(HD, np.float32))
+        assert np.array_equal(a["ss"].to_numpy(H * 8, np.float32),
+                              b["ss"].to_numpy(H * 8, np.float32))
+        assert np.array_equal(a["S"].to_numpy(S.size, np.float32),
+                              b["S"].to_numpy(S.size, np.float32))
+        assert np.array_equal(a["conv"].to_numpy(conv.size, np.float32),
+                              b["conv"].to_numpy(conv.size, np.float32))
+        assert np.array_equal(a["tk"].to_numpy(H * 32, np.uint32),
+                              b["tk"].to_numpy(H * 32, np.uint32))
+
+
 @pytest.mark.parametrize("group", [32, "K", "int4"])
 def test_gemv_mx_headnorm(hip, orc, rng, group):
     """The out-projection over the column-split mixer's output: x = u scaled
