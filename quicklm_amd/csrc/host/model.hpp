@@ -182,8 +182,8 @@ class DecoderModel : public GreedyModel {
     int max_seq_ = 0, max_batch_ = 0, group_ = 32;
     bool int4_ = false;  // --precision int4: Q4_0 weights (lm_head included)
     bool native_ = false;  // --precision bf16: weights kept in the checkpoint dtype
-    // whether the batch-1 DeltaNet mixer brings the out-projection's tiles
-    // into L2 (env QLM_L2_PREFETCH=0 turns it off)
+    // whether the batch-1 DeltaNet mixer brings the out-projection's int8
+    // tiles into L2 (env QLM_L2_PREFETCH=0 turns it off)
     bool l2_plan_ = true;
     int HD_ = 0, PD_ = 0, QR_ = 0, PQ_ = 0, CORE_ = 0;
     size_t weight_bytes_ = 0;
