@@ -162,7 +162,7 @@ int qlm_gemv_i8_mx_shape(int N, int K, int epilogue, int* waves, int* ring, int*
 typedef struct qlm_l2_plan {
     const void* base[QLM_L2_PLAN_SEGMENTS];
     long long stride[QLM_L2_PLAN_SEGMENTS];
-    int bytes[QLM_L2_PLAN_SEGMENTS]; /* a multiple of 16, > 0 */
+    int bytes[QLM_L2_PLAN_SEGMENTS]; /* a multiple of 16, > 0 (bases and strides too) */
     int tiles[QLM_L2_PLAN_SEGMENTS];
     int nseg;
 } qlm_l2_plan;

@@ -32,14 +32,20 @@ inline int l2_plan_workgroups(const qlm_l2_plan& plan) {
     return (int)(wg > 256 ? 256 : wg);
 }
 
-// Whether `plan` is well formed (segment count, sizes, pointers).
+// Whether `plan` is well formed: segment count, sizes, 16-byte aligned
+// pointers and strides (each lane loads 16 aligned bytes), and at most 2^26
+// pieces in all (64 GB; the kernel counts pieces in 32-bit integers).
 inline bool l2_plan_valid(const qlm_l2_plan& plan) {
     if (plan.nseg < 0 || plan.nseg > QLM_L2_PLAN_SEGMENTS) return false;
-    for (int s = 0; s < plan.nseg; ++s)
-        if (!plan.base[s] || plan.bytes[s] <= 0 || plan.bytes[s] % 16 != 0 || plan.tiles[s] < 0 ||
-            plan.stride[s] < 0)
+    long long pieces = 0;
+    for (int s = 0; s < plan.nseg; ++s) {
+        if (!plan.base[s] || (reinterpret_cast<uintptr_t>(plan.base[s]) & 15u) ||
+            plan.bytes[s] <= 0 || plan.bytes[s] % 16 != 0 || plan.tiles[s] < 0 ||
+            plan.stride[s] < 0 || plan.stride[s] % 16 != 0)
             return false;
-    return true;
+        pieces += (long long)plan.tiles[s] * ((plan.bytes[s] + kL2Piece - 1) / kL2Piece);
+    }
+    return pieces <= (1ll << 26);
 }
 
 // Workgroup k of the `per` prefetching workgroups on XCD `xcd` loads its

@@ -157,5 +157,11 @@ def test_mixer_plan_checks_run_before_any_launch():
     args = (fake, 4 * H * d + 2 * H, fake, fake, fake, fake, fake, fake, fake, fake, H * d, fake,
             fake)
     assert L.qlm_deltanet_decode_cols_pf(*args, 1, H, d, ctypes.byref(p), None) == -1
-    p.bytes[0] = 1024
+    p.bytes[0], p.base[0] = 1024, fake + 8  # base not 16-byte aligned
+    assert L.qlm_deltanet_decode_cols_pf(*args, 1, H, d, ctypes.byref(p), None) == -1
+    p.base[0], p.stride[0] = fake, 1000  # stride not a multiple of 16
+    assert L.qlm_deltanet_decode_cols_pf(*args, 1, H, d, ctypes.byref(p), None) == -1
+    p.stride[0], p.tiles[0] = 1024, 1 << 27  # more pieces than the kernel counts
+    assert L.qlm_deltanet_decode_cols_pf(*args, 1, H, d, ctypes.byref(p), None) == -1
+    p.tiles[0] = 8
     assert L.qlm_deltanet_decode_cols_pf(*args, 2, H, d, ctypes.byref(p), None) == -2
