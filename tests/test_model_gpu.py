@@ -104,6 +104,26 @@ def test_graph_replay_equals_eager(engine, golden):
     assert np.array_equal(la, lb)
 
 
+def test_l2_plan_changes_no_result(hip, tiny_dir, golden, engine, monkeypatch):
+    """The batch-1 mixer's L2 plan (on by default) moves bytes into the
+    caches only: an engine loaded with QLM_L2_PREFETCH=0 decodes the same
+    tokens with bit-identical last logits."""
+    from quicklm_amd.engine import Engine
+
+    p = golden["prompt"][None, :40]
+    a, _, _ = engine.generate(p, 16)
+    la = engine.last_logits(0)
+    monkeypatch.setenv("QLM_L2_PREFETCH", "0")
+    e = Engine(tiny_dir, max_seq_len=256, max_batch=1, precision="int8")
+    try:
+        b, _, _ = e.generate(p, 16)
+        lb = e.last_logits(0)
+    finally:
+        e.close()
+    assert np.array_equal(a, b)
+    assert np.array_equal(la, lb)
+
+
 ROWS = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "tiny_greedy_rows.npz")
 
 
