@@ -926,27 +926,41 @@ def test_deltanet_decode_cols(hip, orc, rng, B, H):
         assert np.all(tk[:, 0] == 8 * (step + 1)) and not tk[:, 1:].any()
 
 
-@pytest.mark.parametrize("plan_kind", ["out", "out+gate_up"])
+@pytest.mark.parametrize("plan_kind", ["out", "out+gate_up", "few", "row", "int4"])
 def test_deltanet_decode_cols_with_l2_plan(hip, rng, plan_kind):
-    """The mixer carrying an L2 prefetch plan (the 4B out-projection's tiles,
-    and the gate/up projection's first tiles, as the engine passes them)
-    writes the same bits as without one: u, the partial sums, the state, the
-    conv ring and the tickets, over 3 steps of two copies of the inputs."""
+    """The mixer carrying an L2 prefetch plan writes the same bits as without
+    one: u, the partial sums, the state, the conv ring and the tickets, over
+    3 steps of two copies of the inputs. Plans: the 4B out-projection's tiles
+    (as the engine passes them), with the gate/up projection's first tiles,
+    3 tiles only (XCDs 3-7 get none), per-row scales (weights only) and int4
+    tiles (512-byte fragments)."""
     H, d = 16, 128
     HD = H * d
     ldp = 4 * HD + 2 * H
     Hm, F = 2560, 9728
+    cases = {"out": [(Hm, HD, 1, 1, 32, 0, 1 << 30)],
+             "out+gate_up": [(Hm, HD, 1, 1, 32, 0, 1 << 30), (F, Hm, 2, 2, 32, 0, 1 << 30)],
+             "few": [(Hm, HD, 1, 1, 32, 0, 3)],
+             "row": [(Hm, HD, 1, 1, HD, 0, 1 << 30)],
+             "int4": [(Hm, HD, 1, 1, 32, 1, 1 << 30)]}[plan_kind]
     plan = hip.L2Plan()
     keep = []
-    for N, K, epi, halves in [(Hm, HD, 1, 1), (F, Hm, 2, 2)][:1 if plan_kind == "out" else 2]:
+    for N, K, epi, halves, group, int4, max_tiles in cases:
         qb, sb = C.c_size_t(), C.c_size_t()
-        hip.check(hip.lib().qlm_mx_layout_bytes(N, K, 32, halves, C.byref(qb), C.byref(sb)))
-        qz, sz = hip.DeviceBuffer(qb.value), hip.DeviceBuffer(sb.value)
+        if int4:
+            hip.check(hip.lib().qlm_mx4_layout_bytes(N, K, halves, C.byref(qb), C.byref(sb)))
+        else:
+            hip.check(hip.lib().qlm_mx_layout_bytes(N, K, group, halves, C.byref(qb),
+                                                    C.byref(sb)))
+        qz, sz = hip.DeviceBuffer(qb.value), hip.DeviceBuffer(max(sb.value, 4 * N * halves))
         qz.zero()
         sz.zero()
         keep += [qz, sz]
-        hip.call("qlm_gemv_mx_l2_plan", qz, sz, 32, 0, N, K, epi, 1 << 30, C.byref(plan))
-    assert plan.nseg == (2 if plan_kind == "out" else 6)
+        hip.call("qlm_gemv_mx_l2_plan", qz, sz, group, int4, N, K, epi, max_tiles,
+                 C.byref(plan))
+    assert plan.nseg == {"out": 2, "out+gate_up": 6, "few": 2, "row": 1, "int4": 2}[plan_kind]
+    if plan_kind == "few":
+        assert list(plan.tiles[:2]) == [3, 3]
     wt = (rng.standard_normal((4, 3 * HD)) * 0.3).astype(np.float32)
     A_log = np.log(rng.uniform(1, 16, H)).astype(np.float32)
     dtb = (rng.standard_normal(H) * 0.5 - 4).astype(np.float32)
