@@ -26,6 +26,12 @@ constexpr int kThreads = 512;
 constexpr int kRowGroups = kThreads / 32;     // 16
 constexpr int kRowsPer = kD / kRowGroups;      // 8
 
+// The position of a call without a position array: a zero in device
+// memory, so the position is read by an unconditional load (a load under a
+// branch is waited for where the branch ends, before every other operand
+// has even been requested).
+__device__ int g_pos_zero = 0;
+
 struct DnShared {
     float q[kD], k[kD], v[kD];
     float pad[kD];  // conv results of the threads past the 3d channels (unused)
@@ -143,6 +149,10 @@ __global__ __launch_bounds__(kThreads) void k_deltanet_decode(
     float* __restrict__ state, const int* __restrict__ pos, float* __restrict__ out, int ldo,
     int H) {
     __shared__ DnShared sh;
+    // every argument is read before the position is requested, so the
+    // first wait for arguments does not also wait for the position
+    asm volatile("" ::"s"(proj), "s"(ldp), "s"(conv_state), "s"(wt), "s"(A_log), "s"(dt_bias),
+                 "s"(norm_w), "s"(state), "s"(pos), "s"(out), "s"(ldo), "s"(H));
     const int h = blockIdx.x;
     const int b = blockIdx.y;
     const int tid = threadIdx.x;
@@ -157,8 +167,10 @@ __global__ __launch_bounds__(kThreads) void k_deltanet_decode(
     // loads complete in order, so the conv, norms and gates below wait only
     // for their own operands while the state is still arriving. Every load
     // is unconditional (clamped index; unused values are dropped), since a
-    // load under a branch is waited for where the branch ends.
-    const int pb = pos ? pos[b] : 0;
+    // load under a branch is waited for where the branch ends. The position
+    // stays a vector value until every operand is requested: moved to a
+    // scalar register at once, it would be waited for before them.
+    int pbv = *(pos ? pos + b : &g_pos_zero);
     // conv operands: channel ch = sec*HD + h*d + t for tid < 3d
     const bool conv_t = tid < 3 * kD;
     const int sec = tid / kD, t = tid % kD;
@@ -177,6 +189,8 @@ __global__ __launch_bounds__(kThreads) void k_deltanet_decode(
     const float nwj = norm_w[tid & (kD - 1)];
     float4 s[kRowsPer];
     dn_load_state(Sh, s);
+    asm volatile("" : "+v"(pbv));
+    const int pb = __builtin_amdgcn_readfirstlane(pbv);
 
     // conv1d (kernel 4, taps chronological from the oldest ring row) + SiLU,
     // computed and stored to LDS by every thread (the others into a pad row),
@@ -288,6 +302,11 @@ __global__ __launch_bounds__(kColThreads) void k_deltanet_cols(
     const float* __restrict__ dt_bias, const float* __restrict__ norm_w,
     float* __restrict__ state, const int* __restrict__ pos, float* __restrict__ u, int ldu,
     float* __restrict__ ss, unsigned* __restrict__ ticket, int H, qlm_l2_plan plan) {
+    // The mixer's arguments are read together with H, before the branch
+    // below: otherwise the compiler reads H alone, branches, and only then
+    // requests the rest, one more round trip before the first operand load.
+    asm volatile("" ::"s"(proj), "s"(ldp), "s"(conv_state), "s"(wt), "s"(A_log), "s"(dt_bias),
+                 "s"(norm_w), "s"(state), "s"(pos), "s"(u), "s"(ldu), "s"(ss), "s"(ticket));
     // workgroups past the mixer's carry out the L2 plan (B = 1: blockIdx.x
     // is the dispatch order; H * kSplit is a multiple of 8, so prefetching
     // workgroup p sits on XCD p % 8)
@@ -314,7 +333,7 @@ __global__ __launch_bounds__(kColThreads) void k_deltanet_cols(
     // Operands, all unconditional: the position, this thread's q/k channel
     // (row rg*8 + j%8 of q or k), the v channel of column col, z, gain and
     // gates, then the state slice rows rg*8 .. rg*8+7 of column col.
-    const int pb = pos ? pos[b] : 0;
+    const int pb = *(pos ? pos + b : &g_pos_zero);
     const int chqk = (isk ? HD : 0) + h * kD + rg * kColRows + (j & 7);
     const int chv = 2 * HD + h * kD + col;
     float rq[3], wq[4], rv[3], wv[4];
