@@ -35,6 +35,15 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kNW = kThreads / QLM_WAVE;
 
+// Position reads: a launch with a position array reads pos[b], one without
+// reads this zero and ignores it, so the read is one unconditional load
+// (not a load under a branch, which the compiler waits for where the
+// branch ends). The kernels also name every argument in an empty asm at
+// their start: without it the compiler reads a few arguments, waits and
+// branches, then reads the rest, one more scalar round trip before the
+// first operand load.
+__device__ int g_pos_zero = 0;
+
 template <typename KV>
 __device__ __forceinline__ void load8(const KV* p, float (&o)[8]);
 template <>
@@ -93,11 +102,15 @@ __global__ __launch_bounds__(kThreads) void k_attn(
     __shared__ float kvp[2][HD];
     __shared__ float fsc[G], mstat[G], lstat[G];
 
+    asm volatile("" ::"s"(qsrc), "s"(ldq), "s"(qhs), "s"(qn_w), "s"(kn_w), "s"(cos_tab),
+                 "s"(sin_tab), "s"(rot), "s"(kc), "s"(vc), "s"(max_seq), "s"(n_kv), "s"(pos),
+                 "s"(ctx), "s"(pstep), "s"(kvb), "s"(work), "s"(nchunks), "s"(n_q), "s"(scale));
     const int chunk = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     // query row b sits at position pos[b], or ctx-1 + pstep*b (pstep = 1:
     // consecutive prompt rows over one shared cache, kvb = 0)
-    const int p = pos ? pos[b] : ctx - 1 + pstep * b;
+    const int pp = *(pos ? pos + b : &g_pos_zero);
+    const int p = pos ? pp : ctx - 1 + pstep * b;
     const int L = min(p + 1, max_seq);
     const int nc = (L + CH - 1) / CH;
     if (chunk >= nc || p < 0) return;
@@ -391,10 +404,13 @@ __global__ __launch_bounds__(kCombineThreads) void k_attn_combine(
     __shared__ float fs[kCombineTile];
     __shared__ float4 part[NG][C4];
     __shared__ float red[kCombineThreads / QLM_WAVE], red_l[kCombineThreads / QLM_WAVE];
+    asm volatile("" ::"s"(work), "s"(nchunks), "s"(CH), "s"(max_seq), "s"(pos), "s"(ctx),
+                 "s"(pstep), "s"(gate), "s"(ldg), "s"(ghs), "s"(out), "s"(ldo), "s"(n_q));
     const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
     const int c4 = tid % C4, cg = tid / C4;
     const int cb = blockIdx.z * C4;  // first float4 column of this workgroup
-    const int L = min(pos ? pos[b] + 1 : ctx + pstep * b, max_seq);
+    const int pp = *(pos ? pos + b : &g_pos_zero);
+    const int L = min(pos ? pp + 1 : ctx + pstep * b, max_seq);
     const int nc = min(nchunks, (L + CH - 1) / CH);
     const int last = max(nc, 1) - 1;  // clamp target of the unconditional loads
     const float* base = work + ((size_t)b * n_q + h) * nchunks * RS;

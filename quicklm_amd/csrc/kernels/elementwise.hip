@@ -161,6 +161,10 @@ __global__ void k_argmax_final(const float* __restrict__ pv, const int* __restri
                                int nslice, int* __restrict__ idx, int* __restrict__ tokens,
                                int ld_tokens, int* __restrict__ pos,
                                const int* __restrict__ prompt_len) {
+    // every argument read in one batch (otherwise the compiler reads some,
+    // waits, branches and reads the rest: a second round trip)
+    asm volatile("" ::"s"(pv), "s"(pi), "s"(nslice), "s"(idx), "s"(tokens), "s"(ld_tokens),
+                 "s"(pos), "s"(prompt_len));
     const int b = blockIdx.x;
     float bv = -INFINITY;
     int bi = 0x7fffffff;
@@ -188,6 +192,8 @@ __global__ void k_argmax_final(const float* __restrict__ pv, const int* __restri
 __global__ void k_embed(const float* __restrict__ table, int H, const int* __restrict__ tokens,
                         int ld_tokens, const int* __restrict__ pos, float* __restrict__ out,
                         int ldo, int vocab) {
+    asm volatile("" ::"s"(table), "s"(H), "s"(tokens), "s"(ld_tokens), "s"(pos), "s"(out),
+                 "s"(ldo), "s"(vocab));
     const int b = blockIdx.y;
     const int p = pos ? pos[b] : 0;
     int tok = tokens[(size_t)b * ld_tokens + p];

@@ -75,6 +75,10 @@ __global__ __launch_bounds__(NW * QLM_WAVE) void k_mm_t(
     const float* __restrict__ x, int ldx, const float* __restrict__ gain,
     const int8_t* __restrict__ qz, const float* __restrict__ sz, float* __restrict__ part,
     int M, int NR, int rows_half, int tiles_half, int tiles_total, int nblk, int bps) {
+    // every argument read in one batch (otherwise the compiler reads some,
+    // waits, branches and reads the rest: a second round trip)
+    asm volatile("" ::"s"(x), "s"(ldx), "s"(gain), "s"(qz), "s"(sz), "s"(part), "s"(M), "s"(NR),
+                 "s"(rows_half), "s"(tiles_half), "s"(tiles_total), "s"(nblk), "s"(bps));
     constexpr int NTH = NW * QLM_WAVE;
     __shared__ f32x4 red[NW * NT * QLM_WAVE];  // the waves' partial tiles
 
@@ -220,6 +224,9 @@ __global__ __launch_bounds__(NW * QLM_WAVE) void k_mm_b(
     const float* __restrict__ x, int ldx, const float* __restrict__ gain, float eps,
     const int8_t* __restrict__ qz, const float* __restrict__ sz, float* __restrict__ y, int ldy,
     int M, int N, int tiles_half, int nblk, int bps, float* __restrict__ part) {
+    // every argument read in one batch, as in k_mm_t
+    asm volatile("" ::"s"(x), "s"(ldx), "s"(gain), "s"(eps), "s"(qz), "s"(sz), "s"(y), "s"(ldy),
+                 "s"(M), "s"(N), "s"(tiles_half), "s"(nblk), "s"(bps), "s"(part));
     constexpr int H2 = EPI == EPI_SWIGLU ? 2 : 1;
     constexpr int NT = NTH * H2;  // fragments per ring slot
     constexpr int NTHR = NW * QLM_WAVE;
