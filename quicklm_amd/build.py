@@ -36,7 +36,12 @@ HIP_FLAGS = [
 # default accumulator-register form the group-32 prefill matmul copied every
 # product back (two v_accvgpr_read per MFMA before its scale FMA), at the same
 # register total.
-FILE_FLAGS = {"gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+# deltanet.hip: the column-split mixer's one ticket atomic (a single lane)
+# is issued as it is; the atomic optimizer would turn it into a wave
+# aggregation that waits for the returned value at once, in the middle of
+# the mixer's chain, where the value is needed only at the kernel's end.
+FILE_FLAGS = {"gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+              "deltanet.hip": ["-mllvm", "-amdgpu-atomic-optimizer-strategy=None"]}
 CXX_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function", "-pthread",
              "-I", INCLUDE, "-I", os.path.join(CSRC, "host")]
 
